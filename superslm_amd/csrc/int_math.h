@@ -1,0 +1,401 @@
+// Integer primitives of SuperSLM's forward path, shared by host and device code.
+//
+// Each function restates the reference primitive cited beside it (paths relative to the
+// reference root) and must stay bit-identical to it: the GPU results are compared byte for byte
+// against the CPU path.  128-bit intermediates use clang's __int128, which the AMDGPU backend
+// lowers to 64-bit pairs.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define SSLM_HD __host__ __device__ __forceinline__
+
+namespace sslm {
+
+typedef __int128 s128;
+typedef unsigned __int128 u128;
+
+constexpr int32_t kI32Min = -2147483647 - 1;
+constexpr int32_t kI32Max = 2147483647;
+constexpr int64_t kI64Max = 0x7fffffffffffffffLL;
+constexpr int64_t kI64Min = -kI64Max - 1;
+constexpr int64_t kSoftmaxMaxSafe = ((int64_t)1 << 62) >> 15;  // checked_chain_funnel.h:563
+
+struct Scale {
+	int64_t m;
+	int64_t e;
+};
+
+// src/intmath.cpp:230-236
+SSLM_HD int32_t srdhm(int32_t a, int32_t b) {
+	int64_t ab = (int64_t)a * (int64_t)b;
+	int64_t r = (ab + ((int64_t)1 << 30)) >> 31;
+	return r > kI32Max ? kI32Max : (int32_t)r;
+}
+
+// src/intmath.cpp:244-251 (int32 instance): x / 2^e, ties away from zero, e in [0,31]
+SSLM_HD int32_t rdbpot32(int32_t x, int e) {
+	uint32_t mask = ((uint32_t)1 << e) - 1u;
+	uint32_t rem = (uint32_t)x & mask;
+	uint32_t thr = (mask >> 1) + (x < 0 ? 1u : 0u);
+	return (x >> e) + (rem > thr ? 1 : 0);
+}
+
+// src/intmath.cpp:244-251 (int64 instance), e in [0,63]
+SSLM_HD int64_t rdbpot64(int64_t x, int e) {
+	uint64_t mask = ((uint64_t)1 << e) - 1u;
+	uint64_t rem = (uint64_t)x & mask;
+	uint64_t thr = (mask >> 1) + (x < 0 ? 1u : 0u);
+	return (x >> e) + (rem > thr ? 1 : 0);
+}
+
+// src/intmath.cpp:265-268 composed with forward_sites.cpp:461-470 (WSC1 fold: identity passes
+// the accumulator through, otherwise MBQM of its int32 truncation).
+SSLM_HD int64_t apply_fold(int64_t acc, int32_t identity, int32_t mult, int32_t shift) {
+	if (identity != 0) return acc;
+	return (int64_t)rdbpot32(srdhm((int32_t)acc, mult), shift);
+}
+
+// src/intmath.cpp:270-277
+SSLM_HD int32_t sat_shl32(int32_t x, int shift) {
+	if (shift <= 0) return x;
+	int64_t w = (int64_t)x << shift;
+	if (w > kI32Max) return kI32Max;
+	if (w < kI32Min) return kI32Min;
+	return (int32_t)w;
+}
+
+// forward_sites.cpp:472-481
+SSLM_HD int64_t apply_amp_fold(int64_t acc, int32_t identity, int32_t mult, int32_t exponent) {
+	if (identity != 0) return acc;
+	int32_t hi = srdhm((int32_t)acc, mult);
+	if (exponent >= 0) return (int64_t)rdbpot32(hi, exponent);
+	return (int64_t)sat_shl32(hi, -exponent);
+}
+
+SSLM_HD int clz64(uint64_t n) { return n == 0 ? 64 : __builtin_clzll(n); }
+
+// src/intmath.cpp:296-301
+SSLM_HD int64_t normalize_scale(int64_t d_prime, int* s_out) {
+	int p = 63 - clz64((uint64_t)d_prime);
+	int s = 30 - p;
+	*s_out = s;
+	return s >= 0 ? (d_prime << s) : (d_prime >> 1);
+}
+
+// src/intmath.cpp:303-333 -- 3 Newton steps from a minimax seed, 2 correction steps.
+SSLM_HD int64_t reciprocal(int64_t dn) {
+	const int64_t c32 = (2 * ((int64_t)48 << 31) + 17) / 34;
+	const int64_t c32_2 = (2 * ((int64_t)32 << 31) + 17) / 34;
+	int64_t y = c32 - ((c32_2 * dn) >> 31);
+	for (int i = 0; i < 3; ++i) {
+		int64_t dn_y = (int64_t)(((s128)dn * (s128)y) >> 31);
+		int64_t delta = ((int64_t)1 << 32) - dn_y;
+		y = (int64_t)(((s128)y * (s128)delta) >> 31);
+	}
+	for (int i = 0; i < 2; ++i) {
+		s128 res2 = ((s128)((int64_t)1 << 62) - (s128)y * (s128)dn) * 2;
+		if (res2 >= (s128)dn) {
+			y += 1;
+		} else if (res2 < -(s128)dn) {
+			y -= 1;
+		}
+	}
+	return y;
+}
+
+// src/intmath.cpp:476-490 -- clamp(round_away(x*127*R / 2^(62-s)), +-127).
+SSLM_HD int8_t requant_code(int64_t x, int64_t r, int s) {
+	int exponent = 62 - s;
+	uint64_t ax = x < 0 ? (~(uint64_t)x + 1u) : (uint64_t)x;
+	u128 prod = (u128)ax * (uint64_t)r * 127u;
+	u128 num = prod * 2 + ((u128)1 << exponent);
+	uint64_t mag = (uint64_t)(num >> (exponent + 1));
+	if (mag > 127u) mag = 127u;
+	int32_t q = (int32_t)mag;
+	return (int8_t)(x < 0 ? -q : q);
+}
+
+// Same composite for |x| <= 2^31 (the funnel's whole accepted domain): the product
+// |x|*127*R < 2^70 is formed from 64-bit halves without a full 128-bit multiply.
+SSLM_HD int8_t requant_code_small(int64_t x, uint64_t r, int s) {
+	int exponent = 62 - s;  // 32..63
+	uint64_t ax = x < 0 ? (uint64_t)(-x) : (uint64_t)x;
+	uint64_t a = ax * 127u;  // < 2^38
+	u128 prod = (u128)a * r;
+	u128 num = prod * 2 + ((u128)1 << exponent);
+	uint64_t mag = (uint64_t)(num >> (exponent + 1));
+	if (mag > 127u) mag = 127u;
+	int32_t q = (int32_t)mag;
+	return (int8_t)(x < 0 ? -q : q);
+}
+
+// src/intmath.cpp:502-524
+SSLM_HD int64_t isqrt(int64_t n) {
+	int64_t rem = n, root = 0, bit = (int64_t)1 << 62;
+	for (int i = 0; i < 32; ++i) {
+		int64_t trial = root + bit;
+		if (rem >= trial) {
+			rem -= trial;
+			root = (root >> 1) + bit;
+		} else {
+			root >>= 1;
+		}
+		bit >>= 2;
+	}
+	return root;
+}
+
+SSLM_HD int64_t sat_add64(int64_t a, int64_t b) {
+	int64_t out = (int64_t)((uint64_t)a + (uint64_t)b);
+	bool ovf = ((a >= 0) == (b >= 0)) && ((out >= 0) != (a >= 0));
+	if (!ovf) return out;
+	return a >= 0 ? kI64Max : kI64Min;
+}
+
+SSLM_HD int64_t sat_sub64(int64_t a, int64_t b) {
+	int64_t out = (int64_t)((uint64_t)a - (uint64_t)b);
+	bool ovf = ((a >= 0) != (b >= 0)) && ((out >= 0) != (a >= 0));
+	if (!ovf) return out;
+	return a >= 0 ? kI64Max : kI64Min;
+}
+
+// checked_chain_funnel.cpp:157-180
+SSLM_HD Scale combine_scale(Scale a, Scale b) {
+	int64_t e = sat_add64(sat_add64(a.e, b.e), 31);
+	int64_t m = srdhm((int32_t)a.m, (int32_t)b.m);
+	if (m < ((int64_t)1 << 30)) {
+		m <<= 1;
+		e -= 1;
+	}
+	return Scale{m, e};
+}
+
+SSLM_HD bool fits_i32(int64_t v) { return v >= kI32Min && v <= kI32Max; }
+
+// Reference forward status codes (include/superslm/checked_chain_funnel.h:68-284, same order).
+enum FwdStatus : int32_t {
+	kOk = 0,
+	kChainInputOutOfDomain = 1,
+	kLogitNarrowingOverflow = 2,
+	kIExpConstantsOutOfDomain = 3,
+	kCarriedScaleMantissaOutOfDomain = 4,
+	kSiluCompositionScaleOutOfDomain = 5,
+	kRdbpotExponentOutOfDomain = 6,
+	kSoftmaxRowWidthOutOfDomain = 7,
+	kTokenIdOutOfRange = 8,
+	kPositionOverCap = 9,
+	kSoftmaxKernelRefusedAfterGateAccepted = 20,
+	kResidualReconciliationMagnitudeOutOfDomain = 21,
+	kIExpScaleDerivationOutOfDomain = 23,
+	kBiasReconcileProductOutOfDomain = 24,
+};
+
+// The funnel's scale half (checked_chain_funnel.cpp:268-329): checks, the D'-derived (Dn, s, R)
+// and the left-associated fold of incoming factors, the site constant and (Dn, -s).
+// `d_prime` is the row's max |x| with the all-zero guard applied.  Returns a status; on Ok the
+// per-element codes are requant_code_small(x, r, s).
+struct FunnelPlan {
+	int64_t r;
+	int s;
+	Scale out;
+};
+
+SSLM_HD int32_t funnel_plan(uint64_t d_prime, const Scale* incoming, int n_in, Scale site, FunnelPlan* plan) {
+	for (int i = 0; i < n_in; ++i)
+		if (!fits_i32(incoming[i].m)) return kCarriedScaleMantissaOutOfDomain;
+	if (!fits_i32(site.m)) return kCarriedScaleMantissaOutOfDomain;
+	if (d_prime < 1) d_prime = 1;
+	if (d_prime > ((uint64_t)1 << 31)) return kChainInputOutOfDomain;
+	int s;
+	int64_t dn = normalize_scale((int64_t)d_prime, &s);
+	int64_t r = reciprocal(dn);
+	Scale run;
+	bool have = false;
+	for (int i = 0; i < n_in; ++i) {
+		run = have ? combine_scale(run, incoming[i]) : incoming[i];
+		have = true;
+		if (!fits_i32(run.m)) return kCarriedScaleMantissaOutOfDomain;
+	}
+	run = have ? combine_scale(run, site) : site;
+	if (!fits_i32(run.m)) return kCarriedScaleMantissaOutOfDomain;
+	run = combine_scale(run, Scale{dn, -(int64_t)s});
+	if (!fits_i32(run.m)) return kCarriedScaleMantissaOutOfDomain;
+	plan->r = r;
+	plan->s = s;
+	plan->out = run;
+	return kOk;
+}
+
+// forward_sites.cpp:389-395
+SSLM_HD int64_t composed_exponent(int64_t e_a, int64_t e_t) {
+	int64_t k = sat_sub64(62, sat_sub64(e_a, e_t));
+	if (k > 4096) k = 4096;
+	if (k < -4096) k = -4096;
+	return k;
+}
+
+// forward_sites.cpp:513-653 -- round_away(branch*m_a*r_t / 2^k), k = 62-(e_a-e_t); a negative k
+// is an exact left shift.  *clamped: the saturation-counter predicate; *exceeded: the true
+// magnitude does not fit int64.
+SSLM_HD int64_t landing_rescale(int64_t branch, int64_t m_a, int64_t r_t, int64_t k, bool* clamped,
+                                 bool* exceeded) {
+	bool neg = (branch < 0) != (m_a < 0);
+	uint64_t ab = branch < 0 ? (~(uint64_t)branch + 1u) : (uint64_t)branch;
+	uint64_t am = m_a < 0 ? (~(uint64_t)m_a + 1u) : (uint64_t)m_a;
+	u128 mag = (u128)ab * am * (uint64_t)r_t;
+	int64_t raw;
+	bool exc_clamp, exc_i64;
+	if (k >= 0) {
+		u128 doubled = mag + mag;
+		u128 one_k = k >= 128 ? (u128)0 : ((u128)1 << k);
+		u128 q = (k + 1 >= 128) ? (u128)0 : ((doubled + one_k) >> (k + 1));
+		uint64_t qhi = (uint64_t)(q >> 64), qlo = (uint64_t)q;
+		exc_clamp = (qhi != 0) || qlo > 127;
+		exc_i64 = (qhi != 0) || qlo > (uint64_t)kI64Max;
+		raw = (int64_t)qlo;
+	} else {
+		int sh = (int)(-k);
+		u128 shifted = sh >= 128 ? (u128)0 : (mag << sh);
+		if (sh >= 128) {
+			exc_clamp = mag != 0;
+			exc_i64 = exc_clamp;
+		} else {
+			bool lost = (shifted >> sh) != mag;
+			uint64_t shi = (uint64_t)(shifted >> 64), slo = (uint64_t)shifted;
+			exc_clamp = lost || shi != 0 || slo > 127;
+			exc_i64 = lost || shi != 0 || slo > (uint64_t)kI64Max;
+		}
+		raw = (int64_t)(uint64_t)shifted;
+	}
+	if (neg) raw = (int64_t)(0u - (uint64_t)raw);
+	*clamped = exc_clamp || raw < -127 || raw > 127;
+	*exceeded = exc_i64;
+	return raw;
+}
+
+SSLM_HD int64_t clamp_code(int64_t v) { return v > 127 ? 127 : (v < -127 ? -127 : v); }
+
+// forward_sites.cpp:399-408
+SSLM_HD int64_t floor_div(int64_t a, int64_t b) {
+	int64_t q = a / b, r = a % b;
+	return (r != 0 && r < 0) ? q - 1 : q;
+}
+
+// src/intmath.cpp:782-792
+SSLM_HD void rope_pair(int32_t x, int32_t y, int32_t c, int32_t s, int64_t* ox, int64_t* oy) {
+	int64_t xr = (int64_t)x * c - (int64_t)y * s;
+	int64_t yr = (int64_t)x * s + (int64_t)y * c;
+	*ox = rdbpot64(xr, 30);
+	*oy = rdbpot64(yr, 30);
+}
+
+// src/silu_lut.cpp:16-67
+SSLM_HD int32_t silu_sigmoid_q15(const int32_t* table, int8_t code, int64_t m, int e) {
+	int64_t term = (int64_t)code * m;
+	int shift = e + 5 + 12;
+	int64_t pos = shift >= 0 ? (term << shift) : rdbpot64(term, -shift);
+	const int64_t hi_dom = (int64_t)1024 << 12;
+	pos += hi_dom / 2;
+	if (pos < 0) pos = 0;
+	else if (pos > hi_dom) pos = hi_dom;
+	int64_t i0 = pos >> 12;
+	if (i0 > 1023) i0 = 1023;
+	int64_t frac = pos - (i0 << 12);
+	int64_t lo = table[i0], hi = table[i0 + 1];
+	return (int32_t)(lo + rdbpot64(frac * (hi - lo), 12));
+}
+
+// checked_chain_funnel.cpp:402-405, 484-499
+SSLM_HD int32_t check_silu_scale(int64_t m, int64_t e) {
+	const int64_t max_abs_m = ((int64_t)1 << 31) - 1;
+	if (m < -max_abs_m || m > max_abs_m) return kSiluCompositionScaleOutOfDomain;
+	if (e < -80 || e > 8) return kSiluCompositionScaleOutOfDomain;
+	return kOk;
+}
+
+// src/intmath.cpp:702-778 -- the C30 derivation of the i-exp triple from a carried scale.
+// Returns 0 on success (the reference's kOk), non-zero for every rejection.
+SSLM_HD int iexp_scale_constants(int64_t m, int64_t e, int64_t ln2_q, int64_t b_q, int64_t ca_q, int64_t* q_ln2,
+                                 int64_t* q_b, int64_t* q_c) {
+	const int fmt = 30;
+	if (ln2_q <= 0 || b_q <= 0 || ca_q <= 0) return 1;
+	int64_t sh_ln2 = sat_add64(sat_add64(fmt, 62), e);
+	int64_t sh_b = sat_add64(sat_add64(fmt, 62), e);
+	int64_t sh_c = sat_add64(sat_add64(fmt, 124), sat_add64(e, e));
+	int64_t mn = sh_ln2 < sh_b ? sh_ln2 : sh_b;
+	if (sh_c < mn) mn = sh_c;
+	if (mn < 0) return 2;
+	uint64_t r = (uint64_t)reciprocal(m);
+	u128 n_ln2 = (u128)(uint64_t)ln2_q * r;
+	u128 n_b = (u128)(uint64_t)b_q * r;
+	u128 n_c = (u128)r * r * (uint64_t)ca_q;
+	u128 f_ln2 = sh_ln2 >= 128 ? (u128)0 : (n_ln2 >> sh_ln2);
+	u128 f_b = sh_b >= 128 ? (u128)0 : (n_b >> sh_b);
+	u128 f_c = sh_c >= 128 ? (u128)0 : (n_c >> sh_c);
+	if (f_ln2 > (u128)kI64Max || f_b > (u128)kI64Max || f_c > (u128)kI64Max) return 3;
+	*q_ln2 = (int64_t)f_ln2;
+	*q_b = (int64_t)f_b;
+	*q_c = (int64_t)f_c;
+	return 0;
+}
+
+// checked_chain_funnel.cpp:520-583
+SSLM_HD int32_t check_softmax_width(int64_t q_b, int64_t q_c, int64_t width) {
+	if (q_c < 0) return kSoftmaxRowWidthOutOfDomain;
+	if (width <= 0) return kSoftmaxRowWidthOutOfDomain;
+	s128 m128 = (s128)q_b * q_b + (s128)q_c;
+	if (m128 > (s128)kI64Max || m128 > (s128)kSoftmaxMaxSafe) return kSoftmaxRowWidthOutOfDomain;
+	int64_t m = (int64_t)m128;
+	if (m != 0 && width > kI64Max / m) return kSoftmaxRowWidthOutOfDomain;
+	return kOk;
+}
+
+// src/intmath.cpp:580-668 + :540-567 for one softmax element (intmath.cpp:859-888): returns
+// the i-exp value, or -1 when the element is refused (a kBad* construction, or a value outside
+// [0, M]).  `shifted` = score - row max (<= 0 always, so kBadQ never fires).
+SSLM_HD int64_t iexp_element(int64_t shifted, int64_t q_ln2, int64_t q_b, int64_t q_c, int64_t m_ceiling) {
+	const int64_t max_qln2 = kI64Max / 30;
+	if (shifted > 0) return -1;
+	if (q_ln2 < 1 || q_ln2 > max_qln2) return -1;
+	int64_t clip_lo = -30 * q_ln2;
+	int64_t clipped = shifted < clip_lo ? clip_lo : shifted;
+	int64_t z = (-clipped) / q_ln2;
+	int64_t q_p = clipped + z * q_ln2;
+	if (q_b < kI64Min - q_p) return -1;
+	int64_t base = q_p + q_b;
+	s128 v = (s128)base * base + (s128)q_c;
+	int64_t value = (int64_t)(v >> z);
+	if (m_ceiling <= 0 || value < 0 || value > m_ceiling) return -1;
+	return value;
+}
+
+// The softmax's per-element ceiling M = q_b^2 + q_c when usable (intmath.cpp:831-851), else 0.
+SSLM_HD int64_t softmax_ceiling(int64_t q_b, int64_t q_c) {
+	s128 m128 = (s128)q_b * q_b + (s128)q_c;
+	bool usable = m128 <= (s128)kI64Max && m128 >= 1 && m128 <= (s128)kSoftmaxMaxSafe;
+	return usable ? (int64_t)m128 : 0;
+}
+
+// src/intmath.cpp:381-418 + checked_chain_funnel.cpp:454-482: the bias term
+// round_away(b*r_a / 2^(30+62+e_a)); false when the exponent or the sum with `acc` is out of
+// domain.
+SSLM_HD bool bias_term(int64_t b, int64_t r_a, int64_t e_a, int64_t acc, int64_t* out) {
+	s128 sum = (s128)30 + 62 + (s128)e_a;
+	if (sum < 0 || sum > 63) return false;
+	int exponent = (int)sum;
+	s128 wide = (s128)b * (s128)r_a;
+	uint64_t mask = ((uint64_t)1 << exponent) - 1u;
+	uint64_t rem = (uint64_t)wide & mask;
+	uint64_t thr = (mask >> 1) + (wide < 0 ? 1u : 0u);
+	s128 rounded = (wide >> exponent) + (rem > thr ? 1 : 0);
+	if (rounded != (s128)(int64_t)rounded) return false;
+	int64_t term = (int64_t)rounded;
+	uint64_t s = (uint64_t)acc + (uint64_t)term;
+	if (((((uint64_t)acc ^ (uint64_t)term) >> 63) == 0) && ((((uint64_t)acc ^ s) >> 63) != 0)) return false;
+	*out = term;
+	return true;
+}
+
+}  // namespace sslm

@@ -1,0 +1,212 @@
+// Kernel-side argument structures and launch wrappers for the SuperSLM HIP backend (gfx950).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "int_math.h"
+
+namespace sslm {
+
+// Per-token routing for one batched launch.  Decode batches gather one token per sequence;
+// a prefill chunk is T tokens of one sequence at consecutive positions.
+struct TokenInfo {
+	int64_t pos;     // KV position this token lands at (context_length at its start)
+	int32_t slot;    // sequence slot: stream state, saturation counter, status
+	int32_t block;   // KV pool block of the sequence
+};
+
+// Output segment of a fused projection GEMM (q|k|v or gate|up share one launch).
+enum SegMode : int32_t { kSegFunnel = 0, kSegWide = 1 };
+
+struct Segment {
+	int32_t n_begin, n_end;     // column range in the fused weight matrix
+	int32_t mode;               // SegMode
+	int32_t ld_out;             // row stride of `out` in elements
+	void* out;                  // int32 (funnel, saturated) or int64 (wide) [M, ld_out]
+	uint32_t* maxabs;           // funnel: per-token saturating max |value| (consumer resets)
+	const int32_t* fold;        // [n, 3] (identity, mult, shift)
+	const int64_t* bias;        // [n] BIA1 codes, or null
+	const int8_t* lora_b;       // [n, rank] or null
+	const int32_t* lora_dfold;  // [n, 3] (identity, mult, exponent)
+	const int8_t* lora_u;       // [M, kMaxRank] adapter intermediate codes of this projection
+};
+
+constexpr int kMaxRank = 64;
+constexpr int kMaxSeg = 3;
+
+struct Epilogue {
+	Segment seg[kMaxSeg];
+	int32_t nseg;
+	int32_t rank;
+	const int64_t* in_recip;   // [M] reciprocal of the input scale mantissa (bias reconcile)
+	const Scale* in_scale;     // [M] input carried scale (bias reconcile exponent)
+	const TokenInfo* tok;      // [M]
+	int32_t* status;           // [slots] first rejection, (layer << 8) | status
+	int32_t layer;
+	// logits mode: argmax keys instead of segments
+	unsigned long long* argmax_key;  // [M] or null
+	// raw mode: the int32 accumulator itself, [M, N]
+	int32_t* raw_out;
+};
+
+struct GemmArgs {
+	const int8_t* a;   // [M, K] activation codes, row stride lda
+	const int8_t* w;   // [N, K] weights
+	int32_t M, N, K, lda;
+	int32_t k_split;   // K elements per split (multiple of 64)
+	int32_t* acc;      // split-K partial sums [M, N] (self-cleaning, zero between uses)
+	uint32_t* tile_cnt;
+	Epilogue epi;
+};
+
+// Status word: the first rejection per sequence slot wins.
+__device__ __forceinline__ void set_status(int32_t* status, int32_t slot, int32_t layer, int32_t st) {
+	if (st != kOk) atomicCAS(&status[slot], 0, (layer << 8) | st);
+}
+
+}  // namespace sslm
+
+// Host launch wrappers (kernels.hip).
+namespace sslm_launch {
+using namespace sslm;
+
+void gemm(const GemmArgs& g, hipStream_t s);
+
+struct RowNormArgs {
+	// input stream codes: in_codes[idx[t] * ld_in], input scale ignored (norm kills it)
+	const int8_t* in_codes;
+	const int32_t* in_idx;
+	int32_t ld_in;
+	const int32_t* gain;  // [H]
+	Scale site;
+	int8_t* out;          // [M, H]
+	Scale* out_scale;     // [M]
+	int64_t* out_recip;   // [M] reciprocal(out_scale.m), for bias reconcile downstream
+};
+
+void embed(const int32_t* tokens, int M, const int8_t* embed_w, int H, int vocab, Scale site, int8_t* out_codes,
+           const int32_t* out_idx, Scale* out_scale, const int32_t* scale_idx, const TokenInfo* tok,
+           int32_t* status, hipStream_t s);
+
+// attention-input side: q funnel + RoPE(q); K/V landing + RoPE(K) into the KV pool
+struct QkvPostArgs {
+	int M, H, NH, NKV, D;
+	int64_t cap;
+	const TokenInfo* tok;
+	const int32_t* q_f;       // [M, H] funnel-mode q fold outputs
+	uint32_t* q_maxabs;       // [M]
+	const int64_t* kv_f;      // [M, 2*NKV*D] k then v wide values
+	const Scale* in_scale;    // [M] normed scale (landing operand and q's incoming)
+	Scale q_site;
+	const int64_t* r_t_k;     // [NKV]
+	const int64_t* e_t_k;
+	const int64_t* r_t_v;
+	const int64_t* e_t_v;
+	const int64_t* rope_cos;  // [cap, D/2]
+	const int64_t* rope_sin;
+	int8_t* kv_pool;
+	int64_t block_bytes;
+	int32_t layer;
+	int8_t* q_rot;            // [M, H]
+	Scale* q_scale;           // [M]
+	unsigned long long* sat;  // [slots]
+	int32_t* status;
+};
+void qkv_post(const QkvPostArgs& a, hipStream_t s);
+
+struct AttnArgs {
+	int M, H, NH, NKV, D;
+	int64_t cap;
+	const TokenInfo* tok;
+	const int8_t* q_rot;      // [M, H]
+	const Scale* q_scale;     // [M]
+	const int64_t* khead_m;   // [NKV]
+	const int64_t* khead_e;
+	const int32_t* ctx_fold;  // [NH, 3]
+	const int8_t* kv_pool;
+	int64_t block_bytes;
+	int32_t layer;
+	int64_t ln2_q, b_q, ca_q;
+	int32_t* ctx_f;           // [M, H]
+	uint32_t* ctx_maxabs;     // [M]
+	int64_t* scratch;         // [M, NH, cap] when rows exceed LDS
+	int32_t* status;
+};
+void attention(const AttnArgs& a, hipStream_t s);
+
+// funnel over an int32 fold-output row; `incoming` per token or null (empty span, the attn_ctx site)
+struct FunnelArgs {
+	int M, N;
+	const TokenInfo* tok;
+	const int32_t* f;
+	int32_t ld_f;
+	uint32_t* maxabs;
+	const Scale* incoming;
+	Scale site;
+	int8_t* out;
+	Scale* out_scale;
+	int32_t layer;
+	int32_t* status;
+};
+void funnel(const FunnelArgs& a, hipStream_t s);
+
+// o funnel -> attn residual -> mlp RMSNorm   /  down funnel -> mlp residual (commit) -> next norm
+struct ResidualArgs {
+	int M, H;
+	const TokenInfo* tok;
+	const int32_t* branch_f;   // [M, H] funnel-mode fold outputs of o_proj / down_proj
+	uint32_t* branch_maxabs;
+	const Scale* branch_in;    // [M] incoming scale of the projection (ctx / act)
+	Scale branch_site;
+	int8_t* stream;            // stream codes, row stream_idx[t]
+	const int32_t* stream_idx;
+	Scale* stream_scale;       // row stream_idx[t]
+	Scale res_site;
+	int8_t* out_stream;        // residual output codes, row out_idx[t]
+	const int32_t* out_idx;
+	Scale* out_stream_scale;   // row out_idx[t]
+	const int32_t* gain;       // next RMSNorm (null = none)
+	Scale norm_site;
+	int8_t* norm_out;          // [M, H]
+	Scale* norm_scale;         // [M]
+	int64_t* norm_recip;       // [M]
+	int32_t layer;
+	int32_t* status;
+};
+void residual_norm(const ResidualArgs& a, hipStream_t s);
+
+void rmsnorm(const RowNormArgs& a, int M, int H, const TokenInfo* tok, int32_t* status, int32_t layer,
+             hipStream_t s);
+
+// gate/up funnels -> SiLU LUT product -> act funnel
+struct ActArgs {
+	int M, I;
+	const TokenInfo* tok;
+	const int32_t* gu_f;     // [M, 2I] gate then up
+	uint32_t* gate_maxabs;
+	uint32_t* up_maxabs;
+	const Scale* in_scale;   // [M] mlp-normed scale (incoming of gate and up)
+	Scale gate_site, up_site, act_site;
+	const int32_t* silu;     // [1025]
+	int8_t* act;             // [M, I]
+	Scale* act_scale;        // [M]
+	int32_t layer;
+	int32_t* status;
+};
+void mlp_act(const ActArgs& a, hipStream_t s);
+
+// LoRA intermediate u = clamp(amp_fold(A x)) for up to 3 projections sharing one input
+struct LoraUArgs {
+	int M, K, rank, nproj;
+	const int8_t* x;  // [M, K]
+	const int8_t* a[3];       // [rank, K]
+	const int32_t* ufold[3];  // [rank, 3]
+	int8_t* u[3];             // [M, kMaxRank]
+};
+void lora_u(const LoraUArgs& a, hipStream_t s);
+
+// argmax keys -> token ids, keys reset for the next use
+void argmax_finalize(unsigned long long* keys, int M, int32_t* out_tokens, hipStream_t s);
+
+}  // namespace sslm_launch

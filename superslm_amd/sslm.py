@@ -1,0 +1,208 @@
+"""ctypes binding of the sslm_* C ABI (reference include/superslm/sslm_abi.h and
+include/superslm/sslm_abi_functions*.inc).
+
+The same binding drives any library that exports the ABI: the HIP backend
+(superslm_amd/libsslm_hip.so) and, in the tests, the compiled reference.  Statuses are the
+reference's sslm_status values (sslm_abi.h:96-152); a non-OK status raises SslmError unless the
+caller asks for the raw code.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import numpy as np
+
+SSLM_OK = 0
+STATUS_NAMES = [
+    "SSLM_OK", "SSLM_INVALID_ARGUMENT", "SSLM_BUFFER_TOO_SMALL", "SSLM_MISALIGNED_BUFFER",
+    "SSLM_ARTIFACT_REJECTED", "SSLM_ADAPTER_MODEL_MISMATCH", "SSLM_RESTORE_MODEL_MISMATCH",
+    "SSLM_RESTORE_KV_MISMATCH", "SSLM_MODEL_HAS_LIVE_SEQUENCES", "SSLM_POOL_HAS_LIVE_HANDLES",
+    "SSLM_ADAPTER_HAS_LIVE_SEQUENCES", "SSLM_ADAPTER_SWAP_MIDTOKEN_REJECTED",
+    "SSLM_SEQ_RESET_MIDTOKEN_REJECTED", "SSLM_PREFIX_FROZEN_REJECTED", "SSLM_KV_POOL_EXHAUSTED",
+    "SSLM_TOKEN_ID_OUT_OF_RANGE", "SSLM_CONTEXT_CAP_EXCEEDED", "SSLM_TOKEN_ID_UNMAPPED",
+    "SSLM_SCHEMA_NOT_FOUND", "SSLM_SCHEMA_BIND_REJECTED", "SSLM_SCHEMA_SPAN_UNBOUND",
+    "SSLM_PREFIX_SCHEMA_MISMATCH", "SSLM_RESTORE_SCHEMA_MISMATCH", "SSLM_SCHEMA_SPAN_UNREACHABLE",
+    "SSLM_SCHEMA_UNSATISFIABLE", "SSLM_ALLOCATION_FAILED", "SSLM_NUMERIC_STEP_REFUSED",
+]
+ABI_ALIGNMENT = 64
+SPAN_PROMPT = 0
+
+
+class SslmError(RuntimeError):
+    def __init__(self, where: str, status: int):
+        name = STATUS_NAMES[status] if 0 <= status < len(STATUS_NAMES) else str(status)
+        super().__init__(f"{where}: {name}")
+        self.status = status
+
+
+class DecodeParams(ctypes.Structure):
+    """sslm_decode_params (sslm_abi.h:207-224)."""
+    _fields_ = [("layer_budget", ctypes.c_int32), ("struct_size", ctypes.c_uint32),
+                ("mode", ctypes.c_int32), ("alpha_q15", ctypes.c_int32),
+                ("anti_lm_max_order", ctypes.c_int32), ("top_k", ctypes.c_int32),
+                ("q_ln2", ctypes.c_int64), ("q_b", ctypes.c_int64), ("q_c", ctypes.c_int64)]
+
+
+class Config(ctypes.Structure):
+    """sslm_config (sslm_abi.h:40-46)."""
+    _fields_ = [("max_batch", ctypes.c_int32), ("max_chunk_budget", ctypes.c_int32),
+                ("max_layer_budget", ctypes.c_int32), ("reserved", ctypes.c_uint32)]
+
+
+def _aligned_buffer(nbytes: int):
+    raw = np.zeros(nbytes + ABI_ALIGNMENT, dtype=np.uint8)
+    off = (-raw.ctypes.data) % ABI_ALIGNMENT
+    return raw, raw.ctypes.data + off
+
+
+class SslmLib:
+    """One loaded sslm_* library."""
+
+    def __init__(self, path: str):
+        if not os.path.exists(path):
+            raise FileNotFoundError(path)
+        self.path = path
+        self.lib = ctypes.CDLL(path)
+        L = self.lib
+        vp, sz, i32, u32 = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int32, ctypes.c_uint32
+        pvp = ctypes.POINTER(ctypes.c_void_p)
+        pi32 = ctypes.POINTER(ctypes.c_int32)
+
+        def sig(name, res, *args):
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = list(args)
+
+        sig("sslm_model_map", ctypes.c_int, vp, sz, pvp)
+        sig("sslm_model_unmap", ctypes.c_int, vp)
+        sig("sslm_kv_block_size", sz, vp)
+        sig("sslm_kv_pool_overhead_size", sz, vp, u32)
+        sig("sslm_kv_pool_create", ctypes.c_int, vp, vp, sz, u32, pvp)
+        sig("sslm_kv_pool_destroy", ctypes.c_int, vp)
+        sig("sslm_workspace_size", sz, vp, ctypes.POINTER(Config))
+        sig("sslm_workspace_create", ctypes.c_int, vp, ctypes.POINTER(Config), vp, sz, pvp)
+        sig("sslm_workspace_destroy", ctypes.c_int, vp)
+        sig("sslm_seq_create", ctypes.c_int, vp, pvp, pvp)
+        sig("sslm_seq_release", ctypes.c_int, vp)
+        sig("sslm_seq_reset", ctypes.c_int, vp)
+        sig("sslm_prefill", ctypes.c_int, vp, vp, pi32, i32, i32, ctypes.c_int, vp, pi32)
+        sig("sslm_decode_step", ctypes.c_int, vp, pvp, i32, ctypes.POINTER(DecodeParams), vp, pi32)
+        sig("sslm_decode_params_init", ctypes.c_int, vp, i32, i32, ctypes.POINTER(DecodeParams))
+        sig("sslm_seq_set_adapter", ctypes.c_int, vp, vp)
+        sig("sslm_adapter_map", ctypes.c_int, vp, sz, vp, pvp)
+        sig("sslm_adapter_release", ctypes.c_int, vp)
+        sig("sslm_seq_save", ctypes.c_int, vp, vp, ctypes.POINTER(sz))
+        self.has_peek = hasattr(L, "sslm_g5_test_only_peek_kv_block_bytes")
+        if self.has_peek:
+            sig("sslm_g5_test_only_peek_kv_block_bytes", ctypes.c_int, vp, u32, vp, sz)
+
+    def check(self, where: str, st: int):
+        if st != SSLM_OK:
+            raise SslmError(where, st)
+
+
+class Model:
+    """A mapped artifact.  Keeps the artifact bytes alive (the ABI requires it)."""
+
+    def __init__(self, lib: SslmLib, artifact: bytes):
+        self.lib = lib
+        self._bytes = ctypes.create_string_buffer(artifact, len(artifact))
+        h = ctypes.c_void_p()
+        lib.check("sslm_model_map", lib.lib.sslm_model_map(self._bytes, len(artifact), ctypes.byref(h)))
+        self.handle = h
+        self.block_size = lib.lib.sslm_kv_block_size(h)
+
+    def pool(self, blocks: int) -> "KvPool":
+        return KvPool(self, blocks)
+
+    def decode_params(self, layer_budget: int) -> DecodeParams:
+        p = DecodeParams()
+        self.lib.check("sslm_decode_params_init",
+                       self.lib.lib.sslm_decode_params_init(self.handle, 0, layer_budget, ctypes.byref(p)))
+        return p
+
+    def decode_step(self, seqs, layer_budget: int, raw: bool = False):
+        n = len(seqs)
+        arr = (ctypes.c_void_p * n)(*[s.handle.value for s in seqs])
+        out = (ctypes.c_int32 * n)()
+        p = self.decode_params(layer_budget)
+        st = self.lib.lib.sslm_decode_step(self.handle, arr, n, ctypes.byref(p), None, out)
+        if raw:
+            return st, list(out)
+        self.lib.check("sslm_decode_step", st)
+        return list(out)
+
+    def close(self):
+        if self.handle:
+            self.lib.check("sslm_model_unmap", self.lib.lib.sslm_model_unmap(self.handle))
+            self.handle = None
+
+
+class KvPool:
+    def __init__(self, model: Model, blocks: int):
+        lib = model.lib
+        self.model = model
+        size = blocks * model.block_size + lib.lib.sslm_kv_pool_overhead_size(model.handle, blocks)
+        self._raw, addr = _aligned_buffer(size)
+        h = ctypes.c_void_p()
+        lib.check("sslm_kv_pool_create",
+                  lib.lib.sslm_kv_pool_create(model.handle, ctypes.c_void_p(addr), size, blocks, ctypes.byref(h)))
+        self.handle = h
+
+    def kv_block(self, index: int = 0) -> np.ndarray:
+        """One KV block in the reference layout [layer][K|V][kv_head][context_cap][head_dim]
+        (forward_sites.cpp:1227-1269); a sequence owns exactly one block."""
+        m = self.model
+        out = np.zeros(m.block_size, dtype=np.int8)
+        m.lib.check("peek_kv", m.lib.lib.sslm_g5_test_only_peek_kv_block_bytes(
+            self.handle, index, out.ctypes.data_as(ctypes.c_void_p), out.nbytes))
+        return out
+
+    def seq(self) -> "Seq":
+        return Seq(self)
+
+    def close(self):
+        if self.handle:
+            self.model.lib.check("sslm_kv_pool_destroy", self.model.lib.lib.sslm_kv_pool_destroy(self.handle))
+            self.handle = None
+
+
+class Seq:
+    def __init__(self, pool: KvPool):
+        lib = pool.model.lib
+        self.pool = pool
+        h = ctypes.c_void_p()
+        lib.check("sslm_seq_create", lib.lib.sslm_seq_create(pool.model.handle, ctypes.byref(pool.handle),
+                                                              ctypes.byref(h)))
+        self.handle = h
+
+    def prefill(self, tokens, chunk_budget: int | None = None, raw: bool = False):
+        m = self.pool.model
+        arr = np.ascontiguousarray(np.asarray(tokens, dtype=np.int32))
+        consumed = ctypes.c_int32(0)
+        budget = chunk_budget if chunk_budget is not None else max(1, len(arr))
+        st = m.lib.lib.sslm_prefill(m.handle, self.handle, arr.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)),
+                                    len(arr), budget, SPAN_PROMPT, None, ctypes.byref(consumed))
+        if raw:
+            return st, consumed.value
+        m.lib.check("sslm_prefill", st)
+        return consumed.value
+
+    def set_adapter(self, adapter):
+        m = self.pool.model
+        m.lib.check("sslm_seq_set_adapter",
+                    m.lib.lib.sslm_seq_set_adapter(self.handle, adapter.handle if adapter else None))
+
+    def save(self) -> bytes:
+        lib = self.pool.model.lib
+        n = ctypes.c_size_t(0)
+        lib.lib.sslm_seq_save(self.handle, None, ctypes.byref(n))
+        buf = ctypes.create_string_buffer(n.value)
+        lib.check("sslm_seq_save", lib.lib.sslm_seq_save(self.handle, buf, ctypes.byref(n)))
+        return buf.raw[:n.value]
+
+    def release(self):
+        if self.handle:
+            self.pool.model.lib.check("sslm_seq_release", self.pool.model.lib.lib.sslm_seq_release(self.handle))
+            self.handle = None

@@ -1,0 +1,313 @@
+""".sslm v2 artifact writer and seeded synthetic model generator.
+
+Format restated from the reference's normative spec (docs/sslm_format.md:47-118 header and
+section table, :178-240 WGT1/BIA1/ROP1/WSC1 tensor manifests, :242-290 KVC1 keyed constants,
+:292-327 CFG1, :340-365 SIL1).  Names follow include/superslm/layer_marshal.h:141-330 and
+src/sslm_abi.cpp:609-676 (embed / final_norm.gain / lm_head, site constants).
+
+The generator draws every weight from a seeded numpy PCG64 stream and derives every composition
+constant from one consistent "real value per code" model, so a synthetic stack stays inside the
+reference's load-time value gate (src/model.cpp:940-1180) and inside the runtime domains (funnel
+D' <= 2^31, i-exp constants, SiLU scale range) for whole forwards.  There is no network and no
+checkpoint: synthetic artifacts are how every BASELINE configuration gets a real .sslm.
+"""
+from __future__ import annotations
+
+import hashlib
+import math
+import struct
+from dataclasses import dataclass, field
+
+import numpy as np
+
+# ---- section / dtype enums (docs/sslm_format.md:100-139) ----
+SEC_CONFIG = 0
+SEC_PROVENANCE = 1
+SEC_WEIGHTS = 2
+SEC_BIASES = 3
+SEC_ROPE = 4
+SEC_WEIGHT_SCALES = 6
+SEC_COMPOSITION = 7
+SEC_KV_LANDING_SCALES = 8
+SEC_KV_LANDING_RECIPROCALS = 9
+SEC_SIGMOID_LUT = 12
+SEC_DELTA_FOLD = 40
+SEC_U_FOLD = 41
+
+DT_RAW, DT_I8, DT_I32, DT_I64 = 0, 1, 2, 3
+_DT_SIZE = {DT_RAW: 1, DT_I8: 1, DT_I32: 4, DT_I64: 8}
+
+HEADER_BYTES = 64
+SECTION_DESC_BYTES = 40
+HASH_OFFSET = 32
+
+PROJECTIONS = ("q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj", "down_proj")
+
+
+def _align(n: int, a: int) -> int:
+    return (n + a - 1) // a * a
+
+
+def write_container(sections, flags: int = 0) -> bytes:
+    """sections: list of (type, dtype, payload bytes, alignment).  Returns the whole file with
+    the SHA-256 integrity field filled (docs/sslm_format.md:26-32)."""
+    count = len(sections)
+    table_end = HEADER_BYTES + count * SECTION_DESC_BYTES
+    offsets = []
+    cursor = table_end
+    for _t, _d, payload, align in sections:
+        cursor = _align(cursor, align)
+        offsets.append(cursor)
+        cursor += len(payload)
+    total = cursor
+    buf = bytearray(total)
+    struct.pack_into("<4sIIIIIQ", buf, 0, b"SSLM", 2, HEADER_BYTES, count, flags, 0, total)
+    for i, ((typ, dt, payload, align), off) in enumerate(zip(sections, offsets)):
+        size = len(payload)
+        if size % _DT_SIZE[dt]:
+            raise ValueError(f"section {typ}: {size} bytes is not a multiple of dtype size")
+        struct.pack_into("<IIQQQII", buf, HEADER_BYTES + i * SECTION_DESC_BYTES, typ, dt, off, size,
+                         size // _DT_SIZE[dt], align, 0)
+        buf[off:off + size] = payload
+    digest = hashlib.sha256(buf).digest()  # hash field is still zero here
+    buf[HASH_OFFSET:HASH_OFFSET + 32] = digest
+    return bytes(buf)
+
+
+def tensor_manifest(magic: bytes, elem_size: int, tensors) -> bytes:
+    """WGT1/BIA1/ROP1/WSC1 manifest (docs/sslm_format.md:200-238).  tensors: list of
+    (name, ndarray); data packed contiguously in descriptor order, each element-aligned."""
+    names = [n.encode() for n, _ in tensors]
+    name_blob = b"".join(names)
+    n = len(tensors)
+    head = 16 + 48 * n
+    data_start = _align(head + len(name_blob), elem_size)
+    descs = bytearray()
+    parts = []
+    name_off = 0
+    cursor = data_start
+    for (name, arr), nb in zip(tensors, names):
+        a = np.ascontiguousarray(arr)
+        if a.dtype.itemsize != elem_size:
+            raise ValueError(f"{name}: element size {a.dtype.itemsize} != {elem_size}")
+        shape = list(a.shape) + [0] * (4 - a.ndim)
+        cursor = _align(cursor, elem_size)
+        descs += struct.pack("<III4IQQI", name_off, len(nb), a.ndim, *shape, cursor, a.size, 0)
+        parts.append((cursor, a))
+        cursor += a.nbytes
+        name_off += len(nb)
+    total = _align(cursor, 8)
+    out = bytearray(total)
+    struct.pack_into("<4sIII", out, 0, magic, 1, n, len(name_blob))
+    out[16:16 + len(descs)] = descs
+    out[head:head + len(name_blob)] = name_blob
+    for off, a in parts:
+        out[off:off + a.nbytes] = a.tobytes()
+    return bytes(out)
+
+
+def kvc1(entries, value_words: int) -> bytes:
+    """KVC1 keyed int64 tuples (docs/sslm_format.md:261-271)."""
+    names = [n.encode() for n, _ in entries]
+    name_blob = b"".join(names)
+    out = bytearray(struct.pack("<4sIIIII", b"KVC1", 1, len(entries), value_words, len(name_blob), 0))
+    off = 0
+    for nb in names:
+        out += struct.pack("<II", off, len(nb))
+        off += len(nb)
+    for _n, vals in entries:
+        if len(vals) != value_words:
+            raise ValueError("value_words mismatch")
+        out += struct.pack(f"<{value_words}q", *[int(v) for v in vals])
+    out += name_blob
+    return bytes(out)
+
+
+def cfg1(c: "ModelConfig") -> bytes:
+    """CFG1 fixed 84-byte config (docs/sslm_format.md:301-321)."""
+    return struct.pack("<4s16I2d", b"CFG1", 1, c.hidden, c.layers, c.heads, c.kv_heads, c.head_dim,
+                       c.inter, c.vocab, c.context_cap, 1 if c.tie_embeddings else 0, 0,
+                       c.kv_block_size, 15, 0, 0, 0, c.rope_theta, 1e-6)
+
+
+def sigmoid_lut() -> np.ndarray:
+    """SIL1 nodes: round_half_even(sigmoid(-16 + i/32) * 2^15), i in [0, 1024]
+    (docs/sslm_format.md:346-349), float64 as the converter computes it."""
+    x = -16.0 + np.arange(1025, dtype=np.float64) * (32.0 / 1024.0)
+    return np.rint((1.0 / (1.0 + np.exp(-x))) * 32768.0).astype(np.int32)
+
+
+def sil1(table: np.ndarray) -> bytes:
+    return struct.pack("<4sIII", b"SIL1", 1, 1025, 0) + np.asarray(table, dtype="<i4").tobytes()
+
+
+def rope_tables(cap: int, head_dim: int, theta: float):
+    """Q2.30 cos/sin [cap, head_dim/2] for interleaved pairs (2i, 2i+1), inv_freq theta^(-2i/d)."""
+    pairs = head_dim // 2
+    inv = theta ** (-(np.arange(pairs, dtype=np.float64) * 2.0) / head_dim)
+    ang = np.arange(cap, dtype=np.float64)[:, None] * inv[None, :]
+    one = float(1 << 30)
+    return (np.rint(np.cos(ang) * one).astype(np.int64), np.rint(np.sin(ang) * one).astype(np.int64))
+
+
+def scale_me(value: float):
+    """Canonical carried scale (m, e): value = m * 2^e with m in [2^30, 2^31)."""
+    if value <= 0:
+        raise ValueError("scale must be positive")
+    fr, ex = math.frexp(value)  # value = fr * 2^ex, fr in [0.5, 1)
+    m = int(round(fr * (1 << 31)))
+    e = ex - 31
+    if m >= (1 << 31):
+        m >>= 1
+        e += 1
+    return m, e
+
+
+def reciprocal_round(m: int) -> int:
+    """round_half_up(2^62 / m): KvLandingReciprocals word 2 for a landing mantissa m."""
+    return ((1 << 63) + m) // (2 * m)
+
+
+@dataclass
+class ModelConfig:
+    hidden: int
+    layers: int
+    heads: int
+    kv_heads: int
+    head_dim: int
+    inter: int
+    vocab: int
+    context_cap: int
+    tie_embeddings: bool = True
+    kv_block_size: int = 16
+    rope_theta: float = 1_000_000.0
+    with_bias: bool = False
+
+
+CONFIGS = {
+    # tiny shapes for CPU tests
+    "tiny": ModelConfig(hidden=128, layers=2, heads=4, kv_heads=2, head_dim=32, inter=256, vocab=512,
+                        context_cap=64, tie_embeddings=False, with_bias=True),
+    "small": ModelConfig(hidden=256, layers=3, heads=4, kv_heads=1, head_dim=64, inter=512, vocab=1024,
+                         context_cap=160, tie_embeddings=True, with_bias=True),
+    # Qwen2.5-1.5B shape
+    "qwen1.5b": ModelConfig(hidden=1536, layers=28, heads=12, kv_heads=2, head_dim=128, inter=8960,
+                            vocab=151936, context_cap=1024, tie_embeddings=True),
+    # Qwen2.5-7B shape
+    "qwen7b": ModelConfig(hidden=3584, layers=28, heads=28, kv_heads=4, head_dim=128, inter=18944,
+                          vocab=151936, context_cap=4608, tie_embeddings=False),
+}
+
+
+@dataclass
+class SyntheticModel:
+    config: ModelConfig
+    weights: dict = field(default_factory=dict)    # name -> int8 ndarray
+    folds: dict = field(default_factory=dict)      # name -> int32 [N,3]
+    biases: dict = field(default_factory=dict)     # name -> int64 [N]
+    consts: dict = field(default_factory=dict)     # name -> (m, e)
+    landing: dict = field(default_factory=dict)    # "layer{l}.k_head{h}" -> (m, e, R)
+    rope_cos: np.ndarray = None
+    rope_sin: np.ndarray = None
+    silu: np.ndarray = None
+
+    def to_bytes(self) -> bytes:
+        c = self.config
+        wgt = tensor_manifest(b"WGT1", 1, list(self.weights.items()))
+        wsc = tensor_manifest(b"WSC1", 4, list(self.folds.items()))
+        rop = tensor_manifest(b"ROP1", 8, [("cos", self.rope_cos), ("sin", self.rope_sin)])
+        comp = kvc1(list(self.consts.items()), 2)
+        lscale = kvc1([(k, v[:2]) for k, v in self.landing.items()], 2)
+        lrecip = kvc1(list(self.landing.items()), 3)
+        sections = [
+            (SEC_CONFIG, DT_RAW, cfg1(c), 8),
+            (SEC_WEIGHTS, DT_I8, wgt, 64),
+            (SEC_WEIGHT_SCALES, DT_I32, wsc, 64),
+            (SEC_ROPE, DT_I64, rop, 64),
+            (SEC_COMPOSITION, DT_RAW, comp, 8),
+            (SEC_KV_LANDING_SCALES, DT_RAW, lscale, 8),
+            (SEC_KV_LANDING_RECIPROCALS, DT_RAW, lrecip, 8),
+            (SEC_SIGMOID_LUT, DT_I32, sil1(self.silu), 8),
+        ]
+        if self.biases:
+            sections.append((SEC_BIASES, DT_I64, tensor_manifest(b"BIA1", 8, list(self.biases.items())), 64))
+        return write_container(sections)
+
+
+def _fold_table(rng, n: int, shift_lo: int, shift_hi: int, identity_frac: float) -> np.ndarray:
+    t = np.empty((n, 3), dtype=np.int32)
+    t[:, 0] = (rng.random(n) < identity_frac).astype(np.int32)
+    t[:, 1] = rng.integers(1 << 30, 1 << 31, size=n, dtype=np.int64).astype(np.int32)
+    t[:, 2] = rng.integers(shift_lo, shift_hi + 1, size=n, dtype=np.int32)
+    return t
+
+
+def _codes(rng, shape) -> np.ndarray:
+    return rng.integers(-127, 128, size=shape, dtype=np.int8)
+
+
+def build_synthetic(cfg: ModelConfig, seed: int = 1234, temperature: float = 1.0) -> SyntheticModel:
+    """Seeded synthetic integer model whose constants follow one real-scale model.
+
+    Real value of a code = code * (m * 2^e).  Each projection's WSC1 fold F = acc * mult / 2^(31+s)
+    carries unit x_scale * c_f with c_f = w_s * 2^31 / 2^30.5 (the shift and the per-channel mult
+    spread act as per-channel weight-scale variation), so the projection site constant is c_f/127;
+    norms use g_s / (2^16 * 127); residuals 1/127; the SiLU product 2^-15/127 (it already carries
+    both incoming scales).  K/V land at a fixed code scale, and softmax_khead folds the k code
+    scale with 1/sqrt(head_dim) so the derived i-exp q_ln2 sits near 5e4 score units."""
+    rng = np.random.Generator(np.random.PCG64(seed))
+    c = cfg
+    m = SyntheticModel(config=c)
+    H, I, D, NH, NKV = c.hidden, c.inter, c.head_dim, c.heads, c.kv_heads
+    KVH = NKV * D
+    g_s = 1.0 / 127.0
+    shift_lo, shift_hi = 0, 3
+    mult_ref = 2.0 ** 30.5
+
+    def c_f(k_in: int) -> float:
+        w_s = 1.0 / (127.0 * math.sqrt(k_in))
+        return w_s * 2.0 ** 31 / mult_ref
+
+    m.weights["embed"] = _codes(rng, (c.vocab, H))
+    m.consts["embed"] = scale_me(1.0 / 127.0 / 127.0)
+    shapes = {"q_proj": (H, H), "k_proj": (KVH, H), "v_proj": (KVH, H), "o_proj": (H, H),
+              "gate_proj": (I, H), "up_proj": (I, H), "down_proj": (H, I)}
+    k_code_scale = 1.5 / 127.0
+    v_code_scale = 1.5 / 127.0
+    for layer in range(c.layers):
+        p = f"layer{layer}"
+        for name in PROJECTIONS:
+            m.weights[f"{p}.{name}"] = _codes(rng, shapes[name])
+        m.weights[f"{p}.attn_norm.gain"] = _codes(rng, (H,))
+        m.weights[f"{p}.mlp_norm.gain"] = _codes(rng, (H,))
+        for name in PROJECTIONS:
+            m.folds[f"{p}.{name}"] = _fold_table(rng, shapes[name][0], shift_lo, shift_hi, 0.03)
+        m.folds[f"{p}.ctx_fold"] = _fold_table(rng, NH, 0, 2, 0.0)
+        if c.with_bias:
+            for name in ("q_proj", "k_proj", "v_proj"):
+                b_real = rng.normal(0.0, 0.05, size=shapes[name][0])
+                m.biases[f"{p}.{name}"] = np.rint(b_real * 2.0 ** 30 / c_f(H)).astype(np.int64)
+        norm_site = scale_me(g_s / (2.0 ** 16 * 127.0))
+        m.consts[f"{p}.attn_norm"] = norm_site
+        m.consts[f"{p}.mlp_norm"] = norm_site
+        for name in ("q_proj", "o_proj", "gate_proj", "up_proj"):
+            m.consts[f"{p}.{name}"] = scale_me(c_f(H) / 127.0)
+        m.consts[f"{p}.down_proj"] = scale_me(c_f(I) / 127.0)
+        # ctx_wide = fold(sum p_q15 * v_code): unit v_code_scale * 2^31 / (mult * 2^15)
+        m.consts[f"{p}.attn_ctx"] = scale_me(v_code_scale * 2.0 ** 31 / (mult_ref * 2.0 ** 15) / 127.0)
+        m.consts[f"{p}.attn_residual"] = scale_me(1.0 / 127.0)
+        m.consts[f"{p}.mlp_residual"] = scale_me(1.0 / 127.0)
+        m.consts[f"{p}.mlp_act"] = scale_me(2.0 ** -15 / 127.0)
+        for h in range(NKV):
+            m.consts[f"{p}.softmax_khead{h}"] = scale_me(k_code_scale / math.sqrt(D) / temperature)
+            for kind, code_scale in (("k", k_code_scale), ("v", v_code_scale)):
+                # code = F * normed / landing  ->  landing = code_scale / c_f
+                lm, le = scale_me(code_scale / c_f(H))
+                m.landing[f"{p}.{kind}_head{h}"] = (lm, le, reciprocal_round(lm))
+    m.weights["final_norm.gain"] = _codes(rng, (H,))
+    m.consts["final_norm"] = scale_me(g_s / (2.0 ** 16 * 127.0))
+    if not c.tie_embeddings:
+        m.weights["lm_head"] = _codes(rng, (c.vocab, H))
+    m.rope_cos, m.rope_sin = rope_tables(c.context_cap, D, c.rope_theta)
+    m.silu = sigmoid_lut()
+    return m
