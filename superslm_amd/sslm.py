@@ -105,11 +105,17 @@ class SslmLib:
 class Model:
     """A mapped artifact.  Keeps the artifact bytes alive (the ABI requires it)."""
 
-    def __init__(self, lib: SslmLib, artifact: bytes):
+    def __init__(self, lib: SslmLib, artifact):
+        """`artifact`: bytes, or a uint8 numpy array (mapped in place, no copy)."""
         self.lib = lib
-        self._bytes = ctypes.create_string_buffer(artifact, len(artifact))
+        if isinstance(artifact, np.ndarray):
+            self._bytes = np.ascontiguousarray(artifact, dtype=np.uint8)
+            ptr, size = self._bytes.ctypes.data, self._bytes.nbytes
+        else:
+            self._bytes = ctypes.create_string_buffer(artifact, len(artifact))
+            ptr, size = ctypes.addressof(self._bytes), len(artifact)
         h = ctypes.c_void_p()
-        lib.check("sslm_model_map", lib.lib.sslm_model_map(self._bytes, len(artifact), ctypes.byref(h)))
+        lib.check("sslm_model_map", lib.lib.sslm_model_map(ctypes.c_void_p(ptr), size, ctypes.byref(h)))
         self.handle = h
         self.block_size = lib.lib.sslm_kv_block_size(h)
 

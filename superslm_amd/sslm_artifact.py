@@ -49,8 +49,13 @@ def _align(n: int, a: int) -> int:
 
 
 def write_container(sections, flags: int = 0) -> bytes:
-    """sections: list of (type, dtype, payload bytes, alignment).  Returns the whole file with
-    the SHA-256 integrity field filled (docs/sslm_format.md:26-32)."""
+    """sections: list of (type, dtype, payload, alignment) with payload bytes or a Manifest.
+    Returns the whole file with the SHA-256 integrity field filled (docs/sslm_format.md:26-32)."""
+    return bytes(write_container_array(sections, flags))
+
+
+def write_container_array(sections, flags: int = 0) -> np.ndarray:
+    """Same as write_container, returning the file image as a uint8 array (no extra copy)."""
     count = len(sections)
     table_end = HEADER_BYTES + count * SECTION_DESC_BYTES
     offsets = []
@@ -58,52 +63,101 @@ def write_container(sections, flags: int = 0) -> bytes:
     for _t, _d, payload, align in sections:
         cursor = _align(cursor, align)
         offsets.append(cursor)
-        cursor += len(payload)
+        cursor += payload.size if isinstance(payload, Manifest) else len(payload)
     total = cursor
-    buf = bytearray(total)
-    struct.pack_into("<4sIIIIIQ", buf, 0, b"SSLM", 2, HEADER_BYTES, count, flags, 0, total)
+    buf = np.zeros(total, dtype=np.uint8)
+    buf[:HEADER_BYTES] = np.frombuffer(
+        struct.pack("<4sIIIIIQ", b"SSLM", 2, HEADER_BYTES, count, flags, 0, total).ljust(HEADER_BYTES, b"\0"),
+        dtype=np.uint8)
     for i, ((typ, dt, payload, align), off) in enumerate(zip(sections, offsets)):
-        size = len(payload)
+        size = payload.size if isinstance(payload, Manifest) else len(payload)
         if size % _DT_SIZE[dt]:
             raise ValueError(f"section {typ}: {size} bytes is not a multiple of dtype size")
-        struct.pack_into("<IIQQQII", buf, HEADER_BYTES + i * SECTION_DESC_BYTES, typ, dt, off, size,
-                         size // _DT_SIZE[dt], align, 0)
-        buf[off:off + size] = payload
-    digest = hashlib.sha256(buf).digest()  # hash field is still zero here
-    buf[HASH_OFFSET:HASH_OFFSET + 32] = digest
-    return bytes(buf)
+        row = struct.pack("<IIQQQII", typ, dt, off, size, size // _DT_SIZE[dt], align, 0)
+        base = HEADER_BYTES + i * SECTION_DESC_BYTES
+        buf[base:base + SECTION_DESC_BYTES] = np.frombuffer(row, dtype=np.uint8)
+        if isinstance(payload, Manifest):
+            payload.write_into(buf[off:off + size])
+        else:
+            buf[off:off + size] = np.frombuffer(payload, dtype=np.uint8)
+    digest = hashlib.sha256(memoryview(buf)).digest()  # hash field is still zero here
+    buf[HASH_OFFSET:HASH_OFFSET + 32] = np.frombuffer(digest, dtype=np.uint8)
+    return buf
+
+
+class RandI8:
+    """A weight tensor not yet drawn: uniform int8 codes in [-127, 127] written straight into the
+    artifact image (one pass over fresh memory for multi-GB models)."""
+
+    def __init__(self, shape):
+        self.shape = tuple(shape)
+        self.ndim = len(self.shape)
+        self.size = int(np.prod(self.shape))
+        self.nbytes = self.size
+        self.dtype = np.dtype(np.int8)
+
+
+class Manifest:
+    """A WGT1/BIA1/ROP1/WSC1/DFS1/UFS1 tensor manifest (docs/sslm_format.md:200-238) laid out
+    lazily: `size` is known up front and `write_into` fills a caller buffer, so multi-GB weight
+    sections are copied exactly once, into the final file image."""
+
+    def __init__(self, magic: bytes, elem_size: int, tensors):
+        self.magic = magic
+        self.elem = elem_size
+        self.tensors = [(n, a if isinstance(a, RandI8) else np.ascontiguousarray(a)) for n, a in tensors]
+        self.rng = None
+        names = [n.encode() for n, _ in self.tensors]
+        self.name_blob = b"".join(names)
+        count = len(self.tensors)
+        self.head = 16 + 48 * count
+        cursor = _align(self.head + len(self.name_blob), elem_size)
+        descs = bytearray()
+        self.offsets = []
+        name_off = 0
+        for (name, a), nb in zip(self.tensors, names):
+            if a.dtype.itemsize != elem_size:
+                raise ValueError(f"{name}: element size {a.dtype.itemsize} != {elem_size}")
+            shape = list(a.shape) + [0] * (4 - a.ndim)
+            cursor = _align(cursor, elem_size)
+            descs += struct.pack("<III4IQQI", name_off, len(nb), a.ndim, *shape, cursor, a.size, 0)
+            self.offsets.append(cursor)
+            cursor += a.nbytes
+            name_off += len(nb)
+        self.descs = bytes(descs)
+        self.size = _align(cursor, 8)
+
+    def write_into(self, out: np.ndarray):
+        out[:self.size] = 0
+        out[:16] = np.frombuffer(struct.pack("<4sIII", self.magic, 1, len(self.tensors), len(self.name_blob)),
+                                 dtype=np.uint8)
+        out[16:16 + len(self.descs)] = np.frombuffer(self.descs, dtype=np.uint8)
+        if self.name_blob:
+            out[self.head:self.head + len(self.name_blob)] = np.frombuffer(self.name_blob, dtype=np.uint8)
+        for off, (_n, a) in zip(self.offsets, self.tensors):
+            if isinstance(a, RandI8):
+                step = 1 << 24
+                for c0 in range(0, a.size, step):
+                    n = min(step, a.size - c0)
+                    chunk = self.rng.integers(-127, 128, size=n, dtype=np.int8)
+                    out[off + c0:off + c0 + n] = chunk.view(np.uint8)
+            else:
+                out[off:off + a.nbytes] = a.reshape(-1).view(np.uint8)
+
+    def views(self, image: np.ndarray, base: int):
+        """name -> int view of each tensor inside the written image."""
+        res = {}
+        for off, (n, a) in zip(self.offsets, self.tensors):
+            dt = np.int8 if isinstance(a, RandI8) else a.dtype
+            res[n] = image[base + off:base + off + a.nbytes].view(dt).reshape(a.shape)
+        return res
 
 
 def tensor_manifest(magic: bytes, elem_size: int, tensors) -> bytes:
-    """WGT1/BIA1/ROP1/WSC1 manifest (docs/sslm_format.md:200-238).  tensors: list of
-    (name, ndarray); data packed contiguously in descriptor order, each element-aligned."""
-    names = [n.encode() for n, _ in tensors]
-    name_blob = b"".join(names)
-    n = len(tensors)
-    head = 16 + 48 * n
-    data_start = _align(head + len(name_blob), elem_size)
-    descs = bytearray()
-    parts = []
-    name_off = 0
-    cursor = data_start
-    for (name, arr), nb in zip(tensors, names):
-        a = np.ascontiguousarray(arr)
-        if a.dtype.itemsize != elem_size:
-            raise ValueError(f"{name}: element size {a.dtype.itemsize} != {elem_size}")
-        shape = list(a.shape) + [0] * (4 - a.ndim)
-        cursor = _align(cursor, elem_size)
-        descs += struct.pack("<III4IQQI", name_off, len(nb), a.ndim, *shape, cursor, a.size, 0)
-        parts.append((cursor, a))
-        cursor += a.nbytes
-        name_off += len(nb)
-    total = _align(cursor, 8)
-    out = bytearray(total)
-    struct.pack_into("<4sIII", out, 0, magic, 1, n, len(name_blob))
-    out[16:16 + len(descs)] = descs
-    out[head:head + len(name_blob)] = name_blob
-    for off, a in parts:
-        out[off:off + a.nbytes] = a.tobytes()
-    return bytes(out)
+    m = Manifest(magic, elem_size, tensors)
+    out = np.zeros(m.size, dtype=np.uint8)
+    m.write_into(out)
+    return out.tobytes()
 
 
 def kvc1(entries, value_words: int) -> bytes:
@@ -211,11 +265,25 @@ class SyntheticModel:
     rope_sin: np.ndarray = None
     silu: np.ndarray = None
 
+    image: np.ndarray = None
+    rng: object = None
+
     def to_bytes(self) -> bytes:
+        return bytes(self.to_array())
+
+    def to_array(self) -> np.ndarray:
+        """The artifact file image as a uint8 array.  Built once; afterwards `weights` holds views
+        into it (placeholders are drawn from the model's RNG in manifest order while writing)."""
+        if self.image is None:
+            self.image = self._write()
+        return self.image
+
+    def _write(self) -> np.ndarray:
         c = self.config
-        wgt = tensor_manifest(b"WGT1", 1, list(self.weights.items()))
-        wsc = tensor_manifest(b"WSC1", 4, list(self.folds.items()))
-        rop = tensor_manifest(b"ROP1", 8, [("cos", self.rope_cos), ("sin", self.rope_sin)])
+        wgt = Manifest(b"WGT1", 1, list(self.weights.items()))
+        wgt.rng = self.rng
+        wsc = Manifest(b"WSC1", 4, list(self.folds.items()))
+        rop = Manifest(b"ROP1", 8, [("cos", self.rope_cos), ("sin", self.rope_sin)])
         comp = kvc1(list(self.consts.items()), 2)
         lscale = kvc1([(k, v[:2]) for k, v in self.landing.items()], 2)
         lrecip = kvc1(list(self.landing.items()), 3)
@@ -230,8 +298,12 @@ class SyntheticModel:
             (SEC_SIGMOID_LUT, DT_I32, sil1(self.silu), 8),
         ]
         if self.biases:
-            sections.append((SEC_BIASES, DT_I64, tensor_manifest(b"BIA1", 8, list(self.biases.items())), 64))
-        return write_container(sections)
+            sections.append((SEC_BIASES, DT_I64, Manifest(b"BIA1", 8, list(self.biases.items())), 64))
+        img = write_container_array(sections)
+        base = int.from_bytes(img[HEADER_BYTES + SECTION_DESC_BYTES + 8:HEADER_BYTES + SECTION_DESC_BYTES + 16].tobytes(),
+                              "little")  # offset of the Weights section (second in the table)
+        self.weights.update(wgt.views(img, base))
+        return img
 
 
 def _fold_table(rng, n: int, shift_lo: int, shift_hi: int, identity_frac: float) -> np.ndarray:
@@ -242,8 +314,8 @@ def _fold_table(rng, n: int, shift_lo: int, shift_hi: int, identity_frac: float)
     return t
 
 
-def _codes(rng, shape) -> np.ndarray:
-    return rng.integers(-127, 128, size=shape, dtype=np.int8)
+def _codes(rng, shape):
+    return RandI8(shape)
 
 
 def build_synthetic(cfg: ModelConfig, seed: int = 1234, temperature: float = 1.0) -> SyntheticModel:
@@ -310,4 +382,6 @@ def build_synthetic(cfg: ModelConfig, seed: int = 1234, temperature: float = 1.0
         m.weights["lm_head"] = _codes(rng, (c.vocab, H))
     m.rope_cos, m.rope_sin = rope_tables(c.context_cap, D, c.rope_theta)
     m.silu = sigmoid_lut()
+    m.rng = rng
+    m.to_array()
     return m
