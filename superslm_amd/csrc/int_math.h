@@ -105,6 +105,47 @@ SSLM_HD int64_t reciprocal(int64_t dn) {
 	return y;
 }
 
+// Exact floor(n / d) for 0 <= n < 2^63, d >= 1: a double-precision estimate (off by at most one
+// for these magnitudes) corrected with exact 128-bit residue checks.  Replaces the long 64-bit
+// integer division sequence on the GPU; the result is the integer quotient bit for bit.
+SSLM_HD int64_t div_floor_pos(int64_t n, int64_t d) {
+	int64_t q = (int64_t)((double)n / (double)d);
+	if (q < 0) q = 0;
+	s128 r = (s128)n - (s128)q * d;
+	if (r < 0) {
+		--q;
+		r += d;
+	}
+	if (r < 0) {
+		--q;
+		r += d;
+	}
+	if (r >= d) {
+		++q;
+		r -= d;
+	}
+	if (r >= d) ++q;
+	return q;
+}
+
+// round_half_up(2^62 / dn) for a canonical dn in [2^30, 2^31) -- the value the reference's
+// corrected-Newton DynamicScaleReciprocal returns on that domain (src/intmath.cpp:303-333; its
+// contract, include/superslm/intmath.h:124-131, is correct rounding over the whole normalized
+// domain).  Outside it the reference recurrence itself is replayed.
+SSLM_HD int64_t reciprocal_fast(int64_t dn) {
+	if (dn < ((int64_t)1 << 30) || dn >= ((int64_t)1 << 31)) return reciprocal(dn);
+	int64_t y = (int64_t)(4611686018427387904.0 / (double)dn);
+	for (int i = 0; i < 2; ++i) {  // the reference's correction rule: -dn <= 2(2^62 - y dn) < dn
+		s128 res2 = ((s128)((int64_t)1 << 62) - (s128)y * (s128)dn) * 2;
+		if (res2 >= (s128)dn) {
+			y += 1;
+		} else if (res2 < -(s128)dn) {
+			y -= 1;
+		}
+	}
+	return y;
+}
+
 // src/intmath.cpp:476-490 -- clamp(round_away(x*127*R / 2^(62-s)), +-127).
 SSLM_HD int8_t requant_code(int64_t x, int64_t r, int s) {
 	int exponent = 62 - s;
@@ -210,7 +251,7 @@ SSLM_HD int32_t funnel_plan(uint64_t d_prime, const Scale* incoming, int n_in, S
 	if (d_prime > ((uint64_t)1 << 31)) return kChainInputOutOfDomain;
 	int s;
 	int64_t dn = normalize_scale((int64_t)d_prime, &s);
-	int64_t r = reciprocal(dn);
+	int64_t r = reciprocal_fast(dn);
 	Scale run;
 	bool have = false;
 	for (int i = 0; i < n_in; ++i) {
@@ -327,7 +368,7 @@ SSLM_HD int iexp_scale_constants(int64_t m, int64_t e, int64_t ln2_q, int64_t b_
 	int64_t mn = sh_ln2 < sh_b ? sh_ln2 : sh_b;
 	if (sh_c < mn) mn = sh_c;
 	if (mn < 0) return 2;
-	uint64_t r = (uint64_t)reciprocal(m);
+	uint64_t r = (uint64_t)reciprocal_fast(m);
 	u128 n_ln2 = (u128)(uint64_t)ln2_q * r;
 	u128 n_b = (u128)(uint64_t)b_q * r;
 	u128 n_c = (u128)r * r * (uint64_t)ca_q;
@@ -361,7 +402,7 @@ SSLM_HD int64_t iexp_element(int64_t shifted, int64_t q_ln2, int64_t q_b, int64_
 	if (q_ln2 < 1 || q_ln2 > max_qln2) return -1;
 	int64_t clip_lo = -30 * q_ln2;
 	int64_t clipped = shifted < clip_lo ? clip_lo : shifted;
-	int64_t z = (-clipped) / q_ln2;
+	int64_t z = div_floor_pos(-clipped, q_ln2);
 	int64_t q_p = clipped + z * q_ln2;
 	if (q_b < kI64Min - q_p) return -1;
 	int64_t base = q_p + q_b;

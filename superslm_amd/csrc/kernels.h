@@ -24,7 +24,8 @@ struct Segment {
 	int32_t mode;               // SegMode
 	int32_t ld_out;             // row stride of `out` in elements
 	void* out;                  // int32 (funnel, saturated) or int64 (wide) [M, ld_out]
-	uint32_t* maxabs;           // funnel: per-token saturating max |value| (consumer resets)
+	uint32_t* maxpart;          // funnel: saturating max |value| per (16-column tile, token):
+	                            // maxpart[(col / 16) * kPartLd + t]; the consumer reduces the tiles
 	const int32_t* fold;        // [n, 3] (identity, mult, shift)
 	const int64_t* bias;        // [n] BIA1 codes, or null
 	const int8_t* lora_b;       // [n, rank] or null
@@ -33,6 +34,7 @@ struct Segment {
 };
 
 constexpr int kMaxRank = 64;
+constexpr int kPartLd = 512;  // token stride of the per-tile partial maxima (>= tokens per launch)
 constexpr int kMaxSeg = 3;
 
 struct Epilogue {
@@ -44,8 +46,8 @@ struct Epilogue {
 	const TokenInfo* tok;      // [M]
 	int32_t* status;           // [slots] first rejection, (layer << 8) | status
 	int32_t layer;
-	// logits mode: argmax keys instead of segments
-	unsigned long long* argmax_key;  // [M] or null
+	// logits mode: per (16-column tile, token) argmax keys instead of segments
+	unsigned long long* argmax_key;  // [tiles * kPartLd] or null
 	// raw mode: the int32 accumulator itself, [M, N]
 	int32_t* raw_out;
 };
@@ -54,9 +56,6 @@ struct GemmArgs {
 	const int8_t* a;   // [M, K] activation codes, row stride lda
 	const int8_t* w;   // [N, K] weights
 	int32_t M, N, K, lda;
-	int32_t k_split;   // K elements per split (multiple of 64)
-	int32_t* acc;      // split-K partial sums [M, N] (self-cleaning, zero between uses)
-	uint32_t* tile_cnt;
 	Epilogue epi;
 };
 
@@ -95,7 +94,7 @@ struct QkvPostArgs {
 	int64_t cap;
 	const TokenInfo* tok;
 	const int32_t* q_f;       // [M, H] funnel-mode q fold outputs
-	uint32_t* q_maxabs;       // [M]
+	const uint32_t* q_maxpart;  // tiles [0, H/16) of the q|k|v projection
 	const int64_t* kv_f;      // [M, 2*NKV*D] k then v wide values
 	const Scale* in_scale;    // [M] normed scale (landing operand and q's incoming)
 	Scale q_site;
@@ -129,7 +128,7 @@ struct AttnArgs {
 	int32_t layer;
 	int64_t ln2_q, b_q, ca_q;
 	int32_t* ctx_f;           // [M, H]
-	uint32_t* ctx_maxabs;     // [M]
+	uint32_t* ctx_maxpart;    // [NKV * kPartLd]: one partial per kv head
 	int64_t* scratch;         // [M, NH, cap] when rows exceed LDS
 	int32_t* status;
 };
@@ -141,7 +140,8 @@ struct FunnelArgs {
 	const TokenInfo* tok;
 	const int32_t* f;
 	int32_t ld_f;
-	uint32_t* maxabs;
+	const uint32_t* maxpart;  // [ntiles * kPartLd]
+	int32_t ntiles;
 	const Scale* incoming;
 	Scale site;
 	int8_t* out;
@@ -156,7 +156,7 @@ struct ResidualArgs {
 	int M, H;
 	const TokenInfo* tok;
 	const int32_t* branch_f;   // [M, H] funnel-mode fold outputs of o_proj / down_proj
-	uint32_t* branch_maxabs;
+	const uint32_t* branch_maxpart;  // tiles [0, H/16)
 	const Scale* branch_in;    // [M] incoming scale of the projection (ctx / act)
 	Scale branch_site;
 	int8_t* stream;            // stream codes, row stream_idx[t]
@@ -184,8 +184,7 @@ struct ActArgs {
 	int M, I;
 	const TokenInfo* tok;
 	const int32_t* gu_f;     // [M, 2I] gate then up
-	uint32_t* gate_maxabs;
-	uint32_t* up_maxabs;
+	const uint32_t* gu_maxpart;  // tiles [0, I/16) gate, [I/16, 2I/16) up
 	const Scale* in_scale;   // [M] mlp-normed scale (incoming of gate and up)
 	Scale gate_site, up_site, act_site;
 	const int32_t* silu;     // [1025]
@@ -206,7 +205,7 @@ struct LoraUArgs {
 };
 void lora_u(const LoraUArgs& a, hipStream_t s);
 
-// argmax keys -> token ids, keys reset for the next use
-void argmax_finalize(unsigned long long* keys, int M, int32_t* out_tokens, hipStream_t s);
+// per-tile argmax keys -> token ids (lowest index among equal maxima)
+void argmax_finalize(const unsigned long long* keys, int ntiles, int M, int32_t* out_tokens, hipStream_t s);
 
 }  // namespace sslm_launch

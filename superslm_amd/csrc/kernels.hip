@@ -6,6 +6,8 @@
 // status word instead of aborting (the reference's SslmForwardStatus values).
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+
 #include "kernels.h"
 
 namespace sslm {
@@ -14,6 +16,7 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 
 constexpr int kBlock = 256;
+constexpr int kRowBlock = 1024;  // row kernels: one block per token
 
 // ------------------------------------------------------------------------------------------
 // reductions
@@ -39,7 +42,7 @@ __device__ __forceinline__ int64_t wave_max_i64(int64_t v) {
 	return v;
 }
 
-// block-wide reductions over kBlock threads; `red` holds kBlock/64 slots
+// block-wide reductions over blockDim.x threads; `red` holds blockDim.x/64 (<= 16) slots
 __device__ __forceinline__ uint64_t block_max_u64(uint64_t v, uint64_t* red) {
 	v = wave_max_u64(v);
 	const int w = threadIdx.x >> 6;
@@ -47,7 +50,7 @@ __device__ __forceinline__ uint64_t block_max_u64(uint64_t v, uint64_t* red) {
 	if ((threadIdx.x & 63) == 0) red[w] = v;
 	__syncthreads();
 	uint64_t r = red[0];
-	for (int i = 1; i < kBlock / 64; ++i) r = red[i] > r ? red[i] : r;
+	for (int i = 1; i < (int)(blockDim.x >> 6); ++i) r = red[i] > r ? red[i] : r;
 	return r;
 }
 
@@ -58,7 +61,7 @@ __device__ __forceinline__ int64_t block_sum_i64(int64_t v, int64_t* red) {
 	if ((threadIdx.x & 63) == 0) red[w] = v;
 	__syncthreads();
 	int64_t r = 0;
-	for (int i = 0; i < kBlock / 64; ++i) r += red[i];
+	for (int i = 0; i < (int)(blockDim.x >> 6); ++i) r += red[i];
 	return r;
 }
 
@@ -69,8 +72,19 @@ __device__ __forceinline__ int64_t block_max_i64(int64_t v, int64_t* red) {
 	if ((threadIdx.x & 63) == 0) red[w] = v;
 	__syncthreads();
 	int64_t r = red[0];
-	for (int i = 1; i < kBlock / 64; ++i) r = red[i] > r ? red[i] : r;
+	for (int i = 1; i < (int)(blockDim.x >> 6); ++i) r = red[i] > r ? red[i] : r;
 	return r;
+}
+
+// max over tiles [tile0, tile0 + ntiles) of a per-(tile, token) partial array; every thread of
+// the block must call it
+__device__ __forceinline__ uint64_t reduce_part(const uint32_t* part, int tile0, int ntiles, int t, uint64_t* red) {
+	uint64_t m = 0;
+	for (int i = threadIdx.x; i < ntiles; i += blockDim.x) {
+		const uint64_t v = part[(size_t)(tile0 + i) * kPartLd + t];
+		m = v > m ? v : m;
+	}
+	return block_max_u64(m, red);
 }
 
 __device__ __forceinline__ uint32_t sat_abs_u32(int64_t v) {
@@ -125,254 +139,234 @@ __device__ __forceinline__ void epi_store(const Epilogue& e, const EpiResult& r,
 	}
 }
 
-// ------------------------------------------------------------------------------------------
-// skinny MFMA GEMM for decode (M <= 16*MB per launch row-block): D[t][j] = sum_k x[t][k] w[j][k]
-// One wave owns 16 output channels; v_mfma_i32_16x16x64_i8 with tokens as the 16-row operand.
-// Split-K partials go through int32 atomics and the last-arriving block runs the epilogue.
-// ------------------------------------------------------------------------------------------
 __device__ __forceinline__ v4i load16(const int8_t* p) { return *(const v4i*)p; }
 
-template <int MB>
-__global__ __launch_bounds__(kBlock) void k_gemv(GemmArgs g) {
+// One output element (token t, channel j) of any GEMM: raw accumulator, argmax key, or the
+// projection epilogue; returns the element's contribution to its tile's partial max.
+__device__ __forceinline__ void epi_element(const Epilogue& e, int N, int t, int j, int32_t acc, uint64_t* key,
+                                            uint32_t* mabs, int* seg) {
+	if (e.raw_out) {
+		e.raw_out[(size_t)t * N + j] = acc;
+	} else if (e.argmax_key) {
+		const uint32_t logit = (uint32_t)acc ^ 0x80000000u;
+		*key = ((uint64_t)logit << 32) | (uint64_t)(0xffffffffu - (uint32_t)j);
+	} else {
+		EpiResult r = epi_value(e, t, j, acc);
+		if (!r.ok) set_status(e.status, e.tok[t].slot, e.layer, kBiasReconcileProductOutOfDomain);
+		epi_store(e, r, t, j);
+		*seg = r.seg;
+		if (e.seg[r.seg].mode == kSegFunnel) *mabs = sat_abs_u32(r.v);
+	}
+}
+
+// Reduce over the 16 lanes holding one token's 16 consecutive channels (a 16-column tile; segment
+// bounds are multiples of 16) and store the tile's partial: no atomics, one writer per
+// (tile, token).  Lane groups of 16 must be converged here.
+__device__ __forceinline__ void epi_publish(const Epilogue& e, int tile, int t, bool live, uint64_t key, uint32_t mabs,
+                                            int seg) {
+	for (int o = 8; o > 0; o >>= 1) {
+		uint64_t k2 = __shfl_xor(key, o, 16);
+		key = k2 > key ? k2 : key;
+		uint32_t m2 = __shfl_xor(mabs, o, 16);
+		mabs = m2 > mabs ? m2 : mabs;
+	}
+	if ((threadIdx.x & 15) == 0 && live) {
+		if (e.argmax_key) {
+			e.argmax_key[(size_t)tile * kPartLd + t] = key;
+		} else if (!e.raw_out && e.seg[seg].mode == kSegFunnel && e.seg[seg].maxpart) {
+			e.seg[seg].maxpart[(size_t)tile * kPartLd + t] = mabs;
+		}
+	}
+}
+
+// ------------------------------------------------------------------------------------------
+// Streaming decode GEMV (M <= 64): a block of WAVES waves owns 16 output channels; K is walked in
+// 128-byte chunks dealt round-robin to the waves.  Per chunk a lane loads 32 contiguous bytes of
+// a weight row (a wave covers 16 rows x 128 B) and feeds two v_mfma_i32_16x16x64_i8 with the
+// activations loaded in the same lane->k mapping, so the k permutation is identical on both
+// operands and the integer sum is exact.  The next chunk is in flight while the current one is
+// multiplied.  The waves' partial tiles meet in LDS; no global split, no atomics.
+// ------------------------------------------------------------------------------------------
+template <int MB, int WAVES>
+__global__ __launch_bounds__(64 * WAVES) void k_gemv_stream(GemmArgs g) {
+	__shared__ v4i red[WAVES][MB][64];
 	const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-	const int col0 = (blockIdx.x * 4 + wave) * 16;
-	const int t_base = blockIdx.z * 16 * MB;
-	const int k_begin = blockIdx.y * g.k_split;
-	const int k_end = min(g.K, k_begin + g.k_split);
-	const int kofs = (lane >> 4) * 16;
-	const int my_col = col0 + (lane & 15);
+	const int col0 = blockIdx.x * 16;
+	const int ri = lane & 15, grp = lane >> 4;
+	const int C = g.K >> 7;
+	const int my_col = col0 + ri;
+	const bool col_ok = my_col < g.N;
+	const int8_t* wrow = g.w + (size_t)(col_ok ? my_col : 0) * g.K + grp * 32;
+	const int8_t* arow[MB];
+	bool row_ok[MB];
+#pragma unroll
+	for (int mb = 0; mb < MB; ++mb) {
+		const int r = mb * 16 + ri;
+		row_ok[mb] = r < g.M;
+		arow[mb] = g.a + (size_t)(row_ok[mb] ? r : 0) * g.lda + grp * 32;
+	}
 	v4i acc[MB];
 #pragma unroll
 	for (int mb = 0; mb < MB; ++mb) acc[mb] = v4i{0, 0, 0, 0};
-	const bool col_ok = my_col < g.N;
-	const int8_t* wrow = g.w + (size_t)(col_ok ? my_col : 0) * g.K;
-	for (int k = k_begin; k < k_end; k += 64) {
-		const bool kok = k + kofs < k_end;
-		v4i b = (col_ok && kok) ? load16(wrow + k + kofs) : v4i{0, 0, 0, 0};
+	const v4i z = v4i{0, 0, 0, 0};
+	int c = wave;
+	v4i b0 = z, b1 = z, a0[MB], a1[MB];
+#pragma unroll
+	for (int mb = 0; mb < MB; ++mb) a0[mb] = a1[mb] = z;
+	if (c < C) {
+		const int8_t* wp = wrow + (size_t)c * 128;
+		b0 = col_ok ? load16(wp) : z;
+		b1 = col_ok ? load16(wp + 16) : z;
 #pragma unroll
 		for (int mb = 0; mb < MB; ++mb) {
-			const int row = t_base + mb * 16 + (lane & 15);
-			v4i a = (row < g.M && kok) ? load16(g.a + (size_t)row * g.lda + k + kofs) : v4i{0, 0, 0, 0};
-			acc[mb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, acc[mb], 0, 0, 0);
+			a0[mb] = row_ok[mb] ? load16(arow[mb] + (size_t)c * 128) : z;
+			a1[mb] = row_ok[mb] ? load16(arow[mb] + (size_t)c * 128 + 16) : z;
 		}
 	}
-	const Epilogue& e = g.epi;
-	if (gridDim.y == 1) {
-		// direct epilogue: lane holds channel col0 + lane%16, tokens 4*(lane/16) + v
+	while (c < C) {
+		const int cn = c + WAVES;
+		v4i nb0 = z, nb1 = z, na0[MB], na1[MB];
 #pragma unroll
-		for (int mb = 0; mb < MB; ++mb) {
+		for (int mb = 0; mb < MB; ++mb) na0[mb] = na1[mb] = z;
+		if (cn < C) {
+			const int8_t* wp = wrow + (size_t)cn * 128;
+			nb0 = col_ok ? load16(wp) : z;
+			nb1 = col_ok ? load16(wp + 16) : z;
 #pragma unroll
-			for (int v = 0; v < 4; ++v) {
-				const int t = t_base + mb * 16 + (lane >> 4) * 4 + v;
-				const int j = col0 + (lane & 15);
-				uint64_t key = 0;
-				uint32_t mabs = 0;
-				int seg = 0;
-				bool live = t < g.M && j < g.N;
-				if (live) {
-					if (e.raw_out) {
-						e.raw_out[(size_t)t * g.N + j] = acc[mb][v];
-					} else if (e.argmax_key) {
-						const uint32_t logit = (uint32_t)acc[mb][v] ^ 0x80000000u;
-						key = ((uint64_t)logit << 32) | (uint64_t)(0xffffffffu - (uint32_t)j);
-					} else {
-						EpiResult r = epi_value(e, t, j, acc[mb][v]);
-						if (!r.ok) set_status(e.status, e.tok[t].slot, e.layer, kBiasReconcileProductOutOfDomain);
-						epi_store(e, r, t, j);
-						seg = r.seg;
-						if (e.seg[r.seg].mode == kSegFunnel) mabs = sat_abs_u32(r.v);
-					}
-				}
-				// reduce across the 16 lanes sharing token t (and the segment is uniform per
-				// 16-column wave tile as long as segment bounds are multiples of 16)
-				for (int o = 8; o > 0; o >>= 1) {
-					uint64_t ok2 = __shfl_xor(key, o, 16);
-					key = ok2 > key ? ok2 : key;
-					uint32_t om = __shfl_xor(mabs, o, 16);
-					mabs = om > mabs ? om : mabs;
-				}
-				if ((lane & 15) == 0 && t < g.M) {
-					if (e.argmax_key) {
-						if (key) atomicMax(&e.argmax_key[t], (unsigned long long)key);
-					} else if (col0 < g.N && e.seg[seg].mode == kSegFunnel && e.seg[seg].maxabs) {
-						atomicMax(&e.seg[seg].maxabs[t], mabs);
-					}
-				}
+			for (int mb = 0; mb < MB; ++mb) {
+				na0[mb] = row_ok[mb] ? load16(arow[mb] + (size_t)cn * 128) : z;
+				na1[mb] = row_ok[mb] ? load16(arow[mb] + (size_t)cn * 128 + 16) : z;
 			}
 		}
-		return;
-	}
-	// split-K: accumulate partials
 #pragma unroll
-	for (int mb = 0; mb < MB; ++mb) {
+		for (int mb = 0; mb < MB; ++mb) {
+			acc[mb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0[mb], b0, acc[mb], 0, 0, 0);
+			acc[mb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1[mb], b1, acc[mb], 0, 0, 0);
+		}
+		c = cn;
+		b0 = nb0;
+		b1 = nb1;
+#pragma unroll
+		for (int mb = 0; mb < MB; ++mb) {
+			a0[mb] = na0[mb];
+			a1[mb] = na1[mb];
+		}
+	}
+#pragma unroll
+	for (int mb = 0; mb < MB; ++mb) red[wave][mb][lane] = acc[mb];
+	__syncthreads();
+	// wave w finishes row block mb = w (and w + WAVES, ... when MB > WAVES)
+	const Epilogue& e = g.epi;
+	const int j = col0 + ri;
+	for (int mb = wave; mb < MB; mb += WAVES) {
+		v4i tot = red[0][mb][lane];
+		for (int w = 1; w < WAVES; ++w) {
+			const v4i x = red[w][mb][lane];
+			tot[0] += x[0];
+			tot[1] += x[1];
+			tot[2] += x[2];
+			tot[3] += x[3];
+		}
 #pragma unroll
 		for (int v = 0; v < 4; ++v) {
-			const int t = t_base + mb * 16 + (lane >> 4) * 4 + v;
-			const int j = col0 + (lane & 15);
-			if (t < g.M && j < g.N) atomicAdd(&g.acc[(size_t)t * g.N + j], acc[mb][v]);
+			const int t = mb * 16 + grp * 4 + v;
+			uint64_t key = 0;
+			uint32_t mabs = 0;
+			int seg = 0;
+			if (t < g.M && j < g.N) epi_element(e, g.N, t, j, tot[v], &key, &mabs, &seg);
+			epi_publish(e, blockIdx.x, t, t < g.M && col0 < g.N, key, mabs, seg);
 		}
 	}
-	__threadfence();
-	__shared__ uint32_t s_last;
-	__syncthreads();
-	const int tile = blockIdx.z * gridDim.x + blockIdx.x;
-	if (threadIdx.x == 0) {
-		uint32_t prev = atomicAdd(&g.tile_cnt[tile], 1u);
-		s_last = (prev == gridDim.y - 1) ? 1u : 0u;
-	}
-	__syncthreads();
-	if (!s_last) return;
-	__threadfence();
-	// last block: the tile is 64 columns x 16*MB tokens; thread -> column tid%64, token rows
-	const int j = blockIdx.x * 64 + (threadIdx.x & 63);
-	for (int tt = threadIdx.x >> 6; tt < 16 * MB; tt += kBlock / 64) {
-		const int t = t_base + tt;
-		uint32_t mabs = 0;
-		int seg = 0;
-		uint64_t key = 0;
-		if (t < g.M && j < g.N) {
-			const int32_t a = atomicExch(&g.acc[(size_t)t * g.N + j], 0);
-			if (e.raw_out) {
-				e.raw_out[(size_t)t * g.N + j] = a;
-			} else if (e.argmax_key) {
-				const uint32_t logit = (uint32_t)a ^ 0x80000000u;
-				key = ((uint64_t)logit << 32) | (uint64_t)(0xffffffffu - (uint32_t)j);
-			} else {
-				EpiResult r = epi_value(e, t, j, a);
-				if (!r.ok) set_status(e.status, e.tok[t].slot, e.layer, kBiasReconcileProductOutOfDomain);
-				epi_store(e, r, t, j);
-				seg = r.seg;
-				if (e.seg[r.seg].mode == kSegFunnel) mabs = sat_abs_u32(r.v);
-			}
-		}
-		// a wave covers 64 consecutive columns of one token; segments are multiples of 16 wide
-		// so reduce per 16-lane group
-		for (int o = 8; o > 0; o >>= 1) {
-			uint64_t ok2 = __shfl_xor(key, o, 16);
-			key = ok2 > key ? ok2 : key;
-			uint32_t om = __shfl_xor(mabs, o, 16);
-			mabs = om > mabs ? om : mabs;
-		}
-		if ((threadIdx.x & 15) == 0 && t < g.M && j < g.N) {
-			if (e.argmax_key) {
-				atomicMax(&e.argmax_key[t], (unsigned long long)key);
-			} else if (e.seg[seg].mode == kSegFunnel && e.seg[seg].maxabs) {
-				atomicMax(&e.seg[seg].maxabs[t], mabs);
-			}
-		}
-	}
-	if (threadIdx.x == 0) g.tile_cnt[tile] = 0;
 }
 
 // ------------------------------------------------------------------------------------------
 // tiled MFMA GEMM for prefill chunks: 128x128 block tile, BK=64, LDS-staged A and B,
-// v_mfma_i32_32x32x32_i8, each wave a 64x64 sub-tile (2x2 MFMA tiles).
+// v_mfma_i32_32x32x32_i8, each wave a 64x64 sub-tile (2x2 MFMA tiles).  The accumulators go
+// through LDS for the epilogue so every thread finishes whole 16-column tile rows.
 // ------------------------------------------------------------------------------------------
 constexpr int kBM = 128, kBN = 128, kBK = 64, kLdsStride = 80;  // padded row stride (bytes)
 
 __global__ __launch_bounds__(kBlock) void k_gemm_tiled(GemmArgs g) {
-	__shared__ __attribute__((aligned(16))) int8_t sa[2][kBM * kLdsStride];
-	__shared__ __attribute__((aligned(16))) int8_t sb[2][kBN * kLdsStride];
+	__shared__ __attribute__((aligned(16))) int8_t smem[2 * (kBM + kBN) * kLdsStride];
+	int8_t* sa0 = smem;
+	int8_t* sb0 = smem + kBM * kLdsStride;
 	const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
 	const int m0 = blockIdx.y * kBM, n0 = blockIdx.x * kBN;
 	const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
-	v16i acc[2][2];
-#pragma unroll
-	for (int i = 0; i < 2; ++i)
-#pragma unroll
-		for (int j = 0; j < 2; ++j)
-			for (int v = 0; v < 16; ++v) acc[i][j][v] = 0;
+	v16i acc00, acc01, acc10, acc11;
+	for (int v = 0; v < 16; ++v) acc00[v] = acc01[v] = acc10[v] = acc11[v] = 0;
 
-	// global->LDS: each thread moves 2x16B of A and 2x16B of B per K step
-	// tile 128 rows x 64 bytes = 512 chunks of 16B; thread t handles chunks t and t+256
-	auto gload = [&](int k0, v4i ra[2], v4i rb[2]) {
-#pragma unroll
-		for (int c = 0; c < 2; ++c) {
-			const int chunk = threadIdx.x + c * kBlock;
-			const int r = chunk >> 2, kc = (chunk & 3) * 16;
-			const int gm = m0 + r, gn = n0 + r;
-			const bool kok = k0 + kc < g.K;
-			ra[c] = (gm < g.M && kok) ? load16(g.a + (size_t)gm * g.lda + k0 + kc) : v4i{0, 0, 0, 0};
-			rb[c] = (gn < g.N && kok) ? load16(g.w + (size_t)gn * g.K + k0 + kc) : v4i{0, 0, 0, 0};
-		}
+	const int chunk0 = threadIdx.x, chunk1 = threadIdx.x + kBlock;
+	const int r0 = chunk0 >> 2, kc0 = (chunk0 & 3) * 16;
+	const int r1 = chunk1 >> 2, kc1 = (chunk1 & 3) * 16;
+	v4i ra0, ra1, rb0, rb1;
+	const v4i z = v4i{0, 0, 0, 0};
+	auto gload = [&](int k0) {
+		ra0 = (m0 + r0 < g.M && k0 + kc0 < g.K) ? load16(g.a + (size_t)(m0 + r0) * g.lda + k0 + kc0) : z;
+		ra1 = (m0 + r1 < g.M && k0 + kc1 < g.K) ? load16(g.a + (size_t)(m0 + r1) * g.lda + k0 + kc1) : z;
+		rb0 = (n0 + r0 < g.N && k0 + kc0 < g.K) ? load16(g.w + (size_t)(n0 + r0) * g.K + k0 + kc0) : z;
+		rb1 = (n0 + r1 < g.N && k0 + kc1 < g.K) ? load16(g.w + (size_t)(n0 + r1) * g.K + k0 + kc1) : z;
 	};
-	auto sstore = [&](int buf, const v4i ra[2], const v4i rb[2]) {
-#pragma unroll
-		for (int c = 0; c < 2; ++c) {
-			const int chunk = threadIdx.x + c * kBlock;
-			const int r = chunk >> 2, kc = (chunk & 3) * 16;
-			*(v4i*)&sa[buf][r * kLdsStride + kc] = ra[c];
-			*(v4i*)&sb[buf][r * kLdsStride + kc] = rb[c];
-		}
+	auto sstore = [&](int buf) {
+		int8_t* sa = smem + buf * (kBM + kBN) * kLdsStride;
+		int8_t* sb = sa + kBM * kLdsStride;
+		*(v4i*)&sa[r0 * kLdsStride + kc0] = ra0;
+		*(v4i*)&sa[r1 * kLdsStride + kc1] = ra1;
+		*(v4i*)&sb[r0 * kLdsStride + kc0] = rb0;
+		*(v4i*)&sb[r1 * kLdsStride + kc1] = rb1;
 	};
-	v4i ra[2], rb[2];
-	gload(0, ra, rb);
-	sstore(0, ra, rb);
+	gload(0);
+	sstore(0);
 	__syncthreads();
 	const int nk = (g.K + kBK - 1) / kBK;
 	for (int it = 0; it < nk; ++it) {
 		const int buf = it & 1;
-		if (it + 1 < nk) gload((it + 1) * kBK, ra, rb);
+		const int8_t* sa = smem + buf * (kBM + kBN) * kLdsStride;
+		const int8_t* sb = sa + kBM * kLdsStride;
+		if (it + 1 < nk) gload((it + 1) * kBK);
 #pragma unroll
 		for (int ks = 0; ks < 2; ++ks) {  // two K=32 MFMA steps per BK=64
 			const int kk = ks * 32 + (lane >> 5) * 16;
-			v4i af[2], bf[2];
-#pragma unroll
-			for (int i = 0; i < 2; ++i) af[i] = *(const v4i*)&sa[buf][(wm + i * 32 + (lane & 31)) * kLdsStride + kk];
-#pragma unroll
-			for (int j = 0; j < 2; ++j) bf[j] = *(const v4i*)&sb[buf][(wn + j * 32 + (lane & 31)) * kLdsStride + kk];
-#pragma unroll
-			for (int i = 0; i < 2; ++i)
-#pragma unroll
-				for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
+			const v4i a0 = *(const v4i*)&sa[(wm + (lane & 31)) * kLdsStride + kk];
+			const v4i a1 = *(const v4i*)&sa[(wm + 32 + (lane & 31)) * kLdsStride + kk];
+			const v4i b0 = *(const v4i*)&sb[(wn + (lane & 31)) * kLdsStride + kk];
+			const v4i b1 = *(const v4i*)&sb[(wn + 32 + (lane & 31)) * kLdsStride + kk];
+			acc00 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, b0, acc00, 0, 0, 0);
+			acc01 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, b1, acc01, 0, 0, 0);
+			acc10 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, b0, acc10, 0, 0, 0);
+			acc11 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, b1, acc11, 0, 0, 0);
 		}
-		if (it + 1 < nk) {
-			__syncthreads();
-			sstore(buf ^ 1, ra, rb);
-			__syncthreads();
-		}
+		if (it + 1 < nk) sstore(buf ^ 1);
+		__syncthreads();
 	}
-	// epilogue: 32x32 output layout -- lane holds column lane%32, rows 8*(v/4) + 4*(lane/32) + v%4
+	(void)sa0;
+	(void)sb0;
+	// accumulators -> LDS as int32 [128 rows][128 cols] in two passes of 64 rows (32 KB each)
+	int32_t* ct = (int32_t*)smem;  // 2 * 256 * 80 = 40 KB >= 64 x 128 x 4 = 32 KB
 	const Epilogue& e = g.epi;
-#pragma unroll
-	for (int i = 0; i < 2; ++i) {
-#pragma unroll
-		for (int j = 0; j < 2; ++j) {
-#pragma unroll
+	for (int half = 0; half < 2; ++half) {
+		__syncthreads();
+		if ((wave >> 1) == half) {
+			// 32x32 layout: lane holds column lane%32, rows 8*(v/4) + 4*(lane/32) + v%4
 			for (int v = 0; v < 16; ++v) {
-				const int t = m0 + wm + i * 32 + (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3);
-				const int col = n0 + wn + j * 32 + (lane & 31);
-				uint32_t mabs = 0;
-				int seg = 0;
-				uint64_t key = 0;
-				if (t < g.M && col < g.N) {
-					if (e.raw_out) {
-						e.raw_out[(size_t)t * g.N + col] = acc[i][j][v];
-					} else if (e.argmax_key) {
-						const uint32_t logit = (uint32_t)acc[i][j][v] ^ 0x80000000u;
-						key = ((uint64_t)logit << 32) | (uint64_t)(0xffffffffu - (uint32_t)col);
-					} else {
-						EpiResult r = epi_value(e, t, col, acc[i][j][v]);
-						if (!r.ok) set_status(e.status, e.tok[t].slot, e.layer, kBiasReconcileProductOutOfDomain);
-						epi_store(e, r, t, col);
-						seg = r.seg;
-						if (e.seg[r.seg].mode == kSegFunnel) mabs = sat_abs_u32(r.v);
-					}
-				}
-				for (int o = 8; o > 0; o >>= 1) {  // 16-lane groups share a token and a segment
-					uint64_t ok2 = __shfl_xor(key, o, 16);
-					key = ok2 > key ? ok2 : key;
-					uint32_t om = __shfl_xor(mabs, o, 16);
-					mabs = om > mabs ? om : mabs;
-				}
-				if ((lane & 15) == 0 && t < g.M && col < g.N) {
-					if (e.argmax_key) {
-						atomicMax(&e.argmax_key[t], (unsigned long long)key);
-					} else if (e.seg[seg].mode == kSegFunnel && e.seg[seg].maxabs) {
-						atomicMax(&e.seg[seg].maxabs[t], mabs);
-					}
-				}
+				const int rr = (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3);
+				const int cc = lane & 31;
+				ct[(rr) * kBN + wn + cc] = acc00[v];
+				ct[(rr) * kBN + wn + 32 + cc] = acc01[v];
+				ct[(32 + rr) * kBN + wn + cc] = acc10[v];
+				ct[(32 + rr) * kBN + wn + 32 + cc] = acc11[v];
 			}
+		}
+		__syncthreads();
+		// thread -> (row, 16-column group, column): 64 rows x 8 groups x 16 = 8192 elements
+		for (int idx = threadIdx.x; idx < 64 * kBN; idx += kBlock) {
+			const int rr = idx >> 7, cc = idx & 127;
+			const int t = m0 + half * 64 + rr, col = n0 + cc;
+			uint64_t key = 0;
+			uint32_t mabs = 0;
+			int seg = 0;
+			if (t < g.M && col < g.N) epi_element(e, g.N, t, col, ct[rr * kBN + cc], &key, &mabs, &seg);
+			epi_publish(e, col >> 4, t, t < g.M && (col & ~15) < g.N, key, mabs, seg);
 		}
 	}
 }
@@ -382,11 +376,11 @@ __global__ __launch_bounds__(kBlock) void k_gemm_tiled(GemmArgs g) {
 // ------------------------------------------------------------------------------------------
 
 // forward_sites.cpp:763-787 -- embed row -> funnel ("embed" site, empty incoming)
-__global__ __launch_bounds__(kBlock) void k_embed(const int32_t* tokens, const int8_t* embed_w, int H, int vocab,
+__global__ __launch_bounds__(kRowBlock) void k_embed(const int32_t* tokens, const int8_t* embed_w, int H, int vocab,
                                                   Scale site, int8_t* out_codes, const int32_t* out_idx,
                                                   Scale* out_scale, const int32_t* scale_idx, const TokenInfo* tok,
                                                   int32_t* status) {
-	__shared__ uint64_t red[kBlock / 64];
+	__shared__ uint64_t red[16];
 	__shared__ FunnelPlan plan;
 	__shared__ int32_t st;
 	const int t = blockIdx.x;
@@ -397,7 +391,7 @@ __global__ __launch_bounds__(kBlock) void k_embed(const int32_t* tokens, const i
 	}
 	const int8_t* row = embed_w + (size_t)id * H;
 	uint64_t mx = 0;
-	for (int i = threadIdx.x; i < H; i += kBlock) {
+	for (int i = threadIdx.x; i < H; i += kRowBlock) {
 		int64_t v = row[i];
 		uint64_t a = v < 0 ? -v : v;
 		mx = a > mx ? a : mx;
@@ -410,7 +404,7 @@ __global__ __launch_bounds__(kBlock) void k_embed(const int32_t* tokens, const i
 		return;
 	}
 	int8_t* out = out_codes + (size_t)out_idx[t] * H;
-	for (int i = threadIdx.x; i < H; i += kBlock) out[i] = requant_code_small(row[i], (uint64_t)plan.r, plan.s);
+	for (int i = threadIdx.x; i < H; i += kRowBlock) out[i] = requant_code_small(row[i], (uint64_t)plan.r, plan.s);
 	if (threadIdx.x == 0) out_scale[scale_idx[t]] = plan.out;
 }
 
@@ -419,10 +413,11 @@ __global__ __launch_bounds__(kBlock) void k_embed(const int32_t* tokens, const i
 __device__ int32_t rmsnorm_row(const int8_t* h, const int32_t* g, int H, Scale site, int8_t* out, Scale* out_scale,
                                int64_t* out_recip, uint64_t* red_u, int64_t* red_s) {
 	__shared__ int64_t s_root;
+	__shared__ int64_t fd[256];  // floor((h << 32) / root) for every int8 h
 	__shared__ FunnelPlan plan;
 	__shared__ int32_t st;
 	int64_t ss = 0;
-	for (int i = threadIdx.x; i < H; i += kBlock) ss += (int64_t)h[i] * h[i];
+	for (int i = threadIdx.x; i < H; i += blockDim.x) ss += (int64_t)h[i] * h[i];
 	ss = block_sum_i64(ss, red_s);
 	if (threadIdx.x == 0) {
 		int64_t root = isqrt(floor_div(ss << 32, (int64_t)H));
@@ -430,9 +425,15 @@ __device__ int32_t rmsnorm_row(const int8_t* h, const int32_t* g, int H, Scale s
 	}
 	__syncthreads();
 	const int64_t root = s_root;
+	if (threadIdx.x < 256) {
+		const int64_t hv = (int64_t)threadIdx.x - 128;
+		const int64_t a = hv << 32;
+		fd[threadIdx.x] = a >= 0 ? div_floor_pos(a, root) : -div_floor_pos(-a + root - 1, root);
+	}
+	__syncthreads();
 	uint64_t mx = 0;
-	for (int i = threadIdx.x; i < H; i += kBlock) {
-		int64_t w = floor_div((int64_t)h[i] << 32, root) * (int64_t)g[i];
+	for (int i = threadIdx.x; i < H; i += blockDim.x) {
+		int64_t w = fd[(int)h[i] + 128] * (int64_t)g[i];
 		uint64_t a = w < 0 ? (uint64_t)0 - (uint64_t)w : (uint64_t)w;
 		mx = a > mx ? a : mx;
 	}
@@ -440,22 +441,22 @@ __device__ int32_t rmsnorm_row(const int8_t* h, const int32_t* g, int H, Scale s
 	if (threadIdx.x == 0) st = funnel_plan(mx, nullptr, 0, site, &plan);
 	__syncthreads();
 	if (st != kOk) return st;
-	for (int i = threadIdx.x; i < H; i += kBlock) {
-		int64_t w = floor_div((int64_t)h[i] << 32, root) * (int64_t)g[i];
+	for (int i = threadIdx.x; i < H; i += blockDim.x) {
+		int64_t w = fd[(int)h[i] + 128] * (int64_t)g[i];
 		out[i] = requant_code_small(w, (uint64_t)plan.r, plan.s);
 	}
 	if (threadIdx.x == 0) {
 		*out_scale = plan.out;
-		if (out_recip) *out_recip = fits_i32(plan.out.m) ? reciprocal(plan.out.m) : 0;
+		if (out_recip) *out_recip = fits_i32(plan.out.m) ? reciprocal_fast(plan.out.m) : 0;
 	}
 	__syncthreads();
 	return kOk;
 }
 
-__global__ __launch_bounds__(kBlock) void k_rmsnorm(sslm_launch::RowNormArgs a, int H, const TokenInfo* tok,
+__global__ __launch_bounds__(kRowBlock) void k_rmsnorm(sslm_launch::RowNormArgs a, int H, const TokenInfo* tok,
                                                     int32_t* status, int32_t layer) {
-	__shared__ uint64_t red_u[kBlock / 64];
-	__shared__ int64_t red_s[kBlock / 64];
+	__shared__ uint64_t red_u[16];
+	__shared__ int64_t red_s[16];
 	const int t = blockIdx.x;
 	if (status[tok[t].slot] != 0) return;
 	const int8_t* h = a.in_codes + (size_t)a.in_idx[t] * a.ld_in;
@@ -465,7 +466,7 @@ __global__ __launch_bounds__(kBlock) void k_rmsnorm(sslm_launch::RowNormArgs a, 
 }
 
 // q funnel + RoPE(q); K/V landing, RoPE(K), KV write (forward_sites.cpp:1281-1418, :1748-1787)
-__global__ __launch_bounds__(kBlock) void k_qkv_post(sslm_launch::QkvPostArgs a) {
+__global__ __launch_bounds__(kRowBlock) void k_qkv_post(sslm_launch::QkvPostArgs a) {
 	__shared__ FunnelPlan plan;
 	__shared__ int32_t st;
 	__shared__ unsigned long long sat_block;
@@ -474,11 +475,11 @@ __global__ __launch_bounds__(kBlock) void k_qkv_post(sslm_launch::QkvPostArgs a)
 	if (a.status[ti.slot] != 0) return;
 	const int H = a.H, D = a.D, pairs = D / 2;
 	const int64_t pos = ti.pos;
+	__shared__ uint64_t red_u[16];
+	const uint64_t mx = reduce_part(a.q_maxpart, 0, H / 16, t, red_u);
 	if (threadIdx.x == 0) {
 		sat_block = 0;
 		const Scale inc = a.in_scale[t];
-		uint32_t mx = a.q_maxabs[t];
-		a.q_maxabs[t] = 0;
 		st = funnel_plan(mx, &inc, 1, a.q_site, &plan);
 		if (st == kOk && (pos < 0 || pos >= a.cap)) st = kPositionOverCap;
 	}
@@ -491,7 +492,7 @@ __global__ __launch_bounds__(kBlock) void k_qkv_post(sslm_launch::QkvPostArgs a)
 	const int64_t* sn = a.rope_sin + pos * pairs;
 	// q: codes of pair (2i, 2i+1), rotated, clamped
 	const int32_t* qf = a.q_f + (size_t)t * H;
-	for (int p = threadIdx.x; p < H / 2; p += kBlock) {
+	for (int p = threadIdx.x; p < H / 2; p += kRowBlock) {
 		const int i = p % pairs;
 		const int32_t x = requant_code_small(qf[2 * p], (uint64_t)plan.r, plan.s);
 		const int32_t y = requant_code_small(qf[2 * p + 1], (uint64_t)plan.r, plan.s);
@@ -510,7 +511,7 @@ __global__ __launch_bounds__(kBlock) void k_qkv_post(sslm_launch::QkvPostArgs a)
 	int8_t* kstore = blk + (int64_t)a.layer * half * 2;
 	int8_t* vstore = kstore + half;
 	unsigned long long sat = 0;
-	for (int p = threadIdx.x; p < KVH / 2; p += kBlock) {
+	for (int p = threadIdx.x; p < KVH / 2; p += kRowBlock) {
 		const int h = (2 * p) / D;
 		const int i = p % pairs;
 		const int64_t k_e = composed_exponent(ns.e, a.e_t_k[h]);
@@ -641,7 +642,7 @@ __global__ __launch_bounds__(kBlock) void k_attention(sslm_launch::AttnArgs a, i
 		const int64_t denom = rowsum[g] > 1 ? rowsum[g] : 1;
 		for (int64_t p = threadIdx.x; p < width; p += kBlock) {
 			const int64_t e = sc[(int64_t)g * a.cap + p];
-			sc[(int64_t)g * a.cap + p] = (e << 15) / denom;
+			sc[(int64_t)g * a.cap + p] = div_floor_pos(e << 15, denom);
 		}
 	}
 	__syncthreads();
@@ -660,22 +661,19 @@ __global__ __launch_bounds__(kBlock) void k_attention(sslm_launch::AttnArgs a, i
 		mabs = ab > mabs ? ab : mabs;
 	}
 	mabs = block_max_u64(mabs, red_u);
-	if (threadIdx.x == 0) atomicMax(&a.ctx_maxabs[t], mabs > 0xffffffffull ? 0xffffffffu : (uint32_t)mabs);
+	if (threadIdx.x == 0) a.ctx_maxpart[(size_t)kvh * kPartLd + t] = mabs > 0xffffffffull ? 0xffffffffu : (uint32_t)mabs;
 }
 
 // funnel over an int32 fold-output row (checked_chain_funnel.cpp:257-364)
-__global__ __launch_bounds__(kBlock) void k_funnel(sslm_launch::FunnelArgs a) {
+__global__ __launch_bounds__(kRowBlock) void k_funnel(sslm_launch::FunnelArgs a) {
 	__shared__ FunnelPlan plan;
 	__shared__ int32_t st;
 	const int t = blockIdx.x;
 	const int slot = a.tok[t].slot;
-	if (a.status[slot] != 0) {
-		if (threadIdx.x == 0) a.maxabs[t] = 0;
-		return;
-	}
+	__shared__ uint64_t red_u[16];
+	if (a.status[slot] != 0) return;
+	const uint64_t mx = reduce_part(a.maxpart, 0, a.ntiles, t, red_u);
 	if (threadIdx.x == 0) {
-		uint32_t mx = a.maxabs[t];
-		a.maxabs[t] = 0;
 		Scale inc;
 		if (a.incoming) inc = a.incoming[t];
 		st = funnel_plan(mx, a.incoming ? &inc : nullptr, a.incoming ? 1 : 0, a.site, &plan);
@@ -686,34 +684,30 @@ __global__ __launch_bounds__(kBlock) void k_funnel(sslm_launch::FunnelArgs a) {
 		return;
 	}
 	const int32_t* f = a.f + (size_t)t * a.ld_f;
-	for (int i = threadIdx.x; i < a.N; i += kBlock) a.out[(size_t)t * a.N + i] = requant_code_small(f[i], (uint64_t)plan.r, plan.s);
+	for (int i = threadIdx.x; i < a.N; i += kRowBlock) a.out[(size_t)t * a.N + i] = requant_code_small(f[i], (uint64_t)plan.r, plan.s);
 	if (threadIdx.x == 0) a.out_scale[t] = plan.out;
 }
 
 // projection funnel -> residual reconcile -> (optional) RMSNorm, all on one token's row
 // (forward_sites.cpp:871-989 residual; :410-459 norm)
-__global__ __launch_bounds__(kBlock) void k_residual_norm(sslm_launch::ResidualArgs a) {
+__global__ __launch_bounds__(kRowBlock) void k_residual_norm(sslm_launch::ResidualArgs a) {
 	__shared__ FunnelPlan bplan, rplan;
 	__shared__ int32_t st;
 	__shared__ int64_t r_h;
-	__shared__ uint64_t red_u[kBlock / 64];
-	__shared__ int64_t red_s[kBlock / 64];
+	__shared__ uint64_t red_u[16];
+	__shared__ int64_t red_s[16];
 	const int t = blockIdx.x;
 	const int slot = a.tok[t].slot;
 	const int H = a.H;
-	if (a.status[slot] != 0) {
-		if (threadIdx.x == 0) a.branch_maxabs[t] = 0;
-		return;
-	}
+	if (a.status[slot] != 0) return;
 	const int8_t* stream = a.stream + (size_t)a.stream_idx[t] * H;
 	const Scale ss = a.stream_scale[a.stream_idx[t]];
+	const uint64_t bmx = reduce_part(a.branch_maxpart, 0, H / 16, t, red_u);
 	if (threadIdx.x == 0) {
-		uint32_t mx = a.branch_maxabs[t];
-		a.branch_maxabs[t] = 0;
 		const Scale inc = a.branch_in[t];
-		st = funnel_plan(mx, &inc, 1, a.branch_site, &bplan);
+		st = funnel_plan(bmx, &inc, 1, a.branch_site, &bplan);
 		if (st == kOk && !fits_i32(ss.m)) st = kCarriedScaleMantissaOutOfDomain;
-		if (st == kOk) r_h = reciprocal(ss.m);
+		if (st == kOk) r_h = reciprocal_fast(ss.m);
 	}
 	__syncthreads();
 	if (st != kOk) {
@@ -725,7 +719,7 @@ __global__ __launch_bounds__(kBlock) void k_residual_norm(sslm_launch::ResidualA
 	const int32_t* bf = a.branch_f + (size_t)t * H;
 	uint64_t mx = 0;
 	int bad = 0;
-	for (int i = threadIdx.x; i < H; i += kBlock) {
+	for (int i = threadIdx.x; i < H; i += kRowBlock) {
 		const int8_t code = requant_code_small(bf[i], (uint64_t)bplan.r, bplan.s);
 		bool cl, ex;
 		const int64_t rec = landing_rescale(code, bs.m, r_h, k, &cl, &ex);
@@ -751,7 +745,7 @@ __global__ __launch_bounds__(kBlock) void k_residual_norm(sslm_launch::ResidualA
 	// `out` never aliases `stream` (the host routes attn_stream and the committed stream through
 	// distinct buffers), so codes are written as they are formed.
 	int8_t* out = a.out_stream + (size_t)a.out_idx[t] * H;
-	for (int i = threadIdx.x; i < H; i += kBlock) {
+	for (int i = threadIdx.x; i < H; i += kRowBlock) {
 		const int8_t code = requant_code_small(bf[i], (uint64_t)bplan.r, bplan.s);
 		bool cl, ex;
 		const int64_t w = landing_rescale(code, bs.m, r_h, k, &cl, &ex) + stream[i];
@@ -767,25 +761,18 @@ __global__ __launch_bounds__(kBlock) void k_residual_norm(sslm_launch::ResidualA
 }
 
 // gate/up funnels -> MlpActSite (forward_sites.cpp:796-864) -> act funnel
-__global__ __launch_bounds__(kBlock) void k_mlp_act(sslm_launch::ActArgs a) {
+__global__ __launch_bounds__(kRowBlock) void k_mlp_act(sslm_launch::ActArgs a) {
 	__shared__ FunnelPlan gp, up, ap;
 	__shared__ int32_t st;
-	__shared__ uint64_t red_u[kBlock / 64];
+	__shared__ uint64_t red_u[16];
 	const int t = blockIdx.x;
 	const int slot = a.tok[t].slot;
 	const int I = a.I;
-	if (a.status[slot] != 0) {
-		if (threadIdx.x == 0) {
-			a.gate_maxabs[t] = 0;
-			a.up_maxabs[t] = 0;
-		}
-		return;
-	}
+	if (a.status[slot] != 0) return;
+	const uint64_t gm = reduce_part(a.gu_maxpart, 0, I / 16, t, red_u);
+	const uint64_t um = reduce_part(a.gu_maxpart, I / 16, I / 16, t, red_u);
 	if (threadIdx.x == 0) {
 		const Scale inc = a.in_scale[t];
-		uint32_t gm = a.gate_maxabs[t], um = a.up_maxabs[t];
-		a.gate_maxabs[t] = 0;
-		a.up_maxabs[t] = 0;
 		st = funnel_plan(gm, &inc, 1, a.gate_site, &gp);
 		if (st == kOk) st = funnel_plan(um, &inc, 1, a.up_site, &up);
 		if (st == kOk) st = check_silu_scale(gp.out.m, gp.out.e);
@@ -799,7 +786,7 @@ __global__ __launch_bounds__(kBlock) void k_mlp_act(sslm_launch::ActArgs a) {
 	const int32_t* gf = a.gu_f + (size_t)t * 2 * I;
 	const int32_t* uf = gf + I;
 	uint64_t mx = 0;
-	for (int i = threadIdx.x; i < I; i += kBlock) {
+	for (int i = threadIdx.x; i < I; i += kRowBlock) {
 		const int8_t gc = requant_code_small(gf[i], (uint64_t)gp.r, gp.s);
 		const int8_t uc = requant_code_small(uf[i], (uint64_t)up.r, up.s);
 		const int32_t sig = silu_sigmoid_q15(a.silu, gc, gs.m, (int)gs.e);
@@ -817,7 +804,7 @@ __global__ __launch_bounds__(kBlock) void k_mlp_act(sslm_launch::ActArgs a) {
 		if (threadIdx.x == 0) set_status(a.status, slot, a.layer, st);
 		return;
 	}
-	for (int i = threadIdx.x; i < I; i += kBlock) {
+	for (int i = threadIdx.x; i < I; i += kRowBlock) {
 		const int8_t gc = requant_code_small(gf[i], (uint64_t)gp.r, gp.s);
 		const int8_t uc = requant_code_small(uf[i], (uint64_t)up.r, up.s);
 		const int32_t sig = silu_sigmoid_q15(a.silu, gc, gs.m, (int)gs.e);
@@ -845,12 +832,19 @@ __global__ __launch_bounds__(kBlock) void k_lora_u(sslm_launch::LoraUArgs a) {
 	}
 }
 
-__global__ void k_argmax_finalize(unsigned long long* keys, int M, int32_t* out) {
-	const int t = blockIdx.x * blockDim.x + threadIdx.x;
-	if (t >= M) return;
-	const unsigned long long k = keys[t];
-	out[t] = (int32_t)(0xffffffffu - (uint32_t)(k & 0xffffffffull));
-	keys[t] = 0;
+// lowest-index argmax (forward_sites.cpp:2427-2437) from per-tile keys: the key orders by
+// logit, then by the complement of the index, so the maximum key is the lowest maximal index
+__global__ __launch_bounds__(kBlock) void k_argmax_finalize(const unsigned long long* keys, int ntiles,
+                                                            int32_t* out) {
+	__shared__ uint64_t red[16];
+	const int t = blockIdx.x;
+	uint64_t k = 0;
+	for (int i = threadIdx.x; i < ntiles; i += blockDim.x) {
+		const uint64_t v = keys[(size_t)i * kPartLd + t];
+		k = v > k ? v : k;
+	}
+	k = block_max_u64(k, red);
+	if (threadIdx.x == 0) out[t] = (int32_t)(0xffffffffu - (uint32_t)(k & 0xffffffffull));
 }
 
 }  // namespace sslm
@@ -860,38 +854,48 @@ __global__ void k_argmax_finalize(unsigned long long* keys, int M, int32_t* out)
 // ------------------------------------------------------------------------------------------
 namespace sslm_launch {
 
+template <int MB>
+static void launch_gemv(const GemmArgs& g, int waves, hipStream_t s) {
+	dim3 grid((g.N + 15) / 16);
+	if (waves >= 16) hipLaunchKernelGGL((k_gemv_stream<MB, 16>), grid, dim3(64 * 16), 0, s, g);
+	else if (waves >= 8) hipLaunchKernelGGL((k_gemv_stream<MB, 8>), grid, dim3(64 * 8), 0, s, g);
+	else hipLaunchKernelGGL((k_gemv_stream<MB, 4>), grid, dim3(64 * 4), 0, s, g);
+}
+
 void gemm(const GemmArgs& g, hipStream_t s) {
 	if (g.M <= 0 || g.N <= 0) return;
-	if (g.M > 64) {
-		dim3 grid((g.N + kBN - 1) / kBN, (g.M + kBM - 1) / kBM);
-		hipLaunchKernelGGL(k_gemm_tiled, grid, dim3(kBlock), 0, s, g);
+	if (g.M <= 64 && g.K % 128 == 0) {
+		// enough waves to cover the chip: few output tiles -> more waves per tile along K
+		const int tiles = (g.N + 15) / 16;
+		int waves = tiles >= 1024 ? 4 : (tiles >= 256 ? 8 : 16);
+		const int mblocks = (g.M + 15) / 16;
+		if (mblocks >= 3 && waves > 8) waves = 8;
+		switch (mblocks) {
+			case 1: launch_gemv<1>(g, waves, s); break;
+			case 2: launch_gemv<2>(g, waves, s); break;
+			case 3: launch_gemv<3>(g, waves, s); break;
+			default: launch_gemv<4>(g, waves, s); break;
+		}
 		return;
 	}
-	const int splits = (g.K + g.k_split - 1) / g.k_split;
-	const int mblocks = (g.M + 15) / 16;
-	dim3 grid((g.N + 63) / 64, splits, 1);
-	switch (mblocks) {
-		case 1: hipLaunchKernelGGL(k_gemv<1>, grid, dim3(kBlock), 0, s, g); break;
-		case 2: hipLaunchKernelGGL(k_gemv<2>, grid, dim3(kBlock), 0, s, g); break;
-		case 3: hipLaunchKernelGGL(k_gemv<3>, grid, dim3(kBlock), 0, s, g); break;
-		default: hipLaunchKernelGGL(k_gemv<4>, grid, dim3(kBlock), 0, s, g); break;
-	}
+	dim3 grid((g.N + kBN - 1) / kBN, (g.M + kBM - 1) / kBM);
+	hipLaunchKernelGGL(k_gemm_tiled, grid, dim3(kBlock), 0, s, g);
 }
 
 void embed(const int32_t* tokens, int M, const int8_t* embed_w, int H, int vocab, Scale site, int8_t* out_codes,
            const int32_t* out_idx, Scale* out_scale, const int32_t* scale_idx, const TokenInfo* tok,
            int32_t* status, hipStream_t s) {
-	hipLaunchKernelGGL(k_embed, dim3(M), dim3(kBlock), 0, s, tokens, embed_w, H, vocab, site, out_codes, out_idx,
+	hipLaunchKernelGGL(k_embed, dim3(M), dim3(kRowBlock), 0, s, tokens, embed_w, H, vocab, site, out_codes, out_idx,
 	                   out_scale, scale_idx, tok, status);
 }
 
 void rmsnorm(const RowNormArgs& a, int M, int H, const TokenInfo* tok, int32_t* status, int32_t layer,
              hipStream_t s) {
-	hipLaunchKernelGGL(k_rmsnorm, dim3(M), dim3(kBlock), 0, s, a, H, tok, status, layer);
+	hipLaunchKernelGGL(k_rmsnorm, dim3(M), dim3(kRowBlock), 0, s, a, H, tok, status, layer);
 }
 
 void qkv_post(const QkvPostArgs& a, hipStream_t s) {
-	hipLaunchKernelGGL(k_qkv_post, dim3(a.M), dim3(kBlock), 0, s, a);
+	hipLaunchKernelGGL(k_qkv_post, dim3(a.M), dim3(kRowBlock), 0, s, a);
 }
 
 void attention(const AttnArgs& a, hipStream_t s) {
@@ -901,18 +905,18 @@ void attention(const AttnArgs& a, hipStream_t s) {
 	hipLaunchKernelGGL(k_attention, dim3(a.NKV, a.M), dim3(kBlock), use_lds ? lds : 0, s, a, use_lds);
 }
 
-void funnel(const FunnelArgs& a, hipStream_t s) { hipLaunchKernelGGL(k_funnel, dim3(a.M), dim3(kBlock), 0, s, a); }
+void funnel(const FunnelArgs& a, hipStream_t s) { hipLaunchKernelGGL(k_funnel, dim3(a.M), dim3(kRowBlock), 0, s, a); }
 
 void residual_norm(const ResidualArgs& a, hipStream_t s) {
-	hipLaunchKernelGGL(k_residual_norm, dim3(a.M), dim3(kBlock), 0, s, a);
+	hipLaunchKernelGGL(k_residual_norm, dim3(a.M), dim3(kRowBlock), 0, s, a);
 }
 
-void mlp_act(const ActArgs& a, hipStream_t s) { hipLaunchKernelGGL(k_mlp_act, dim3(a.M), dim3(kBlock), 0, s, a); }
+void mlp_act(const ActArgs& a, hipStream_t s) { hipLaunchKernelGGL(k_mlp_act, dim3(a.M), dim3(kRowBlock), 0, s, a); }
 
 void lora_u(const LoraUArgs& a, hipStream_t s) { hipLaunchKernelGGL(k_lora_u, dim3(a.M), dim3(kBlock), 0, s, a); }
 
-void argmax_finalize(unsigned long long* keys, int M, int32_t* out_tokens, hipStream_t s) {
-	hipLaunchKernelGGL(k_argmax_finalize, dim3((M + 63) / 64), dim3(64), 0, s, keys, M, out_tokens);
+void argmax_finalize(const unsigned long long* keys, int ntiles, int M, int32_t* out_tokens, hipStream_t s) {
+	hipLaunchKernelGGL(k_argmax_finalize, dim3(M), dim3(kBlock), 0, s, keys, ntiles, out_tokens);
 }
 
 }  // namespace sslm_launch

@@ -177,9 +177,7 @@ struct sslm_model_s {
 	    *final_scale;
 	int64_t *normed_recip, *mlp_recip, *kv_f, *attn_scratch;
 	int32_t *q_f, *ctx_f, *o_f, *gu_f, *down_f;
-	uint32_t *mx_q, *mx_ctx, *mx_o, *mx_gate, *mx_up, *mx_down;
-	int32_t* acc;
-	uint32_t* tile_cnt;
+	uint32_t *mx_q, *mx_ctx, *mx_o, *mx_gu, *mx_down;  // per (16-column tile, token) partial maxima
 	unsigned long long* argmax_key;
 	int8_t* lora_u[3];
 	int8_t* pool_dev = nullptr;  // KV pool of the launch sequence being recorded
@@ -226,15 +224,6 @@ std::set<sslm_seq_s*> g_live_seqs;
 // ------------------------------------------------------------------------------------------
 // launch helpers
 // ------------------------------------------------------------------------------------------
-int choose_k_split(int N, int K) {
-	const int colblocks = (N + 63) / 64;
-	int splits = (512 + colblocks - 1) / colblocks;
-	splits = std::max(1, std::min(splits, K / 128));
-	int ks = (K + splits - 1) / splits;
-	ks = (ks + 63) / 64 * 64;
-	return ks;
-}
-
 GemmArgs gemm_args(sslm_model m, const int8_t* a, int M, int lda, const int8_t* w, int N, int K) {
 	GemmArgs g{};
 	g.a = a;
@@ -243,9 +232,6 @@ GemmArgs gemm_args(sslm_model m, const int8_t* a, int M, int lda, const int8_t* 
 	g.N = N;
 	g.K = K;
 	g.lda = lda;
-	g.k_split = M <= 64 ? choose_k_split(N, K) : K;
-	g.acc = m->acc;
-	g.tile_cnt = m->tile_cnt;
 	g.epi.tok = m->tok;
 	g.epi.status = m->status;
 	return g;
@@ -258,7 +244,7 @@ Segment funnel_seg(int n0, int n1, int32_t* out, int ld, uint32_t* mx, const int
 	s.mode = kSegFunnel;
 	s.out = out;
 	s.ld_out = ld;
-	s.maxabs = mx;
+	s.maxpart = mx;
 	s.fold = fold;
 	s.bias = bias;
 	return s;
@@ -367,7 +353,7 @@ void run_layers(sslm_model m, int M, StreamRef st, int l0, int l1, sslm_adapter 
 			a.cap = m->cap;
 			a.tok = m->tok;
 			a.q_f = m->q_f;
-			a.q_maxabs = m->mx_q;
+			a.q_maxpart = m->mx_q;
 			a.kv_f = m->kv_f;
 			a.in_scale = m->normed_scale;
 			a.q_site = lw.q;
@@ -409,7 +395,7 @@ void run_layers(sslm_model m, int M, StreamRef st, int l0, int l1, sslm_adapter 
 			a.b_q = m->b_q;
 			a.ca_q = m->ca_q;
 			a.ctx_f = m->ctx_f;
-			a.ctx_maxabs = m->mx_ctx;
+			a.ctx_maxpart = m->mx_ctx;
 			a.scratch = m->attn_scratch;
 			a.status = m->status;
 			ProfScope p(s, kProfAttn, 0, 0);
@@ -423,7 +409,8 @@ void run_layers(sslm_model m, int M, StreamRef st, int l0, int l1, sslm_adapter 
 			a.tok = m->tok;
 			a.f = m->ctx_f;
 			a.ld_f = H;
-			a.maxabs = m->mx_ctx;
+			a.maxpart = m->mx_ctx;
+			a.ntiles = m->NKV;
 			a.incoming = nullptr;
 			a.site = lw.ctx;
 			a.out = m->ctx;
@@ -451,7 +438,7 @@ void run_layers(sslm_model m, int M, StreamRef st, int l0, int l1, sslm_adapter 
 			a.H = H;
 			a.tok = m->tok;
 			a.branch_f = m->o_f;
-			a.branch_maxabs = m->mx_o;
+			a.branch_maxpart = m->mx_o;
 			a.branch_in = m->ctx_scale;
 			a.branch_site = lw.o;
 			a.stream = st.codes;
@@ -479,8 +466,8 @@ void run_layers(sslm_model m, int M, StreamRef st, int l0, int l1, sslm_adapter 
 			g.epi.layer = l;
 			g.epi.rank = ad ? (int)ad->rank : 0;
 			g.epi.nseg = 2;
-			g.epi.seg[0] = funnel_seg(0, I, m->gu_f, 2 * I, m->mx_gate, lw.f_gu, nullptr);
-			g.epi.seg[1] = funnel_seg(I, 2 * I, m->gu_f + I, 2 * I, m->mx_up, lw.f_gu + 3 * I, nullptr);
+			g.epi.seg[0] = funnel_seg(0, I, m->gu_f, 2 * I, m->mx_gu, lw.f_gu, nullptr);
+			g.epi.seg[1] = funnel_seg(I, 2 * I, m->gu_f + I, 2 * I, m->mx_gu, lw.f_gu + 3 * I, nullptr);
 			attach_lora(m, ad, l, 4, &g.epi.seg[0], 0);
 			attach_lora(m, ad, l, 5, &g.epi.seg[1], 1);
 			run_gemm(m, g, kProfGemm);
@@ -491,8 +478,7 @@ void run_layers(sslm_model m, int M, StreamRef st, int l0, int l1, sslm_adapter 
 			a.I = I;
 			a.tok = m->tok;
 			a.gu_f = m->gu_f;
-			a.gate_maxabs = m->mx_gate;
-			a.up_maxabs = m->mx_up;
+			a.gu_maxpart = m->mx_gu;
 			a.in_scale = m->mlp_scale;
 			a.gate_site = lw.gate;
 			a.up_site = lw.up;
@@ -523,7 +509,7 @@ void run_layers(sslm_model m, int M, StreamRef st, int l0, int l1, sslm_adapter 
 			a.H = H;
 			a.tok = m->tok;
 			a.branch_f = m->down_f;
-			a.branch_maxabs = m->mx_down;
+			a.branch_maxpart = m->mx_down;
 			a.branch_in = m->act_scale;
 			a.branch_site = lw.down;
 			a.stream = m->attn_stream;
@@ -562,11 +548,10 @@ void run_logits(sslm_model m, int M, StreamRef st) {
 		ck(hipGetLastError());
 	}
 	GemmArgs g = gemm_args(m, m->final_codes, M, m->H, m->head, m->V, m->H);
-	g.k_split = m->H;  // the vocab dimension alone fills the chip
 	g.epi.argmax_key = m->argmax_key;
 	g.epi.layer = m->L;
 	run_gemm(m, g, kProfHead);
-	sslm_launch::argmax_finalize(m->argmax_key, M, m->out_tokens, s);
+	sslm_launch::argmax_finalize(m->argmax_key, (m->V + 15) / 16, M, m->out_tokens, s);
 	ck(hipGetLastError());
 }
 
@@ -833,12 +818,12 @@ bool build_device_model(sslm_model m, std::string* err) {
 	m->o_f = dalloc<int32_t>((size_t)T * H, &own);
 	m->gu_f = dalloc<int32_t>((size_t)T * 2 * I, &own);
 	m->down_f = dalloc<int32_t>((size_t)T * H, &own);
-	for (uint32_t** mp : {&m->mx_q, &m->mx_ctx, &m->mx_o, &m->mx_gate, &m->mx_up, &m->mx_down})
-		*mp = dalloc<uint32_t>(T, &own);
-	const size_t max_n = std::max<size_t>({(size_t)H + 2 * KVH, (size_t)2 * I, (size_t)H});
-	m->acc = dalloc<int32_t>(64 * max_n, &own);
-	m->tile_cnt = dalloc<uint32_t>(max_n / 16 + 64, &own);
-	m->argmax_key = dalloc<unsigned long long>(T, &own);
+	m->mx_q = dalloc<uint32_t>((size_t)(H + 2 * KVH) / 16 * kPartLd, &own);
+	m->mx_ctx = dalloc<uint32_t>((size_t)m->NKV * kPartLd, &own);
+	m->mx_o = dalloc<uint32_t>((size_t)H / 16 * kPartLd, &own);
+	m->mx_gu = dalloc<uint32_t>((size_t)2 * I / 16 * kPartLd, &own);
+	m->mx_down = dalloc<uint32_t>((size_t)H / 16 * kPartLd, &own);
+	m->argmax_key = dalloc<unsigned long long>((size_t)(m->V + 15) / 16 * kPartLd, &own);
 	for (int i = 0; i < 3; ++i) m->lora_u[i] = dalloc<int8_t>((size_t)T * kMaxRank, &own);
 	const int group = m->NH / m->NKV;
 	if ((size_t)group * m->cap * 8 > 48 * 1024)
@@ -1451,12 +1436,10 @@ namespace {
 struct StandaloneCtx {
 	hipStream_t stream = nullptr;
 	std::vector<void*> owned;
-	int32_t* acc = nullptr;
-	uint32_t* cnt = nullptr;
-	size_t acc_n = 0;
 	int32_t* f = nullptr;
 	size_t f_n = 0;
 	uint32_t* mx = nullptr;
+	size_t mx_n = 0;
 	TokenInfo* tok = nullptr;
 	Scale* in = nullptr;
 	int cap_m = 0;
@@ -1471,14 +1454,11 @@ void sa_reserve(int m, int n) {
 		g_sa.f = dalloc<int32_t>(mn, &g_sa.owned);
 		g_sa.f_n = mn;
 	}
-	const size_t an = (size_t)std::min(m, 64) * n;
-	if (an > g_sa.acc_n) {
-		g_sa.acc = dalloc<int32_t>(an, &g_sa.owned);
-		g_sa.cnt = dalloc<uint32_t>((size_t)n / 16 + 64, &g_sa.owned);
-		g_sa.acc_n = an;
+	if ((size_t)n > g_sa.mx_n) {
+		g_sa.mx = dalloc<uint32_t>((size_t)(n + 15) / 16 * kPartLd, &g_sa.owned);
+		g_sa.mx_n = n;
 	}
 	if (m > g_sa.cap_m) {
-		g_sa.mx = dalloc<uint32_t>(m, &g_sa.owned);
 		g_sa.tok = dalloc<TokenInfo>(m, &g_sa.owned);
 		g_sa.in = dalloc<Scale>(m, &g_sa.owned);
 		std::vector<TokenInfo> ti(m);
@@ -1496,9 +1476,6 @@ GemmArgs sa_args(const int8_t* a, const int8_t* w, int m, int n, int k) {
 	g.N = n;
 	g.K = k;
 	g.lda = k;
-	g.k_split = m <= 64 ? choose_k_split(n, k) : k;
-	g.acc = g_sa.acc;
-	g.tile_cnt = g_sa.cnt;
 	g.epi.tok = g_sa.tok;
 	return g;
 }
@@ -1507,7 +1484,8 @@ GemmArgs sa_args(const int8_t* a, const int8_t* w, int m, int n, int k) {
 sslm_status sslm_hip_gemm_requant(const int8_t* a, const int8_t* w, const int32_t* fold, int32_t m, int32_t n,
                                   int32_t k, int64_t in_m, int64_t in_e, int64_t site_m, int64_t site_e,
                                   int8_t* out_codes, int64_t* out_me, int32_t* out_status) {
-	if (!a || !w || !fold || !out_codes || !out_me || !out_status || m < 1 || n < 1 || k < 16 || k % 16 || n % 16)
+	if (!a || !w || !fold || !out_codes || !out_me || !out_status || m < 1 || m > kPartLd || n < 1 || k < 16 ||
+	    k % 16 || n % 16)
 		return SSLM_INVALID_ARGUMENT;
 	return guarded([&]() -> sslm_status {
 		std::lock_guard<std::mutex> lk(g_sa.mu);
@@ -1531,7 +1509,8 @@ sslm_status sslm_hip_gemm_requant(const int8_t* a, const int8_t* w, const int32_
 		fa.tok = g_sa.tok;
 		fa.f = g_sa.f;
 		fa.ld_f = n;
-		fa.maxabs = g_sa.mx;
+		fa.maxpart = g_sa.mx;
+		fa.ntiles = (n + 15) / 16;
 		fa.incoming = g_sa.in;
 		fa.site = Scale{site_m, site_e};
 		fa.out = out_codes;
@@ -1550,7 +1529,7 @@ sslm_status sslm_hip_gemm_requant(const int8_t* a, const int8_t* w, const int32_
 }
 
 sslm_status sslm_hip_gemm_i32(const int8_t* a, const int8_t* w, int32_t m, int32_t n, int32_t k, int32_t* out) {
-	if (!a || !w || !out || m < 1 || n < 1 || k < 16 || k % 16) return SSLM_INVALID_ARGUMENT;
+	if (!a || !w || !out || m < 1 || m > kPartLd || n < 1 || k < 16 || k % 16) return SSLM_INVALID_ARGUMENT;
 	return guarded([&]() -> sslm_status {
 		std::lock_guard<std::mutex> lk(g_sa.mu);
 		sa_reserve(m, n);
