@@ -7,6 +7,7 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include <math.h>
 #include <stdint.h>
 
 #define SSLM_HD __host__ __device__ __forceinline__
@@ -110,6 +111,7 @@ SSLM_HD int64_t reciprocal(int64_t dn) {
 // integer division sequence on the GPU; the result is the integer quotient bit for bit.
 SSLM_HD int64_t div_floor_pos(int64_t n, int64_t d) {
 	int64_t q = (int64_t)((double)n / (double)d);
+	if (q >= ((int64_t)1 << 51)) return n / d;  // estimate no longer within one of the quotient
 	if (q < 0) q = 0;
 	s128 r = (s128)n - (s128)q * d;
 	if (r < 0) {
@@ -158,17 +160,20 @@ SSLM_HD int8_t requant_code(int64_t x, int64_t r, int s) {
 	return (int8_t)(x < 0 ? -q : q);
 }
 
-// Same composite for |x| <= 2^31 (the funnel's whole accepted domain): the product
-// |x|*127*R < 2^70 is formed from 64-bit halves without a full 128-bit multiply.
+// Same composite for |x| <= 2^31 (the funnel's whole accepted domain): |x|*127*R < 2^70 is
+// held as a (hi, lo) pair and the rounding shift 2^(62-s) (s in [-1, 30]) is done on 64-bit
+// halves -- mag = (prod + 2^(e-1)) >> e is the reference's (2 prod + 2^e) >> (e + 1).
 SSLM_HD int8_t requant_code_small(int64_t x, uint64_t r, int s) {
-	int exponent = 62 - s;  // 32..63
-	uint64_t ax = x < 0 ? (uint64_t)(-x) : (uint64_t)x;
-	uint64_t a = ax * 127u;  // < 2^38
-	u128 prod = (u128)a * r;
-	u128 num = prod * 2 + ((u128)1 << exponent);
-	uint64_t mag = (uint64_t)(num >> (exponent + 1));
-	if (mag > 127u) mag = 127u;
-	int32_t q = (int32_t)mag;
+	const int e = 62 - s;  // 32..63
+	const uint64_t ax = x < 0 ? (uint64_t)0 - (uint64_t)x : (uint64_t)x;
+	const uint64_t a = ax * 127u;  // < 2^39
+	const uint64_t lo = a * r;
+	uint64_t hi = (uint64_t)(((u128)a * r) >> 64);
+	const uint64_t lo2 = lo + ((uint64_t)1 << (e - 1));
+	hi += lo2 < lo ? 1u : 0u;
+	uint64_t mag = (lo2 >> e) | (hi << (64 - e));
+	if ((hi >> e) != 0 || mag > 127u) mag = 127u;
+	const int32_t q = (int32_t)mag;
 	return (int8_t)(x < 0 ? -q : q);
 }
 
@@ -186,6 +191,17 @@ SSLM_HD int64_t isqrt(int64_t n) {
 		bit >>= 2;
 	}
 	return root;
+}
+
+// floor(sqrt(n)) -- the value isqrt() returns for every int64 n (0 for n <= 0) -- from a
+// double-precision estimate corrected with exact 64-bit squares.
+SSLM_HD int64_t isqrt_fast(int64_t n) {
+	if (n <= 0) return 0;
+	const uint64_t un = (uint64_t)n;
+	uint64_t r = (uint64_t)sqrt((double)n);
+	while (r * r > un) --r;
+	while ((r + 1) * (r + 1) <= un) ++r;
+	return (int64_t)r;
 }
 
 SSLM_HD int64_t sat_add64(int64_t a, int64_t b) {
@@ -310,6 +326,51 @@ SSLM_HD int64_t landing_rescale(int64_t branch, int64_t m_a, int64_t r_t, int64_
 		}
 		raw = (int64_t)(uint64_t)shifted;
 	}
+	if (neg) raw = (int64_t)(0u - (uint64_t)raw);
+	*clamped = exc_clamp || raw < -127 || raw > 127;
+	*exceeded = exc_i64;
+	return raw;
+}
+
+// landing_rescale for the residual site's operands (|branch| <= 127 code, |m_a| < 2^31 + 1,
+// r_t < 2^33) on 64-bit halves when the composed exponent k is non-negative; every other case
+// takes the general 128-bit path above.  Same outputs bit for bit.
+SSLM_HD int64_t landing_small(int64_t branch, int64_t m_a, int64_t r_t, int64_t k, bool* clamped, bool* exceeded) {
+	const uint64_t ab = branch < 0 ? (uint64_t)0 - (uint64_t)branch : (uint64_t)branch;
+	const uint64_t am = m_a < 0 ? (uint64_t)0 - (uint64_t)m_a : (uint64_t)m_a;
+	if (k < 0 || ab > 127u || am > ((uint64_t)1 << 31) || (uint64_t)r_t >= ((uint64_t)1 << 33))
+		return landing_rescale(branch, m_a, r_t, k, clamped, exceeded);
+	const bool neg = (branch < 0) != (m_a < 0);
+	const uint64_t a = ab * am;  // < 2^39
+	const uint64_t lo = a * (uint64_t)r_t;
+	const uint64_t hi = (uint64_t)(((u128)a * (uint64_t)r_t) >> 64);  // prod < 2^72
+	uint64_t qlo, qhi;
+	if (k == 0) {
+		qlo = lo;
+		qhi = hi;
+	} else if (k >= 73) {
+		qlo = 0;
+		qhi = 0;
+	} else {
+		// (prod + 2^(k-1)) >> k
+		uint64_t alo = lo, ahi = hi;
+		if (k - 1 < 64) {
+			alo = lo + ((uint64_t)1 << (k - 1));
+			ahi = hi + (alo < lo ? 1u : 0u);
+		} else {
+			ahi = hi + ((uint64_t)1 << (k - 1 - 64));
+		}
+		if (k < 64) {
+			qlo = (alo >> k) | (ahi << (64 - k));
+			qhi = ahi >> k;
+		} else {
+			qlo = ahi >> (k - 64);
+			qhi = 0;
+		}
+	}
+	const bool exc_clamp = qhi != 0 || qlo > 127;
+	const bool exc_i64 = qhi != 0 || qlo > (uint64_t)kI64Max;
+	int64_t raw = (int64_t)qlo;
 	if (neg) raw = (int64_t)(0u - (uint64_t)raw);
 	*clamped = exc_clamp || raw < -127 || raw > 127;
 	*exceeded = exc_i64;

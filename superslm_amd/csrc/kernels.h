@@ -128,11 +128,15 @@ struct AttnArgs {
 	int32_t layer;
 	int64_t ln2_q, b_q, ca_q;
 	int32_t* ctx_f;           // [M, H]
-	uint32_t* ctx_maxpart;    // [NKV * kPartLd]: one partial per kv head
+	uint32_t* ctx_maxpart;    // [NH * kPartLd]: one partial per query head
 	int64_t* scratch;         // [M, NH, cap] when rows exceed LDS
 	int32_t* status;
 };
 void attention(const AttnArgs& a, hipStream_t s);
+// the attention row (cap int64 values) lives in LDS up to this context capacity, else in
+// AttnArgs::scratch ([M, NH, cap] int64)
+constexpr int64_t kAttnLdsCap = 6144;
+inline bool attention_in_lds(int64_t cap) { return cap <= kAttnLdsCap; }
 
 // funnel over an int32 fold-output row; `incoming` per token or null (empty span, the attn_ctx site)
 struct FunnelArgs {
@@ -194,6 +198,9 @@ struct ActArgs {
 	int32_t* status;
 };
 void mlp_act(const ActArgs& a, hipStream_t s);
+
+// whether the row kernels' register tiling covers this geometry
+bool row_geometry_ok(int H, int I, int NKV, int D);
 
 // LoRA intermediate u = clamp(amp_fold(A x)) for up to 3 projections sharing one input
 struct LoraUArgs {

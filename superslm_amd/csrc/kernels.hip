@@ -10,6 +10,11 @@
 
 #include "kernels.h"
 
+// Optional phase timestamps for latency studies of the row kernels; compiled out by default.
+#ifndef KT
+#define KT(i)
+#endif
+
 namespace sslm {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
@@ -52,39 +57,6 @@ __device__ __forceinline__ uint64_t block_max_u64(uint64_t v, uint64_t* red) {
 	uint64_t r = red[0];
 	for (int i = 1; i < (int)(blockDim.x >> 6); ++i) r = red[i] > r ? red[i] : r;
 	return r;
-}
-
-__device__ __forceinline__ int64_t block_sum_i64(int64_t v, int64_t* red) {
-	v = wave_sum_i64(v);
-	const int w = threadIdx.x >> 6;
-	__syncthreads();
-	if ((threadIdx.x & 63) == 0) red[w] = v;
-	__syncthreads();
-	int64_t r = 0;
-	for (int i = 0; i < (int)(blockDim.x >> 6); ++i) r += red[i];
-	return r;
-}
-
-__device__ __forceinline__ int64_t block_max_i64(int64_t v, int64_t* red) {
-	v = wave_max_i64(v);
-	const int w = threadIdx.x >> 6;
-	__syncthreads();
-	if ((threadIdx.x & 63) == 0) red[w] = v;
-	__syncthreads();
-	int64_t r = red[0];
-	for (int i = 1; i < (int)(blockDim.x >> 6); ++i) r = red[i] > r ? red[i] : r;
-	return r;
-}
-
-// max over tiles [tile0, tile0 + ntiles) of a per-(tile, token) partial array; every thread of
-// the block must call it
-__device__ __forceinline__ uint64_t reduce_part(const uint32_t* part, int tile0, int ntiles, int t, uint64_t* red) {
-	uint64_t m = 0;
-	for (int i = threadIdx.x; i < ntiles; i += blockDim.x) {
-		const uint64_t v = part[(size_t)(tile0 + i) * kPartLd + t];
-		m = v > m ? v : m;
-	}
-	return block_max_u64(m, red);
 }
 
 __device__ __forceinline__ uint32_t sat_abs_u32(int64_t v) {
@@ -372,7 +344,7 @@ __global__ __launch_bounds__(kBlock) void k_gemm_tiled(GemmArgs g) {
 }
 
 // ------------------------------------------------------------------------------------------
-// row kernels (one 256-thread block per token)
+// row kernels (one block per token)
 // ------------------------------------------------------------------------------------------
 
 // forward_sites.cpp:763-787 -- embed row -> funnel ("embed" site, empty incoming)
@@ -408,410 +380,581 @@ __global__ __launch_bounds__(kRowBlock) void k_embed(const int32_t* tokens, cons
 	if (threadIdx.x == 0) out_scale[scale_idx[t]] = plan.out;
 }
 
-// forward_sites.cpp:410-459 -- the RMSNorm site body, shared by the fused row kernels.
-// Writes codes to `out` (row of the current token) and returns the status.
-__device__ int32_t rmsnorm_row(const int8_t* h, const int32_t* g, int H, Scale site, int8_t* out, Scale* out_scale,
-                               int64_t* out_recip, uint64_t* red_u, int64_t* red_s) {
-	__shared__ int64_t s_root;
-	__shared__ int64_t fd[256];  // floor((h << 32) / root) for every int8 h
-	__shared__ FunnelPlan plan;
-	__shared__ int32_t st;
+// ------------------------------------------------------------------------------------------
+// Latency-oriented row kernels.  A decode row is short (H or I elements) and its funnel is a
+// chain of dependent steps (max -> scale plan -> codes -> max -> ...), so these kernels are
+// shaped for latency, not bandwidth: every independent global load is issued at entry, the row
+// stays in registers (EPT values per thread, element i = threadIdx.x + k * BS), each block
+// reduction costs a single barrier (every call site owns its LDS slots), and the scalar scale
+// plans are evaluated redundantly by all threads instead of by one thread and a broadcast.
+// A slot's status is read once by thread 0 and tested after the first barrier, so the whole
+// block leaves together.
+// ------------------------------------------------------------------------------------------
+template <int BS>
+__device__ __forceinline__ uint64_t blk_max(uint64_t v, uint64_t* slots) {
+	v = wave_max_u64(v);
+	if ((threadIdx.x & 63) == 0) slots[threadIdx.x >> 6] = v;
+	__syncthreads();
+	uint64_t r = slots[0];
+#pragma unroll
+	for (int i = 1; i < BS / 64; ++i) r = slots[i] > r ? slots[i] : r;
+	return r;
+}
+
+// two maxima, one barrier; `slots` holds 2 * BS / 64 entries
+template <int BS>
+__device__ __forceinline__ void blk_max2(uint64_t& x, uint64_t& y, uint64_t* slots) {
+	x = wave_max_u64(x);
+	y = wave_max_u64(y);
+	if ((threadIdx.x & 63) == 0) {
+		slots[threadIdx.x >> 6] = x;
+		slots[BS / 64 + (threadIdx.x >> 6)] = y;
+	}
+	__syncthreads();
+	x = slots[0];
+	y = slots[BS / 64];
+#pragma unroll
+	for (int i = 1; i < BS / 64; ++i) {
+		x = slots[i] > x ? slots[i] : x;
+		y = slots[BS / 64 + i] > y ? slots[BS / 64 + i] : y;
+	}
+}
+
+template <int BS>
+__device__ __forceinline__ int64_t blk_sum(int64_t v, int64_t* slots) {
+	v = wave_sum_i64(v);
+	if ((threadIdx.x & 63) == 0) slots[threadIdx.x >> 6] = v;
+	__syncthreads();
+	int64_t r = 0;
+#pragma unroll
+	for (int i = 0; i < BS / 64; ++i) r += slots[i];
+	return r;
+}
+
+template <int BS>
+__device__ __forceinline__ int64_t blk_max_i64(int64_t v, int64_t* slots) {
+	v = wave_max_i64(v);
+	if ((threadIdx.x & 63) == 0) slots[threadIdx.x >> 6] = v;
+	__syncthreads();
+	int64_t r = slots[0];
+#pragma unroll
+	for (int i = 1; i < BS / 64; ++i) r = slots[i] > r ? slots[i] : r;
+	return r;
+}
+
+// this thread's share of the max over tiles [tile0, tile0 + ntiles) of a per-(tile, token)
+// partial array; combine across the block with blk_max
+template <int BS>
+__device__ __forceinline__ uint64_t part_max(const uint32_t* part, int tile0, int ntiles, int t) {
+	uint64_t m = 0;
+	for (int i = threadIdx.x; i < ntiles; i += BS) {
+		const uint64_t v = part[(size_t)(tile0 + i) * kPartLd + t];
+		m = v > m ? v : m;
+	}
+	return m;
+}
+
+__device__ __forceinline__ uint64_t abs_u64(int64_t v) { return v < 0 ? (uint64_t)0 - (uint64_t)v : (uint64_t)v; }
+
+constexpr int32_t kSkipped = -1;  // the slot had already failed: nothing written, no status
+
+// forward_sites.cpp:410-459 -- the RMSNorm site body on a register-resident row of codes `h`
+// (zero beyond H) with gains `g`.  `prior` (LDS, or null) is the slot status read before entry.
+template <int BS, int EPT>
+__device__ __forceinline__ int32_t rmsnorm_regs(const int32_t (&h)[EPT], const int32_t (&g)[EPT], int H, Scale site,
+                                                int8_t* out, Scale* out_scale, int64_t* out_recip, int64_t* fd,
+                                                int64_t* s_sum, uint64_t* s_max, const int32_t* prior) {
 	int64_t ss = 0;
-	for (int i = threadIdx.x; i < H; i += blockDim.x) ss += (int64_t)h[i] * h[i];
-	ss = block_sum_i64(ss, red_s);
-	if (threadIdx.x == 0) {
-		int64_t root = isqrt(floor_div(ss << 32, (int64_t)H));
-		s_root = root > 1 ? root : 1;
+#pragma unroll
+	for (int k = 0; k < EPT; ++k) ss += (int64_t)(h[k] * h[k]);
+	ss = blk_sum<BS>(ss, s_sum);
+	if (prior && *prior != 0) return kSkipped;
+	int64_t root = isqrt_fast(div_floor_pos(ss << 32, (int64_t)H));
+	root = root > 1 ? root : 1;
+	if (threadIdx.x < 256) {  // floor((v << 32) / root) for every int8 v
+		const int64_t v = ((int64_t)threadIdx.x - 128) << 32;
+		fd[threadIdx.x] = v >= 0 ? div_floor_pos(v, root) : -div_floor_pos(-v + root - 1, root);
 	}
 	__syncthreads();
-	const int64_t root = s_root;
-	if (threadIdx.x < 256) {
-		const int64_t hv = (int64_t)threadIdx.x - 128;
-		const int64_t a = hv << 32;
-		fd[threadIdx.x] = a >= 0 ? div_floor_pos(a, root) : -div_floor_pos(-a + root - 1, root);
-	}
-	__syncthreads();
+	int64_t w[EPT];
 	uint64_t mx = 0;
-	for (int i = threadIdx.x; i < H; i += blockDim.x) {
-		int64_t w = fd[(int)h[i] + 128] * (int64_t)g[i];
-		uint64_t a = w < 0 ? (uint64_t)0 - (uint64_t)w : (uint64_t)w;
-		mx = a > mx ? a : mx;
+#pragma unroll
+	for (int k = 0; k < EPT; ++k) {
+		w[k] = fd[h[k] + 128] * (int64_t)g[k];
+		const uint64_t ab = abs_u64(w[k]);
+		mx = ab > mx ? ab : mx;
 	}
-	mx = block_max_u64(mx, red_u);
-	if (threadIdx.x == 0) st = funnel_plan(mx, nullptr, 0, site, &plan);
-	__syncthreads();
+	mx = blk_max<BS>(mx, s_max);
+	FunnelPlan plan;
+	const int32_t st = funnel_plan(mx, nullptr, 0, site, &plan);
 	if (st != kOk) return st;
-	for (int i = threadIdx.x; i < H; i += blockDim.x) {
-		int64_t w = fd[(int)h[i] + 128] * (int64_t)g[i];
-		out[i] = requant_code_small(w, (uint64_t)plan.r, plan.s);
+#pragma unroll
+	for (int k = 0; k < EPT; ++k) {
+		const int i = threadIdx.x + k * BS;
+		if (i < H) out[i] = requant_code_small(w[k], (uint64_t)plan.r, plan.s);
 	}
 	if (threadIdx.x == 0) {
 		*out_scale = plan.out;
 		if (out_recip) *out_recip = fits_i32(plan.out.m) ? reciprocal_fast(plan.out.m) : 0;
 	}
-	__syncthreads();
 	return kOk;
 }
 
-__global__ __launch_bounds__(kRowBlock) void k_rmsnorm(sslm_launch::RowNormArgs a, int H, const TokenInfo* tok,
-                                                    int32_t* status, int32_t layer) {
-	__shared__ uint64_t red_u[16];
-	__shared__ int64_t red_s[16];
+template <int BS, int EPT>
+__global__ __launch_bounds__(BS) void k_rmsnorm(sslm_launch::RowNormArgs a, int H, const TokenInfo* tok,
+                                              int32_t* status, int32_t layer) {
+	__shared__ int64_t fd[256];
+	__shared__ int64_t s_sum[BS / 64];
+	__shared__ uint64_t s_max[BS / 64];
+	__shared__ int32_t s_st;
 	const int t = blockIdx.x;
-	if (status[tok[t].slot] != 0) return;
-	const int8_t* h = a.in_codes + (size_t)a.in_idx[t] * a.ld_in;
-	int32_t st = rmsnorm_row(h, a.gain, H, a.site, a.out + (size_t)t * H, &a.out_scale[t],
-	                         a.out_recip ? &a.out_recip[t] : nullptr, red_u, red_s);
-	if (threadIdx.x == 0) set_status(status, tok[t].slot, layer, st);
+	const int slot = tok[t].slot;
+	const int8_t* hrow = a.in_codes + (size_t)a.in_idx[t] * a.ld_in;
+	int32_t h[EPT], g[EPT];
+#pragma unroll
+	for (int k = 0; k < EPT; ++k) {
+		const int i = threadIdx.x + k * BS;
+		h[k] = i < H ? hrow[i] : 0;
+		g[k] = i < H ? a.gain[i] : 0;
+	}
+	if (threadIdx.x == 0) s_st = status[slot];
+	const int32_t st = rmsnorm_regs<BS, EPT>(h, g, H, a.site, a.out + (size_t)t * H, &a.out_scale[t],
+	                                         a.out_recip ? &a.out_recip[t] : nullptr, fd, s_sum, s_max, &s_st);
+	if (threadIdx.x == 0 && st > 0) set_status(status, slot, layer, st);
 }
 
-// q funnel + RoPE(q); K/V landing, RoPE(K), KV write (forward_sites.cpp:1281-1418, :1748-1787)
-__global__ __launch_bounds__(kRowBlock) void k_qkv_post(sslm_launch::QkvPostArgs a) {
-	__shared__ FunnelPlan plan;
-	__shared__ int32_t st;
-	__shared__ unsigned long long sat_block;
+// q funnel + RoPE(q); K/V landing, RoPE(K), KV write (forward_sites.cpp:1281-1418, :1748-1787).
+// The K/V landing does not depend on the q funnel, so it is computed while the q maximum is
+// reduced.  Up to 2 K (and 2 V) pairs per thread: NKV * D <= 4 * BS.
+template <int BS, int EQ>
+__global__ __launch_bounds__(BS) void k_qkv_post(sslm_launch::QkvPostArgs a) {
+	__shared__ uint64_t s_red[BS / 64];
+	__shared__ int32_t s_st;
 	const int t = blockIdx.x;
 	const TokenInfo ti = a.tok[t];
-	if (a.status[ti.slot] != 0) return;
+	const Scale ns = a.in_scale[t];
 	const int H = a.H, D = a.D, pairs = D / 2;
+	const int KVH = a.NKV * D;
 	const int64_t pos = ti.pos;
-	__shared__ uint64_t red_u[16];
-	const uint64_t mx = reduce_part(a.q_maxpart, 0, H / 16, t, red_u);
-	if (threadIdx.x == 0) {
-		sat_block = 0;
-		const Scale inc = a.in_scale[t];
-		st = funnel_plan(mx, &inc, 1, a.q_site, &plan);
-		if (st == kOk && (pos < 0 || pos >= a.cap)) st = kPositionOverCap;
+	const bool pos_ok = pos >= 0 && pos < a.cap;
+	const int64_t* cs = a.rope_cos + (pos_ok ? pos : 0) * pairs;
+	const int64_t* sn = a.rope_sin + (pos_ok ? pos : 0) * pairs;
+	// q pair values
+	const int2* qf = (const int2*)(a.q_f + (size_t)t * H);
+	int2 qv[EQ];
+#pragma unroll
+	for (int k = 0; k < EQ; ++k) {
+		const int p = threadIdx.x + k * BS;
+		qv[k] = p < H / 2 ? qf[p] : make_int2(0, 0);
 	}
-	__syncthreads();
+	uint64_t qmx = part_max<BS>(a.q_maxpart, 0, H / 16, t);
+	if (threadIdx.x == 0) s_st = a.status[ti.slot];
+	// K/V landing (LandingRescale at the normed scale, per kv head) and RoPE(K)
+	const int64_t* kv = a.kv_f + (size_t)t * 2 * KVH;
+	int8_t kq[2][2], vq[2][2];
+	uint64_t sat = 0;
+#pragma unroll
+	for (int k = 0; k < 2; ++k) {
+		const int p = threadIdx.x + k * BS;
+		if (p < KVH / 2 && pos_ok) {
+			const int hd = (2 * p) / D;
+			const int i = p % pairs;
+			const longlong2 kk = ((const longlong2*)kv)[p];
+			const longlong2 vv = ((const longlong2*)(kv + KVH))[p];
+			const int64_t k_e = composed_exponent(ns.e, a.e_t_k[hd]);
+			const int64_t v_e = composed_exponent(ns.e, a.e_t_v[hd]);
+			const int64_t rtk = a.r_t_k[hd], rtv = a.r_t_v[hd];
+			bool c0, c1, c2, c3, x0;
+			const int64_t k0 = clamp_code(landing_rescale(kk.x, ns.m, rtk, k_e, &c0, &x0));
+			const int64_t k1 = clamp_code(landing_rescale(kk.y, ns.m, rtk, k_e, &c1, &x0));
+			int64_t xr, yr;
+			rope_pair((int32_t)k0, (int32_t)k1, (int32_t)cs[i], (int32_t)sn[i], &xr, &yr);
+			kq[k][0] = (int8_t)clamp_code(xr);
+			kq[k][1] = (int8_t)clamp_code(yr);
+			vq[k][0] = (int8_t)clamp_code(landing_rescale(vv.x, ns.m, rtv, v_e, &c2, &x0));
+			vq[k][1] = (int8_t)clamp_code(landing_rescale(vv.y, ns.m, rtv, v_e, &c3, &x0));
+			sat += (uint64_t)c0 + (uint64_t)c1 + (uint64_t)c2 + (uint64_t)c3;
+		}
+	}
+	qmx = blk_max<BS>(qmx, s_red);
+	if (s_st != 0) return;
+	FunnelPlan plan;
+	int32_t st = funnel_plan(qmx, &ns, 1, a.q_site, &plan);
+	if (st == kOk && !pos_ok) st = kPositionOverCap;
 	if (st != kOk) {
 		if (threadIdx.x == 0) set_status(a.status, ti.slot, a.layer, st);
 		return;
 	}
-	const int64_t* cs = a.rope_cos + pos * pairs;
-	const int64_t* sn = a.rope_sin + pos * pairs;
 	// q: codes of pair (2i, 2i+1), rotated, clamped
-	const int32_t* qf = a.q_f + (size_t)t * H;
-	for (int p = threadIdx.x; p < H / 2; p += kRowBlock) {
-		const int i = p % pairs;
-		const int32_t x = requant_code_small(qf[2 * p], (uint64_t)plan.r, plan.s);
-		const int32_t y = requant_code_small(qf[2 * p + 1], (uint64_t)plan.r, plan.s);
-		int64_t xr, yr;
-		rope_pair(x, y, (int32_t)cs[i], (int32_t)sn[i], &xr, &yr);
-		a.q_rot[(size_t)t * H + 2 * p] = (int8_t)clamp_code(xr);
-		a.q_rot[(size_t)t * H + 2 * p + 1] = (int8_t)clamp_code(yr);
+	char2* qo = (char2*)(a.q_rot + (size_t)t * H);
+#pragma unroll
+	for (int k = 0; k < EQ; ++k) {
+		const int p = threadIdx.x + k * BS;
+		if (p < H / 2) {
+			const int i = p % pairs;
+			const int32_t x = requant_code_small(qv[k].x, (uint64_t)plan.r, plan.s);
+			const int32_t y = requant_code_small(qv[k].y, (uint64_t)plan.r, plan.s);
+			int64_t xr, yr;
+			rope_pair(x, y, (int32_t)cs[i], (int32_t)sn[i], &xr, &yr);
+			qo[p] = make_char2((char)clamp_code(xr), (char)clamp_code(yr));
+		}
 	}
 	if (threadIdx.x == 0) a.q_scale[t] = plan.out;
-	// K/V landing: LandingRescale at the normed scale, per kv head
-	const Scale ns = a.in_scale[t];
-	const int KVH = a.NKV * D;
-	const int64_t* kv = a.kv_f + (size_t)t * 2 * KVH;
 	int8_t* blk = a.kv_pool + (int64_t)ti.block * a.block_bytes;
 	const int64_t half = a.cap * (int64_t)KVH;
 	int8_t* kstore = blk + (int64_t)a.layer * half * 2;
 	int8_t* vstore = kstore + half;
-	unsigned long long sat = 0;
-	for (int p = threadIdx.x; p < KVH / 2; p += kRowBlock) {
-		const int h = (2 * p) / D;
-		const int i = p % pairs;
-		const int64_t k_e = composed_exponent(ns.e, a.e_t_k[h]);
-		bool c0, c1, x0, x1;
-		const int64_t k0 = clamp_code(landing_rescale(kv[2 * p], ns.m, a.r_t_k[h], k_e, &c0, &x0));
-		const int64_t k1 = clamp_code(landing_rescale(kv[2 * p + 1], ns.m, a.r_t_k[h], k_e, &c1, &x1));
-		sat += (unsigned long long)c0 + (unsigned long long)c1;
-		int64_t xr, yr;
-		rope_pair((int32_t)k0, (int32_t)k1, (int32_t)cs[i], (int32_t)sn[i], &xr, &yr);
-		int8_t* krow = kstore + ((int64_t)h * a.cap + pos) * D;
-		krow[2 * i] = (int8_t)clamp_code(xr);
-		krow[2 * i + 1] = (int8_t)clamp_code(yr);
-		const int64_t v_e = composed_exponent(ns.e, a.e_t_v[h]);
-		const int64_t* vv = kv + KVH;
-		int8_t* vrow = vstore + ((int64_t)h * a.cap + pos) * D;
-		bool c2, c3;
-		vrow[2 * i] = (int8_t)clamp_code(landing_rescale(vv[2 * p], ns.m, a.r_t_v[h], v_e, &c2, &x0));
-		vrow[2 * i + 1] = (int8_t)clamp_code(landing_rescale(vv[2 * p + 1], ns.m, a.r_t_v[h], v_e, &c3, &x1));
-		sat += (unsigned long long)c2 + (unsigned long long)c3;
-	}
-	if (sat) atomicAdd(&sat_block, sat);
-	__syncthreads();
-	if (threadIdx.x == 0 && sat_block) atomicAdd(&a.sat[ti.slot], sat_block);
-}
-
-// Attention for one (token, kv head): the group's query heads against positions [0, pos]
-// (forward_sites.cpp:1791-1905).  Scores/exps/probabilities live in LDS when they fit, else in
-// the per-launch global scratch.
-__global__ __launch_bounds__(kBlock) void k_attention(sslm_launch::AttnArgs a, int use_lds) {
-	extern __shared__ int64_t dyn[];
-	__shared__ int64_t red_s[kBlock / 64];
-	__shared__ uint64_t red_u[kBlock / 64];
-	__shared__ int64_t c_qln2, c_qb, c_qc, c_M;
-	__shared__ int32_t st;
-	__shared__ int64_t rowmax[16];
-	__shared__ int64_t rowsum[16];
-	const int kvh = blockIdx.x, t = blockIdx.y;
-	const TokenInfo ti = a.tok[t];
-	if (a.status[ti.slot] != 0) return;
-	const int D = a.D, group = a.NH / a.NKV;
-	const int64_t width = ti.pos + 1;
-	if (threadIdx.x == 0) {
-		st = kOk;
-		const Scale qs = a.q_scale[t];
-		const int64_t km = a.khead_m[kvh], ke = a.khead_e[kvh];
-		if (!fits_i32(qs.m) || !fits_i32(km)) {
-			st = kCarriedScaleMantissaOutOfDomain;
-		} else {
-			const Scale sm = combine_scale(qs, Scale{km, ke});
-			if (!fits_i32(sm.m)) {
-				st = kCarriedScaleMantissaOutOfDomain;
-			} else {
-				int64_t ql, qb, qc;
-				if (iexp_scale_constants(sm.m, sm.e, a.ln2_q, a.b_q, a.ca_q, &ql, &qb, &qc) != 0) {
-					st = kIExpScaleDerivationOutOfDomain;
-				} else {
-					st = check_softmax_width(qb, qc, width);
-					c_qln2 = ql;
-					c_qb = qb;
-					c_qc = qc;
-					c_M = softmax_ceiling(qb, qc);
-				}
-			}
+#pragma unroll
+	for (int k = 0; k < 2; ++k) {
+		const int p = threadIdx.x + k * BS;
+		if (p < KVH / 2) {
+			const int hd = (2 * p) / D;
+			const int i = p % pairs;
+			const int64_t off = ((int64_t)hd * a.cap + pos) * D + 2 * i;
+			*(char2*)(kstore + off) = make_char2(kq[k][0], kq[k][1]);
+			*(char2*)(vstore + off) = make_char2(vq[k][0], vq[k][1]);
 		}
 	}
-	__syncthreads();
-	if (st != kOk) {
-		if (threadIdx.x == 0) set_status(a.status, ti.slot, a.layer, st);
-		return;
-	}
-	int64_t* sc = use_lds ? dyn : a.scratch + ((int64_t)t * a.NH + (int64_t)kvh * group) * a.cap;
-	const int8_t* blk = a.kv_pool + (int64_t)ti.block * a.block_bytes;
-	const int64_t half = a.cap * (int64_t)a.NKV * D;
-	const int8_t* kbase = blk + (int64_t)a.layer * half * 2 + (int64_t)kvh * a.cap * D;
-	const int8_t* vbase = kbase + half;
-	const int8_t* q = a.q_rot + (size_t)t * a.H + (size_t)kvh * group * D;
-	// pass 1: scores (int32-exact dots, widened) -- 8 lanes per position, 16 bytes each
-	const int sub = threadIdx.x & 7;
-	for (int64_t p0 = threadIdx.x >> 3; p0 < width; p0 += kBlock / 8) {
-		const int8_t* kr = kbase + p0 * D;
-		for (int g = 0; g < group; ++g) {
-			int32_t acc = 0;
-			for (int d = sub * 4; d < D; d += 32) {
-				const int32_t kw = *(const int32_t*)(kr + d);
-				const int32_t qw = *(const int32_t*)(q + g * D + d);
-				acc = __builtin_amdgcn_sdot4(qw, kw, acc, false);
-			}
-			acc += __shfl_xor(acc, 1, 8);
-			acc += __shfl_xor(acc, 2, 8);
-			acc += __shfl_xor(acc, 4, 8);
-			if (sub == 0) sc[(int64_t)g * a.cap + p0] = acc;
-		}
-	}
-	__syncthreads();
-	// pass 2: row max per query head
-	for (int g = 0; g < group; ++g) {
-		int64_t mx = INT64_MIN;
-		for (int64_t p = threadIdx.x; p < width; p += kBlock) mx = max(mx, sc[(int64_t)g * a.cap + p]);
-		mx = block_max_i64(mx, red_s);
-		if (threadIdx.x == 0) rowmax[g] = mx;
-		__syncthreads();
-	}
-	// pass 3: i-exp values (SoftmaxRowQ15, intmath.cpp:853-889) and the row sums
-	int refused = 0;
-	for (int g = 0; g < group; ++g) {
-		int64_t sum = 0;
-		const int64_t mx = rowmax[g];
-		for (int64_t p = threadIdx.x; p < width; p += kBlock) {
-			int64_t v = iexp_element(sc[(int64_t)g * a.cap + p] - mx, c_qln2, c_qb, c_qc, c_M);
-			if (v < 0) {
-				refused = 1;
-				v = 0;
-			}
-			sc[(int64_t)g * a.cap + p] = v;
-			sum += v;
-		}
-		sum = block_sum_i64(sum, red_s);
-		if (threadIdx.x == 0) rowsum[g] = sum;
-		__syncthreads();
-	}
-	uint64_t anyref = block_max_u64((uint64_t)refused, red_u);
-	if (anyref) {
-		if (threadIdx.x == 0) set_status(a.status, ti.slot, a.layer, kSoftmaxKernelRefusedAfterGateAccepted);
-		return;
-	}
-	// pass 4: Q15 probabilities p = (e << 15) / max(total, 1)
-	for (int g = 0; g < group; ++g) {
-		const int64_t denom = rowsum[g] > 1 ? rowsum[g] : 1;
-		for (int64_t p = threadIdx.x; p < width; p += kBlock) {
-			const int64_t e = sc[(int64_t)g * a.cap + p];
-			sc[(int64_t)g * a.cap + p] = div_floor_pos(e << 15, denom);
-		}
-	}
-	__syncthreads();
-	// pass 5: context = sum_p prob * V[p] (int32-exact: sum of probs <= 2^15), per-head ctx fold
-	uint64_t mabs = 0;
-	for (int idx = threadIdx.x; idx < group * D; idx += kBlock) {
-		const int g = idx / D, d = idx % D;
-		int32_t acc = 0;
-		const int64_t* pr = sc + (int64_t)g * a.cap;
-		for (int64_t p = 0; p < width; ++p) acc += (int32_t)pr[p] * (int32_t)vbase[p * D + d];
-		const int h = kvh * group + g;
-		const int32_t* cf = a.ctx_fold + 3 * h;
-		const int64_t f = apply_fold(acc, cf[0], cf[1], cf[2]);
-		a.ctx_f[(size_t)t * a.H + (size_t)h * D + d] = sat_i32(f);
-		uint64_t ab = f < 0 ? (uint64_t)0 - (uint64_t)f : (uint64_t)f;
-		mabs = ab > mabs ? ab : mabs;
-	}
-	mabs = block_max_u64(mabs, red_u);
-	if (threadIdx.x == 0) a.ctx_maxpart[(size_t)kvh * kPartLd + t] = mabs > 0xffffffffull ? 0xffffffffu : (uint32_t)mabs;
+	sat = wave_sum_i64((int64_t)sat);
+	if ((threadIdx.x & 63) == 0 && sat) atomicAdd(&a.sat[ti.slot], (unsigned long long)sat);
 }
 
 // funnel over an int32 fold-output row (checked_chain_funnel.cpp:257-364)
-__global__ __launch_bounds__(kRowBlock) void k_funnel(sslm_launch::FunnelArgs a) {
-	__shared__ FunnelPlan plan;
-	__shared__ int32_t st;
-	const int t = blockIdx.x;
+template <int BS, int EPT>
+__global__ __launch_bounds__(BS) void k_funnel(sslm_launch::FunnelArgs a) {
+	__shared__ uint64_t s_m[BS / 64];
+	__shared__ int32_t s_st;
+	const int t = blockIdx.x, N = a.N;
 	const int slot = a.tok[t].slot;
-	__shared__ uint64_t red_u[16];
-	if (a.status[slot] != 0) return;
-	const uint64_t mx = reduce_part(a.maxpart, 0, a.ntiles, t, red_u);
-	if (threadIdx.x == 0) {
-		Scale inc;
-		if (a.incoming) inc = a.incoming[t];
-		st = funnel_plan(mx, a.incoming ? &inc : nullptr, a.incoming ? 1 : 0, a.site, &plan);
+	const int32_t* frow = a.f + (size_t)t * a.ld_f;
+	int32_t f[EPT];
+#pragma unroll
+	for (int k = 0; k < EPT; ++k) {
+		const int i = threadIdx.x + k * BS;
+		f[k] = i < N ? frow[i] : 0;
 	}
-	__syncthreads();
+	uint64_t mx = part_max<BS>(a.maxpart, 0, a.ntiles, t);
+	Scale inc{0, 0};
+	if (a.incoming) inc = a.incoming[t];
+	if (threadIdx.x == 0) s_st = a.status[slot];
+	mx = blk_max<BS>(mx, s_m);
+	if (s_st != 0) return;
+	FunnelPlan plan;
+	const int32_t st = funnel_plan(mx, a.incoming ? &inc : nullptr, a.incoming ? 1 : 0, a.site, &plan);
 	if (st != kOk) {
 		if (threadIdx.x == 0) set_status(a.status, slot, a.layer, st);
 		return;
 	}
-	const int32_t* f = a.f + (size_t)t * a.ld_f;
-	for (int i = threadIdx.x; i < a.N; i += kRowBlock) a.out[(size_t)t * a.N + i] = requant_code_small(f[i], (uint64_t)plan.r, plan.s);
+	int8_t* out = a.out + (size_t)t * N;
+#pragma unroll
+	for (int k = 0; k < EPT; ++k) {
+		const int i = threadIdx.x + k * BS;
+		if (i < N) out[i] = requant_code_small(f[k], (uint64_t)plan.r, plan.s);
+	}
 	if (threadIdx.x == 0) a.out_scale[t] = plan.out;
 }
 
 // projection funnel -> residual reconcile -> (optional) RMSNorm, all on one token's row
-// (forward_sites.cpp:871-989 residual; :410-459 norm)
-__global__ __launch_bounds__(kRowBlock) void k_residual_norm(sslm_launch::ResidualArgs a) {
-	__shared__ FunnelPlan bplan, rplan;
-	__shared__ int32_t st;
-	__shared__ int64_t r_h;
-	__shared__ uint64_t red_u[16];
-	__shared__ int64_t red_s[16];
-	const int t = blockIdx.x;
+// (forward_sites.cpp:871-989 residual; :410-459 norm).  `out_stream` never aliases `stream`.
+template <int BS, int EPT>
+__global__ __launch_bounds__(BS) void k_residual_norm(sslm_launch::ResidualArgs a) {
+	__shared__ uint64_t s_b[BS / 64], s_r[BS / 64], s_n[BS / 64];
+	__shared__ int64_t s_ss[BS / 64];
+	__shared__ int64_t fd[256];
+	__shared__ int32_t s_st;
+	const int t = blockIdx.x, H = a.H;
+	KT(0);
 	const int slot = a.tok[t].slot;
-	const int H = a.H;
-	if (a.status[slot] != 0) return;
-	const int8_t* stream = a.stream + (size_t)a.stream_idx[t] * H;
-	const Scale ss = a.stream_scale[a.stream_idx[t]];
-	const uint64_t bmx = reduce_part(a.branch_maxpart, 0, H / 16, t, red_u);
-	if (threadIdx.x == 0) {
-		const Scale inc = a.branch_in[t];
-		st = funnel_plan(bmx, &inc, 1, a.branch_site, &bplan);
-		if (st == kOk && !fits_i32(ss.m)) st = kCarriedScaleMantissaOutOfDomain;
-		if (st == kOk) r_h = reciprocal_fast(ss.m);
+	const int sidx = a.stream_idx[t], oidx = a.out_idx[t];
+	const Scale bin = a.branch_in[t];
+	const int32_t* bfr = a.branch_f + (size_t)t * H;
+	const int8_t* srow = a.stream + (size_t)sidx * H;
+	int32_t bf[EPT], g[EPT], sv[EPT];
+#pragma unroll
+	for (int k = 0; k < EPT; ++k) {
+		const int i = threadIdx.x + k * BS;
+		bf[k] = i < H ? bfr[i] : 0;
+		sv[k] = i < H ? srow[i] : 0;
+		g[k] = (a.gain && i < H) ? a.gain[i] : 0;
 	}
-	__syncthreads();
+	uint64_t bmx = part_max<BS>(a.branch_maxpart, 0, H / 16, t);
+	const Scale ss = a.stream_scale[sidx];
+	if (threadIdx.x == 0) s_st = a.status[slot];
+	bmx = blk_max<BS>(bmx, s_b);
+	KT(1);
+	if (s_st != 0) return;
+	FunnelPlan bplan;
+	int32_t st = funnel_plan(bmx, &bin, 1, a.branch_site, &bplan);
+	if (st == kOk && !fits_i32(ss.m)) st = kCarriedScaleMantissaOutOfDomain;
 	if (st != kOk) {
 		if (threadIdx.x == 0) set_status(a.status, slot, a.layer, st);
 		return;
 	}
+	const int64_t r_h = reciprocal_fast(ss.m);
 	const Scale bs = bplan.out;
-	const int64_t k = composed_exponent(bs.e, ss.e);
-	const int32_t* bf = a.branch_f + (size_t)t * H;
+	const int64_t kx = composed_exponent(bs.e, ss.e);
+	KT(2);
+	constexpr uint64_t kBad = ~(uint64_t)0;  // |w| <= 2^63 + 127, so the sentinel is unambiguous
+	int64_t w[EPT];
 	uint64_t mx = 0;
-	int bad = 0;
-	for (int i = threadIdx.x; i < H; i += kRowBlock) {
-		const int8_t code = requant_code_small(bf[i], (uint64_t)bplan.r, bplan.s);
-		bool cl, ex;
-		const int64_t rec = landing_rescale(code, bs.m, r_h, k, &cl, &ex);
-		if (ex) {
-			bad = 1;
-			continue;
+#pragma unroll
+	for (int k = 0; k < EPT; ++k) {
+		const int i = threadIdx.x + k * BS;
+		w[k] = 0;
+		if (i < H) {
+			const int8_t code = requant_code_small(bf[k], (uint64_t)bplan.r, bplan.s);
+			bool cl, ex;
+			const int64_t rec = landing_small(code, bs.m, r_h, kx, &cl, &ex);
+			if (ex) {
+				mx = kBad;
+			} else {
+				w[k] = rec + sv[k];
+				const uint64_t ab = abs_u64(w[k]);
+				mx = ab > mx ? ab : mx;
+			}
 		}
-		const int64_t w = rec + stream[i];
-		const uint64_t ab = w < 0 ? (uint64_t)0 - (uint64_t)w : (uint64_t)w;
-		mx = ab > mx ? ab : mx;
 	}
-	const uint64_t anybad = block_max_u64((uint64_t)bad, red_u);
-	mx = block_max_u64(mx, red_u);
-	if (threadIdx.x == 0) {
-		if (anybad) st = kResidualReconciliationMagnitudeOutOfDomain;
-		else st = funnel_plan(mx, &ss, 1, a.res_site, &rplan);
-	}
-	__syncthreads();
+	mx = blk_max<BS>(mx, s_r);
+	KT(3);
+	FunnelPlan rplan;
+	st = mx == kBad ? kResidualReconciliationMagnitudeOutOfDomain : funnel_plan(mx, &ss, 1, a.res_site, &rplan);
 	if (st != kOk) {
 		if (threadIdx.x == 0) set_status(a.status, slot, a.layer, st);
 		return;
 	}
-	// `out` never aliases `stream` (the host routes attn_stream and the committed stream through
-	// distinct buffers), so codes are written as they are formed.
-	int8_t* out = a.out_stream + (size_t)a.out_idx[t] * H;
-	for (int i = threadIdx.x; i < H; i += kRowBlock) {
-		const int8_t code = requant_code_small(bf[i], (uint64_t)bplan.r, bplan.s);
-		bool cl, ex;
-		const int64_t w = landing_rescale(code, bs.m, r_h, k, &cl, &ex) + stream[i];
-		out[i] = requant_code_small(w, (uint64_t)rplan.r, rplan.s);
+	KT(4);
+	int8_t* out = a.out_stream + (size_t)oidx * H;
+	int32_t c[EPT];
+#pragma unroll
+	for (int k = 0; k < EPT; ++k) {
+		const int i = threadIdx.x + k * BS;
+		c[k] = 0;
+		if (i < H) {
+			c[k] = requant_code_small(w[k], (uint64_t)rplan.r, rplan.s);
+			out[i] = (int8_t)c[k];
+		}
 	}
-	if (threadIdx.x == 0) a.out_stream_scale[a.out_idx[t]] = rplan.out;
-	__syncthreads();
+	if (threadIdx.x == 0) a.out_stream_scale[oidx] = rplan.out;
+	KT(5);
 	if (a.gain) {
-		const int32_t st2 = rmsnorm_row(out, a.gain, H, a.norm_site, a.norm_out + (size_t)t * H, &a.norm_scale[t],
-		                                a.norm_recip ? &a.norm_recip[t] : nullptr, red_u, red_s);
-		if (threadIdx.x == 0) set_status(a.status, slot, a.layer, st2);
+		const int32_t st2 = rmsnorm_regs<BS, EPT>(c, g, H, a.norm_site, a.norm_out + (size_t)t * H, &a.norm_scale[t],
+		                                          a.norm_recip ? &a.norm_recip[t] : nullptr, fd, s_ss, s_n, nullptr);
+		if (threadIdx.x == 0 && st2 > 0) set_status(a.status, slot, a.layer, st2);
 	}
+	KT(6);
 }
 
-// gate/up funnels -> MlpActSite (forward_sites.cpp:796-864) -> act funnel
-__global__ __launch_bounds__(kRowBlock) void k_mlp_act(sslm_launch::ActArgs a) {
-	__shared__ FunnelPlan gp, up, ap;
-	__shared__ int32_t st;
-	__shared__ uint64_t red_u[16];
-	const int t = blockIdx.x;
+// gate/up funnels -> MlpActSite (forward_sites.cpp:796-864) -> act funnel.  The sigmoid of a
+// gate code depends only on the code and the token's gate scale, so the 256 possible values
+// are tabulated per block once the gate plan is known.
+template <int BS, int EPT>
+__global__ __launch_bounds__(BS) void k_mlp_act(sslm_launch::ActArgs a) {
+	__shared__ uint64_t s_gu[2 * BS / 64], s_a[BS / 64];
+	__shared__ int32_t sig[256];
+	__shared__ int32_t s_st;
+	const int t = blockIdx.x, I = a.I;
 	const int slot = a.tok[t].slot;
-	const int I = a.I;
-	if (a.status[slot] != 0) return;
-	const uint64_t gm = reduce_part(a.gu_maxpart, 0, I / 16, t, red_u);
-	const uint64_t um = reduce_part(a.gu_maxpart, I / 16, I / 16, t, red_u);
-	if (threadIdx.x == 0) {
-		const Scale inc = a.in_scale[t];
-		st = funnel_plan(gm, &inc, 1, a.gate_site, &gp);
-		if (st == kOk) st = funnel_plan(um, &inc, 1, a.up_site, &up);
-		if (st == kOk) st = check_silu_scale(gp.out.m, gp.out.e);
+	const int32_t* gfr = a.gu_f + (size_t)t * 2 * I;
+	const int32_t* ufr = gfr + I;
+	int32_t gf[EPT], uf[EPT];
+#pragma unroll
+	for (int k = 0; k < EPT; ++k) {
+		const int i = threadIdx.x + k * BS;
+		gf[k] = i < I ? gfr[i] : 0;
+		uf[k] = i < I ? ufr[i] : 0;
 	}
-	__syncthreads();
+	uint64_t gm = part_max<BS>(a.gu_maxpart, 0, I / 16, t);
+	uint64_t um = part_max<BS>(a.gu_maxpart, I / 16, I / 16, t);
+	const Scale inc = a.in_scale[t];
+	if (threadIdx.x == 0) s_st = a.status[slot];
+	blk_max2<BS>(gm, um, s_gu);
+	if (s_st != 0) return;
+	FunnelPlan gp, up;
+	int32_t st = funnel_plan(gm, &inc, 1, a.gate_site, &gp);
+	if (st == kOk) st = funnel_plan(um, &inc, 1, a.up_site, &up);
+	if (st == kOk) st = check_silu_scale(gp.out.m, gp.out.e);
 	if (st != kOk) {
 		if (threadIdx.x == 0) set_status(a.status, slot, a.layer, st);
 		return;
 	}
 	const Scale gs = gp.out;
-	const int32_t* gf = a.gu_f + (size_t)t * 2 * I;
-	const int32_t* uf = gf + I;
-	uint64_t mx = 0;
-	for (int i = threadIdx.x; i < I; i += kRowBlock) {
-		const int8_t gc = requant_code_small(gf[i], (uint64_t)gp.r, gp.s);
-		const int8_t uc = requant_code_small(uf[i], (uint64_t)up.r, up.s);
-		const int32_t sig = silu_sigmoid_q15(a.silu, gc, gs.m, (int)gs.e);
-		const int64_t w = (int64_t)gc * sig * (int64_t)uc;
-		const uint64_t ab = w < 0 ? (uint64_t)0 - (uint64_t)w : (uint64_t)w;
-		mx = ab > mx ? ab : mx;
-	}
-	mx = block_max_u64(mx, red_u);
-	if (threadIdx.x == 0) {
-		const Scale inc2[2] = {gp.out, up.out};
-		st = funnel_plan(mx, inc2, 2, a.act_site, &ap);
+	if (threadIdx.x < 256) sig[threadIdx.x] = silu_sigmoid_q15(a.silu, (int8_t)(threadIdx.x - 128), gs.m, (int)gs.e);
+	int32_t gc[EPT], uc[EPT];
+#pragma unroll
+	for (int k = 0; k < EPT; ++k) {
+		gc[k] = requant_code_small(gf[k], (uint64_t)gp.r, gp.s);
+		uc[k] = requant_code_small(uf[k], (uint64_t)up.r, up.s);
 	}
 	__syncthreads();
+	int64_t w[EPT];
+	uint64_t mx = 0;
+#pragma unroll
+	for (int k = 0; k < EPT; ++k) {
+		w[k] = (int64_t)gc[k] * sig[gc[k] + 128] * (int64_t)uc[k];
+		const uint64_t ab = abs_u64(w[k]);
+		mx = ab > mx ? ab : mx;
+	}
+	mx = blk_max<BS>(mx, s_a);
+	const Scale inc2[2] = {gp.out, up.out};
+	FunnelPlan ap;
+	st = funnel_plan(mx, inc2, 2, a.act_site, &ap);
 	if (st != kOk) {
 		if (threadIdx.x == 0) set_status(a.status, slot, a.layer, st);
 		return;
 	}
-	for (int i = threadIdx.x; i < I; i += kRowBlock) {
-		const int8_t gc = requant_code_small(gf[i], (uint64_t)gp.r, gp.s);
-		const int8_t uc = requant_code_small(uf[i], (uint64_t)up.r, up.s);
-		const int32_t sig = silu_sigmoid_q15(a.silu, gc, gs.m, (int)gs.e);
-		const int64_t w = (int64_t)gc * sig * (int64_t)uc;
-		a.act[(size_t)t * I + i] = requant_code_small(w, (uint64_t)ap.r, ap.s);
+	int8_t* act = a.act + (size_t)t * I;
+#pragma unroll
+	for (int k = 0; k < EPT; ++k) {
+		const int i = threadIdx.x + k * BS;
+		if (i < I) act[i] = requant_code_small(w[k], (uint64_t)ap.r, ap.s);
 	}
 	if (threadIdx.x == 0) a.act_scale[t] = ap.out;
+}
+
+// Attention for one (query head, token): the head's query against positions [0, pos]
+// (forward_sites.cpp:1791-1905).  Scores, i-exp values and Q15 probabilities of the row live in
+// LDS when the context fits (else in the per-launch global scratch); each thread owns the
+// positions p = threadIdx.x + k * BS through the score, exp and probability passes, so those
+// passes meet only at the row max and row sum.  PV: D / 4 threads cover one V row (4 channels
+// each); the position groups' int32 partials meet in LDS (exact: probabilities sum to <= 2^15).
+template <int BS, int D>
+__global__ __launch_bounds__(BS) void k_attention(sslm_launch::AttnArgs a, int use_lds) {
+	extern __shared__ int64_t dyn[];
+	__shared__ int64_t s_mx[BS / 64];
+	__shared__ int64_t s_sum[BS / 64];
+	__shared__ uint64_t s_ref[BS / 64], s_ab[BS / 64];
+	__shared__ int32_t s_ctx[BS * 4];
+	__shared__ int32_t s_st;
+	constexpr int TPR = D / 4, PG = BS / TPR;
+	const int h = blockIdx.x, t = blockIdx.y;
+	const int group = a.NH / a.NKV, kvh = h / group;
+	const TokenInfo ti = a.tok[t];
+	const Scale qs = a.q_scale[t];
+	const int64_t km = a.khead_m[kvh], ke = a.khead_e[kvh];
+	const int8_t* qrow = a.q_rot + (size_t)t * a.H + (size_t)h * D;
+	v4i q[D / 16];
+#pragma unroll
+	for (int j = 0; j < D / 16; ++j) q[j] = load16(qrow + 16 * j);
+	const int32_t* cf = a.ctx_fold + 3 * h;
+	const int32_t f0 = cf[0], f1 = cf[1], f2 = cf[2];
+	if (threadIdx.x == 0) s_st = a.status[ti.slot];
+	// i-exp constants of the row's scale (every thread, redundantly)
+	int32_t st = kOk;
+	int64_t c_qln2 = 0, c_qb = 0, c_qc = 0, c_M = 0;
+	const int64_t width = ti.pos + 1;
+	if (!fits_i32(qs.m) || !fits_i32(km)) {
+		st = kCarriedScaleMantissaOutOfDomain;
+	} else {
+		const Scale sm = combine_scale(qs, Scale{km, ke});
+		if (!fits_i32(sm.m)) {
+			st = kCarriedScaleMantissaOutOfDomain;
+		} else if (iexp_scale_constants(sm.m, sm.e, a.ln2_q, a.b_q, a.ca_q, &c_qln2, &c_qb, &c_qc) != 0) {
+			st = kIExpScaleDerivationOutOfDomain;
+		} else {
+			st = check_softmax_width(c_qb, c_qc, width);
+			c_M = softmax_ceiling(c_qb, c_qc);
+		}
+	}
+	const bool live = st == kOk && width >= 1 && width <= a.cap;
+	int64_t* ex = use_lds ? dyn : a.scratch + ((int64_t)t * a.NH + h) * a.cap;
+	const int8_t* blk = a.kv_pool + (int64_t)ti.block * a.block_bytes;
+	const int64_t half = a.cap * (int64_t)a.NKV * D;
+	const int8_t* kbase = blk + (int64_t)a.layer * half * 2 + (int64_t)kvh * a.cap * D;
+	const int8_t* vbase = kbase + half;
+	// pass 1: scores (int32-exact dots) and the row max
+	int64_t mx = INT64_MIN;
+	if (live) {
+		for (int64_t p = threadIdx.x; p < width; p += BS) {
+			const int8_t* kr = kbase + p * D;
+			int32_t acc = 0;
+#pragma unroll
+			for (int j = 0; j < D / 16; ++j) {
+				const v4i kw = load16(kr + 16 * j);
+				acc = __builtin_amdgcn_sdot4(q[j].x, kw.x, acc, false);
+				acc = __builtin_amdgcn_sdot4(q[j].y, kw.y, acc, false);
+				acc = __builtin_amdgcn_sdot4(q[j].z, kw.z, acc, false);
+				acc = __builtin_amdgcn_sdot4(q[j].w, kw.w, acc, false);
+			}
+			ex[p] = acc;
+			mx = acc > mx ? acc : mx;
+		}
+	}
+	mx = blk_max_i64<BS>(mx, s_mx);
+	if (s_st != 0) return;
+	if (st != kOk) {
+		if (threadIdx.x == 0) set_status(a.status, ti.slot, a.layer, st);
+		return;
+	}
+	if (!live) {  // width outside [1, cap]: the KV landing of this position already refused it
+		if (threadIdx.x == 0) set_status(a.status, ti.slot, a.layer, kPositionOverCap);
+		return;
+	}
+	// pass 2: i-exp values (SoftmaxRowQ15, intmath.cpp:853-889) and the row sum
+	int64_t sum = 0;
+	uint64_t refused = 0;
+	for (int64_t p = threadIdx.x; p < width; p += BS) {
+		int64_t v = iexp_element(ex[p] - mx, c_qln2, c_qb, c_qc, c_M);
+		if (v < 0) {
+			refused = 1;
+			v = 0;
+		}
+		ex[p] = v;
+		sum += v;
+	}
+	sum = wave_sum_i64(sum);
+	refused = wave_max_u64(refused);
+	if ((threadIdx.x & 63) == 0) {
+		s_sum[threadIdx.x >> 6] = sum;
+		s_ref[threadIdx.x >> 6] = refused;
+	}
+	__syncthreads();
+	sum = 0;
+	refused = 0;
+#pragma unroll
+	for (int i = 0; i < BS / 64; ++i) {
+		sum += s_sum[i];
+		refused |= s_ref[i];
+	}
+	if (refused) {
+		if (threadIdx.x == 0) set_status(a.status, ti.slot, a.layer, kSoftmaxKernelRefusedAfterGateAccepted);
+		return;
+	}
+	// pass 3: Q15 probabilities p = (e << 15) / max(total, 1)
+	const int64_t denom = sum > 1 ? sum : 1;
+	for (int64_t p = threadIdx.x; p < width; p += BS) ex[p] = div_floor_pos(ex[p] << 15, denom);
+	__syncthreads();
+	// pass 4: context = sum_p prob * V[p]
+	const int dq = threadIdx.x % TPR, pg = threadIdx.x / TPR;
+	int32_t acc0 = 0, acc1 = 0, acc2 = 0, acc3 = 0;
+	if (pg < PG) {
+		const int8_t* vc = vbase + 4 * dq;
+#pragma unroll 4
+		for (int64_t p = pg; p < width; p += PG) {
+			const int32_t v = *(const int32_t*)(vc + p * D);
+			const int32_t pr = (int32_t)ex[p];
+			acc0 += pr * (int32_t)(int8_t)(v & 0xff);
+			acc1 += pr * (int32_t)(int8_t)((v >> 8) & 0xff);
+			acc2 += pr * (int32_t)(int8_t)((v >> 16) & 0xff);
+			acc3 += pr * (v >> 24);
+		}
+		int32_t* sc = s_ctx + pg * D + 4 * dq;
+		sc[0] = acc0;
+		sc[1] = acc1;
+		sc[2] = acc2;
+		sc[3] = acc3;
+	}
+	__syncthreads();
+	uint64_t mabs = 0;
+	if (threadIdx.x < D) {
+		int32_t c = 0;
+#pragma unroll
+		for (int g2 = 0; g2 < PG; ++g2) c += s_ctx[g2 * D + threadIdx.x];
+		const int64_t f = apply_fold(c, f0, f1, f2);
+		a.ctx_f[(size_t)t * a.H + (size_t)h * D + threadIdx.x] = sat_i32(f);
+		mabs = abs_u64(f);
+	}
+	mabs = blk_max<BS>(mabs, s_ab);
+	if (threadIdx.x == 0) a.ctx_maxpart[(size_t)h * kPartLd + t] = mabs > 0xffffffffull ? 0xffffffffu : (uint32_t)mabs;
 }
 
 // LoRA intermediate (forward_sites.cpp:1066-1086): u[k] = clamp(amp_fold(A[k] . x))
@@ -889,29 +1032,88 @@ void embed(const int32_t* tokens, int M, const int8_t* embed_w, int H, int vocab
 	                   out_scale, scale_idx, tok, status);
 }
 
+// Row kernels are instantiated for a set of per-thread element counts; the smallest one that
+// covers the row is launched.
+constexpr int kRowBS = 512;   // rmsnorm, qkv_post, funnel, residual
+constexpr int kActBS = 1024;  // mlp_act (rows of I elements)
+
+#define SSLM_EPT_CASES(X) X(1) X(2) X(3) X(4) X(6) X(8) X(12) X(16)
+#define SSLM_ACT_EPT_CASES(X) X(1) X(2) X(4) X(9) X(12) X(20)
+
+static int row_ept(int n, int bs) { return (n + bs - 1) / bs; }
+
 void rmsnorm(const RowNormArgs& a, int M, int H, const TokenInfo* tok, int32_t* status, int32_t layer,
              hipStream_t s) {
-	hipLaunchKernelGGL(k_rmsnorm, dim3(M), dim3(kRowBlock), 0, s, a, H, tok, status, layer);
+	const int need = row_ept(H, kRowBS);
+#define X(E)                                                                                               \
+	if (need <= E) {                                                                                       \
+		hipLaunchKernelGGL((k_rmsnorm<kRowBS, E>), dim3(M), dim3(kRowBS), 0, s, a, H, tok, status, layer); \
+		return;                                                                                            \
+	}
+	SSLM_EPT_CASES(X)
+#undef X
 }
 
 void qkv_post(const QkvPostArgs& a, hipStream_t s) {
-	hipLaunchKernelGGL(k_qkv_post, dim3(a.M), dim3(kRowBlock), 0, s, a);
+	const int need = row_ept(a.H / 2, kRowBS);
+#define X(E)                                                                                 \
+	if (need <= E) {                                                                         \
+		hipLaunchKernelGGL((k_qkv_post<kRowBS, E>), dim3(a.M), dim3(kRowBS), 0, s, a); \
+		return;                                                                              \
+	}
+	X(1) X(2) X(4) X(8)
+#undef X
 }
 
 void attention(const AttnArgs& a, hipStream_t s) {
-	const int group = a.NH / a.NKV;
-	const size_t lds = (size_t)group * a.cap * sizeof(int64_t);
-	const int use_lds = lds <= 48 * 1024 ? 1 : 0;
-	hipLaunchKernelGGL(k_attention, dim3(a.NKV, a.M), dim3(kBlock), use_lds ? lds : 0, s, a, use_lds);
+	const size_t lds = (size_t)a.cap * sizeof(int64_t);
+	const int use_lds = attention_in_lds(a.cap) ? 1 : 0;
+	const dim3 grid(a.NH, a.M);
+	switch (a.D) {
+		case 32: hipLaunchKernelGGL((k_attention<kBlock, 32>), grid, dim3(kBlock), use_lds ? lds : 0, s, a, use_lds); break;
+		case 64: hipLaunchKernelGGL((k_attention<kBlock, 64>), grid, dim3(kBlock), use_lds ? lds : 0, s, a, use_lds); break;
+		case 128: hipLaunchKernelGGL((k_attention<kBlock, 128>), grid, dim3(kBlock), use_lds ? lds : 0, s, a, use_lds); break;
+		default: hipLaunchKernelGGL((k_attention<kBlock, 256>), grid, dim3(kBlock), use_lds ? lds : 0, s, a, use_lds); break;
+	}
 }
 
-void funnel(const FunnelArgs& a, hipStream_t s) { hipLaunchKernelGGL(k_funnel, dim3(a.M), dim3(kRowBlock), 0, s, a); }
+void funnel(const FunnelArgs& a, hipStream_t s) {
+	const int need = row_ept(a.N, kRowBS);
+#define X(E)                                                                               \
+	if (need <= E) {                                                                       \
+		hipLaunchKernelGGL((k_funnel<kRowBS, E>), dim3(a.M), dim3(kRowBS), 0, s, a); \
+		return;                                                                            \
+	}
+	SSLM_EPT_CASES(X)
+#undef X
+}
 
 void residual_norm(const ResidualArgs& a, hipStream_t s) {
-	hipLaunchKernelGGL(k_residual_norm, dim3(a.M), dim3(kRowBlock), 0, s, a);
+	const int need = row_ept(a.H, kRowBS);
+#define X(E)                                                                                      \
+	if (need <= E) {                                                                              \
+		hipLaunchKernelGGL((k_residual_norm<kRowBS, E>), dim3(a.M), dim3(kRowBS), 0, s, a); \
+		return;                                                                                   \
+	}
+	SSLM_EPT_CASES(X)
+#undef X
 }
 
-void mlp_act(const ActArgs& a, hipStream_t s) { hipLaunchKernelGGL(k_mlp_act, dim3(a.M), dim3(kRowBlock), 0, s, a); }
+void mlp_act(const ActArgs& a, hipStream_t s) {
+	const int need = row_ept(a.I, kActBS);
+#define X(E)                                                                                \
+	if (need <= E) {                                                                        \
+		hipLaunchKernelGGL((k_mlp_act<kActBS, E>), dim3(a.M), dim3(kActBS), 0, s, a); \
+		return;                                                                             \
+	}
+	SSLM_ACT_EPT_CASES(X)
+#undef X
+}
+
+bool row_geometry_ok(int H, int I, int NKV, int D) {
+	return H <= 16 * kRowBS && I <= 20 * kActBS && NKV * D <= 4 * kRowBS && H / 2 <= 8 * kRowBS &&
+	       (D == 32 || D == 64 || D == 128 || D == 256);
+}
 
 void lora_u(const LoraUArgs& a, hipStream_t s) { hipLaunchKernelGGL(k_lora_u, dim3(a.M), dim3(kBlock), 0, s, a); }
 

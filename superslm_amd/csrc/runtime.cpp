@@ -410,7 +410,7 @@ void run_layers(sslm_model m, int M, StreamRef st, int l0, int l1, sslm_adapter 
 			a.f = m->ctx_f;
 			a.ld_f = H;
 			a.maxpart = m->mx_ctx;
-			a.ntiles = m->NKV;
+			a.ntiles = m->NH;
 			a.incoming = nullptr;
 			a.site = lw.ctx;
 			a.out = m->ctx;
@@ -627,9 +627,10 @@ bool build_device_model(sslm_model m, std::string* err) {
 		*err = "int16 KV precision has no decode path (forward_sites.cpp:2503)";
 		return false;
 	}
-	if (m->H % 64 || m->I % 64 || m->KVH % 16 || m->D % 32 || m->NH / m->NKV > 16) {
-		*err = "geometry outside this backend's tiling (hidden, intermediate multiple of 64; head_dim of 32; "
-		       "GQA group <= 16)";
+	if (m->H % 64 || m->I % 64 || m->KVH % 16 || m->NH % m->NKV ||
+	    !sslm_launch::row_geometry_ok(m->H, m->I, m->NKV, m->D)) {
+		*err = "geometry outside this backend's tiling (hidden, intermediate multiple of 64; hidden <= 8192; "
+		       "intermediate <= 20480; head_dim 32, 64, 128 or 256; kv width <= 2048)";
 		return false;
 	}
 	auto& own = m->owned;
@@ -819,14 +820,13 @@ bool build_device_model(sslm_model m, std::string* err) {
 	m->gu_f = dalloc<int32_t>((size_t)T * 2 * I, &own);
 	m->down_f = dalloc<int32_t>((size_t)T * H, &own);
 	m->mx_q = dalloc<uint32_t>((size_t)(H + 2 * KVH) / 16 * kPartLd, &own);
-	m->mx_ctx = dalloc<uint32_t>((size_t)m->NKV * kPartLd, &own);
+	m->mx_ctx = dalloc<uint32_t>((size_t)m->NH * kPartLd, &own);
 	m->mx_o = dalloc<uint32_t>((size_t)H / 16 * kPartLd, &own);
 	m->mx_gu = dalloc<uint32_t>((size_t)2 * I / 16 * kPartLd, &own);
 	m->mx_down = dalloc<uint32_t>((size_t)H / 16 * kPartLd, &own);
 	m->argmax_key = dalloc<unsigned long long>((size_t)(m->V + 15) / 16 * kPartLd, &own);
 	for (int i = 0; i < 3; ++i) m->lora_u[i] = dalloc<int8_t>((size_t)T * kMaxRank, &own);
-	const int group = m->NH / m->NKV;
-	if ((size_t)group * m->cap * 8 > 48 * 1024)
+	if (!sslm_launch::attention_in_lds(m->cap))
 		m->attn_scratch = dalloc<int64_t>((size_t)T * m->NH * m->cap, &own);
 	else
 		m->attn_scratch = nullptr;
