@@ -57,6 +57,28 @@ struct GemmArgs {
 	const int8_t* w;   // [N, K] weights
 	int32_t M, N, K, lda;
 	Epilogue epi;
+	// Decode GEMV split-K: with splits > 1 every split stores its raw int32 partial sums to plane
+	// `split` of split_part ([splits][M][N]) and the epilogue is left to the consumer (RawIn).
+	int32_t splits;
+	int32_t* split_part;
+};
+
+// decode GEMV launch shape
+struct GemvPlan {
+	int tpw;     // 16-column tiles per block
+	int splits;  // K splits over gridDim.y
+	int cps;     // 128-byte K chunks per split
+	int cpw;     // chunks per wave per load batch
+};
+constexpr int kGemvTargetBlocks = 512;
+constexpr int kMaxRawSplits = 8;  // split planes a raw consumer adds
+
+// A projection's output as split-K partial sums whose epilogue (fold, LoRA, bias) the consuming
+// row kernel applies: element j of token t is epi_value(epi, t, j, sum_s part[(s * M + t) * ld + j]).
+struct RawIn {
+	const int32_t* part;  // null: the producer already applied the epilogue
+	int32_t splits, ld;
+	Epilogue epi;
 };
 
 // Status word: the first rejection per sequence slot wins.
@@ -71,6 +93,10 @@ namespace sslm_launch {
 using namespace sslm;
 
 void gemm(const GemmArgs& g, hipStream_t s);
+// launch shape of the decode GEMV (M <= 64, K % 128 == 0); `split_ok`: the caller consumes raw
+// split-K partials
+GemvPlan gemv_plan(int M, int N, int K, bool split_ok);
+bool gemv_eligible(int M, int K);
 
 struct RowNormArgs {
 	// input stream codes: in_codes[idx[t] * ld_in], input scale ignored (norm kills it)
@@ -95,6 +121,7 @@ struct QkvPostArgs {
 	const TokenInfo* tok;
 	const int32_t* q_f;       // [M, H] funnel-mode q fold outputs
 	const uint32_t* q_maxpart;  // tiles [0, H/16) of the q|k|v projection
+	RawIn raw;                  // or: raw q|k|v partials (q_f, q_maxpart and kv_f unused)
 	const int64_t* kv_f;      // [M, 2*NKV*D] k then v wide values
 	const Scale* in_scale;    // [M] normed scale (landing operand and q's incoming)
 	Scale q_site;
@@ -161,6 +188,7 @@ struct ResidualArgs {
 	const TokenInfo* tok;
 	const int32_t* branch_f;   // [M, H] funnel-mode fold outputs of o_proj / down_proj
 	const uint32_t* branch_maxpart;  // tiles [0, H/16)
+	RawIn raw;                       // or: raw projection partials (branch_f, branch_maxpart unused)
 	const Scale* branch_in;    // [M] incoming scale of the projection (ctx / act)
 	Scale branch_site;
 	int8_t* stream;            // stream codes, row stream_idx[t]
@@ -189,6 +217,7 @@ struct ActArgs {
 	const TokenInfo* tok;
 	const int32_t* gu_f;     // [M, 2I] gate then up
 	const uint32_t* gu_maxpart;  // tiles [0, I/16) gate, [I/16, 2I/16) up
+	RawIn raw;                   // or: raw gate|up partials (gu_f, gu_maxpart unused)
 	const Scale* in_scale;   // [M] mlp-normed scale (incoming of gate and up)
 	Scale gate_site, up_site, act_site;
 	const int32_t* silu;     // [1025]

@@ -152,23 +152,37 @@ __device__ __forceinline__ void epi_publish(const Epilogue& e, int tile, int t, 
 }
 
 // ------------------------------------------------------------------------------------------
-// Streaming decode GEMV (M <= 64): a block of WAVES waves owns 16 output channels; K is walked in
-// 128-byte chunks dealt round-robin to the waves.  Per chunk a lane loads 32 contiguous bytes of
-// a weight row (a wave covers 16 rows x 128 B) and feeds two v_mfma_i32_16x16x64_i8 with the
-// activations loaded in the same lane->k mapping, so the k permutation is identical on both
-// operands and the integer sum is exact.  The next chunk is in flight while the current one is
-// multiplied.  The waves' partial tiles meet in LDS; no global split, no atomics.
+// Decode GEMV (M <= 64).  A decode projection streams each weight byte once and lasts a few
+// microseconds, so the kernel puts as much of the matrix in flight as it can: a block of 4 waves
+// owns TPW 16-column tiles and a range of K (split-K over gridDim.y), and each wave issues the
+// loads of CPW 128-byte chunks of all its tiles before the MFMAs that consume them.  Per chunk a
+// lane holds 32 contiguous bytes of one weight row (a wave covers 16 rows x 128 B per tile) and
+// the activations in the same lane->k mapping -- reused across the TPW tiles -- feeding two
+// v_mfma_i32_16x16x64_i8 per tile; the k permutation is identical on both operands, so the
+// integer sum is exact.  The waves' tiles meet in LDS.  With one split the block runs the
+// epilogue; with several, each split stores its raw partial plane and the consumer adds them
+// (no cross-block synchronisation inside the kernel).
 // ------------------------------------------------------------------------------------------
-template <int MB, int WAVES>
-__global__ __launch_bounds__(64 * WAVES) void k_gemv_stream(GemmArgs g) {
-	__shared__ v4i red[WAVES][MB][64];
+constexpr int kGemvWaves = 4;
+
+template <int MB, int TPW, int CPW>
+__global__ __launch_bounds__(64 * kGemvWaves) void k_gemv(GemmArgs g, int cps) {
+	__shared__ v4i red[kGemvWaves][MB * TPW][64];
 	const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-	const int col0 = blockIdx.x * 16;
+	const int tile0 = blockIdx.x * TPW, split = blockIdx.y;
 	const int ri = lane & 15, grp = lane >> 4;
 	const int C = g.K >> 7;
-	const int my_col = col0 + ri;
-	const bool col_ok = my_col < g.N;
-	const int8_t* wrow = g.w + (size_t)(col_ok ? my_col : 0) * g.K + grp * 32;
+	const int c_begin = split * cps;
+	const int c_end = min(C, c_begin + cps);
+	const v4i z = v4i{0, 0, 0, 0};
+	const int8_t* wrow[TPW];
+	bool col_ok[TPW];
+#pragma unroll
+	for (int tt = 0; tt < TPW; ++tt) {
+		const int col = (tile0 + tt) * 16 + ri;
+		col_ok[tt] = col < g.N;
+		wrow[tt] = g.w + (size_t)(col_ok[tt] ? col : 0) * g.K + grp * 32;
+	}
 	const int8_t* arow[MB];
 	bool row_ok[MB];
 #pragma unroll
@@ -177,67 +191,63 @@ __global__ __launch_bounds__(64 * WAVES) void k_gemv_stream(GemmArgs g) {
 		row_ok[mb] = r < g.M;
 		arow[mb] = g.a + (size_t)(row_ok[mb] ? r : 0) * g.lda + grp * 32;
 	}
-	v4i acc[MB];
+	v4i acc[MB][TPW];
 #pragma unroll
-	for (int mb = 0; mb < MB; ++mb) acc[mb] = v4i{0, 0, 0, 0};
-	const v4i z = v4i{0, 0, 0, 0};
-	int c = wave;
-	v4i b0 = z, b1 = z, a0[MB], a1[MB];
+	for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
-	for (int mb = 0; mb < MB; ++mb) a0[mb] = a1[mb] = z;
-	if (c < C) {
-		const int8_t* wp = wrow + (size_t)c * 128;
-		b0 = col_ok ? load16(wp) : z;
-		b1 = col_ok ? load16(wp + 16) : z;
+		for (int tt = 0; tt < TPW; ++tt) acc[mb][tt] = z;
+	for (int base = c_begin + wave; base < c_end; base += kGemvWaves * CPW) {
+		v4i b[CPW][TPW][2], x[CPW][MB][2];
 #pragma unroll
-		for (int mb = 0; mb < MB; ++mb) {
-			a0[mb] = row_ok[mb] ? load16(arow[mb] + (size_t)c * 128) : z;
-			a1[mb] = row_ok[mb] ? load16(arow[mb] + (size_t)c * 128 + 16) : z;
-		}
-	}
-	while (c < C) {
-		const int cn = c + WAVES;
-		v4i nb0 = z, nb1 = z, na0[MB], na1[MB];
+		for (int i = 0; i < CPW; ++i) {
+			const int c = base + i * kGemvWaves;
+			const bool ok = c < c_end;
 #pragma unroll
-		for (int mb = 0; mb < MB; ++mb) na0[mb] = na1[mb] = z;
-		if (cn < C) {
-			const int8_t* wp = wrow + (size_t)cn * 128;
-			nb0 = col_ok ? load16(wp) : z;
-			nb1 = col_ok ? load16(wp + 16) : z;
+			for (int tt = 0; tt < TPW; ++tt) {
+				b[i][tt][0] = ok && col_ok[tt] ? load16(wrow[tt] + (size_t)c * 128) : z;
+				b[i][tt][1] = ok && col_ok[tt] ? load16(wrow[tt] + (size_t)c * 128 + 16) : z;
+			}
 #pragma unroll
 			for (int mb = 0; mb < MB; ++mb) {
-				na0[mb] = row_ok[mb] ? load16(arow[mb] + (size_t)cn * 128) : z;
-				na1[mb] = row_ok[mb] ? load16(arow[mb] + (size_t)cn * 128 + 16) : z;
+				x[i][mb][0] = ok && row_ok[mb] ? load16(arow[mb] + (size_t)c * 128) : z;
+				x[i][mb][1] = ok && row_ok[mb] ? load16(arow[mb] + (size_t)c * 128 + 16) : z;
 			}
 		}
 #pragma unroll
-		for (int mb = 0; mb < MB; ++mb) {
-			acc[mb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0[mb], b0, acc[mb], 0, 0, 0);
-			acc[mb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1[mb], b1, acc[mb], 0, 0, 0);
-		}
-		c = cn;
-		b0 = nb0;
-		b1 = nb1;
+		for (int i = 0; i < CPW; ++i)
 #pragma unroll
-		for (int mb = 0; mb < MB; ++mb) {
-			a0[mb] = na0[mb];
-			a1[mb] = na1[mb];
-		}
+			for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+				for (int tt = 0; tt < TPW; ++tt) {
+					acc[mb][tt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(x[i][mb][0], b[i][tt][0], acc[mb][tt], 0, 0, 0);
+					acc[mb][tt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(x[i][mb][1], b[i][tt][1], acc[mb][tt], 0, 0, 0);
+				}
 	}
 #pragma unroll
-	for (int mb = 0; mb < MB; ++mb) red[wave][mb][lane] = acc[mb];
+	for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+		for (int tt = 0; tt < TPW; ++tt) red[wave][mb * TPW + tt][lane] = acc[mb][tt];
 	__syncthreads();
-	// wave w finishes row block mb = w (and w + WAVES, ... when MB > WAVES)
 	const Epilogue& e = g.epi;
-	const int j = col0 + ri;
-	for (int mb = wave; mb < MB; mb += WAVES) {
-		v4i tot = red[0][mb][lane];
-		for (int w = 1; w < WAVES; ++w) {
-			const v4i x = red[w][mb][lane];
-			tot[0] += x[0];
-			tot[1] += x[1];
-			tot[2] += x[2];
-			tot[3] += x[3];
+	for (int o = wave; o < MB * TPW; o += kGemvWaves) {
+		const int mb = o / TPW, tile = tile0 + o % TPW;
+		v4i tot = red[0][o][lane];
+#pragma unroll
+		for (int w = 1; w < kGemvWaves; ++w) {
+			const v4i y = red[w][o][lane];
+			tot[0] += y[0];
+			tot[1] += y[1];
+			tot[2] += y[2];
+			tot[3] += y[3];
+		}
+		const int j = tile * 16 + ri;
+		if (g.splits > 1) {
+#pragma unroll
+			for (int v = 0; v < 4; ++v) {
+				const int t = mb * 16 + grp * 4 + v;
+				if (t < g.M && j < g.N) g.split_part[((size_t)split * g.M + t) * g.N + j] = tot[v];
+			}
+			continue;
 		}
 #pragma unroll
 		for (int v = 0; v < 4; ++v) {
@@ -246,7 +256,7 @@ __global__ __launch_bounds__(64 * WAVES) void k_gemv_stream(GemmArgs g) {
 			uint32_t mabs = 0;
 			int seg = 0;
 			if (t < g.M && j < g.N) epi_element(e, g.N, t, j, tot[v], &key, &mabs, &seg);
-			epi_publish(e, blockIdx.x, t, t < g.M && col0 < g.N, key, mabs, seg);
+			epi_publish(e, tile, t, t < g.M && tile * 16 < g.N, key, mabs, seg);
 		}
 	}
 }
@@ -456,6 +466,67 @@ __device__ __forceinline__ uint64_t part_max(const uint32_t* part, int tile0, in
 
 __device__ __forceinline__ uint64_t abs_u64(int64_t v) { return v < 0 ? (uint64_t)0 - (uint64_t)v : (uint64_t)v; }
 
+// N elements (columns j[k] of segment `si`) of token t of a raw split-K projection with the
+// segment's epilogue applied (RawIn).  Every load -- all split planes, fold triples and biases
+// -- is issued before the first use, in straight-line code, so the row pays one memory round
+// trip.  Columns with live[k] false read a valid column and return 0.  Returns false when a bias
+// reconcile refused its product (epi_value's rule).
+template <int N>
+__device__ __forceinline__ bool raw_row(const RawIn& r, int si, int M, int t, const int (&j)[N], const bool (&live)[N],
+                                        int64_t (&v)[N]) {
+	const Segment& sg = r.epi.seg[si];
+	const size_t plane = (size_t)M * r.ld;
+	const int32_t* row = r.part + (size_t)t * r.ld;
+	int32_t jj[N];
+	uint32_t acc[N];
+	int32_t f0[N], f1[N], f2[N];
+#pragma unroll
+	for (int k = 0; k < N; ++k) {
+		const int jc = live[k] ? j[k] : sg.n_begin;
+		jj[k] = jc - sg.n_begin;
+		acc[k] = 0;
+#pragma unroll
+		for (int s2 = 0; s2 < kMaxRawSplits; ++s2) {  // clamped plane index: no branch, no extra round trip
+			const uint32_t x = (uint32_t)row[(size_t)min(s2, r.splits - 1) * plane + jc];
+			acc[k] += s2 < r.splits ? x : 0u;  // the true sum fits int32; partials wrap harmlessly
+		}
+		const int32_t* f = sg.fold + 3 * jj[k];
+		f0[k] = f[0];
+		f1[k] = f[1];
+		f2[k] = f[2];
+	}
+	int64_t bias[N];
+	int64_t rcp = 0, ein = 0;
+	if (sg.bias) {
+#pragma unroll
+		for (int k = 0; k < N; ++k) bias[k] = sg.bias[jj[k]];
+		rcp = r.epi.in_recip[t];
+		ein = r.epi.in_scale[t].e;
+	}
+	bool ok = true;
+#pragma unroll
+	for (int k = 0; k < N; ++k) {
+		v[k] = apply_fold((int64_t)(int32_t)acc[k], f0[k], f1[k], f2[k]);
+		if (sg.lora_b) {
+			const int8_t* br = sg.lora_b + (size_t)jj[k] * r.epi.rank;
+			const int8_t* ur = sg.lora_u + (size_t)t * kMaxRank;
+			int64_t d = 0;
+			for (int q = 0; q < r.epi.rank; ++q) d += (int32_t)br[q] * (int32_t)ur[q];
+			const int32_t* df = sg.lora_dfold + 3 * jj[k];
+			v[k] += apply_amp_fold(d, df[0], df[1], df[2]);
+		}
+		if (sg.bias) {
+			int64_t term;
+			if (bias_term(bias[k], rcp, ein, v[k], &term)) v[k] += term;
+			else if (live[k]) ok = false;
+		}
+		if (!live[k]) v[k] = 0;
+	}
+	return ok;
+}
+
+constexpr uint64_t kBad = ~(uint64_t)0;  // max-reduction sentinel: a refusal somewhere in the row
+
 constexpr int32_t kSkipped = -1;  // the slot had already failed: nothing written, no status
 
 // forward_sites.cpp:410-459 -- the RMSNorm site body on a register-resident row of codes `h`
@@ -526,7 +597,7 @@ __global__ __launch_bounds__(BS) void k_rmsnorm(sslm_launch::RowNormArgs a, int 
 // q funnel + RoPE(q); K/V landing, RoPE(K), KV write (forward_sites.cpp:1281-1418, :1748-1787).
 // The K/V landing does not depend on the q funnel, so it is computed while the q maximum is
 // reduced.  Up to 2 K (and 2 V) pairs per thread: NKV * D <= 4 * BS.
-template <int BS, int EQ>
+template <int BS, int EQ, bool RAW>
 __global__ __launch_bounds__(BS) void k_qkv_post(sslm_launch::QkvPostArgs a) {
 	__shared__ uint64_t s_red[BS / 64];
 	__shared__ int32_t s_st;
@@ -540,27 +611,71 @@ __global__ __launch_bounds__(BS) void k_qkv_post(sslm_launch::QkvPostArgs a) {
 	const int64_t* cs = a.rope_cos + (pos_ok ? pos : 0) * pairs;
 	const int64_t* sn = a.rope_sin + (pos_ok ? pos : 0) * pairs;
 	// q pair values
-	const int2* qf = (const int2*)(a.q_f + (size_t)t * H);
 	int2 qv[EQ];
+	uint64_t qmx = 0;
+	if (RAW) {
+		int j[2 * EQ];
+		bool live[2 * EQ];
+		int64_t v[2 * EQ];
 #pragma unroll
-	for (int k = 0; k < EQ; ++k) {
-		const int p = threadIdx.x + k * BS;
-		qv[k] = p < H / 2 ? qf[p] : make_int2(0, 0);
+		for (int k = 0; k < EQ; ++k) {
+			const int p = threadIdx.x + k * BS;
+			j[2 * k] = 2 * p;
+			j[2 * k + 1] = 2 * p + 1;
+			live[2 * k] = live[2 * k + 1] = p < H / 2;
+		}
+		const bool ok = raw_row<2 * EQ>(a.raw, 0, a.M, t, j, live, v);
+#pragma unroll
+		for (int k = 0; k < EQ; ++k) {
+			qv[k] = make_int2(sat_i32(v[2 * k]), sat_i32(v[2 * k + 1]));
+			qmx = std::max(qmx, (uint64_t)std::max(sat_abs_u32(v[2 * k]), sat_abs_u32(v[2 * k + 1])));
+		}
+		if (!ok) qmx = kBad;
+	} else {
+		const int2* qf = (const int2*)(a.q_f + (size_t)t * H);
+#pragma unroll
+		for (int k = 0; k < EQ; ++k) {
+			const int p = threadIdx.x + k * BS;
+			qv[k] = p < H / 2 ? qf[p] : make_int2(0, 0);
+		}
+		qmx = part_max<BS>(a.q_maxpart, 0, H / 16, t);
 	}
-	uint64_t qmx = part_max<BS>(a.q_maxpart, 0, H / 16, t);
 	if (threadIdx.x == 0) s_st = a.status[ti.slot];
 	// K/V landing (LandingRescale at the normed scale, per kv head) and RoPE(K)
-	const int64_t* kv = a.kv_f + (size_t)t * 2 * KVH;
+	const int64_t* kv = RAW ? nullptr : a.kv_f + (size_t)t * 2 * KVH;
 	int8_t kq[2][2], vq[2][2];
 	uint64_t sat = 0;
+	int64_t rk[4], rv[4];
+	if (RAW) {
+		int jk[4], jv[4];
+		bool live[4];
+#pragma unroll
+		for (int k = 0; k < 2; ++k) {
+			const int p = threadIdx.x + k * BS;
+			jk[2 * k] = H + 2 * p;
+			jk[2 * k + 1] = H + 2 * p + 1;
+			jv[2 * k] = H + KVH + 2 * p;
+			jv[2 * k + 1] = H + KVH + 2 * p + 1;
+			live[2 * k] = live[2 * k + 1] = p < KVH / 2;
+		}
+		const bool okk = raw_row<4>(a.raw, 1, a.M, t, jk, live, rk);
+		const bool okv = raw_row<4>(a.raw, 2, a.M, t, jv, live, rv);
+		if (!(okk && okv)) qmx = kBad;
+	}
 #pragma unroll
 	for (int k = 0; k < 2; ++k) {
 		const int p = threadIdx.x + k * BS;
-		if (p < KVH / 2 && pos_ok) {
+		if (p < KVH / 2) {  // (an out-of-range position is refused below; its values are unused)
 			const int hd = (2 * p) / D;
 			const int i = p % pairs;
-			const longlong2 kk = ((const longlong2*)kv)[p];
-			const longlong2 vv = ((const longlong2*)(kv + KVH))[p];
+			longlong2 kk, vv;
+			if (RAW) {
+				kk = make_longlong2(rk[2 * k], rk[2 * k + 1]);
+				vv = make_longlong2(rv[2 * k], rv[2 * k + 1]);
+			} else {
+				kk = ((const longlong2*)kv)[p];
+				vv = ((const longlong2*)(kv + KVH))[p];
+			}
 			const int64_t k_e = composed_exponent(ns.e, a.e_t_k[hd]);
 			const int64_t v_e = composed_exponent(ns.e, a.e_t_v[hd]);
 			const int64_t rtk = a.r_t_k[hd], rtv = a.r_t_v[hd];
@@ -579,7 +694,7 @@ __global__ __launch_bounds__(BS) void k_qkv_post(sslm_launch::QkvPostArgs a) {
 	qmx = blk_max<BS>(qmx, s_red);
 	if (s_st != 0) return;
 	FunnelPlan plan;
-	int32_t st = funnel_plan(qmx, &ns, 1, a.q_site, &plan);
+	int32_t st = qmx == kBad ? kBiasReconcileProductOutOfDomain : funnel_plan(qmx, &ns, 1, a.q_site, &plan);
 	if (st == kOk && !pos_ok) st = kPositionOverCap;
 	if (st != kOk) {
 		if (threadIdx.x == 0) set_status(a.status, ti.slot, a.layer, st);
@@ -656,7 +771,7 @@ __global__ __launch_bounds__(BS) void k_funnel(sslm_launch::FunnelArgs a) {
 
 // projection funnel -> residual reconcile -> (optional) RMSNorm, all on one token's row
 // (forward_sites.cpp:871-989 residual; :410-459 norm).  `out_stream` never aliases `stream`.
-template <int BS, int EPT>
+template <int BS, int EPT, bool RAW>
 __global__ __launch_bounds__(BS) void k_residual_norm(sslm_launch::ResidualArgs a) {
 	__shared__ uint64_t s_b[BS / 64], s_r[BS / 64], s_n[BS / 64];
 	__shared__ int64_t s_ss[BS / 64];
@@ -670,21 +785,39 @@ __global__ __launch_bounds__(BS) void k_residual_norm(sslm_launch::ResidualArgs 
 	const int32_t* bfr = a.branch_f + (size_t)t * H;
 	const int8_t* srow = a.stream + (size_t)sidx * H;
 	int32_t bf[EPT], g[EPT], sv[EPT];
+	uint64_t bmx = 0;
+	if (RAW) {
+		int j[EPT];
+		bool live[EPT];
+		int64_t v[EPT];
+#pragma unroll
+		for (int k = 0; k < EPT; ++k) {
+			j[k] = threadIdx.x + k * BS;
+			live[k] = j[k] < H;
+		}
+		const bool ok = raw_row<EPT>(a.raw, 0, a.M, t, j, live, v);
+#pragma unroll
+		for (int k = 0; k < EPT; ++k) {
+			bf[k] = sat_i32(v[k]);
+			bmx = std::max(bmx, (uint64_t)sat_abs_u32(v[k]));
+		}
+		if (!ok) bmx = kBad;
+	}
 #pragma unroll
 	for (int k = 0; k < EPT; ++k) {
 		const int i = threadIdx.x + k * BS;
-		bf[k] = i < H ? bfr[i] : 0;
+		if (!RAW) bf[k] = i < H ? bfr[i] : 0;
 		sv[k] = i < H ? srow[i] : 0;
 		g[k] = (a.gain && i < H) ? a.gain[i] : 0;
 	}
-	uint64_t bmx = part_max<BS>(a.branch_maxpart, 0, H / 16, t);
+	if (!RAW) bmx = part_max<BS>(a.branch_maxpart, 0, H / 16, t);
 	const Scale ss = a.stream_scale[sidx];
 	if (threadIdx.x == 0) s_st = a.status[slot];
 	bmx = blk_max<BS>(bmx, s_b);
 	KT(1);
 	if (s_st != 0) return;
 	FunnelPlan bplan;
-	int32_t st = funnel_plan(bmx, &bin, 1, a.branch_site, &bplan);
+	int32_t st = bmx == kBad ? kBiasReconcileProductOutOfDomain : funnel_plan(bmx, &bin, 1, a.branch_site, &bplan);
 	if (st == kOk && !fits_i32(ss.m)) st = kCarriedScaleMantissaOutOfDomain;
 	if (st != kOk) {
 		if (threadIdx.x == 0) set_status(a.status, slot, a.layer, st);
@@ -694,7 +827,6 @@ __global__ __launch_bounds__(BS) void k_residual_norm(sslm_launch::ResidualArgs 
 	const Scale bs = bplan.out;
 	const int64_t kx = composed_exponent(bs.e, ss.e);
 	KT(2);
-	constexpr uint64_t kBad = ~(uint64_t)0;  // |w| <= 2^63 + 127, so the sentinel is unambiguous
 	int64_t w[EPT];
 	uint64_t mx = 0;
 #pragma unroll
@@ -747,7 +879,7 @@ __global__ __launch_bounds__(BS) void k_residual_norm(sslm_launch::ResidualArgs 
 // gate/up funnels -> MlpActSite (forward_sites.cpp:796-864) -> act funnel.  The sigmoid of a
 // gate code depends only on the code and the token's gate scale, so the 256 possible values
 // are tabulated per block once the gate plan is known.
-template <int BS, int EPT>
+template <int BS, int EPT, bool RAW>
 __global__ __launch_bounds__(BS) void k_mlp_act(sslm_launch::ActArgs a) {
 	__shared__ uint64_t s_gu[2 * BS / 64], s_a[BS / 64];
 	__shared__ int32_t sig[256];
@@ -757,20 +889,45 @@ __global__ __launch_bounds__(BS) void k_mlp_act(sslm_launch::ActArgs a) {
 	const int32_t* gfr = a.gu_f + (size_t)t * 2 * I;
 	const int32_t* ufr = gfr + I;
 	int32_t gf[EPT], uf[EPT];
+	uint64_t gm = 0, um = 0;
+	if (RAW) {
+		int jg[EPT], ju[EPT];
+		bool live[EPT];
+		int64_t vg[EPT], vu[EPT];
 #pragma unroll
-	for (int k = 0; k < EPT; ++k) {
-		const int i = threadIdx.x + k * BS;
-		gf[k] = i < I ? gfr[i] : 0;
-		uf[k] = i < I ? ufr[i] : 0;
+		for (int k = 0; k < EPT; ++k) {
+			jg[k] = threadIdx.x + k * BS;
+			ju[k] = I + jg[k];
+			live[k] = jg[k] < I;
+		}
+		const bool okg = raw_row<EPT>(a.raw, 0, a.M, t, jg, live, vg);
+		const bool oku = raw_row<EPT>(a.raw, 1, a.M, t, ju, live, vu);
+#pragma unroll
+		for (int k = 0; k < EPT; ++k) {
+			gf[k] = sat_i32(vg[k]);
+			uf[k] = sat_i32(vu[k]);
+			gm = std::max(gm, (uint64_t)sat_abs_u32(vg[k]));
+			um = std::max(um, (uint64_t)sat_abs_u32(vu[k]));
+		}
+		if (!(okg && oku)) gm = kBad;
+	} else {
+#pragma unroll
+		for (int k = 0; k < EPT; ++k) {
+			const int i = threadIdx.x + k * BS;
+			gf[k] = i < I ? gfr[i] : 0;
+			uf[k] = i < I ? ufr[i] : 0;
+		}
 	}
-	uint64_t gm = part_max<BS>(a.gu_maxpart, 0, I / 16, t);
-	uint64_t um = part_max<BS>(a.gu_maxpart, I / 16, I / 16, t);
+	if (!RAW) {
+		gm = part_max<BS>(a.gu_maxpart, 0, I / 16, t);
+		um = part_max<BS>(a.gu_maxpart, I / 16, I / 16, t);
+	}
 	const Scale inc = a.in_scale[t];
 	if (threadIdx.x == 0) s_st = a.status[slot];
 	blk_max2<BS>(gm, um, s_gu);
 	if (s_st != 0) return;
 	FunnelPlan gp, up;
-	int32_t st = funnel_plan(gm, &inc, 1, a.gate_site, &gp);
+	int32_t st = gm == kBad ? kBiasReconcileProductOutOfDomain : funnel_plan(gm, &inc, 1, a.gate_site, &gp);
 	if (st == kOk) st = funnel_plan(um, &inc, 1, a.up_site, &up);
 	if (st == kOk) st = check_silu_scale(gp.out.m, gp.out.e);
 	if (st != kOk) {
@@ -997,27 +1154,51 @@ __global__ __launch_bounds__(kBlock) void k_argmax_finalize(const unsigned long 
 // ------------------------------------------------------------------------------------------
 namespace sslm_launch {
 
-template <int MB>
-static void launch_gemv(const GemmArgs& g, int waves, hipStream_t s) {
-	dim3 grid((g.N + 15) / 16);
-	if (waves >= 16) hipLaunchKernelGGL((k_gemv_stream<MB, 16>), grid, dim3(64 * 16), 0, s, g);
-	else if (waves >= 8) hipLaunchKernelGGL((k_gemv_stream<MB, 8>), grid, dim3(64 * 8), 0, s, g);
-	else hipLaunchKernelGGL((k_gemv_stream<MB, 4>), grid, dim3(64 * 4), 0, s, g);
+template <int MB, int TPW>
+static void launch_gemv(const GemmArgs& g, const GemvPlan& p, hipStream_t s) {
+	const dim3 grid((g.N + 16 * TPW - 1) / (16 * TPW), p.splits), block(64 * kGemvWaves);
+	switch (p.cpw) {
+		case 1: hipLaunchKernelGGL((k_gemv<MB, TPW, 1>), grid, block, 0, s, g, p.cps); break;
+		case 2: hipLaunchKernelGGL((k_gemv<MB, TPW, 2>), grid, block, 0, s, g, p.cps); break;
+		default: hipLaunchKernelGGL((k_gemv<MB, TPW, 3>), grid, block, 0, s, g, p.cps); break;
+	}
+}
+
+bool gemv_eligible(int M, int K) { return M >= 1 && M <= 64 && K % 128 == 0; }
+
+GemvPlan gemv_plan(int M, int N, int K, bool split_ok) {
+	GemvPlan p{};
+	const int mblocks = (M + 15) / 16;
+	const int tiles = (N + 15) / 16;
+	const int C = K / 128;
+	p.tpw = (mblocks == 1 && tiles >= 1024) ? 2 : 1;
+	const int blocks = (tiles + p.tpw - 1) / p.tpw;
+	p.splits = 1;
+	if (split_ok && blocks < kGemvTargetBlocks)
+		p.splits = std::max(1, std::min({(kGemvTargetBlocks + blocks - 1) / blocks, C / kGemvWaves, kMaxRawSplits}));
+	p.cps = (C + p.splits - 1) / p.splits;
+	p.splits = (C + p.cps - 1) / p.cps;
+	const int cpw_max = mblocks <= 2 ? 3 : 2;
+	p.cpw = std::min(cpw_max, (p.cps + kGemvWaves - 1) / kGemvWaves);
+	if (p.cpw < 1) p.cpw = 1;
+	return p;
 }
 
 void gemm(const GemmArgs& g, hipStream_t s) {
 	if (g.M <= 0 || g.N <= 0) return;
-	if (g.M <= 64 && g.K % 128 == 0) {
-		// enough waves to cover the chip: few output tiles -> more waves per tile along K
-		const int tiles = (g.N + 15) / 16;
-		int waves = tiles >= 1024 ? 4 : (tiles >= 256 ? 8 : 16);
+	if (gemv_eligible(g.M, g.K)) {
+		// g.splits > 1 only as gemv_plan(M, N, K, true).splits, for which the caller sized split_part
+		const GemvPlan p = gemv_plan(g.M, g.N, g.K, g.splits > 1);
 		const int mblocks = (g.M + 15) / 16;
-		if (mblocks >= 3 && waves > 8) waves = 8;
-		switch (mblocks) {
-			case 1: launch_gemv<1>(g, waves, s); break;
-			case 2: launch_gemv<2>(g, waves, s); break;
-			case 3: launch_gemv<3>(g, waves, s); break;
-			default: launch_gemv<4>(g, waves, s); break;
+		if (p.tpw == 2 && mblocks == 1) {
+			launch_gemv<1, 2>(g, p, s);
+		} else {
+			switch (mblocks) {
+				case 1: launch_gemv<1, 1>(g, p, s); break;
+				case 2: launch_gemv<2, 1>(g, p, s); break;
+				case 3: launch_gemv<3, 1>(g, p, s); break;
+				default: launch_gemv<4, 1>(g, p, s); break;
+			}
 		}
 		return;
 	}
@@ -1056,10 +1237,13 @@ void rmsnorm(const RowNormArgs& a, int M, int H, const TokenInfo* tok, int32_t* 
 
 void qkv_post(const QkvPostArgs& a, hipStream_t s) {
 	const int need = row_ept(a.H / 2, kRowBS);
-#define X(E)                                                                                 \
-	if (need <= E) {                                                                         \
-		hipLaunchKernelGGL((k_qkv_post<kRowBS, E>), dim3(a.M), dim3(kRowBS), 0, s, a); \
-		return;                                                                              \
+#define X(E)                                                                                          \
+	if (need <= E) {                                                                                  \
+		if (a.raw.part)                                                                               \
+			hipLaunchKernelGGL((k_qkv_post<kRowBS, E, true>), dim3(a.M), dim3(kRowBS), 0, s, a);  \
+		else                                                                                          \
+			hipLaunchKernelGGL((k_qkv_post<kRowBS, E, false>), dim3(a.M), dim3(kRowBS), 0, s, a); \
+		return;                                                                                       \
 	}
 	X(1) X(2) X(4) X(8)
 #undef X
@@ -1090,10 +1274,13 @@ void funnel(const FunnelArgs& a, hipStream_t s) {
 
 void residual_norm(const ResidualArgs& a, hipStream_t s) {
 	const int need = row_ept(a.H, kRowBS);
-#define X(E)                                                                                      \
-	if (need <= E) {                                                                              \
-		hipLaunchKernelGGL((k_residual_norm<kRowBS, E>), dim3(a.M), dim3(kRowBS), 0, s, a); \
-		return;                                                                                   \
+#define X(E)                                                                                               \
+	if (need <= E) {                                                                                       \
+		if (a.raw.part)                                                                                    \
+			hipLaunchKernelGGL((k_residual_norm<kRowBS, E, true>), dim3(a.M), dim3(kRowBS), 0, s, a);  \
+		else                                                                                               \
+			hipLaunchKernelGGL((k_residual_norm<kRowBS, E, false>), dim3(a.M), dim3(kRowBS), 0, s, a); \
+		return;                                                                                            \
 	}
 	SSLM_EPT_CASES(X)
 #undef X
@@ -1101,10 +1288,13 @@ void residual_norm(const ResidualArgs& a, hipStream_t s) {
 
 void mlp_act(const ActArgs& a, hipStream_t s) {
 	const int need = row_ept(a.I, kActBS);
-#define X(E)                                                                                \
-	if (need <= E) {                                                                        \
-		hipLaunchKernelGGL((k_mlp_act<kActBS, E>), dim3(a.M), dim3(kActBS), 0, s, a); \
-		return;                                                                             \
+#define X(E)                                                                                         \
+	if (need <= E) {                                                                                 \
+		if (a.raw.part)                                                                              \
+			hipLaunchKernelGGL((k_mlp_act<kActBS, E, true>), dim3(a.M), dim3(kActBS), 0, s, a);  \
+		else                                                                                         \
+			hipLaunchKernelGGL((k_mlp_act<kActBS, E, false>), dim3(a.M), dim3(kActBS), 0, s, a); \
+		return;                                                                                      \
 	}
 	SSLM_ACT_EPT_CASES(X)
 #undef X

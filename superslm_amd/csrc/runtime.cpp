@@ -179,6 +179,7 @@ struct sslm_model_s {
 	int32_t *q_f, *ctx_f, *o_f, *gu_f, *down_f;
 	uint32_t *mx_q, *mx_ctx, *mx_o, *mx_gu, *mx_down;  // per (16-column tile, token) partial maxima
 	unsigned long long* argmax_key;
+	int32_t* raw_part;  // decode GEMV split-K partial planes, consumed by the next row kernel
 	int8_t* lora_u[3];
 	int8_t* pool_dev = nullptr;  // KV pool of the launch sequence being recorded
 	std::atomic<int> live_refs{0};
@@ -258,6 +259,23 @@ void run_gemm(sslm_model m, const GemmArgs& g, int cls) {
 	ck(hipGetLastError());
 }
 
+// Decode projections whose GEMV splits K hand their raw partial planes to the next row kernel,
+// which applies the epilogue; call once g.epi is complete.  Returns a null RawIn otherwise.
+// `allow`: the consumer's raw variant holds its row in registers without spilling.
+RawIn split_raw(sslm_model m, GemmArgs& g, bool allow) {
+	RawIn r{};
+	if (!allow || !m->raw_part || !sslm_launch::gemv_eligible(g.M, g.K)) return r;
+	const sslm_launch::GemvPlan p = sslm_launch::gemv_plan(g.M, g.N, g.K, true);
+	if (p.splits <= 1) return r;
+	g.splits = p.splits;
+	g.split_part = m->raw_part;
+	r.part = m->raw_part;
+	r.splits = p.splits;
+	r.ld = g.N;
+	r.epi = g.epi;
+	return r;
+}
+
 void attach_lora(sslm_model m, sslm_adapter ad, int layer, int proj, Segment* seg, int slot_u) {
 	if (!ad) return;
 	const AdapterProj& p = ad->proj[(size_t)layer * 7 + proj];
@@ -311,6 +329,7 @@ void run_layers(sslm_model m, int M, StreamRef st, int l0, int l1, sslm_adapter 
 	}
 	for (int l = l0; l < l1; ++l) {
 		const DevLayer& lw = m->layers[l];
+		RawIn raw{};  // the last projection's split-K partials, when it split
 		// q | k | v projection (forward_sites.cpp:1699-1735)
 		{
 			const int pj[3] = {0, 1, 2};
@@ -341,6 +360,7 @@ void run_layers(sslm_model m, int M, StreamRef st, int l0, int l1, sslm_adapter 
 			attach_lora(m, ad, l, 0, &g.epi.seg[0], 0);
 			attach_lora(m, ad, l, 1, &g.epi.seg[1], 1);
 			attach_lora(m, ad, l, 2, &g.epi.seg[2], 2);
+			raw = split_raw(m, g, H <= 4096);
 			run_gemm(m, g, kProfGemm);
 		}
 		{
@@ -370,6 +390,7 @@ void run_layers(sslm_model m, int M, StreamRef st, int l0, int l1, sslm_adapter 
 			a.sat = m->sat;
 			a.status = m->status;
 			a.kv_pool = m->pool_dev;
+			a.raw = raw;
 			ProfScope p(s, kProfRow, 0, 0);
 			sslm_launch::qkv_post(a, s);
 			ck(hipGetLastError());
@@ -430,6 +451,7 @@ void run_layers(sslm_model m, int M, StreamRef st, int l0, int l1, sslm_adapter 
 			g.epi.nseg = 1;
 			g.epi.seg[0] = funnel_seg(0, H, m->o_f, H, m->mx_o, lw.f_o, nullptr);
 			attach_lora(m, ad, l, 3, &g.epi.seg[0], 0);
+			raw = split_raw(m, g, H <= 6144);
 			run_gemm(m, g, kProfGemm);
 		}
 		{  // attn residual -> mlp norm (forward_sites.cpp:1923-1936)
@@ -455,6 +477,7 @@ void run_layers(sslm_model m, int M, StreamRef st, int l0, int l1, sslm_adapter 
 			a.norm_recip = m->mlp_recip;
 			a.layer = l;
 			a.status = m->status;
+			a.raw = raw;
 			ProfScope p(s, kProfRow, 0, 0);
 			sslm_launch::residual_norm(a, s);
 			ck(hipGetLastError());
@@ -470,6 +493,7 @@ void run_layers(sslm_model m, int M, StreamRef st, int l0, int l1, sslm_adapter 
 			g.epi.seg[1] = funnel_seg(I, 2 * I, m->gu_f + I, 2 * I, m->mx_gu, lw.f_gu + 3 * I, nullptr);
 			attach_lora(m, ad, l, 4, &g.epi.seg[0], 0);
 			attach_lora(m, ad, l, 5, &g.epi.seg[1], 1);
+			raw = split_raw(m, g, I <= 4096);
 			run_gemm(m, g, kProfGemm);
 		}
 		{
@@ -488,6 +512,7 @@ void run_layers(sslm_model m, int M, StreamRef st, int l0, int l1, sslm_adapter 
 			a.act_scale = m->act_scale;
 			a.layer = l;
 			a.status = m->status;
+			a.raw = raw;
 			ProfScope p(s, kProfRow, 0, 0);
 			sslm_launch::mlp_act(a, s);
 			ck(hipGetLastError());
@@ -501,6 +526,7 @@ void run_layers(sslm_model m, int M, StreamRef st, int l0, int l1, sslm_adapter 
 			g.epi.nseg = 1;
 			g.epi.seg[0] = funnel_seg(0, H, m->down_f, H, m->mx_down, lw.f_down, nullptr);
 			attach_lora(m, ad, l, 6, &g.epi.seg[0], 0);
+			raw = split_raw(m, g, H <= 6144);
 			run_gemm(m, g, kProfGemm);
 		}
 		{  // mlp residual -> commit -> next layer's attn norm (forward_sites.cpp:1982-2009)
@@ -528,6 +554,7 @@ void run_layers(sslm_model m, int M, StreamRef st, int l0, int l1, sslm_adapter 
 			}
 			a.layer = l;
 			a.status = m->status;
+			a.raw = raw;
 			ProfScope p(s, kProfRow, 0, 0);
 			sslm_launch::residual_norm(a, s);
 			ck(hipGetLastError());
@@ -825,6 +852,14 @@ bool build_device_model(sslm_model m, std::string* err) {
 	m->mx_gu = dalloc<uint32_t>((size_t)2 * I / 16 * kPartLd, &own);
 	m->mx_down = dalloc<uint32_t>((size_t)H / 16 * kPartLd, &own);
 	m->argmax_key = dalloc<unsigned long long>((size_t)(m->V + 15) / 16 * kPartLd, &own);
+	{
+		const int shapes[4][2] = {{H + 2 * KVH, H}, {H, H}, {2 * I, H}, {H, I}};
+		size_t elems = 0;
+		for (auto& sh : shapes)
+			if (sslm_launch::gemv_eligible(64, sh[1]))
+				elems = std::max(elems, (size_t)sslm_launch::gemv_plan(64, sh[0], sh[1], true).splits * 64 * sh[0]);
+		m->raw_part = elems ? dalloc<int32_t>(elems, &own) : nullptr;
+	}
 	for (int i = 0; i < 3; ++i) m->lora_u[i] = dalloc<int8_t>((size_t)T * kMaxRank, &own);
 	if (!sslm_launch::attention_in_lds(m->cap))
 		m->attn_scratch = dalloc<int64_t>((size_t)T * m->NH * m->cap, &own);
@@ -1449,6 +1484,7 @@ StandaloneCtx g_sa;
 
 void sa_reserve(int m, int n) {
 	if (!g_sa.stream) ck(hipStreamCreate(&g_sa.stream));
+
 	const size_t mn = (size_t)m * n;
 	if (mn > g_sa.f_n) {
 		g_sa.f = dalloc<int32_t>(mn, &g_sa.owned);

@@ -244,6 +244,9 @@ CONFIGS = {
                         context_cap=64, tie_embeddings=False, with_bias=True),
     "small": ModelConfig(hidden=256, layers=3, heads=4, kv_heads=1, head_dim=64, inter=512, vocab=1024,
                          context_cap=160, tie_embeddings=True, with_bias=True),
+    # wide enough that the decode GEMVs split K (hidden 1024, intermediate 2816)
+    "medium": ModelConfig(hidden=1024, layers=2, heads=8, kv_heads=2, head_dim=128, inter=2816, vocab=4096,
+                          context_cap=96, tie_embeddings=False, with_bias=True),
     # Qwen2.5-1.5B shape
     "qwen1.5b": ModelConfig(hidden=1536, layers=28, heads=12, kv_heads=2, head_dim=128, inter=8960,
                             vocab=151936, context_cap=1024, tie_embeddings=True),
