@@ -47,7 +47,8 @@ struct Epilogue {
 	int32_t* status;           // [slots] first rejection, (layer << 8) | status
 	int32_t layer;
 	// logits mode: per (16-column tile, token) argmax keys instead of segments
-	unsigned long long* argmax_key;  // [tiles * kPartLd] or null
+	unsigned long long* argmax_key;  // [M][key_ld] per (token, 16-column tile) keys, or null
+	int32_t key_ld;
 	// raw mode: the int32 accumulator itself, [M, N]
 	int32_t* raw_out;
 };

@@ -144,7 +144,7 @@ __device__ __forceinline__ void epi_publish(const Epilogue& e, int tile, int t, 
 	}
 	if ((threadIdx.x & 15) == 0 && live) {
 		if (e.argmax_key) {
-			e.argmax_key[(size_t)tile * kPartLd + t] = key;
+			e.argmax_key[(size_t)t * e.key_ld + tile] = key;
 		} else if (!e.raw_out && e.seg[seg].mode == kSegFunnel && e.seg[seg].maxpart) {
 			e.seg[seg].maxpart[(size_t)tile * kPartLd + t] = mabs;
 		}
@@ -1133,17 +1133,25 @@ __global__ __launch_bounds__(kBlock) void k_lora_u(sslm_launch::LoraUArgs a) {
 }
 
 // lowest-index argmax (forward_sites.cpp:2427-2437) from per-tile keys: the key orders by
-// logit, then by the complement of the index, so the maximum key is the lowest maximal index
-__global__ __launch_bounds__(kBlock) void k_argmax_finalize(const unsigned long long* keys, int ntiles,
-                                                            int32_t* out) {
-	__shared__ uint64_t red[16];
+// logit, then by the complement of the index, so the maximum key is the lowest maximal index.
+// One block per token over its contiguous key row; loads go out in batches of 8 per thread.
+__global__ __launch_bounds__(kRowBlock) void k_argmax_finalize(const unsigned long long* keys, int ntiles,
+                                                               int32_t* out) {
+	__shared__ uint64_t red[kRowBlock / 64];
 	const int t = blockIdx.x;
+	const unsigned long long* row = keys + (size_t)t * ntiles;
 	uint64_t k = 0;
-	for (int i = threadIdx.x; i < ntiles; i += blockDim.x) {
-		const uint64_t v = keys[(size_t)i * kPartLd + t];
-		k = v > k ? v : k;
+	for (int base = 0; base < ntiles; base += 8 * kRowBlock) {
+		uint64_t v[8];
+#pragma unroll
+		for (int i = 0; i < 8; ++i) {
+			const int idx = base + i * kRowBlock + (int)threadIdx.x;
+			v[i] = row[min(idx, ntiles - 1)];
+		}
+#pragma unroll
+		for (int i = 0; i < 8; ++i) k = v[i] > k ? v[i] : k;
 	}
-	k = block_max_u64(k, red);
+	k = blk_max<kRowBlock>(k, red);
 	if (threadIdx.x == 0) out[t] = (int32_t)(0xffffffffu - (uint32_t)(k & 0xffffffffull));
 }
 
@@ -1308,7 +1316,7 @@ bool row_geometry_ok(int H, int I, int NKV, int D) {
 void lora_u(const LoraUArgs& a, hipStream_t s) { hipLaunchKernelGGL(k_lora_u, dim3(a.M), dim3(kBlock), 0, s, a); }
 
 void argmax_finalize(const unsigned long long* keys, int ntiles, int M, int32_t* out_tokens, hipStream_t s) {
-	hipLaunchKernelGGL(k_argmax_finalize, dim3(M), dim3(kBlock), 0, s, keys, ntiles, out_tokens);
+	hipLaunchKernelGGL(k_argmax_finalize, dim3(M), dim3(kRowBlock), 0, s, keys, ntiles, out_tokens);
 }
 
 }  // namespace sslm_launch

@@ -576,6 +576,7 @@ void run_logits(sslm_model m, int M, StreamRef st) {
 	}
 	GemmArgs g = gemm_args(m, m->final_codes, M, m->H, m->head, m->V, m->H);
 	g.epi.argmax_key = m->argmax_key;
+	g.epi.key_ld = (m->V + 15) / 16;
 	g.epi.layer = m->L;
 	run_gemm(m, g, kProfHead);
 	sslm_launch::argmax_finalize(m->argmax_key, (m->V + 15) / 16, M, m->out_tokens, s);
