@@ -72,6 +72,14 @@ struct GemvPlan {
 	int cpw;     // chunks per wave per load batch
 };
 constexpr int kGemvTargetBlocks = 512;
+
+// prefill GEMM launch shape (M > 64)
+struct PrefillPlan {
+	int bm;      // block rows (256 or 128); block columns are 128
+	int splits;  // K splits over gridDim.z
+	int kspan;   // K per split (multiple of 64)
+};
+constexpr int kPrefillTargetBlocks = 256;
 constexpr int kMaxRawSplits = 8;  // split planes a raw consumer adds
 
 // A projection's output as split-K partial sums whose epilogue (fold, LoRA, bias) the consuming
@@ -98,6 +106,8 @@ void gemm(const GemmArgs& g, hipStream_t s);
 // split-K partials
 GemvPlan gemv_plan(int M, int N, int K, bool split_ok);
 bool gemv_eligible(int M, int K);
+// launch shape of the prefill GEMM; `split_ok` as for gemv_plan
+PrefillPlan prefill_plan(int M, int N, int K, bool split_ok);
 
 struct RowNormArgs {
 	// input stream codes: in_codes[idx[t] * ld_in], input scale ignored (norm kills it)

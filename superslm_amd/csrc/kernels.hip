@@ -354,6 +354,226 @@ __global__ __launch_bounds__(kBlock) void k_gemm_tiled(GemmArgs g) {
 }
 
 // ------------------------------------------------------------------------------------------
+// Prefill GEMM (M > 64): block tile BM x 128 (BM = 256: 4 waves, BM = 128: 2 waves), each wave a
+// 128x64 tile of v_mfma_i32_32x32x32_i8 (4x2; the larger wave tile halves LDS reads per MAC
+// against 64x64), BK = 64.  Global tiles travel through two register stages (the loads of
+// K-step t + 2 are issued before step t's MFMAs) into two LDS stages with XOR-swizzled 16-byte
+// chunks (lds_chunk: conflict-free for both the operand reads and the row writes; 48 KB per
+// block at BM = 256, so up to three blocks share a CU), one barrier per K-step.  Loads are unconditional: rows past M or N read a
+// clamped valid row whose products land only in discarded outputs, and K is a multiple of 64.
+// gridDim.z splits K; with several splits each stores its raw int32 partial plane and the
+// consumer applies the epilogue (RawIn), as for the decode GEMV.  With one split the block runs
+// the epilogue (see below).
+// ------------------------------------------------------------------------------------------
+constexpr int kPBN = 128, kPBK = 64, kPStride = kPBK;
+
+// LDS placement of the 16-byte chunk `q` (0..3) of tile row `row`: the chunk index is XORed with
+// bits of the row so that 16 consecutive rows read at one chunk (the MFMA operand pattern) and 4
+// rows written whole (the global-load pattern) both spread over distinct banks, for 32- and
+// 64-bank LDS alike.
+__device__ __forceinline__ int lds_chunk(int row, int q) { return row * kPStride + ((q ^ (((row >> 1) ^ (row >> 3)) & 3)) << 4); }
+
+__device__ __forceinline__ uint32_t dpp_max16(uint32_t v) {
+	// row_ror:8, 4, 2, 1 -- every lane of the 16-lane row ends with the row maximum
+	uint32_t w = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x128, 0xf, 0xf, false);
+	v = w > v ? w : v;
+	w = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x124, 0xf, 0xf, false);
+	v = w > v ? w : v;
+	w = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x122, 0xf, 0xf, false);
+	v = w > v ? w : v;
+	w = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x121, 0xf, 0xf, false);
+	return w > v ? w : v;
+}
+
+// WSC1 fold without a branch on the identity flag (same value as apply_fold)
+__device__ __forceinline__ int64_t fold_select(int32_t acc, int32_t identity, int32_t mult, int32_t shift) {
+	const int64_t folded = (int64_t)rdbpot32(srdhm(acc, mult), shift);
+	return identity != 0 ? (int64_t)acc : folded;
+}
+
+template <int BM>
+__global__ __launch_bounds__(BM / 128 * 2 * 64, 2) void k_gemm_mfma(GemmArgs g, int kspan) {
+	constexpr int WAVES = BM / 128 * 2, NT = WAVES * 64;
+	constexpr int ROWS = BM + kPBN;
+	constexpr int CPR = kPBK / 16;         // 16-byte chunks per row and stage
+	constexpr int CPT = ROWS * CPR / NT;   // per thread
+	static_assert(CPT * NT == ROWS * CPR, "stage must split evenly over the block");
+	__shared__ __attribute__((aligned(16))) int8_t smem[2 * ROWS * kPStride];
+	const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+	const int m0 = blockIdx.y * BM, n0 = blockIdx.x * kPBN;
+	const int split = blockIdx.z;
+	const int k_begin = split * kspan;
+	const int ntile = (min(g.K, k_begin + kspan) - k_begin) / kPBK;
+	const int wm = (wave >> 1) * 128, wn = (wave & 1) * 64;
+
+	// per-thread chunk sources (A rows first, then B rows), rows clamped into the operands
+	const int8_t* src[CPT];
+	int lds_off[CPT];
+#pragma unroll
+	for (int j = 0; j < CPT; ++j) {
+		const int c = threadIdx.x + j * NT;
+		const int row = c / CPR, kc = (c % CPR) * 16;
+		lds_off[j] = lds_chunk(row, c % CPR);
+		if (row < BM) src[j] = g.a + (size_t)min(m0 + row, g.M - 1) * g.lda + k_begin + kc;
+		else src[j] = g.w + (size_t)min(n0 + row - BM, g.N - 1) * g.K + k_begin + kc;
+	}
+	auto gload = [&](v4i (&r)[CPT], int t) {
+		const size_t kb = (size_t)min(t, ntile - 1) * kPBK;
+#pragma unroll
+		for (int j = 0; j < CPT; ++j) r[j] = load16(src[j] + kb);
+	};
+	auto sstore = [&](const v4i (&r)[CPT], int buf) {
+		int8_t* sm = smem + buf * ROWS * kPStride;
+#pragma unroll
+		for (int j = 0; j < CPT; ++j) *(v4i*)&sm[lds_off[j]] = r[j];
+	};
+	v16i acc[4][2];
+#pragma unroll
+	for (int i = 0; i < 4; ++i)
+#pragma unroll
+		for (int j = 0; j < 2; ++j)
+#pragma unroll
+			for (int v = 0; v < 16; ++v) acc[i][j][v] = 0;
+	// operand addresses: row wm + lane % 32 (+ 32 i) of A, wn + lane % 32 (+ 32 j) of B, chunk
+	// 2 ks + lane / 32; the swizzle depends only on the row's low bits, so +32 rows keep it
+	const int arow = wm + (lane & 31), brow = BM + wn + (lane & 31);
+	int aoff[2], boff[2];
+#pragma unroll
+	for (int ks = 0; ks < 2; ++ks) {
+		aoff[ks] = lds_chunk(arow, 2 * ks + (lane >> 5));
+		boff[ks] = lds_chunk(brow, 2 * ks + (lane >> 5));
+	}
+	auto compute = [&](int buf) {
+		const int8_t* sm = smem + buf * ROWS * kPStride;
+#pragma unroll
+		for (int ks = 0; ks < kPBK / 32; ++ks) {
+			v4i a[4], b[2];
+#pragma unroll
+			for (int i = 0; i < 4; ++i) a[i] = *(const v4i*)&sm[aoff[ks] + i * 32 * kPStride];
+#pragma unroll
+			for (int j = 0; j < 2; ++j) b[j] = *(const v4i*)&sm[boff[ks] + j * 32 * kPStride];
+#pragma unroll
+			for (int i = 0; i < 4; ++i)
+#pragma unroll
+				for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], b[j], acc[i][j], 0, 0, 0);
+		}
+	};
+	v4i ra[CPT], rb[CPT];
+	gload(ra, 0);
+	gload(rb, 1);
+	sstore(ra, 0);
+	__syncthreads();
+	// step t: tile t in LDS stage t & 1; tile t + 1 in flight in the other register set; the
+	// loads of tile t + 2 go out before step t's MFMAs
+	for (int t = 0; t < ntile; t += 2) {
+		gload(ra, t + 2);
+		compute(0);
+		sstore(rb, 1);
+		__syncthreads();
+		gload(rb, t + 3);
+		if (t + 1 < ntile) compute(1);
+		sstore(ra, 0);
+		__syncthreads();
+	}
+
+	// Epilogue, 32 rows at a time: each wave parks a 32x64 slice of its accumulators in its own
+	// 8 KB of LDS (the main loop's stages are free now); then lane l owns the 4 columns
+	// wn + 4 (l % 16) .. +3 and rows l / 16 + 4 p of the slice -- 16-byte loads and stores,
+	// per-column parameters in registers, each 16-column tile's partial maximum reduced over a
+	// lane quad with DPP.
+	int32_t* slab = (int32_t*)smem + wave * 32 * 64;
+	const int c4 = (lane & 15) * 4, rsub = lane >> 4;
+	const int col0 = n0 + wn + c4;  // first of this lane's 4 columns (with an epilogue N % 16 == 0)
+	const bool col_ok = col0 < g.N;
+	const Epilogue& e = g.epi;
+	const bool raw = gridDim.z > 1 || e.raw_out;
+	int32_t* raw_out = gridDim.z > 1 ? g.split_part + (size_t)split * g.M * g.N : e.raw_out;
+	int32_t f0[4], f1[4], f2[4];
+	int64_t bias[4];
+	int ldc = 0;
+	bool wide = false, has_bias = false;
+	int32_t* fout = nullptr;
+	int64_t* wout = nullptr;
+	uint32_t* mpart = nullptr;
+	if (!raw) {
+		int s2 = 0;
+		while (s2 + 1 < e.nseg && col0 >= e.seg[s2].n_end) ++s2;
+		const Segment sg = e.seg[s2];  // segment bounds are multiples of 16: one per lane
+		const int jc = (col_ok ? col0 : sg.n_begin) - sg.n_begin;
+		const int32_t* f = sg.fold + 3 * jc;
+#pragma unroll
+		for (int q = 0; q < 4; ++q) {
+			f0[q] = f[3 * q];
+			f1[q] = f[3 * q + 1];
+			f2[q] = f[3 * q + 2];
+			bias[q] = sg.bias ? sg.bias[jc + q] : 0;
+		}
+		has_bias = sg.bias != nullptr;
+		wide = sg.mode == kSegWide;
+		ldc = sg.ld_out;
+		fout = (int32_t*)sg.out + jc;
+		wout = (int64_t*)sg.out + jc;
+		mpart = sg.maxpart ? sg.maxpart + (size_t)(col0 >> 4) * kPartLd : nullptr;
+	}
+	__syncthreads();  // every wave is done reading the last LDS stage
+#pragma unroll
+	for (int mt = 0; mt < 4; ++mt) {
+		// 32x32 accumulator layout: lane holds column lane % 32 of the sub-tile, rows
+		// 8 * (v / 4) + 4 * (lane / 32) + v % 4
+#pragma unroll
+		for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+			for (int v = 0; v < 16; ++v)
+				slab[(8 * (v >> 2) + 4 * (lane >> 5) + (v & 3)) * 64 + nt * 32 + (lane & 31)] = acc[mt][nt][v];
+		__builtin_amdgcn_wave_barrier();
+		for (int p = 0; p < 8; ++p) {
+			const int r = 4 * p + rsub;
+			const int t = m0 + wm + mt * 32 + r;
+			const bool ok = t < g.M && col_ok;
+			const v4i a = *(const v4i*)&slab[r * 64 + c4];
+			if (raw) {
+				if (ok && col0 + 4 <= g.N) {
+					*(v4i*)&raw_out[(size_t)t * g.N + col0] = a;
+				} else if (ok) {
+					for (int q = 0; q < 4 && col0 + q < g.N; ++q) raw_out[(size_t)t * g.N + col0 + q] = a[q];
+				}
+				continue;
+			}
+			int64_t val[4];
+			uint32_t mx = 0;
+#pragma unroll
+			for (int q = 0; q < 4; ++q) {
+				val[q] = f0[q] != 0 ? (int64_t)a[q] : (int64_t)rdbpot32(srdhm(a[q], f1[q]), f2[q]);
+				if (has_bias && ok) {
+					int64_t term;
+					if (bias_term(bias[q], e.in_recip[t], e.in_scale[t].e, val[q], &term)) val[q] += term;
+					else set_status(e.status, e.tok[t].slot, e.layer, kBiasReconcileProductOutOfDomain);
+				}
+				const uint32_t m1 = sat_abs_u32(val[q]);
+				mx = m1 > mx ? m1 : mx;
+			}
+			if (ok) {
+				if (wide) {
+					int64_t* o = wout + (size_t)t * ldc;
+					*(longlong2*)o = make_longlong2(val[0], val[1]);
+					*(longlong2*)(o + 2) = make_longlong2(val[2], val[3]);
+				} else {
+					*(v4i*)(fout + (size_t)t * ldc) = v4i{sat_i32(val[0]), sat_i32(val[1]), sat_i32(val[2]), sat_i32(val[3])};
+				}
+			}
+			// quad max (quad_perm [1,0,3,2] then [2,3,0,1]): the 4 lanes of one 16-column tile
+			if (!ok || wide) mx = 0;
+			uint32_t w2 = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)mx, 0xb1, 0xf, 0xf, false);
+			mx = w2 > mx ? w2 : mx;
+			w2 = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)mx, 0x4e, 0xf, 0xf, false);
+			mx = w2 > mx ? w2 : mx;
+			if ((lane & 3) == 0 && t < g.M && col_ok && mpart && !wide) mpart[t] = mx;
+		}
+		__builtin_amdgcn_wave_barrier();
+	}
+}
+
+// ------------------------------------------------------------------------------------------
 // row kernels (one block per token)
 // ------------------------------------------------------------------------------------------
 
@@ -1210,8 +1430,32 @@ void gemm(const GemmArgs& g, hipStream_t s) {
 		}
 		return;
 	}
+	bool lora = false;
+	for (int i = 0; i < g.epi.nseg; ++i) lora = lora || g.epi.seg[i].lora_b;
+	if (!lora && !g.epi.argmax_key && g.K % kPBK == 0 && (g.epi.raw_out || g.N % 16 == 0)) {
+		// g.splits > 1 only as prefill_plan(M, N, K, true).splits, sized by the caller
+		const PrefillPlan p = prefill_plan(g.M, g.N, g.K, g.splits > 1);
+		const dim3 grid((g.N + kPBN - 1) / kPBN, (g.M + p.bm - 1) / p.bm, p.splits);
+		if (p.bm == 256) hipLaunchKernelGGL(k_gemm_mfma<256>, grid, dim3(256), 0, s, g, p.kspan);
+		else hipLaunchKernelGGL(k_gemm_mfma<128>, grid, dim3(128), 0, s, g, p.kspan);
+		return;
+	}
 	dim3 grid((g.N + kBN - 1) / kBN, (g.M + kBM - 1) / kBM);
 	hipLaunchKernelGGL(k_gemm_tiled, grid, dim3(kBlock), 0, s, g);
+}
+
+PrefillPlan prefill_plan(int M, int N, int K, bool split_ok) {
+	PrefillPlan p{};
+	p.bm = M >= 256 ? 256 : 128;
+	const int tiles = ((M + p.bm - 1) / p.bm) * ((N + kPBN - 1) / kPBN);
+	const int steps = (K + kPBK - 1) / kPBK;
+	p.splits = 1;
+	if (split_ok && tiles < kPrefillTargetBlocks)
+		p.splits = std::max(1, std::min({(kPrefillTargetBlocks + tiles - 1) / tiles, steps / 3, kMaxRawSplits}));
+	const int steps_per = (steps + p.splits - 1) / p.splits;
+	p.kspan = steps_per * kPBK;
+	p.splits = (K + p.kspan - 1) / p.kspan;
+	return p;
 }
 
 void embed(const int32_t* tokens, int M, const int8_t* embed_w, int H, int vocab, Scale site, int8_t* out_codes,

@@ -264,13 +264,17 @@ void run_gemm(sslm_model m, const GemmArgs& g, int cls) {
 // `allow`: the consumer's raw variant holds its row in registers without spilling.
 RawIn split_raw(sslm_model m, GemmArgs& g, bool allow) {
 	RawIn r{};
-	if (!allow || !m->raw_part || !sslm_launch::gemv_eligible(g.M, g.K)) return r;
-	const sslm_launch::GemvPlan p = sslm_launch::gemv_plan(g.M, g.N, g.K, true);
-	if (p.splits <= 1) return r;
-	g.splits = p.splits;
+	if (!allow || !m->raw_part) return r;
+	bool lora = false;
+	for (int i = 0; i < g.epi.nseg; ++i) lora = lora || g.epi.seg[i].lora_b;
+	int splits = 1;
+	if (sslm_launch::gemv_eligible(g.M, g.K)) splits = sslm_launch::gemv_plan(g.M, g.N, g.K, true).splits;
+	else if (!lora && g.K % 64 == 0) splits = sslm_launch::prefill_plan(g.M, g.N, g.K, true).splits;
+	if (splits <= 1) return r;
+	g.splits = splits;
 	g.split_part = m->raw_part;
 	r.part = m->raw_part;
-	r.splits = p.splits;
+	r.splits = splits;
 	r.ld = g.N;
 	r.epi = g.epi;
 	return r;
@@ -856,9 +860,14 @@ bool build_device_model(sslm_model m, std::string* err) {
 	{
 		const int shapes[4][2] = {{H + 2 * KVH, H}, {H, H}, {2 * I, H}, {H, I}};
 		size_t elems = 0;
-		for (auto& sh : shapes)
+		for (auto& sh : shapes) {
 			if (sslm_launch::gemv_eligible(64, sh[1]))
 				elems = std::max(elems, (size_t)sslm_launch::gemv_plan(64, sh[0], sh[1], true).splits * 64 * sh[0]);
+			for (int rows = 65; rows <= kMaxTokens; ++rows) {
+				const int sp = sslm_launch::prefill_plan(rows, sh[0], sh[1], true).splits;
+				if (sp > 1) elems = std::max(elems, (size_t)sp * rows * sh[0]);
+			}
+		}
 		m->raw_part = elems ? dalloc<int32_t>(elems, &own) : nullptr;
 	}
 	for (int i = 0; i < 3; ++i) m->lora_u[i] = dalloc<int8_t>((size_t)T * kMaxRank, &own);

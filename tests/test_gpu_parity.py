@@ -101,3 +101,20 @@ def test_batched_decode_matches_reference(name, hip_lib, ref_lib):
         assert h[0] == r[0], f"tokens differ: hip {h[0]} ref {r[0]}"
         for i in range(len(prompts)):
             assert np.array_equal(h[1][i], r[1][i]), f"KV of sequence {i} differs"
+
+
+@pytest.mark.parametrize("name,n", [("small", 150), ("medium", 90)])
+def test_long_prefill_chunk_matches_reference(name, n, hip_lib, ref_lib):
+    """Prefill chunks of more than 64 tokens run the tiled MFMA GEMM (split-K partial planes for
+    the narrow projections); every KV byte and the following tokens must still match."""
+    sm, art = synthetic(name)
+    rng = np.random.default_rng(31)
+    prompt = rng.integers(0, sm.config.vocab, size=n)
+    L = sm.config.layers
+    print(f"case long prefill {name} n={n}", flush=True)
+    r = _run(ref_lib, art, prompt, 3, L)
+    h = _run(hip_lib, art, prompt, 3, L)
+    assert h[0] == r[0]
+    assert np.array_equal(h[1], r[1]), "KV after prefill differs"
+    assert h[2] == r[2], f"tokens differ: hip {h[2]} ref {r[2]}"
+    assert np.array_equal(h[3], r[3]), "KV after decode differs"
