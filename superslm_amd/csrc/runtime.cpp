@@ -13,7 +13,10 @@
 
 #include <algorithm>
 #include <atomic>
+#include <deque>
+#include <functional>
 #include <memory>
+#include <map>
 #include <mutex>
 #include <set>
 #include <string>
@@ -28,6 +31,8 @@ using namespace sslm;
 namespace {
 
 constexpr int kMaxTokens = 512;      // tokens per launch sequence (prefill chunk / decode group)
+constexpr int kTracks = 4;           // concurrent token groups of one decode step
+constexpr int kTrackTokens = 128;    // tokens per launch on tracks 1..kTracks-1
 constexpr int kSlotCapacity = 1024;  // live sequences per model
 
 struct HipError {
@@ -104,6 +109,8 @@ struct ProfScope {
 	}
 };
 
+bool prof_enabled() { return g_prof.on; }
+
 void prof_collect() {
 	if (g_prof.pending.empty()) return;
 	for (auto& p : g_prof.pending) {
@@ -149,13 +156,34 @@ struct sslm_adapter_s {
 	std::atomic<int> live_refs{0};
 };
 
+// Scratch of one launch sequence: a stream and every per-token buffer the layer loop and the
+// head use.  Several tracks run independent token groups of one decode step concurrently.
+struct Track {
+	hipStream_t stream = nullptr;
+	int capacity = 0;  // tokens per launch
+	TokenInfo* tok;
+	int32_t *tok_ids, *ident, *slot_idx, *out_tokens;
+	int8_t *hid_chunk, *normed, *q_rot, *ctx, *attn_stream, *mlp_normed, *act, *final_codes;
+	Scale *hid_chunk_scale, *normed_scale, *q_scale, *ctx_scale, *attn_stream_scale, *mlp_scale, *act_scale,
+	    *final_scale;
+	int64_t *normed_recip, *mlp_recip, *kv_f, *attn_scratch;
+	int32_t *q_f, *ctx_f, *o_f, *gu_f, *down_f;
+	uint32_t *mx_q, *mx_ctx, *mx_o, *mx_gu, *mx_down;  // per (16-column tile, token) partial maxima
+	unsigned long long* argmax_key;                    // [token][tile], head tracks only
+	int32_t* raw_part;  // split-K partial planes, consumed by the next row kernel
+	int8_t* lora_u[3];
+	TokenInfo* lg_tok;    // head tracks: tokens of the joined final norm + head
+	int32_t* lg_slot;
+	hipEvent_t done = nullptr;
+	hipEvent_t fork = nullptr;
+};
+
 struct sslm_model_s {
 	Artifact art;
 	ModelConfig c;
 	int H, L, NH, NKV, D, I, V, KVH;
 	int64_t cap;
 	size_t block_bytes;
-	hipStream_t stream = nullptr;
 	std::vector<void*> owned;
 	std::vector<DevLayer> layers;
 	int8_t *embed, *head;
@@ -169,18 +197,8 @@ struct sslm_model_s {
 	unsigned long long* sat;  // [kSlotCapacity]
 	int32_t* status;        // [kSlotCapacity]
 	std::vector<int> free_slots;
-	// launch workspace (kMaxTokens rows)
-	TokenInfo* tok;
-	int32_t *tok_ids, *ident, *slot_idx, *out_tokens;
-	int8_t *hid_chunk, *normed, *q_rot, *ctx, *attn_stream, *mlp_normed, *act, *final_codes;
-	Scale *hid_chunk_scale, *normed_scale, *q_scale, *ctx_scale, *attn_stream_scale, *mlp_scale, *act_scale,
-	    *final_scale;
-	int64_t *normed_recip, *mlp_recip, *kv_f, *attn_scratch;
-	int32_t *q_f, *ctx_f, *o_f, *gu_f, *down_f;
-	uint32_t *mx_q, *mx_ctx, *mx_o, *mx_gu, *mx_down;  // per (16-column tile, token) partial maxima
-	unsigned long long* argmax_key;
-	int32_t* raw_part;  // decode GEMV split-K partial planes, consumed by the next row kernel
-	int8_t* lora_u[3];
+	std::vector<Track> tracks;  // tracks[0]: prefill and head; all: decode token groups
+	std::map<std::string, hipGraphExec_t> graphs;  // captured decode submissions by shape
 	int8_t* pool_dev = nullptr;  // KV pool of the launch sequence being recorded
 	std::atomic<int> live_refs{0};
 	std::mutex mu;  // serializes GPU submission on this model
@@ -225,15 +243,15 @@ std::set<sslm_seq_s*> g_live_seqs;
 // ------------------------------------------------------------------------------------------
 // launch helpers
 // ------------------------------------------------------------------------------------------
-GemmArgs gemm_args(sslm_model m, const int8_t* a, int M, int lda, const int8_t* w, int N, int K) {
+GemmArgs gemm_args(sslm_model m, Track& w, const int8_t* a, int M, int lda, const int8_t* wt, int N, int K) {
 	GemmArgs g{};
 	g.a = a;
-	g.w = w;
+	g.w = wt;
 	g.M = M;
 	g.N = N;
 	g.K = K;
 	g.lda = lda;
-	g.epi.tok = m->tok;
+	g.epi.tok = w.tok;
 	g.epi.status = m->status;
 	return g;
 }
@@ -251,20 +269,20 @@ Segment funnel_seg(int n0, int n1, int32_t* out, int ld, uint32_t* mx, const int
 	return s;
 }
 
-void run_gemm(sslm_model m, const GemmArgs& g, int cls) {
+void run_gemm(sslm_model m, Track& w, const GemmArgs& g, int cls) {
 	const int64_t out_bytes = g.epi.argmax_key ? 0 : (int64_t)g.M * g.N * 4;
-	ProfScope p(m->stream, cls, (int64_t)g.N * g.K + (int64_t)g.M * g.K + 12LL * g.N + out_bytes,
+	ProfScope p(w.stream, cls, (int64_t)g.N * g.K + (int64_t)g.M * g.K + 12LL * g.N + out_bytes,
 	            2LL * g.M * g.N * g.K);
-	sslm_launch::gemm(g, m->stream);
+	sslm_launch::gemm(g, w.stream);
 	ck(hipGetLastError());
 }
 
 // Decode projections whose GEMV splits K hand their raw partial planes to the next row kernel,
 // which applies the epilogue; call once g.epi is complete.  Returns a null RawIn otherwise.
 // `allow`: the consumer's raw variant holds its row in registers without spilling.
-RawIn split_raw(sslm_model m, GemmArgs& g, bool allow) {
+RawIn split_raw(sslm_model m, Track& w, GemmArgs& g, bool allow) {
 	RawIn r{};
-	if (!allow || !m->raw_part) return r;
+	if (!allow || !w.raw_part) return r;
 	bool lora = false;
 	for (int i = 0; i < g.epi.nseg; ++i) lora = lora || g.epi.seg[i].lora_b;
 	int splits = 1;
@@ -272,24 +290,24 @@ RawIn split_raw(sslm_model m, GemmArgs& g, bool allow) {
 	else if (!lora && g.K % 64 == 0) splits = sslm_launch::prefill_plan(g.M, g.N, g.K, true).splits;
 	if (splits <= 1) return r;
 	g.splits = splits;
-	g.split_part = m->raw_part;
-	r.part = m->raw_part;
+	g.split_part = w.raw_part;
+	r.part = w.raw_part;
 	r.splits = splits;
 	r.ld = g.N;
 	r.epi = g.epi;
 	return r;
 }
 
-void attach_lora(sslm_model m, sslm_adapter ad, int layer, int proj, Segment* seg, int slot_u) {
+void attach_lora(sslm_model m, Track& w, sslm_adapter ad, int layer, int proj, Segment* seg, int slot_u) {
 	if (!ad) return;
 	const AdapterProj& p = ad->proj[(size_t)layer * 7 + proj];
 	if (!p.a) return;
 	seg->lora_b = p.b;
 	seg->lora_dfold = p.dfold;
-	seg->lora_u = m->lora_u[slot_u];
+	seg->lora_u = w.lora_u[slot_u];
 }
 
-void run_lora_u(sslm_model m, sslm_adapter ad, int layer, const int* projs, int n, const int8_t* x, int M, int K) {
+void run_lora_u(sslm_model m, Track& w, sslm_adapter ad, int layer, const int* projs, int n, const int8_t* x, int M, int K) {
 	if (!ad) return;
 	sslm_launch::LoraUArgs a{};
 	a.M = M;
@@ -302,13 +320,13 @@ void run_lora_u(sslm_model m, sslm_adapter ad, int layer, const int* projs, int 
 		if (!p.a) continue;
 		a.a[cnt] = p.a;
 		a.ufold[cnt] = p.ufold;
-		a.u[cnt] = m->lora_u[i];
+		a.u[cnt] = w.lora_u[i];
 		++cnt;
 	}
 	if (!cnt) return;
 	a.nproj = cnt;
-	ProfScope ps(m->stream, kProfLora, (int64_t)cnt * ad->rank * K + (int64_t)M * K, 2LL * M * cnt * ad->rank * K);
-	sslm_launch::lora_u(a, m->stream);
+	ProfScope ps(w.stream, kProfLora, (int64_t)cnt * ad->rank * K + (int64_t)M * K, 2LL * M * cnt * ad->rank * K);
+	sslm_launch::lora_u(a, w.stream);
 	ck(hipGetLastError());
 }
 
@@ -321,14 +339,14 @@ struct StreamRef {
 };
 
 // Layers [l0, l1) for M tokens whose TokenInfo is already on the device.
-void run_layers(sslm_model m, int M, StreamRef st, int l0, int l1, sslm_adapter ad) {
+void run_layers(sslm_model m, Track& w, int M, StreamRef st, int l0, int l1, sslm_adapter ad) {
 	const int H = m->H, I = m->I, KVH = m->KVH;
-	hipStream_t s = m->stream;
+	hipStream_t s = w.stream;
 	{
 		ProfScope p(s, kProfRow, 0, 0);
 		sslm_launch::RowNormArgs a{st.codes, st.idx, H, m->layers[l0].attn_gain, m->layers[l0].attn_norm,
-		                           m->normed, m->normed_scale, m->normed_recip};
-		sslm_launch::rmsnorm(a, M, H, m->tok, m->status, l0, s);
+		                           w.normed, w.normed_scale, w.normed_recip};
+		sslm_launch::rmsnorm(a, M, H, w.tok, m->status, l0, s);
 		ck(hipGetLastError());
 	}
 	for (int l = l0; l < l1; ++l) {
@@ -337,35 +355,35 @@ void run_layers(sslm_model m, int M, StreamRef st, int l0, int l1, sslm_adapter 
 		// q | k | v projection (forward_sites.cpp:1699-1735)
 		{
 			const int pj[3] = {0, 1, 2};
-			run_lora_u(m, ad, l, pj, 3, m->normed, M, H);
-			GemmArgs g = gemm_args(m, m->normed, M, H, lw.w_qkv, H + 2 * KVH, H);
+			run_lora_u(m, w, ad, l, pj, 3, w.normed, M, H);
+			GemmArgs g = gemm_args(m, w, w.normed, M, H, lw.w_qkv, H + 2 * KVH, H);
 			g.epi.layer = l;
-			g.epi.in_recip = m->normed_recip;
-			g.epi.in_scale = m->normed_scale;
+			g.epi.in_recip = w.normed_recip;
+			g.epi.in_scale = w.normed_scale;
 			g.epi.rank = ad ? (int)ad->rank : 0;
 			g.epi.nseg = 3;
-			g.epi.seg[0] = funnel_seg(0, H, m->q_f, H, m->mx_q, lw.f_qkv, lw.b_q);
+			g.epi.seg[0] = funnel_seg(0, H, w.q_f, H, w.mx_q, lw.f_qkv, lw.b_q);
 			Segment sk{};
 			sk.n_begin = H;
 			sk.n_end = H + KVH;
 			sk.mode = kSegWide;
-			sk.out = m->kv_f;
+			sk.out = w.kv_f;
 			sk.ld_out = 2 * KVH;
 			sk.fold = lw.f_qkv + 3 * H;
 			sk.bias = lw.b_k;
 			Segment sv = sk;
 			sv.n_begin = H + KVH;
 			sv.n_end = H + 2 * KVH;
-			sv.out = m->kv_f + KVH;
+			sv.out = w.kv_f + KVH;
 			sv.fold = lw.f_qkv + 3 * (H + KVH);
 			sv.bias = lw.b_v;
 			g.epi.seg[1] = sk;
 			g.epi.seg[2] = sv;
-			attach_lora(m, ad, l, 0, &g.epi.seg[0], 0);
-			attach_lora(m, ad, l, 1, &g.epi.seg[1], 1);
-			attach_lora(m, ad, l, 2, &g.epi.seg[2], 2);
-			raw = split_raw(m, g, H <= 4096);
-			run_gemm(m, g, kProfGemm);
+			attach_lora(m, w, ad, l, 0, &g.epi.seg[0], 0);
+			attach_lora(m, w, ad, l, 1, &g.epi.seg[1], 1);
+			attach_lora(m, w, ad, l, 2, &g.epi.seg[2], 2);
+			raw = split_raw(m, w, g, H <= 4096);
+			run_gemm(m, w, g, kProfGemm);
 		}
 		{
 			sslm_launch::QkvPostArgs a{};
@@ -375,11 +393,11 @@ void run_layers(sslm_model m, int M, StreamRef st, int l0, int l1, sslm_adapter 
 			a.NKV = m->NKV;
 			a.D = m->D;
 			a.cap = m->cap;
-			a.tok = m->tok;
-			a.q_f = m->q_f;
-			a.q_maxpart = m->mx_q;
-			a.kv_f = m->kv_f;
-			a.in_scale = m->normed_scale;
+			a.tok = w.tok;
+			a.q_f = w.q_f;
+			a.q_maxpart = w.mx_q;
+			a.kv_f = w.kv_f;
+			a.in_scale = w.normed_scale;
 			a.q_site = lw.q;
 			a.r_t_k = lw.r_t_k;
 			a.e_t_k = lw.e_t_k;
@@ -389,8 +407,8 @@ void run_layers(sslm_model m, int M, StreamRef st, int l0, int l1, sslm_adapter 
 			a.rope_sin = m->rope_sin;
 			a.block_bytes = (int64_t)m->block_bytes;
 			a.layer = l;
-			a.q_rot = m->q_rot;
-			a.q_scale = m->q_scale;
+			a.q_rot = w.q_rot;
+			a.q_scale = w.q_scale;
 			a.sat = m->sat;
 			a.status = m->status;
 			a.kv_pool = m->pool_dev;
@@ -407,9 +425,9 @@ void run_layers(sslm_model m, int M, StreamRef st, int l0, int l1, sslm_adapter 
 			a.NKV = m->NKV;
 			a.D = m->D;
 			a.cap = m->cap;
-			a.tok = m->tok;
-			a.q_rot = m->q_rot;
-			a.q_scale = m->q_scale;
+			a.tok = w.tok;
+			a.q_rot = w.q_rot;
+			a.q_scale = w.q_scale;
 			a.khead_m = lw.khead_m;
 			a.khead_e = lw.khead_e;
 			a.ctx_fold = lw.ctx_fold;
@@ -419,9 +437,9 @@ void run_layers(sslm_model m, int M, StreamRef st, int l0, int l1, sslm_adapter 
 			a.ln2_q = m->ln2_q;
 			a.b_q = m->b_q;
 			a.ca_q = m->ca_q;
-			a.ctx_f = m->ctx_f;
-			a.ctx_maxpart = m->mx_ctx;
-			a.scratch = m->attn_scratch;
+			a.ctx_f = w.ctx_f;
+			a.ctx_maxpart = w.mx_ctx;
+			a.scratch = w.attn_scratch;
 			a.status = m->status;
 			ProfScope p(s, kProfAttn, 0, 0);
 			sslm_launch::attention(a, s);
@@ -431,15 +449,15 @@ void run_layers(sslm_model m, int M, StreamRef st, int l0, int l1, sslm_adapter 
 			sslm_launch::FunnelArgs a{};
 			a.M = M;
 			a.N = H;
-			a.tok = m->tok;
-			a.f = m->ctx_f;
+			a.tok = w.tok;
+			a.f = w.ctx_f;
 			a.ld_f = H;
-			a.maxpart = m->mx_ctx;
+			a.maxpart = w.mx_ctx;
 			a.ntiles = m->NH;
 			a.incoming = nullptr;
 			a.site = lw.ctx;
-			a.out = m->ctx;
-			a.out_scale = m->ctx_scale;
+			a.out = w.ctx;
+			a.out_scale = w.ctx_scale;
 			a.layer = l;
 			a.status = m->status;
 			ProfScope p(s, kProfRow, 0, 0);
@@ -448,37 +466,37 @@ void run_layers(sslm_model m, int M, StreamRef st, int l0, int l1, sslm_adapter 
 		}
 		{  // o_proj (forward_sites.cpp:1907-1914)
 			const int pj[1] = {3};
-			run_lora_u(m, ad, l, pj, 1, m->ctx, M, H);
-			GemmArgs g = gemm_args(m, m->ctx, M, H, lw.w_o, H, H);
+			run_lora_u(m, w, ad, l, pj, 1, w.ctx, M, H);
+			GemmArgs g = gemm_args(m, w, w.ctx, M, H, lw.w_o, H, H);
 			g.epi.layer = l;
 			g.epi.rank = ad ? (int)ad->rank : 0;
 			g.epi.nseg = 1;
-			g.epi.seg[0] = funnel_seg(0, H, m->o_f, H, m->mx_o, lw.f_o, nullptr);
-			attach_lora(m, ad, l, 3, &g.epi.seg[0], 0);
-			raw = split_raw(m, g, H <= 6144);
-			run_gemm(m, g, kProfGemm);
+			g.epi.seg[0] = funnel_seg(0, H, w.o_f, H, w.mx_o, lw.f_o, nullptr);
+			attach_lora(m, w, ad, l, 3, &g.epi.seg[0], 0);
+			raw = split_raw(m, w, g, H <= 6144);
+			run_gemm(m, w, g, kProfGemm);
 		}
 		{  // attn residual -> mlp norm (forward_sites.cpp:1923-1936)
 			sslm_launch::ResidualArgs a{};
 			a.M = M;
 			a.H = H;
-			a.tok = m->tok;
-			a.branch_f = m->o_f;
-			a.branch_maxpart = m->mx_o;
-			a.branch_in = m->ctx_scale;
+			a.tok = w.tok;
+			a.branch_f = w.o_f;
+			a.branch_maxpart = w.mx_o;
+			a.branch_in = w.ctx_scale;
 			a.branch_site = lw.o;
 			a.stream = st.codes;
 			a.stream_idx = st.idx;
 			a.stream_scale = st.scale;
 			a.res_site = lw.attn_res;
-			a.out_stream = m->attn_stream;
-			a.out_idx = m->ident;
-			a.out_stream_scale = m->attn_stream_scale;
+			a.out_stream = w.attn_stream;
+			a.out_idx = w.ident;
+			a.out_stream_scale = w.attn_stream_scale;
 			a.gain = lw.mlp_gain;
 			a.norm_site = lw.mlp_norm;
-			a.norm_out = m->mlp_normed;
-			a.norm_scale = m->mlp_scale;
-			a.norm_recip = m->mlp_recip;
+			a.norm_out = w.mlp_normed;
+			a.norm_scale = w.mlp_scale;
+			a.norm_recip = w.mlp_recip;
 			a.layer = l;
 			a.status = m->status;
 			a.raw = raw;
@@ -488,32 +506,32 @@ void run_layers(sslm_model m, int M, StreamRef st, int l0, int l1, sslm_adapter 
 		}
 		{  // gate | up (forward_sites.cpp:1938-1955)
 			const int pj[2] = {4, 5};
-			run_lora_u(m, ad, l, pj, 2, m->mlp_normed, M, H);
-			GemmArgs g = gemm_args(m, m->mlp_normed, M, H, lw.w_gu, 2 * I, H);
+			run_lora_u(m, w, ad, l, pj, 2, w.mlp_normed, M, H);
+			GemmArgs g = gemm_args(m, w, w.mlp_normed, M, H, lw.w_gu, 2 * I, H);
 			g.epi.layer = l;
 			g.epi.rank = ad ? (int)ad->rank : 0;
 			g.epi.nseg = 2;
-			g.epi.seg[0] = funnel_seg(0, I, m->gu_f, 2 * I, m->mx_gu, lw.f_gu, nullptr);
-			g.epi.seg[1] = funnel_seg(I, 2 * I, m->gu_f + I, 2 * I, m->mx_gu, lw.f_gu + 3 * I, nullptr);
-			attach_lora(m, ad, l, 4, &g.epi.seg[0], 0);
-			attach_lora(m, ad, l, 5, &g.epi.seg[1], 1);
-			raw = split_raw(m, g, I <= 4096);
-			run_gemm(m, g, kProfGemm);
+			g.epi.seg[0] = funnel_seg(0, I, w.gu_f, 2 * I, w.mx_gu, lw.f_gu, nullptr);
+			g.epi.seg[1] = funnel_seg(I, 2 * I, w.gu_f + I, 2 * I, w.mx_gu, lw.f_gu + 3 * I, nullptr);
+			attach_lora(m, w, ad, l, 4, &g.epi.seg[0], 0);
+			attach_lora(m, w, ad, l, 5, &g.epi.seg[1], 1);
+			raw = split_raw(m, w, g, I <= 4096);
+			run_gemm(m, w, g, kProfGemm);
 		}
 		{
 			sslm_launch::ActArgs a{};
 			a.M = M;
 			a.I = I;
-			a.tok = m->tok;
-			a.gu_f = m->gu_f;
-			a.gu_maxpart = m->mx_gu;
-			a.in_scale = m->mlp_scale;
+			a.tok = w.tok;
+			a.gu_f = w.gu_f;
+			a.gu_maxpart = w.mx_gu;
+			a.in_scale = w.mlp_scale;
 			a.gate_site = lw.gate;
 			a.up_site = lw.up;
 			a.act_site = lw.act;
 			a.silu = m->silu;
-			a.act = m->act;
-			a.act_scale = m->act_scale;
+			a.act = w.act;
+			a.act_scale = w.act_scale;
 			a.layer = l;
 			a.status = m->status;
 			a.raw = raw;
@@ -523,28 +541,28 @@ void run_layers(sslm_model m, int M, StreamRef st, int l0, int l1, sslm_adapter 
 		}
 		{  // down_proj (forward_sites.cpp:1969-1977)
 			const int pj[1] = {6};
-			run_lora_u(m, ad, l, pj, 1, m->act, M, I);
-			GemmArgs g = gemm_args(m, m->act, M, I, lw.w_down, H, I);
+			run_lora_u(m, w, ad, l, pj, 1, w.act, M, I);
+			GemmArgs g = gemm_args(m, w, w.act, M, I, lw.w_down, H, I);
 			g.epi.layer = l;
 			g.epi.rank = ad ? (int)ad->rank : 0;
 			g.epi.nseg = 1;
-			g.epi.seg[0] = funnel_seg(0, H, m->down_f, H, m->mx_down, lw.f_down, nullptr);
-			attach_lora(m, ad, l, 6, &g.epi.seg[0], 0);
-			raw = split_raw(m, g, H <= 6144);
-			run_gemm(m, g, kProfGemm);
+			g.epi.seg[0] = funnel_seg(0, H, w.down_f, H, w.mx_down, lw.f_down, nullptr);
+			attach_lora(m, w, ad, l, 6, &g.epi.seg[0], 0);
+			raw = split_raw(m, w, g, H <= 6144);
+			run_gemm(m, w, g, kProfGemm);
 		}
 		{  // mlp residual -> commit -> next layer's attn norm (forward_sites.cpp:1982-2009)
 			sslm_launch::ResidualArgs a{};
 			a.M = M;
 			a.H = H;
-			a.tok = m->tok;
-			a.branch_f = m->down_f;
-			a.branch_maxpart = m->mx_down;
-			a.branch_in = m->act_scale;
+			a.tok = w.tok;
+			a.branch_f = w.down_f;
+			a.branch_maxpart = w.mx_down;
+			a.branch_in = w.act_scale;
 			a.branch_site = lw.down;
-			a.stream = m->attn_stream;
-			a.stream_idx = m->ident;
-			a.stream_scale = m->attn_stream_scale;
+			a.stream = w.attn_stream;
+			a.stream_idx = w.ident;
+			a.stream_scale = w.attn_stream_scale;
 			a.res_site = lw.mlp_res;
 			a.out_stream = st.codes;
 			a.out_idx = st.idx;
@@ -552,9 +570,9 @@ void run_layers(sslm_model m, int M, StreamRef st, int l0, int l1, sslm_adapter 
 			if (l + 1 < l1) {
 				a.gain = m->layers[l + 1].attn_gain;
 				a.norm_site = m->layers[l + 1].attn_norm;
-				a.norm_out = m->normed;
-				a.norm_scale = m->normed_scale;
-				a.norm_recip = m->normed_recip;
+				a.norm_out = w.normed;
+				a.norm_scale = w.normed_scale;
+				a.norm_recip = w.normed_recip;
 			}
 			a.layer = l;
 			a.status = m->status;
@@ -569,21 +587,22 @@ void run_layers(sslm_model m, int M, StreamRef st, int l0, int l1, sslm_adapter 
 
 // final norm + LM head + lowest-index argmax for M tokens whose stream rows are st.idx
 // (src/sslm_abi.cpp:2280-2289, forward_sites.cpp:2412-2441)
-void run_logits(sslm_model m, int M, StreamRef st) {
-	hipStream_t s = m->stream;
+void run_logits(sslm_model m, Track& w, int M, StreamRef st, const TokenInfo* tok) {
+	hipStream_t s = w.stream;
 	{
 		ProfScope p(s, kProfRow, 0, 0);
-		sslm_launch::RowNormArgs a{st.codes, st.idx, m->H, m->final_gain, m->final_site, m->final_codes,
-		                           m->final_scale, nullptr};
-		sslm_launch::rmsnorm(a, M, m->H, m->tok, m->status, m->L, s);
+		sslm_launch::RowNormArgs a{st.codes, st.idx, m->H, m->final_gain, m->final_site, w.final_codes,
+		                           w.final_scale, nullptr};
+		sslm_launch::rmsnorm(a, M, m->H, tok, m->status, m->L, s);
 		ck(hipGetLastError());
 	}
-	GemmArgs g = gemm_args(m, m->final_codes, M, m->H, m->head, m->V, m->H);
-	g.epi.argmax_key = m->argmax_key;
+	GemmArgs g = gemm_args(m, w, w.final_codes, M, m->H, m->head, m->V, m->H);
+	g.epi.tok = tok;
+	g.epi.argmax_key = w.argmax_key;
 	g.epi.key_ld = (m->V + 15) / 16;
 	g.epi.layer = m->L;
-	run_gemm(m, g, kProfHead);
-	sslm_launch::argmax_finalize(m->argmax_key, (m->V + 15) / 16, M, m->out_tokens, s);
+	run_gemm(m, w, g, kProfHead);
+	sslm_launch::argmax_finalize(w.argmax_key, (m->V + 15) / 16, M, w.out_tokens, s);
 	ck(hipGetLastError());
 }
 
@@ -641,6 +660,67 @@ void append_le(std::vector<T>* out, const TensorView& t) {
 }
 
 // Upload one model (layer_marshal.h:141-330 naming; src/sslm_abi.cpp:609-676 embed/head/final).
+void alloc_track(sslm_model m, Track& w, int T, bool head) {
+	auto& own = m->owned;
+	const int H = m->H, I = m->I, KVH = m->KVH;
+	w.capacity = T;
+	w.tok = dalloc<TokenInfo>(T, &own);
+	w.tok_ids = dalloc<int32_t>(T, &own);
+	w.ident = dalloc<int32_t>(T, &own);
+	{
+		std::vector<int32_t> id(T);
+		for (int i = 0; i < T; ++i) id[i] = i;
+		ck(hipMemcpy(w.ident, id.data(), T * 4, hipMemcpyHostToDevice));
+	}
+	w.slot_idx = dalloc<int32_t>(T, &own);
+	w.out_tokens = dalloc<int32_t>(T, &own);
+	w.hid_chunk = dalloc<int8_t>((size_t)T * H, &own);
+	w.normed = dalloc<int8_t>((size_t)T * H, &own);
+	w.q_rot = dalloc<int8_t>((size_t)T * H, &own);
+	w.ctx = dalloc<int8_t>((size_t)T * H, &own);
+	w.attn_stream = dalloc<int8_t>((size_t)T * H, &own);
+	w.mlp_normed = dalloc<int8_t>((size_t)T * H, &own);
+	w.act = dalloc<int8_t>((size_t)T * I, &own);
+	w.final_codes = dalloc<int8_t>((size_t)T * H, &own);
+	for (Scale** sp : {&w.hid_chunk_scale, &w.normed_scale, &w.q_scale, &w.ctx_scale, &w.attn_stream_scale,
+	                   &w.mlp_scale, &w.act_scale, &w.final_scale})
+		*sp = dalloc<Scale>(T, &own);
+	w.normed_recip = dalloc<int64_t>(T, &own);
+	w.mlp_recip = dalloc<int64_t>(T, &own);
+	w.kv_f = dalloc<int64_t>((size_t)T * 2 * KVH, &own);
+	w.q_f = dalloc<int32_t>((size_t)T * H, &own);
+	w.ctx_f = dalloc<int32_t>((size_t)T * H, &own);
+	w.o_f = dalloc<int32_t>((size_t)T * H, &own);
+	w.gu_f = dalloc<int32_t>((size_t)T * 2 * I, &own);
+	w.down_f = dalloc<int32_t>((size_t)T * H, &own);
+	w.mx_q = dalloc<uint32_t>((size_t)(H + 2 * KVH) / 16 * kPartLd, &own);
+	w.mx_ctx = dalloc<uint32_t>((size_t)m->NH * kPartLd, &own);
+	w.mx_o = dalloc<uint32_t>((size_t)H / 16 * kPartLd, &own);
+	w.mx_gu = dalloc<uint32_t>((size_t)2 * I / 16 * kPartLd, &own);
+	w.mx_down = dalloc<uint32_t>((size_t)H / 16 * kPartLd, &own);
+	w.argmax_key = head ? dalloc<unsigned long long>((size_t)(m->V + 15) / 16 * T, &own) : nullptr;
+	{
+		const int shapes[4][2] = {{H + 2 * KVH, H}, {H, H}, {2 * I, H}, {H, I}};
+		size_t elems = 0;
+		for (auto& sh : shapes) {
+			for (int rows = 1; rows <= T; ++rows) {
+				int sp = 1;
+				if (sslm_launch::gemv_eligible(rows, sh[1])) sp = sslm_launch::gemv_plan(rows, sh[0], sh[1], true).splits;
+				else if (sh[1] % 64 == 0) sp = sslm_launch::prefill_plan(rows, sh[0], sh[1], true).splits;
+				if (sp > 1) elems = std::max(elems, (size_t)sp * rows * sh[0]);
+			}
+		}
+		w.raw_part = elems ? dalloc<int32_t>(elems, &own) : nullptr;
+	}
+	for (int i = 0; i < 3; ++i) w.lora_u[i] = dalloc<int8_t>((size_t)T * kMaxRank, &own);
+	w.attn_scratch = sslm_launch::attention_in_lds(m->cap) ? nullptr : dalloc<int64_t>((size_t)T * m->NH * m->cap, &own);
+	w.lg_tok = head ? dalloc<TokenInfo>(T, &own) : nullptr;
+	w.lg_slot = head ? dalloc<int32_t>(T, &own) : nullptr;
+	ck(hipStreamCreate(&w.stream));
+	ck(hipEventCreateWithFlags(&w.done, hipEventDisableTiming));
+	ck(hipEventCreateWithFlags(&w.fork, hipEventDisableTiming));
+}
+
 bool build_device_model(sslm_model m, std::string* err) {
 	const Artifact& A = m->art;
 	const ModelConfig& c = A.config;
@@ -820,80 +900,37 @@ bool build_device_model(sslm_model m, std::string* err) {
 	m->sat = dalloc<unsigned long long>(kSlotCapacity, &own);
 	m->status = dalloc<int32_t>(kSlotCapacity, &own);
 	for (int i = kSlotCapacity - 1; i >= 0; --i) m->free_slots.push_back(i);
-	// workspace
-	const int T = kMaxTokens;
-	m->tok = dalloc<TokenInfo>(T, &own);
-	m->tok_ids = dalloc<int32_t>(T, &own);
-	m->ident = dalloc<int32_t>(T, &own);
-	{
-		std::vector<int32_t> id(T);
-		for (int i = 0; i < T; ++i) id[i] = i;
-		ck(hipMemcpy(m->ident, id.data(), T * 4, hipMemcpyHostToDevice));
-	}
-	m->slot_idx = dalloc<int32_t>(T, &own);
-	m->out_tokens = dalloc<int32_t>(T, &own);
-	m->hid_chunk = dalloc<int8_t>((size_t)T * H, &own);
-	m->normed = dalloc<int8_t>((size_t)T * H, &own);
-	m->q_rot = dalloc<int8_t>((size_t)T * H, &own);
-	m->ctx = dalloc<int8_t>((size_t)T * H, &own);
-	m->attn_stream = dalloc<int8_t>((size_t)T * H, &own);
-	m->mlp_normed = dalloc<int8_t>((size_t)T * H, &own);
-	m->act = dalloc<int8_t>((size_t)T * I, &own);
-	m->final_codes = dalloc<int8_t>((size_t)T * H, &own);
-	for (Scale** sp : {&m->hid_chunk_scale, &m->normed_scale, &m->q_scale, &m->ctx_scale, &m->attn_stream_scale,
-	                   &m->mlp_scale, &m->act_scale, &m->final_scale})
-		*sp = dalloc<Scale>(T, &own);
-	m->normed_recip = dalloc<int64_t>(T, &own);
-	m->mlp_recip = dalloc<int64_t>(T, &own);
-	m->kv_f = dalloc<int64_t>((size_t)T * 2 * KVH, &own);
-	m->q_f = dalloc<int32_t>((size_t)T * H, &own);
-	m->ctx_f = dalloc<int32_t>((size_t)T * H, &own);
-	m->o_f = dalloc<int32_t>((size_t)T * H, &own);
-	m->gu_f = dalloc<int32_t>((size_t)T * 2 * I, &own);
-	m->down_f = dalloc<int32_t>((size_t)T * H, &own);
-	m->mx_q = dalloc<uint32_t>((size_t)(H + 2 * KVH) / 16 * kPartLd, &own);
-	m->mx_ctx = dalloc<uint32_t>((size_t)m->NH * kPartLd, &own);
-	m->mx_o = dalloc<uint32_t>((size_t)H / 16 * kPartLd, &own);
-	m->mx_gu = dalloc<uint32_t>((size_t)2 * I / 16 * kPartLd, &own);
-	m->mx_down = dalloc<uint32_t>((size_t)H / 16 * kPartLd, &own);
-	m->argmax_key = dalloc<unsigned long long>((size_t)(m->V + 15) / 16 * kPartLd, &own);
-	{
-		const int shapes[4][2] = {{H + 2 * KVH, H}, {H, H}, {2 * I, H}, {H, I}};
-		size_t elems = 0;
-		for (auto& sh : shapes) {
-			if (sslm_launch::gemv_eligible(64, sh[1]))
-				elems = std::max(elems, (size_t)sslm_launch::gemv_plan(64, sh[0], sh[1], true).splits * 64 * sh[0]);
-			for (int rows = 65; rows <= kMaxTokens; ++rows) {
-				const int sp = sslm_launch::prefill_plan(rows, sh[0], sh[1], true).splits;
-				if (sp > 1) elems = std::max(elems, (size_t)sp * rows * sh[0]);
-			}
-		}
-		m->raw_part = elems ? dalloc<int32_t>(elems, &own) : nullptr;
-	}
-	for (int i = 0; i < 3; ++i) m->lora_u[i] = dalloc<int8_t>((size_t)T * kMaxRank, &own);
-	if (!sslm_launch::attention_in_lds(m->cap))
-		m->attn_scratch = dalloc<int64_t>((size_t)T * m->NH * m->cap, &own);
-	else
-		m->attn_scratch = nullptr;
-	ck(hipStreamCreate(&m->stream));
+	// tracks: track 0 carries prefill chunks and the LM head; the others run extra token groups
+	// of a decode step concurrently
+	m->tracks.resize(kTracks);
+	for (int i = 0; i < kTracks; ++i) alloc_track(m, m->tracks[i], i == 0 ? kMaxTokens : kTrackTokens, i == 0);
 	return true;
 }
 
 void free_model(sslm_model m) {
-	if (m->stream) (void)hipStreamSynchronize(m->stream);
+	for (Track& w : m->tracks)
+		if (w.stream) (void)hipStreamSynchronize(w.stream);
 	for (void* p : m->owned) (void)hipFree(p);
 	m->owned.clear();
-	if (m->stream) (void)hipStreamDestroy(m->stream);
-	m->stream = nullptr;
+	for (Track& w : m->tracks) {
+		if (w.stream) (void)hipStreamDestroy(w.stream);
+		if (w.done) (void)hipEventDestroy(w.done);
+		if (w.fork) (void)hipEventDestroy(w.fork);
+		w.stream = nullptr;
+		w.done = nullptr;
+		w.fork = nullptr;
+	}
+	for (auto& kv : m->graphs) (void)hipGraphExecDestroy(kv.second);
+	m->graphs.clear();
 }
-
 // Upload the TokenInfo of one launch sequence.
-void put_tokens(sslm_model m, const std::vector<TokenInfo>& ti) {
-	ck(hipMemcpyAsync(m->tok, ti.data(), ti.size() * sizeof(TokenInfo), hipMemcpyHostToDevice, m->stream));
+void put_tokens(Track& w, const std::vector<TokenInfo>& ti) {
+	ck(hipMemcpyAsync(w.tok, ti.data(), ti.size() * sizeof(TokenInfo), hipMemcpyHostToDevice, w.stream));
 }
 
 // prefill of `n` admitted tokens (PrefillWholeTokensImpl, src/sslm_abi.cpp:1481-1535)
 sslm_status prefill_tokens(sslm_model m, sslm_seq s, const int32_t* tokens, int n) {
+	Track& w = m->tracks[0];
 	m->pool_dev = s->pool->dev;
 	const int H = m->H;
 	int done = 0;
@@ -901,33 +938,33 @@ sslm_status prefill_tokens(sslm_model m, sslm_seq s, const int32_t* tokens, int 
 		const int T = std::min(kMaxTokens, n - done);
 		std::vector<TokenInfo> ti(T);
 		for (int t = 0; t < T; ++t) ti[t] = TokenInfo{s->context_length + done + t, s->slot, (int32_t)s->block};
-		put_tokens(m, ti);
-		ck(hipMemcpyAsync(m->tok_ids, tokens + done, T * 4, hipMemcpyHostToDevice, m->stream));
+		put_tokens(w, ti);
+		ck(hipMemcpyAsync(w.tok_ids, tokens + done, T * 4, hipMemcpyHostToDevice, w.stream));
 		{
-			ProfScope p(m->stream, kProfRow, 0, 0);
-			sslm_launch::embed(m->tok_ids, T, m->embed, H, m->V, m->embed_site, m->hid_chunk, m->ident,
-			                   m->hid_chunk_scale, m->ident, m->tok, m->status, m->stream);
+			ProfScope p(w.stream, kProfRow, 0, 0);
+			sslm_launch::embed(w.tok_ids, T, m->embed, H, m->V, m->embed_site, w.hid_chunk, w.ident,
+			                   w.hid_chunk_scale, w.ident, w.tok, m->status, w.stream);
 			ck(hipGetLastError());
 		}
-		run_layers(m, T, StreamRef{m->hid_chunk, m->hid_chunk_scale, m->ident}, 0, m->L, s->adapter);
+		run_layers(m, w, T, StreamRef{w.hid_chunk, w.hid_chunk_scale, w.ident}, 0, m->L, s->adapter);
 		int32_t word = 0;
-		ck(hipMemcpyAsync(&word, m->status + s->slot, 4, hipMemcpyDeviceToHost, m->stream));
-		ck(hipStreamSynchronize(m->stream));
+		ck(hipMemcpyAsync(&word, m->status + s->slot, 4, hipMemcpyDeviceToHost, w.stream));
+		ck(hipStreamSynchronize(w.stream));
 		prof_collect();
 		if (word != 0) {
 			ck(hipMemset(m->status + s->slot, 0, 4));
 			return map_forward_status(word);
 		}
 		// the chunk's last row becomes the sequence's stream state
-		ck(hipMemcpyAsync(m->stream_codes + (size_t)s->slot * H, m->hid_chunk + (size_t)(T - 1) * H, H,
-		                  hipMemcpyDeviceToDevice, m->stream));
-		ck(hipMemcpyAsync(m->stream_scale + s->slot, m->hid_chunk_scale + (T - 1), sizeof(Scale),
-		                  hipMemcpyDeviceToDevice, m->stream));
+		ck(hipMemcpyAsync(m->stream_codes + (size_t)s->slot * H, w.hid_chunk + (size_t)(T - 1) * H, H,
+		                  hipMemcpyDeviceToDevice, w.stream));
+		ck(hipMemcpyAsync(m->stream_scale + s->slot, w.hid_chunk_scale + (T - 1), sizeof(Scale),
+		                  hipMemcpyDeviceToDevice, w.stream));
 		s->context_length += T;
 		s->layer_index = 0;
 		done += T;
 	}
-	ck(hipStreamSynchronize(m->stream));
+	ck(hipStreamSynchronize(w.stream));
 	return SSLM_OK;
 }
 
@@ -1016,7 +1053,7 @@ sslm_status sslm_kv_pool_create(sslm_model model, void* buf, size_t buf_size, ui
 sslm_status sslm_kv_pool_destroy(sslm_kv_pool pool) {
 	if (!pool) return SSLM_INVALID_ARGUMENT;
 	if (pool->live_refs.load() != 0) return SSLM_POOL_HAS_LIVE_HANDLES;
-	(void)hipStreamSynchronize(pool->model->stream);
+	(void)hipStreamSynchronize(pool->model->tracks[0].stream);
 	(void)hipFree(pool->dev);
 	pool->model->live_refs--;
 	delete pool;
@@ -1075,12 +1112,12 @@ sslm_status sslm_seq_create(sslm_model model, sslm_kv_pool* pool, sslm_seq* out)
 		}
 		const int slot = model->free_slots.back();
 		model->free_slots.pop_back();
-		ck(hipMemsetAsync(p->dev + (size_t)block * p->block_size, 0, p->block_size, model->stream));
-		ck(hipMemsetAsync(model->stream_codes + (size_t)slot * model->H, 0, model->H, model->stream));
-		ck(hipMemsetAsync(model->stream_scale + slot, 0, sizeof(Scale), model->stream));
-		ck(hipMemsetAsync(model->sat + slot, 0, 8, model->stream));
-		ck(hipMemsetAsync(model->status + slot, 0, 4, model->stream));
-		ck(hipStreamSynchronize(model->stream));
+		ck(hipMemsetAsync(p->dev + (size_t)block * p->block_size, 0, p->block_size, model->tracks[0].stream));
+		ck(hipMemsetAsync(model->stream_codes + (size_t)slot * model->H, 0, model->H, model->tracks[0].stream));
+		ck(hipMemsetAsync(model->stream_scale + slot, 0, sizeof(Scale), model->tracks[0].stream));
+		ck(hipMemsetAsync(model->sat + slot, 0, 8, model->tracks[0].stream));
+		ck(hipMemsetAsync(model->status + slot, 0, 4, model->tracks[0].stream));
+		ck(hipStreamSynchronize(model->tracks[0].stream));
 		sslm_seq_s* s = new sslm_seq_s();
 		s->model = model;
 		s->pool = p;
@@ -1125,11 +1162,11 @@ sslm_status sslm_seq_reset(sslm_seq seq) {
 	return guarded([&]() -> sslm_status {
 		std::lock_guard<std::mutex> lk(m->mu);
 		ck(hipMemsetAsync(seq->pool->dev + (size_t)seq->block * seq->pool->block_size, 0, seq->pool->block_size,
-		                  m->stream));
-		ck(hipMemsetAsync(m->stream_codes + (size_t)seq->slot * m->H, 0, m->H, m->stream));
-		ck(hipMemsetAsync(m->stream_scale + seq->slot, 0, sizeof(Scale), m->stream));
-		ck(hipMemsetAsync(m->sat + seq->slot, 0, 8, m->stream));
-		ck(hipStreamSynchronize(m->stream));
+		                  m->tracks[0].stream));
+		ck(hipMemsetAsync(m->stream_codes + (size_t)seq->slot * m->H, 0, m->H, m->tracks[0].stream));
+		ck(hipMemsetAsync(m->stream_scale + seq->slot, 0, sizeof(Scale), m->tracks[0].stream));
+		ck(hipMemsetAsync(m->sat + seq->slot, 0, 8, m->tracks[0].stream));
+		ck(hipStreamSynchronize(m->tracks[0].stream));
 		seq->context_length = 0;
 		seq->layer_index = 0;
 		seq->current_token = -1;
@@ -1175,62 +1212,70 @@ sslm_status sslm_prefill(sslm_model model, sslm_seq seq, const int32_t* tokens, 
 	});
 }
 
+// Decode tokens are independent, so a batch's layer work is dealt to up to kTracks streams as
+// token groups of at least track_min() tokens each: while one group runs its latency-bound row
+// kernels on a few CUs, another's GEMVs fill the rest of the chip.  Everything -- embeds,
+// layers, the joined LM head and the status read-back -- is one submission with one host sync.
+bool graphs_enabled() {
+	static const bool v = [] {
+		const char* e = getenv("SSLM_HIP_GRAPHS");
+		return !(e && atoi(e) == 0);
+	}();
+	return v;
+}
+constexpr size_t kGraphCache = 64;
+
+int track_limit() {
+	static const int v = [] {
+		const char* e = getenv("SSLM_HIP_TRACKS");
+		const int x = e ? atoi(e) : kTracks;
+		return std::max(1, std::min(kTracks, x));
+	}();
+	return v;
+}
+int track_min() {
+	static const int v = [] {
+		const char* e = getenv("SSLM_HIP_TRACK_MIN_TOKENS");
+		return std::max(1, e ? atoi(e) : 4);
+	}();
+	return v;
+}
+
 static sslm_status decode_batch(sslm_model m, sslm_seq* seqs, int32_t n, uint32_t budget, int32_t* out_tokens,
                                 bool* stop_cap) {
 	// Partition: sequences needing layers, grouped by their current layer; sequences needing logits.
 	std::vector<int> need_logits;
 	std::vector<std::pair<uint32_t, std::vector<int>>> groups;
-	std::vector<int> embed_list;
 	for (int i = 0; i < n; ++i) {
 		sslm_seq s = seqs[i];
 		if (s->ready_for_logits) {
 			need_logits.push_back(i);
 			continue;
 		}
-		if (s->layer_index == 0) {
-			if (s->context_length >= m->cap) {  // src/sslm_abi.cpp:2233-2236
-				*stop_cap = true;
-				out_tokens[i] = -1;
-				n = i;
-				break;
-			}
-			embed_list.push_back(i);
+		if (s->layer_index == 0 && s->context_length >= m->cap) {  // src/sslm_abi.cpp:2233-2236
+			*stop_cap = true;
+			out_tokens[i] = -1;
+			n = i;
+			break;
 		}
 		auto it = std::find_if(groups.begin(), groups.end(), [&](auto& g) { return g.first == s->layer_index; });
 		if (it == groups.end()) groups.push_back({s->layer_index, {i}});
 		else it->second.push_back(i);
 	}
-	// drop group members past a cap stop
-	for (auto& g : groups) g.second.erase(std::remove_if(g.second.begin(), g.second.end(), [&](int i) { return i >= n; }), g.second.end());
-	need_logits.erase(std::remove_if(need_logits.begin(), need_logits.end(), [&](int i) { return i >= n; }), need_logits.end());
-	embed_list.erase(std::remove_if(embed_list.begin(), embed_list.end(), [&](int i) { return i >= n; }), embed_list.end());
+	need_logits.erase(std::remove_if(need_logits.begin(), need_logits.end(), [&](int i) { return i >= n; }),
+	                  need_logits.end());
 
-	// embeds (src/sslm_abi.cpp:2237-2249)
-	for (size_t b = 0; b < embed_list.size(); b += kMaxTokens) {
-		const int M = (int)std::min(embed_list.size() - b, (size_t)kMaxTokens);
-		std::vector<TokenInfo> ti(M);
-		std::vector<int32_t> ids(M), slots(M);
-		for (int t = 0; t < M; ++t) {
-			sslm_seq s = seqs[embed_list[b + t]];
-			ti[t] = TokenInfo{s->context_length, s->slot, (int32_t)s->block};
-			ids[t] = s->current_token;
-			slots[t] = s->slot;
-		}
-		put_tokens(m, ti);
-		ck(hipMemcpyAsync(m->tok_ids, ids.data(), M * 4, hipMemcpyHostToDevice, m->stream));
-		ck(hipMemcpyAsync(m->slot_idx, slots.data(), M * 4, hipMemcpyHostToDevice, m->stream));
-		ProfScope p(m->stream, kProfRow, 0, 0);
-		sslm_launch::embed(m->tok_ids, M, m->embed, m->H, m->V, m->embed_site, m->stream_codes, m->slot_idx,
-		                   m->stream_scale, m->slot_idx, m->tok, m->status, m->stream);
-		ck(hipGetLastError());
-		ck(hipStreamSynchronize(m->stream));  // slot_idx and tok are reused below
-	}
-	// layers, per group and per adapter
+	// launch units: (layer range, adapter, tokens), at most kTrackTokens tokens each
+	struct Unit {
+		uint32_t l0, l1;
+		sslm_adapter ad;
+		std::vector<int> idx;
+	};
+	std::vector<Unit> units;
 	std::vector<int> finished;
 	for (auto& g : groups) {
 		const uint32_t l0 = g.first;
 		const uint32_t l1 = std::min<uint32_t>(m->L, l0 + budget);
-		// one launch sequence per (adapter) partition of <= kMaxTokens tokens
 		std::vector<sslm_adapter> ads;
 		for (int i : g.second)
 			if (std::find(ads.begin(), ads.end(), seqs[i]->adapter) == ads.end()) ads.push_back(seqs[i]->adapter);
@@ -1238,85 +1283,190 @@ static sslm_status decode_batch(sslm_model m, sslm_seq* seqs, int32_t n, uint32_
 			std::vector<int> members;
 			for (int i : g.second)
 				if (seqs[i]->adapter == ad) members.push_back(i);
-			for (size_t b = 0; b < members.size(); b += kMaxTokens) {
-				const int M = (int)std::min(members.size() - b, (size_t)kMaxTokens);
-				std::vector<TokenInfo> ti(M);
-				std::vector<int32_t> slots(M);
-				for (int t = 0; t < M; ++t) {
-					sslm_seq s = seqs[members[b + t]];
-					ti[t] = TokenInfo{s->context_length, s->slot, (int32_t)s->block};
-					slots[t] = s->slot;
-				}
-				// every sequence of one call shares the pool of the first (checked by the caller)
-				m->pool_dev = seqs[members[b]]->pool->dev;
-				put_tokens(m, ti);
-				ck(hipMemcpyAsync(m->slot_idx, slots.data(), M * 4, hipMemcpyHostToDevice, m->stream));
-				run_layers(m, M, StreamRef{m->stream_codes, m->stream_scale, m->slot_idx}, (int)l0, (int)l1, ad);
-				ck(hipStreamSynchronize(m->stream));
+			const int total = (int)members.size();
+			int parts = std::max(1, std::min(track_limit(), total / track_min()));
+			parts = std::max(parts, (total + kTrackTokens - 1) / kTrackTokens);
+			for (int p = 0; p < parts; ++p) {
+				const int b = (int)((int64_t)total * p / parts), e = (int)((int64_t)total * (p + 1) / parts);
+				if (e > b) units.push_back(Unit{l0, l1, ad, std::vector<int>(members.begin() + b, members.begin() + e)});
 			}
 		}
-		for (int i : g.second) {
-			seqs[i]->layer_index = l1;
-			if (l1 == (uint32_t)m->L) finished.push_back(i);
-		}
+		if (l1 == (uint32_t)m->L)
+			for (int i : g.second) finished.push_back(i);
 	}
-	// status check: a failure leaves its sequence at the failing layer (its last commit); every
-	// other sequence of the batch advances normally
-	std::vector<int32_t> words(kSlotCapacity);
-	ck(hipMemcpy(words.data(), m->status, kSlotCapacity * 4, hipMemcpyDeviceToHost));
-	prof_collect();
-	sslm_status first_err = SSLM_OK;
-	for (int i = 0; i < n; ++i) {
-		sslm_seq s = seqs[i];
-		const int32_t w = words[s->slot];
-		if (w == 0) continue;
-		s->layer_index = (uint32_t)std::min(w >> 8, m->L);
-		ck(hipMemset(m->status + s->slot, 0, 4));
-		if (first_err == SSLM_OK) first_err = map_forward_status(w);
-		finished.erase(std::remove(finished.begin(), finished.end(), i), finished.end());
-		need_logits.erase(std::remove(need_logits.begin(), need_logits.end(), i), need_logits.end());
-		out_tokens[i] = -1;
-	}
-	for (int i : finished) seqs[i]->context_length += 1;
-	for (auto& g : groups)
-		for (int i : g.second)
-			if (seqs[i]->layer_index < (uint32_t)m->L) out_tokens[i] = -1;
-	// logits
 	std::vector<int> lg = need_logits;
 	lg.insert(lg.end(), finished.begin(), finished.end());
-	for (size_t b = 0; b < lg.size(); b += kMaxTokens) {
-		const int M = (int)std::min(lg.size() - b, (size_t)kMaxTokens);
-		std::vector<TokenInfo> ti(M);
-		std::vector<int32_t> slots(M);
+
+	// Host staging, uploaded before the kernels (kept alive until the sync below).  The common
+	// shape -- at most one unit per track and one head chunk -- stages every unit's tokens in its
+	// track's own buffers up front and replays a captured graph of the whole submission;
+	// anything else launches directly, uploading as it goes.
+	Track& t0 = m->tracks[0];
+	const size_t ntr = m->tracks.size();
+	const bool one_per_track = units.size() <= ntr && lg.size() <= (size_t)kMaxTokens;
+	const bool use_graph = one_per_track && graphs_enabled() && !prof_enabled();
+	std::deque<std::vector<TokenInfo>> h_tok;  // deque: references to earlier entries stay valid
+	std::deque<std::vector<int32_t>> h_i32;
+	auto stage_unit = [&](size_t u, hipStream_t s) {
+		const Unit& un = units[u];
+		Track& w = m->tracks[u % ntr];
+		const int M = (int)un.idx.size();
+		h_tok.emplace_back(M);
+		std::vector<TokenInfo>& ti = h_tok.back();
+		h_i32.emplace_back(M);
+		std::vector<int32_t>& slots = h_i32.back();
+		h_i32.emplace_back(M);
+		std::vector<int32_t>& ids = h_i32.back();
 		for (int t = 0; t < M; ++t) {
-			sslm_seq s = seqs[lg[b + t]];
-			ti[t] = TokenInfo{s->context_length, s->slot, (int32_t)s->block};
-			slots[t] = s->slot;
+			sslm_seq q = seqs[un.idx[t]];
+			ti[t] = TokenInfo{q->context_length, q->slot, (int32_t)q->block};
+			slots[t] = q->slot;
+			ids[t] = q->current_token;
 		}
-		put_tokens(m, ti);
-		ck(hipMemcpyAsync(m->slot_idx, slots.data(), M * 4, hipMemcpyHostToDevice, m->stream));
-		run_logits(m, M, StreamRef{m->stream_codes, m->stream_scale, m->slot_idx});
-		std::vector<int32_t> toks(M);
-		ck(hipMemcpyAsync(toks.data(), m->out_tokens, M * 4, hipMemcpyDeviceToHost, m->stream));
-		ck(hipStreamSynchronize(m->stream));
+		ck(hipMemcpyAsync(w.tok, ti.data(), M * sizeof(TokenInfo), hipMemcpyHostToDevice, s));
+		ck(hipMemcpyAsync(w.slot_idx, slots.data(), M * 4, hipMemcpyHostToDevice, s));
+		if (un.l0 == 0) ck(hipMemcpyAsync(w.tok_ids, ids.data(), M * 4, hipMemcpyHostToDevice, s));
+	};
+	auto launch_unit = [&](size_t u) {
+		const Unit& un = units[u];
+		Track& w = m->tracks[u % ntr];
+		const int M = (int)un.idx.size();
+		if (un.l0 == 0) {  // embed the pending token (src/sslm_abi.cpp:2237-2249)
+			ProfScope p(w.stream, kProfRow, 0, 0);
+			sslm_launch::embed(w.tok_ids, M, m->embed, m->H, m->V, m->embed_site, m->stream_codes, w.slot_idx,
+			                   m->stream_scale, w.slot_idx, w.tok, m->status, w.stream);
+			ck(hipGetLastError());
+		}
+		run_layers(m, w, M, StreamRef{m->stream_codes, m->stream_scale, w.slot_idx}, (int)un.l0, (int)un.l1, un.ad);
+	};
+	auto stage_logits = [&](size_t b, int M, hipStream_t s) {
+		h_tok.emplace_back(M);
+		std::vector<TokenInfo>& ti = h_tok.back();
+		h_i32.emplace_back(M);
+		std::vector<int32_t>& slots = h_i32.back();
 		for (int t = 0; t < M; ++t) {
-			sslm_seq s = seqs[lg[b + t]];
-			s->ready_for_logits = false;
-			s->current_token = toks[t];
-			s->layer_index = 0;
-			out_tokens[lg[b + t]] = toks[t];
+			sslm_seq q = seqs[lg[b + t]];
+			ti[t] = TokenInfo{q->context_length, q->slot, (int32_t)q->block};
+			slots[t] = q->slot;
+		}
+		ck(hipMemcpyAsync(t0.lg_tok, ti.data(), M * sizeof(TokenInfo), hipMemcpyHostToDevice, s));
+		ck(hipMemcpyAsync(t0.lg_slot, slots.data(), M * 4, hipMemcpyHostToDevice, s));
+	};
+	auto launch_logits = [&](int M) {
+		run_logits(m, t0, M, StreamRef{m->stream_codes, m->stream_scale, t0.lg_slot}, t0.lg_tok);
+	};
+	// every sequence of one call shares the pool of the first (checked by the caller)
+	m->pool_dev = seqs[0]->pool->dev;
+	std::vector<int32_t> toks(lg.size());
+	if (one_per_track) {
+		for (size_t u = 0; u < units.size(); ++u) stage_unit(u, t0.stream);
+		if (!lg.empty()) stage_logits(0, (int)lg.size(), t0.stream);
+		// Each unit is its own captured graph on its own track's stream (a graph runs its nodes
+		// in order on the stream it is launched on, so one graph per track keeps the tracks
+		// concurrent), forked from and joined back into track 0; the head is one more graph.
+		auto graph_of = [&](const std::string& key, hipStream_t s, const std::function<void()>& body) {
+			auto it = m->graphs.find(key);
+			if (it == m->graphs.end()) {
+				if (m->graphs.size() >= kGraphCache) {
+					for (auto& kv : m->graphs) (void)hipGraphExecDestroy(kv.second);
+					m->graphs.clear();
+				}
+				hipGraph_t graph = nullptr;
+				ck(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+				body();
+				ck(hipStreamEndCapture(s, &graph));
+				hipGraphExec_t exec = nullptr;
+				ck(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0));
+				(void)hipGraphDestroy(graph);
+				it = m->graphs.emplace(key, exec).first;
+			}
+			return it->second;
+		};
+		const size_t nt = std::min(ntr, units.size());
+		ck(hipEventRecord(t0.fork, t0.stream));
+		for (size_t k = 1; k < nt; ++k) ck(hipStreamWaitEvent(m->tracks[k].stream, t0.fork, 0));
+		for (size_t u = 0; u < units.size(); ++u) {
+			Track& w = m->tracks[u % ntr];
+			if (use_graph) {
+				const Unit& un = units[u];
+				const std::string key = "u" + std::to_string(u % ntr) + "|" + std::to_string(un.idx.size()) + "|" +
+				                        std::to_string(un.l0) + "|" + std::to_string(un.l1) + "|" +
+				                        std::to_string((uintptr_t)un.ad) + "|" + std::to_string((uintptr_t)m->pool_dev);
+				ck(hipGraphLaunch(graph_of(key, w.stream, [&] { launch_unit(u); }), w.stream));
+			} else {
+				launch_unit(u);
+			}
+		}
+		for (size_t k = 1; k < nt; ++k) {
+			ck(hipEventRecord(m->tracks[k].done, m->tracks[k].stream));
+			ck(hipStreamWaitEvent(t0.stream, m->tracks[k].done, 0));
+		}
+		if (!lg.empty()) {
+			const int M = (int)lg.size();
+			if (use_graph) ck(hipGraphLaunch(graph_of("lg|" + std::to_string(M), t0.stream, [&] { launch_logits(M); }), t0.stream));
+			else launch_logits(M);
+		}
+		if (!lg.empty()) ck(hipMemcpyAsync(toks.data(), t0.out_tokens, lg.size() * 4, hipMemcpyDeviceToHost, t0.stream));
+	} else {
+		std::vector<bool> used(ntr, false);
+		for (size_t u = 0; u < units.size(); ++u) {
+			stage_unit(u, m->tracks[u % ntr].stream);
+			used[u % ntr] = true;
+			launch_unit(u);
+		}
+		for (size_t k = 1; k < ntr; ++k) {
+			if (!used[k]) continue;
+			ck(hipEventRecord(m->tracks[k].done, m->tracks[k].stream));
+			ck(hipStreamWaitEvent(t0.stream, m->tracks[k].done, 0));
+		}
+		for (size_t b = 0; b < lg.size(); b += kMaxTokens) {
+			const int M = (int)std::min(lg.size() - b, (size_t)kMaxTokens);
+			stage_logits(b, M, t0.stream);
+			launch_logits(M);
+			ck(hipMemcpyAsync(toks.data() + b, t0.out_tokens, M * 4, hipMemcpyDeviceToHost, t0.stream));
 		}
 	}
-	ck(hipMemcpy(words.data(), m->status, kSlotCapacity * 4, hipMemcpyDeviceToHost));
+	std::vector<int32_t> words(kSlotCapacity);
+	ck(hipMemcpyAsync(words.data(), m->status, kSlotCapacity * 4, hipMemcpyDeviceToHost, t0.stream));
+	ck(hipStreamSynchronize(t0.stream));
 	prof_collect();
-	for (int i : lg) {
+
+	// A failure leaves its sequence at the failing layer (its last commit); every other sequence
+	// of the batch advances normally.  Layer failures carry their layer in the status word, head
+	// failures the layer count.
+	sslm_status first_err = SSLM_OK;
+	std::vector<char> failed_layers(n, 0), failed_head(n, 0);
+	for (int i = 0; i < n; ++i) {
 		const int32_t w = words[seqs[i]->slot];
-		if (w != 0) {
-			ck(hipMemset(m->status + seqs[i]->slot, 0, 4));
-			out_tokens[i] = -1;
-			if (first_err == SSLM_OK) first_err = map_forward_status(w);
+		if (w == 0) continue;
+		if ((w >> 8) < m->L) failed_layers[i] = 1;
+		else failed_head[i] = 1;
+		ck(hipMemsetAsync(m->status + seqs[i]->slot, 0, 4, t0.stream));
+		if (first_err == SSLM_OK) first_err = map_forward_status(w);
+		out_tokens[i] = -1;
+	}
+	for (auto& g : groups) {
+		const uint32_t l1 = std::min<uint32_t>(m->L, g.first + budget);
+		for (int i : g.second) {
+			if (failed_layers[i]) {
+				seqs[i]->layer_index = (uint32_t)std::min(words[seqs[i]->slot] >> 8, m->L);
+				continue;
+			}
+			seqs[i]->layer_index = l1;
+			if (l1 < (uint32_t)m->L) out_tokens[i] = -1;
+			else seqs[i]->context_length += 1;
 		}
 	}
+	for (size_t k = 0; k < lg.size(); ++k) {
+		const int i = lg[k];
+		if (failed_layers[i]) continue;
+		sslm_seq s = seqs[i];
+		s->ready_for_logits = false;
+		s->current_token = toks[k];
+		s->layer_index = 0;
+		out_tokens[i] = failed_head[i] ? -1 : toks[k];
+	}
+	ck(hipStreamSynchronize(t0.stream));
 	return first_err;
 }
 
@@ -1410,7 +1560,7 @@ sslm_status sslm_g5_test_only_peek_kv_block_bytes(sslm_kv_pool pool, uint32_t bl
 	if (block_index >= pool->block_count || n > pool->block_size) return SSLM_INVALID_ARGUMENT;
 	return guarded([&]() -> sslm_status {
 		std::lock_guard<std::mutex> lk(pool->model->mu);
-		ck(hipStreamSynchronize(pool->model->stream));
+		ck(hipStreamSynchronize(pool->model->tracks[0].stream));
 		ck(hipMemcpy(out_buf, pool->dev + (size_t)block_index * pool->block_size, n, hipMemcpyDeviceToHost));
 		return SSLM_OK;
 	});

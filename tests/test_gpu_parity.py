@@ -89,10 +89,12 @@ def _run_batch(lib, artifact, prompts, steps, budget):
 
 @pytest.mark.parametrize("name", ["small", "medium"])
 def test_batched_decode_matches_reference(name, hip_lib, ref_lib):
-    """Several sequences of different lengths decoded together (one GEMV row per sequence)."""
+    """Several sequences of different lengths decoded together (one GEMV row per sequence, token
+    groups on concurrent streams)."""
     sm, art = synthetic(name)
     rng = np.random.default_rng(23)
-    prompts = [rng.integers(0, sm.config.vocab, size=n) for n in (3, 9, 1, 14, 6)]
+    # 13 sequences: split over several concurrent token groups (tracks) of at least 4 tokens
+    prompts = [rng.integers(0, sm.config.vocab, size=n) for n in (3, 9, 1, 14, 6, 2, 11, 5, 7, 4, 8, 12, 10)]
     L = sm.config.layers
     for budget in sorted({L, 1}):
         print(f"case batch {name} budget={budget}", flush=True)
