@@ -3,13 +3,20 @@
 One step = one sslm_decode_step over a batch of sequences through all 28 layers and the LM head
 (greedy token out), with every weight, KV block and stream state resident in HBM.  Prints one
 JSON line.  Alongside it, the same run measures:
-  * the int8 prefill GEMM rate of a 512-token chunk (BASELINE configuration 2's prefill),
+  * the decode GEMV roofline: algorithmic bytes of every projection GEMV and the LM head of a
+    step over their launch durations (HIP events around each launch on the library's stream, in
+    a profiled pass of the same steps), per launch shape and in aggregate; HBM traffic per
+    launch from rocprofv3 PMC runs when profiles/decode_gemv_traffic.json holds them,
   * single-sequence decode,
+  * the int8 prefill GEMM rate of a 512-token chunk (BASELINE configuration 2's prefill),
   * the reference's own CPU path (oracle/_ref, compiled from the reference sources) on a bounded
     sample of the same workload, whose tokens must equal the GPU's.
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--batch B]
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--batch B] [--phase all|decode|prefill]
+       python bench.py --traffic-from FETCH.csv WRITE.csv   (summarise two rocprofv3 --pmc runs)
 """
 import argparse
+import csv
 import ctypes
 import json
 import os
@@ -17,6 +24,7 @@ import platform
 import subprocess
 import sys
 import time
+from collections import defaultdict
 
 import numpy as np
 
@@ -30,12 +38,13 @@ METRIC = "int8 prefill GEMM TOPS + decode tok/s (1.5B shape), bit-exact vs CPU, 
 HBM_PEAK_GBS = 8000.0
 INT8_PEAK_TOPS = 5000.0
 CLASSES = 5
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "decode_gemv_traffic.json")
+CALIBRATION_BYTES = 256 << 20  # device-to-device copy whose PMC counts scale FETCH/WRITE_SIZE
 
 
 def profile(lib, on):
     L = lib.lib
     L.sslm_hip_profile_enable.argtypes = [ctypes.c_int]
-    L.sslm_hip_profile_read.argtypes = [ctypes.c_void_p] * 4 + [ctypes.c_int]
     if on:
         L.sslm_hip_profile_reset()
     L.sslm_hip_profile_enable(1 if on else 0)
@@ -46,8 +55,28 @@ def profile_read(lib):
     la = (ctypes.c_int64 * CLASSES)()
     by = (ctypes.c_int64 * CLASSES)()
     op = (ctypes.c_int64 * CLASSES)()
+    lib.lib.sslm_hip_profile_read.argtypes = [ctypes.c_void_p] * 4 + [ctypes.c_int]
     lib.lib.sslm_hip_profile_read(ms, la, by, op, CLASSES)
     return list(ms), list(la), list(by), list(op)
+
+
+def profile_shapes(lib):
+    """[(cls, M, N, K, ms, launches, bytes, ops)] per GEMM launch shape."""
+    L = lib.lib
+    L.sslm_hip_profile_shapes.restype = ctypes.c_int
+    L.sslm_hip_profile_shapes.argtypes = [ctypes.c_void_p] * 5 + [ctypes.c_int]
+    cap = 256
+    keys = (ctypes.c_int64 * cap)()
+    ms = (ctypes.c_double * cap)()
+    la = (ctypes.c_int64 * cap)()
+    by = (ctypes.c_int64 * cap)()
+    op = (ctypes.c_int64 * cap)()
+    n = min(cap, L.sslm_hip_profile_shapes(keys, ms, la, by, op, cap))
+    out = []
+    for i in range(n):
+        k = keys[i]
+        out.append((k >> 56, (k >> 40) & 0xFFFF, (k >> 20) & 0xFFFFF, k & 0xFFFFF, ms[i], la[i], by[i], op[i]))
+    return out
 
 
 def cpu_model():
@@ -61,6 +90,55 @@ def cpu_model():
     return platform.processor()
 
 
+def copy_calibration(hip):
+    """A plain device-to-device copy of CALIBRATION_BYTES (rocprof sees __amd_rocclr_copyBuffer)."""
+    from superslm_amd.device import Device
+    dev = Device(hip)
+    a = dev.zeros((CALIBRATION_BYTES,), np.int8)
+    b = dev.zeros((CALIBRATION_BYTES,), np.int8)
+    for _ in range(3):
+        dev.copy_device(b, a)
+    hip.lib.sslm_hip_synchronize()
+
+
+def traffic_from(fetch_csv, write_csv):
+    """HBM bytes per decode-GEMV launch from two rocprofv3 --pmc runs of
+    `bench.py --phase decode --calibrate`: FETCH_SIZE and WRITE_SIZE (KiB per dispatch), each
+    scaled by what the counter reads for the calibration copy of known size."""
+    def per_kernel(path, counter):
+        vals = defaultdict(list)
+        for r in csv.DictReader(open(path)):
+            if r["Counter_Name"] != counter:
+                continue
+            vals[(r["Dispatch_Id"], r["Kernel_Name"])].append(float(r["Counter_Value"]))
+        agg = defaultdict(list)
+        for (d, name), v in vals.items():
+            agg[name].append(sum(v))
+        return agg
+    fetch = per_kernel(fetch_csv, "FETCH_SIZE")
+    write = per_kernel(write_csv, "WRITE_SIZE")
+    copy_name = next(n for n in fetch if "copyBuffer" in n)
+    f_scale = CALIBRATION_BYTES / (max(fetch[copy_name]) * 1024.0)
+    w_scale = CALIBRATION_BYTES / (max(write[copy_name]) * 1024.0)
+    kernels = {}
+    for name in fetch:
+        if "k_gemv<1," not in name:  # decode-step GEMVs (M <= 16); the prompts' prefill runs M = 32
+            continue
+        f = np.mean(fetch[name]) * 1024.0 * f_scale
+        w = np.mean(write.get(name, [0.0])) * 1024.0 * w_scale
+        kernels[name] = {"dispatches": len(fetch[name]), "fetch_bytes": round(f), "write_bytes": round(w)}
+    total_d = sum(k["dispatches"] for k in kernels.values())
+    total_b = sum((k["fetch_bytes"] + k["write_bytes"]) * k["dispatches"] for k in kernels.values())
+    out = {"calibration": {"copy_bytes": CALIBRATION_BYTES, "fetch_scale": f_scale, "write_scale": w_scale},
+           "kernels": kernels, "mean_traffic_bytes_per_launch": round(total_b / max(1, total_d)),
+           "dispatches": total_d,
+           "command": "rocprofv3 --pmc FETCH_SIZE (then WRITE_SIZE) --output-format csv -- "
+                      "python3 bench.py --phase decode --steps 5 --warmup 2 --no-cpu --calibrate"}
+    os.makedirs(os.path.dirname(TRAFFIC_FILE), exist_ok=True)
+    json.dump(out, open(TRAFFIC_FILE, "w"), indent=1)
+    print(json.dumps(out, indent=1))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -70,7 +148,13 @@ def main():
     ap.add_argument("--prompt", type=int, default=32)
     ap.add_argument("--cpu-seqs", type=int, default=2)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--phase", choices=["all", "decode", "prefill"], default="all")
+    ap.add_argument("--calibrate", action="store_true", help="add the PMC calibration copy")
+    ap.add_argument("--traffic-from", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"))
     args = ap.parse_args()
+    if args.traffic_from:
+        traffic_from(*args.traffic_from)
+        return
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
               "(sequences shard across GPUs with no exchange; see DESIGN.md)", file=sys.stderr)
@@ -80,80 +164,143 @@ def main():
     t0 = time.time()
     sm = build_synthetic(cfg, seed=1515)
     image = sm.to_array()
-    gen_s = time.time() - t0
-    print(f"[bench] synthetic 1.5B artifact {image.nbytes / 1e9:.2f} GB in {gen_s:.1f}s", file=sys.stderr, flush=True)
+    print(f"[bench] synthetic 1.5B artifact {image.nbytes / 1e9:.2f} GB in {time.time() - t0:.1f}s",
+          file=sys.stderr, flush=True)
 
     hip = SslmLib(os.path.join(ROOT, "superslm_amd", "libsslm_hip.so"))
+    if args.calibrate:
+        copy_calibration(hip)
     model = Model(hip, image)
     B = args.batch
     pool = model.pool(B + 1)
     rng = np.random.default_rng(99)
     prompts = [rng.integers(0, cfg.vocab, size=args.prompt) for _ in range(B)]
-    seqs = [pool.seq() for _ in range(B)]
-    for s, p in zip(seqs, prompts):
-        s.prefill(p)
-    print("[bench] prefilled", B, "sequences", file=sys.stderr, flush=True)
+    line = None
+    first_tokens = second_tokens = None
+    if args.phase in ("all", "decode"):
+        seqs = [pool.seq() for _ in range(B)]
+        for s, p in zip(seqs, prompts):
+            s.prefill(p)
+        print("[bench] prefilled", B, "sequences", file=sys.stderr, flush=True)
+        # decode: warmup (the first step only computes logits for the prefilled rows)
+        first_tokens = model.decode_step(seqs, cfg.layers)
+        second_tokens = model.decode_step(seqs, cfg.layers)
+        for _ in range(max(0, args.warmup - 2)):
+            model.decode_step(seqs, cfg.layers)
+        hip.lib.sslm_hip_synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            model.decode_step(seqs, cfg.layers)
+        hip.lib.sslm_hip_synchronize()
+        dt = time.perf_counter() - t0
+        tok_s = B * args.steps / dt
+        ms_step = dt * 1000.0 / args.steps
+        print(f"[bench] decode B={B}: {ms_step:.3f} ms/step, {tok_s:.1f} tok/s", file=sys.stderr, flush=True)
 
-    # decode: warmup (the first step only computes logits for the prefilled rows)
-    first_tokens = model.decode_step(seqs, cfg.layers)
-    second_tokens = model.decode_step(seqs, cfg.layers)
-    for _ in range(max(0, args.warmup - 2)):
-        model.decode_step(seqs, cfg.layers)
-    hip.lib.sslm_hip_synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        model.decode_step(seqs, cfg.layers)
-    hip.lib.sslm_hip_synchronize()
-    dt = time.perf_counter() - t0
-    tok_s = B * args.steps / dt
-    ms_step = dt * 1000.0 / args.steps
-    print(f"[bench] decode B={B}: {ms_step:.3f} ms/step, {tok_s:.1f} tok/s", file=sys.stderr, flush=True)
+        # profiled pass of the same steps: events around every launch, per class and per shape
+        profile(hip, True)
+        for _ in range(args.steps):
+            model.decode_step(seqs, cfg.layers)
+        ms, la, by, op = profile_read(hip)
+        shapes = profile_shapes(hip)
+        profile(hip, False)
+        # the dominant kernel: the decode GEMVs, each shape timed back to back with HIP events
+        L = hip.lib
+        L.sslm_hip_bench_decode_gemv.restype = ctypes.c_int32
+        L.sslm_hip_bench_decode_gemv.argtypes = [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32] + [ctypes.c_void_p] * 3 + [ctypes.c_int32]
+        us = (ctypes.c_double * 8)()
+        gb = (ctypes.c_int64 * 8)()
+        gk = (ctypes.c_int64 * 8)()
+        ng = L.sslm_hip_bench_decode_gemv(model.handle, B, 50, us, gb, gk, 8)
+        if ng != 5:
+            raise RuntimeError("sslm_hip_bench_decode_gemv failed")
+        names = ["q|k|v", "o", "gate|up", "down", "lm_head"]
+        per_step = [cfg.layers] * 4 + [1]
+        per_shape = [{"gemv": names[i], "M": B, "N": gk[i] >> 20, "K": gk[i] & 0xFFFFF, "launches_per_step": per_step[i],
+                      "us_per_launch": round(us[i], 3), "bytes_per_launch": gb[i],
+                      "gbs": round(gb[i] / (us[i] * 1e-6) / 1e9, 1)} for i in range(5)]
+        g_bytes = sum(per_step[i] * gb[i] for i in range(5))
+        g_us = sum(per_step[i] * us[i] for i in range(5))
+        g_launch = sum(per_step)
+        all_gbs = g_bytes / (g_us * 1e-6) / 1e9
+        step_prof = {"gemv_ms": ms[0] / args.steps, "head_ms": ms[1] / args.steps,
+                     "attention_ms": ms[2] / args.steps, "row_ms": ms[3] / args.steps,
+                     "launches_per_step": sum(la) / args.steps}
+        traffic = None
+        if os.path.exists(TRAFFIC_FILE):
+            traffic = json.load(open(TRAFFIC_FILE)).get("mean_traffic_bytes_per_launch")
 
-    # profiled pass (events around every launch) for the roofline figures
-    profile(hip, True)
-    for _ in range(args.steps):
-        model.decode_step(seqs, cfg.layers)
-    ms, la, by, op = profile_read(hip)
-    profile(hip, False)
-    gemv_gbs = by[0] / (ms[0] * 1e-3) / 1e9 if ms[0] else 0.0
-    head_gbs = by[1] / (ms[1] * 1e-3) / 1e9 if ms[1] else 0.0
-    dec_bytes = by[0] + by[1]
-    dec_ms = ms[0] + ms[1]
-    all_gbs = dec_bytes / (dec_ms * 1e-3) / 1e9 if dec_ms else 0.0
-    step_prof = {"gemv_ms": ms[0] / args.steps, "head_ms": ms[1] / args.steps, "attention_ms": ms[2] / args.steps,
-                 "row_ms": ms[3] / args.steps, "launches_per_step": sum(la) / args.steps}
+        # single-sequence decode (M = 1)
+        one = seqs[:1]
+        for _ in range(2):
+            model.decode_step(one, cfg.layers)
+        t0 = time.perf_counter()
+        n1 = max(4, args.steps // 2)
+        for _ in range(n1):
+            model.decode_step(one, cfg.layers)
+        m1_tok_s = n1 / (time.perf_counter() - t0)
+        line = {
+            "metric": METRIC,
+            "value": round(tok_s, 2),
+            "unit": "tok/s",
+            "n_gpus": 1,
+            "steps": args.steps,
+            "warmup": args.warmup,
+            "ms_per_step": round(ms_step, 4),
+            "higher_is_better": True,
+            "scaling": "weak",
+            "vs_baseline": None,
+            "dtype": "int8",
+            "data": "synthetic",
+            "config": {"workload": f"config1: Qwen2.5-1.5B-shape integer decode, {B} sequences, 28 layers + "
+                                   f"LM head per step, seeded random int8 weights", "batch": B,
+                       "prompt_tokens": args.prompt, "hidden": cfg.hidden, "layers": cfg.layers,
+                       "intermediate": cfg.inter, "vocab": cfg.vocab},
+            "roofline": {"bound": "hbm", "achieved": round(all_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(all_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
+                         "kernel": "decode GEMV k_gemv over one step's launches (28 x q|k|v, o, gate|up, down + "
+                                   "LM head), each timed back to back with HIP events: sum of algorithmic bytes / "
+                                   "sum of launch durations; traffic = mean HBM bytes per launch (rocprofv3 "
+                                   "FETCH_SIZE + WRITE_SIZE, copy-calibrated)",
+                         "bytes_per_launch": g_bytes // g_launch,
+                         "us_per_launch": round(g_us / g_launch, 3)},
+            "cpu_baseline": None,
+            "bit_exact_vs_cpu": None,
+            "decode_m1_tok_s": round(m1_tok_s, 2),
+            "decode_gemv_shapes": per_shape,
+            "step_profile_ms": {k: round(v, 4) for k, v in step_prof.items()},
+        }
 
-    # single-sequence decode (M = 1)
-    one = seqs[:1]
-    for _ in range(2):
-        model.decode_step(one, cfg.layers)
-    t0 = time.perf_counter()
-    n1 = max(4, args.steps // 2)
-    for _ in range(n1):
-        model.decode_step(one, cfg.layers)
-    m1_tok_s = n1 / (time.perf_counter() - t0)
-
-    # prefill: one 512-token chunk (BASELINE configuration 2's chunk), GEMM rate from the profile
-    pseq = pool.seq()
-    chunk = rng.integers(0, cfg.vocab, size=512)
-    pseq.prefill(chunk[:8])  # warm
-    pseq.release()
-    pseq = pool.seq()
-    profile(hip, True)
-    t0 = time.perf_counter()
-    pseq.prefill(chunk)
-    pre_s = time.perf_counter() - t0
-    pms, pla, pby, pop = profile_read(hip)
-    profile(hip, False)
-    prefill_tops = pop[0] / (pms[0] * 1e-3) / 1e12 if pms[0] else 0.0
-    prefill_tok_s = 512 / pre_s
-    print(f"[bench] prefill 512: {pre_s * 1e3:.1f} ms, GEMM {prefill_tops:.1f} TOPS", file=sys.stderr, flush=True)
+    if args.phase in ("all", "prefill"):
+        # prefill: one 512-token chunk (BASELINE configuration 2's chunk), GEMM rate from the profile
+        chunk = rng.integers(0, cfg.vocab, size=512)
+        pseq = pool.seq()
+        pseq.prefill(chunk[:8])  # warm
+        pseq.release()
+        pseq = pool.seq()
+        pseq.prefill(chunk)  # warm the 512-token shapes
+        pseq.release()
+        pseq = pool.seq()
+        profile(hip, True)
+        t0 = time.perf_counter()
+        pseq.prefill(chunk)
+        pre_s = time.perf_counter() - t0
+        pms, pla, pby, pop = profile_read(hip)
+        profile(hip, False)
+        prefill_tops = pop[0] / (pms[0] * 1e-3) / 1e12 if pms[0] else 0.0
+        print(f"[bench] prefill 512: {pre_s * 1e3:.1f} ms, GEMM {prefill_tops:.1f} TOPS", file=sys.stderr, flush=True)
+        pre = {"prefill_512_tok_s": round(512 / pre_s, 1), "prefill_gemm_tops": round(prefill_tops, 2),
+               "prefill_gemm_mfma_frac": round(prefill_tops / INT8_PEAK_TOPS, 4)}
+        if line is None:
+            line = {"metric": METRIC, "value": round(prefill_tops, 2), "unit": "TOPS", "n_gpus": 1, "steps": 1,
+                    "warmup": 2, "ms_per_step": round(pre_s * 1e3, 3), "higher_is_better": True,
+                    "scaling": "weak", "vs_baseline": None, "dtype": "int8", "data": "synthetic",
+                    "config": {"workload": "config2 prefill: one 512-token chunk through 28 layers, 1.5B shape"}}
+        line.update(pre)
 
     # CPU baseline: the reference compiled from its sources, same artifact, bounded sample
-    cpu = None
-    bit_exact = None
     ref_so = os.path.join(ROOT, "oracle", "_ref", "libsuperslm_ref.so")
-    if not args.no_cpu and os.path.exists(ref_so):
+    if args.phase in ("all", "decode") and not args.no_cpu and os.path.exists(ref_so):
         ref = SslmLib(ref_so)
         t0 = time.time()
         rmodel = Model(ref, image)
@@ -166,42 +313,13 @@ def main():
         r_second = rmodel.decode_step(rseqs, cfg.layers)  # one full decode step per sequence
         cpu_dt = time.perf_counter() - t1
         bit_exact = (r_first == first_tokens[:args.cpu_seqs]) and (r_second == second_tokens[:args.cpu_seqs])
-        cpu = {"value": round(args.cpu_seqs / cpu_dt, 3), "unit": "tok/s", "cores": 1, "kind": "reference",
-               "sample": f"{args.cpu_seqs} sequences x 1 decode step (28 layers + LM head) after a "
-                         f"{args.prompt}-token prefill, same artifact; host {cpu_model()}, nproc {os.cpu_count()}"}
-        print(f"[bench] CPU reference: {cpu['value']} tok/s, tokens equal: {bit_exact} "
+        line["cpu_baseline"] = {
+            "value": round(args.cpu_seqs / cpu_dt, 3), "unit": "tok/s", "cores": 1, "kind": "reference",
+            "sample": f"{args.cpu_seqs} sequences x 1 decode step (28 layers + LM head) after a "
+                      f"{args.prompt}-token prefill, same artifact; host {cpu_model()}, nproc {os.cpu_count()}"}
+        line["bit_exact_vs_cpu"] = bit_exact
+        print(f"[bench] CPU reference: {line['cpu_baseline']['value']} tok/s, tokens equal: {bit_exact} "
               f"({time.time() - t0:.1f}s)", file=sys.stderr, flush=True)
-
-    line = {
-        "metric": METRIC,
-        "value": round(tok_s, 2),
-        "unit": "tok/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(ms_step, 4),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "int8",
-        "data": "synthetic",
-        "config": {"workload": f"config1: Qwen2.5-1.5B-shape integer decode, {B} sequences, 28 layers + "
-                               f"LM head per step, seeded random int8 weights", "batch": B,
-                   "prompt_tokens": args.prompt, "hidden": cfg.hidden, "layers": cfg.layers,
-                   "intermediate": cfg.inter, "vocab": cfg.vocab},
-        "roofline": {"bound": "hbm", "achieved": round(all_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(all_gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "decode GEMV (projection GEMVs + LM head), algorithmic bytes / kernel time"},
-        "cpu_baseline": cpu,
-        "bit_exact_vs_cpu": bit_exact,
-        "decode_m1_tok_s": round(m1_tok_s, 2),
-        "decode_gemv_gbs": round(gemv_gbs, 1),
-        "lm_head_gbs": round(head_gbs, 1),
-        "step_profile_ms": {k: round(v, 4) for k, v in step_prof.items()},
-        "prefill_512_tok_s": round(prefill_tok_s, 1),
-        "prefill_gemm_tops": round(prefill_tops, 2),
-        "prefill_gemm_mfma_frac": round(prefill_tops / INT8_PEAK_TOPS, 4),
-    }
     print(json.dumps(line))
 
 

@@ -178,6 +178,16 @@ sslm_status sslm_detokenize_stream(sslm_model model, sslm_detok_state* state, co
 void sslm_hip_profile_enable(int on);
 void sslm_hip_profile_read(double* ms, int64_t* launches, int64_t* bytes, int64_t* ops, int classes);
 void sslm_hip_profile_reset(void);
+/* The decode GEMVs of one step (layer 0's q|k|v, o, gate|up and down projections and the LM
+ * head, as the layer loop launches them for M tokens) timed back to back, `iters` launches each,
+ * with HIP events on the model's stream.  Writes per GEMV the mean microseconds per launch, the
+ * algorithmic bytes per launch (weights + activations + outputs + fold tables) and N << 20 | K;
+ * returns the number written (5), or -1.  Sequence state is not touched. */
+int32_t sslm_hip_bench_decode_gemv(sslm_model model, int32_t M, int32_t iters, double* us, int64_t* bytes,
+                                   int64_t* shapes, int32_t cap);
+/* Per GEMM launch shape: key = class << 56 | M << 40 | N << 20 | K; returns the number of
+ * shapes recorded (entries beyond `cap` are not written). */
+int sslm_hip_profile_shapes(int64_t* keys, double* ms, int64_t* launches, int64_t* bytes, int64_t* ops, int cap);
 
 /* The single GEMM + requant of BASELINE configuration 0, on device buffers: int8 A [m, k] x int8
  * W [n, k]^T, int32 accumulate, per-output-row WSC1 fold `fold` [n, 3] (identity, mult, shift),

@@ -71,8 +71,14 @@ struct ProfState {
 	struct Pending {
 		hipEvent_t a, b;
 		int cls;
+		int64_t key;  // launch shape, 0 for none
+	};
+	struct ShapeAgg {
+		double ms = 0;
+		int64_t launches = 0, bytes = 0, ops = 0;
 	};
 	std::vector<Pending> pending;
+	std::map<int64_t, ShapeAgg> shapes;
 	std::vector<hipEvent_t> pool;
 	std::mutex mu;
 };
@@ -93,23 +99,35 @@ struct ProfScope {
 	hipStream_t s;
 	int cls;
 	hipEvent_t a = nullptr;
-	ProfScope(hipStream_t s_, int c, int64_t bytes, int64_t ops) : s(s_), cls(c) {
+	int64_t key;
+	ProfScope(hipStream_t s_, int c, int64_t bytes, int64_t ops, int64_t shape_key = 0) : s(s_), cls(c), key(shape_key) {
 		if (!g_prof.on) return;
 		a = prof_event();
 		ck(hipEventRecord(a, s));
 		g_prof.bytes[c] += bytes;
 		g_prof.ops[c] += ops;
 		g_prof.launches[c] += 1;
+		if (key) {
+			auto& sa = g_prof.shapes[key];
+			sa.launches += 1;
+			sa.bytes += bytes;
+			sa.ops += ops;
+		}
 	}
 	~ProfScope() {
 		if (!a) return;
 		hipEvent_t b = prof_event();
 		(void)hipEventRecord(b, s);
-		g_prof.pending.push_back({a, b, cls});
+		g_prof.pending.push_back({a, b, cls, key});
 	}
 };
 
 bool prof_enabled() { return g_prof.on; }
+
+// (class, M, N, K) packed as class << 56 | M << 40 | N << 20 | K (M < 65536, N and K < 2^20)
+int64_t profile_shape_key(int cls, int64_t M, int64_t N, int64_t K) {
+	return ((int64_t)cls << 56) | (M << 40) | (N << 20) | K;
+}
 
 void prof_collect() {
 	if (g_prof.pending.empty()) return;
@@ -118,6 +136,7 @@ void prof_collect() {
 		float ms = 0;
 		(void)hipEventElapsedTime(&ms, p.a, p.b);
 		g_prof.ms[p.cls] += ms;
+		if (p.key) g_prof.shapes[p.key].ms += ms;
 		g_prof.pool.push_back(p.a);
 		g_prof.pool.push_back(p.b);
 	}
@@ -272,7 +291,7 @@ Segment funnel_seg(int n0, int n1, int32_t* out, int ld, uint32_t* mx, const int
 void run_gemm(sslm_model m, Track& w, const GemmArgs& g, int cls) {
 	const int64_t out_bytes = g.epi.argmax_key ? 0 : (int64_t)g.M * g.N * 4;
 	ProfScope p(w.stream, cls, (int64_t)g.N * g.K + (int64_t)g.M * g.K + 12LL * g.N + out_bytes,
-	            2LL * g.M * g.N * g.K);
+	            2LL * g.M * g.N * g.K, profile_shape_key(cls, g.M, g.N, g.K));
 	sslm_launch::gemm(g, w.stream);
 	ck(hipGetLastError());
 }
@@ -330,8 +349,103 @@ void run_lora_u(sslm_model m, Track& w, sslm_adapter ad, int layer, const int* p
 	ck(hipGetLastError());
 }
 
-// The stream (committed hidden state) a launch sequence reads and commits: decode batches use the
-// per-slot state, prefill chunks the chunk rows.
+// The projections' GEMM arguments (forward_sites.cpp:1699-1735, :1907-1914, :1938-1955,
+// :1969-1977), shared by the layer loop and the GEMV benchmark entry.  split_raw() decides
+// whether the consumer adds split-K planes.
+struct ProjArgs {
+	GemmArgs g;
+	RawIn raw;
+};
+
+ProjArgs qkv_args(sslm_model m, Track& w, int l, int M, sslm_adapter ad) {
+	const DevLayer& lw = m->layers[l];
+	const int H = m->H, KVH = m->KVH;
+	GemmArgs g = gemm_args(m, w, w.normed, M, H, lw.w_qkv, H + 2 * KVH, H);
+	g.epi.layer = l;
+	g.epi.in_recip = w.normed_recip;
+	g.epi.in_scale = w.normed_scale;
+	g.epi.rank = ad ? (int)ad->rank : 0;
+	g.epi.nseg = 3;
+	g.epi.seg[0] = funnel_seg(0, H, w.q_f, H, w.mx_q, lw.f_qkv, lw.b_q);
+	Segment sk{};
+	sk.n_begin = H;
+	sk.n_end = H + KVH;
+	sk.mode = kSegWide;
+	sk.out = w.kv_f;
+	sk.ld_out = 2 * KVH;
+	sk.fold = lw.f_qkv + 3 * H;
+	sk.bias = lw.b_k;
+	Segment sv = sk;
+	sv.n_begin = H + KVH;
+	sv.n_end = H + 2 * KVH;
+	sv.out = w.kv_f + KVH;
+	sv.fold = lw.f_qkv + 3 * (H + KVH);
+	sv.bias = lw.b_v;
+	g.epi.seg[1] = sk;
+	g.epi.seg[2] = sv;
+	attach_lora(m, w, ad, l, 0, &g.epi.seg[0], 0);
+	attach_lora(m, w, ad, l, 1, &g.epi.seg[1], 1);
+	attach_lora(m, w, ad, l, 2, &g.epi.seg[2], 2);
+	ProjArgs pa{g, RawIn{}};
+	pa.raw = split_raw(m, w, pa.g, H <= 4096);
+	return pa;
+}
+
+ProjArgs o_args(sslm_model m, Track& w, int l, int M, sslm_adapter ad) {
+	const DevLayer& lw = m->layers[l];
+	const int H = m->H;
+	GemmArgs g = gemm_args(m, w, w.ctx, M, H, lw.w_o, H, H);
+	g.epi.layer = l;
+	g.epi.rank = ad ? (int)ad->rank : 0;
+	g.epi.nseg = 1;
+	g.epi.seg[0] = funnel_seg(0, H, w.o_f, H, w.mx_o, lw.f_o, nullptr);
+	attach_lora(m, w, ad, l, 3, &g.epi.seg[0], 0);
+	ProjArgs pa{g, RawIn{}};
+	pa.raw = split_raw(m, w, pa.g, H <= 6144);
+	return pa;
+}
+
+ProjArgs gu_args(sslm_model m, Track& w, int l, int M, sslm_adapter ad) {
+	const DevLayer& lw = m->layers[l];
+	const int H = m->H, I = m->I;
+	GemmArgs g = gemm_args(m, w, w.mlp_normed, M, H, lw.w_gu, 2 * I, H);
+	g.epi.layer = l;
+	g.epi.rank = ad ? (int)ad->rank : 0;
+	g.epi.nseg = 2;
+	g.epi.seg[0] = funnel_seg(0, I, w.gu_f, 2 * I, w.mx_gu, lw.f_gu, nullptr);
+	g.epi.seg[1] = funnel_seg(I, 2 * I, w.gu_f + I, 2 * I, w.mx_gu, lw.f_gu + 3 * I, nullptr);
+	attach_lora(m, w, ad, l, 4, &g.epi.seg[0], 0);
+	attach_lora(m, w, ad, l, 5, &g.epi.seg[1], 1);
+	ProjArgs pa{g, RawIn{}};
+	pa.raw = split_raw(m, w, pa.g, I <= 4096);
+	return pa;
+}
+
+ProjArgs down_args(sslm_model m, Track& w, int l, int M, sslm_adapter ad) {
+	const DevLayer& lw = m->layers[l];
+	const int H = m->H, I = m->I;
+	GemmArgs g = gemm_args(m, w, w.act, M, I, lw.w_down, H, I);
+	g.epi.layer = l;
+	g.epi.rank = ad ? (int)ad->rank : 0;
+	g.epi.nseg = 1;
+	g.epi.seg[0] = funnel_seg(0, H, w.down_f, H, w.mx_down, lw.f_down, nullptr);
+	attach_lora(m, w, ad, l, 6, &g.epi.seg[0], 0);
+	ProjArgs pa{g, RawIn{}};
+	pa.raw = split_raw(m, w, pa.g, H <= 6144);
+	return pa;
+}
+
+GemmArgs head_args(sslm_model m, Track& w, int M, const TokenInfo* tok) {
+	GemmArgs g = gemm_args(m, w, w.final_codes, M, m->H, m->head, m->V, m->H);
+	g.epi.tok = tok;
+	g.epi.argmax_key = w.argmax_key;
+	g.epi.key_ld = (m->V + 15) / 16;
+	g.epi.layer = m->L;
+	return g;
+}
+
+// The stream (committed hidden state) a launch sequence reads and commits: decode batches use
+// the per-slot state, prefill chunks the chunk rows.
 struct StreamRef {
 	int8_t* codes;
 	Scale* scale;
@@ -356,34 +470,9 @@ void run_layers(sslm_model m, Track& w, int M, StreamRef st, int l0, int l1, ssl
 		{
 			const int pj[3] = {0, 1, 2};
 			run_lora_u(m, w, ad, l, pj, 3, w.normed, M, H);
-			GemmArgs g = gemm_args(m, w, w.normed, M, H, lw.w_qkv, H + 2 * KVH, H);
-			g.epi.layer = l;
-			g.epi.in_recip = w.normed_recip;
-			g.epi.in_scale = w.normed_scale;
-			g.epi.rank = ad ? (int)ad->rank : 0;
-			g.epi.nseg = 3;
-			g.epi.seg[0] = funnel_seg(0, H, w.q_f, H, w.mx_q, lw.f_qkv, lw.b_q);
-			Segment sk{};
-			sk.n_begin = H;
-			sk.n_end = H + KVH;
-			sk.mode = kSegWide;
-			sk.out = w.kv_f;
-			sk.ld_out = 2 * KVH;
-			sk.fold = lw.f_qkv + 3 * H;
-			sk.bias = lw.b_k;
-			Segment sv = sk;
-			sv.n_begin = H + KVH;
-			sv.n_end = H + 2 * KVH;
-			sv.out = w.kv_f + KVH;
-			sv.fold = lw.f_qkv + 3 * (H + KVH);
-			sv.bias = lw.b_v;
-			g.epi.seg[1] = sk;
-			g.epi.seg[2] = sv;
-			attach_lora(m, w, ad, l, 0, &g.epi.seg[0], 0);
-			attach_lora(m, w, ad, l, 1, &g.epi.seg[1], 1);
-			attach_lora(m, w, ad, l, 2, &g.epi.seg[2], 2);
-			raw = split_raw(m, w, g, H <= 4096);
-			run_gemm(m, w, g, kProfGemm);
+			ProjArgs pa = qkv_args(m, w, l, M, ad);
+			raw = pa.raw;
+			run_gemm(m, w, pa.g, kProfGemm);
 		}
 		{
 			sslm_launch::QkvPostArgs a{};
@@ -467,14 +556,9 @@ void run_layers(sslm_model m, Track& w, int M, StreamRef st, int l0, int l1, ssl
 		{  // o_proj (forward_sites.cpp:1907-1914)
 			const int pj[1] = {3};
 			run_lora_u(m, w, ad, l, pj, 1, w.ctx, M, H);
-			GemmArgs g = gemm_args(m, w, w.ctx, M, H, lw.w_o, H, H);
-			g.epi.layer = l;
-			g.epi.rank = ad ? (int)ad->rank : 0;
-			g.epi.nseg = 1;
-			g.epi.seg[0] = funnel_seg(0, H, w.o_f, H, w.mx_o, lw.f_o, nullptr);
-			attach_lora(m, w, ad, l, 3, &g.epi.seg[0], 0);
-			raw = split_raw(m, w, g, H <= 6144);
-			run_gemm(m, w, g, kProfGemm);
+			ProjArgs pa = o_args(m, w, l, M, ad);
+			raw = pa.raw;
+			run_gemm(m, w, pa.g, kProfGemm);
 		}
 		{  // attn residual -> mlp norm (forward_sites.cpp:1923-1936)
 			sslm_launch::ResidualArgs a{};
@@ -507,16 +591,9 @@ void run_layers(sslm_model m, Track& w, int M, StreamRef st, int l0, int l1, ssl
 		{  // gate | up (forward_sites.cpp:1938-1955)
 			const int pj[2] = {4, 5};
 			run_lora_u(m, w, ad, l, pj, 2, w.mlp_normed, M, H);
-			GemmArgs g = gemm_args(m, w, w.mlp_normed, M, H, lw.w_gu, 2 * I, H);
-			g.epi.layer = l;
-			g.epi.rank = ad ? (int)ad->rank : 0;
-			g.epi.nseg = 2;
-			g.epi.seg[0] = funnel_seg(0, I, w.gu_f, 2 * I, w.mx_gu, lw.f_gu, nullptr);
-			g.epi.seg[1] = funnel_seg(I, 2 * I, w.gu_f + I, 2 * I, w.mx_gu, lw.f_gu + 3 * I, nullptr);
-			attach_lora(m, w, ad, l, 4, &g.epi.seg[0], 0);
-			attach_lora(m, w, ad, l, 5, &g.epi.seg[1], 1);
-			raw = split_raw(m, w, g, I <= 4096);
-			run_gemm(m, w, g, kProfGemm);
+			ProjArgs pa = gu_args(m, w, l, M, ad);
+			raw = pa.raw;
+			run_gemm(m, w, pa.g, kProfGemm);
 		}
 		{
 			sslm_launch::ActArgs a{};
@@ -542,14 +619,9 @@ void run_layers(sslm_model m, Track& w, int M, StreamRef st, int l0, int l1, ssl
 		{  // down_proj (forward_sites.cpp:1969-1977)
 			const int pj[1] = {6};
 			run_lora_u(m, w, ad, l, pj, 1, w.act, M, I);
-			GemmArgs g = gemm_args(m, w, w.act, M, I, lw.w_down, H, I);
-			g.epi.layer = l;
-			g.epi.rank = ad ? (int)ad->rank : 0;
-			g.epi.nseg = 1;
-			g.epi.seg[0] = funnel_seg(0, H, w.down_f, H, w.mx_down, lw.f_down, nullptr);
-			attach_lora(m, w, ad, l, 6, &g.epi.seg[0], 0);
-			raw = split_raw(m, w, g, H <= 6144);
-			run_gemm(m, w, g, kProfGemm);
+			ProjArgs pa = down_args(m, w, l, M, ad);
+			raw = pa.raw;
+			run_gemm(m, w, pa.g, kProfGemm);
 		}
 		{  // mlp residual -> commit -> next layer's attn norm (forward_sites.cpp:1982-2009)
 			sslm_launch::ResidualArgs a{};
@@ -596,11 +668,7 @@ void run_logits(sslm_model m, Track& w, int M, StreamRef st, const TokenInfo* to
 		sslm_launch::rmsnorm(a, M, m->H, tok, m->status, m->L, s);
 		ck(hipGetLastError());
 	}
-	GemmArgs g = gemm_args(m, w, w.final_codes, M, m->H, m->head, m->V, m->H);
-	g.epi.tok = tok;
-	g.epi.argmax_key = w.argmax_key;
-	g.epi.key_ld = (m->V + 15) / 16;
-	g.epi.layer = m->L;
+	GemmArgs g = head_args(m, w, M, tok);
 	run_gemm(m, w, g, kProfHead);
 	sslm_launch::argmax_finalize(w.argmax_key, (m->V + 15) / 16, M, w.out_tokens, s);
 	ck(hipGetLastError());
@@ -1212,10 +1280,12 @@ sslm_status sslm_prefill(sslm_model model, sslm_seq seq, const int32_t* tokens, 
 	});
 }
 
-// Decode tokens are independent, so a batch's layer work is dealt to up to kTracks streams as
-// token groups of at least track_min() tokens each: while one group runs its latency-bound row
-// kernels on a few CUs, another's GEMVs fill the rest of the chip.  Everything -- embeds,
-// layers, the joined LM head and the status read-back -- is one submission with one host sync.
+// Decode tokens are independent, so a batch's layer work can be dealt to up to kTracks streams
+// as token groups of at least track_min() tokens each, so that one group's latency-bound row
+// kernels could overlap another's GEMVs.  Measured on MI355X this is slower than one group (the
+// groups' kernels do not overlap usefully), so one track is the default and SSLM_HIP_TRACKS
+// opts in.  Everything -- embeds, layers, the joined LM head and the status read-back -- is one
+// submission with one host sync.
 bool graphs_enabled() {
 	static const bool v = [] {
 		const char* e = getenv("SSLM_HIP_GRAPHS");
@@ -1228,7 +1298,7 @@ constexpr size_t kGraphCache = 64;
 int track_limit() {
 	static const int v = [] {
 		const char* e = getenv("SSLM_HIP_TRACKS");
-		const int x = e ? atoi(e) : kTracks;
+		const int x = e ? atoi(e) : 1;
 		return std::max(1, std::min(kTracks, x));
 	}();
 	return v;
@@ -1760,13 +1830,71 @@ sslm_status sslm_hip_copy(void* dst, const void* src, size_t bytes, int kind) {
 
 sslm_status sslm_hip_synchronize(void) { return hipDeviceSynchronize() == hipSuccess ? SSLM_OK : SSLM_INVALID_ARGUMENT; }
 
+
+int32_t sslm_hip_bench_decode_gemv(sslm_model model, int32_t M, int32_t iters, double* us, int64_t* bytes,
+                                   int64_t* shapes, int32_t cap) {
+	if (!model || M < 1 || M > 64 || iters < 1 || cap < 5) return -1;
+	sslm_model m = model;
+	std::lock_guard<std::mutex> lk(m->mu);
+	int32_t n = 0;
+	const sslm_status st = guarded([&]() -> sslm_status {
+		Track& w = m->tracks[0];
+		std::vector<TokenInfo> ti(M);
+		for (int t = 0; t < M; ++t) ti[t] = TokenInfo{0, t, 0};
+		ck(hipMemcpyAsync(w.tok, ti.data(), M * sizeof(TokenInfo), hipMemcpyHostToDevice, w.stream));
+		ck(hipMemcpyAsync(w.lg_tok, ti.data(), M * sizeof(TokenInfo), hipMemcpyHostToDevice, w.stream));
+		std::vector<GemmArgs> gs = {qkv_args(m, w, 0, M, nullptr).g, o_args(m, w, 0, M, nullptr).g,
+		                            gu_args(m, w, 0, M, nullptr).g, down_args(m, w, 0, M, nullptr).g,
+		                            head_args(m, w, M, w.lg_tok)};
+		hipEvent_t a, b;
+		ck(hipEventCreate(&a));
+		ck(hipEventCreate(&b));
+		for (const GemmArgs& g : gs) {
+			for (int i = 0; i < 3; ++i) sslm_launch::gemm(g, w.stream);
+			ck(hipEventRecord(a, w.stream));
+			for (int i = 0; i < iters; ++i) sslm_launch::gemm(g, w.stream);
+			ck(hipEventRecord(b, w.stream));
+			ck(hipEventSynchronize(b));
+			float ms = 0;
+			ck(hipEventElapsedTime(&ms, a, b));
+			const int64_t out_bytes = g.epi.argmax_key ? 0 : (int64_t)g.M * g.N * 4;
+			us[n] = ms * 1e3 / iters;
+			bytes[n] = (int64_t)g.N * g.K + (int64_t)g.M * g.K + 12LL * g.N + out_bytes;
+			shapes[n] = ((int64_t)g.N << 20) | g.K;
+			++n;
+		}
+		(void)hipEventDestroy(a);
+		(void)hipEventDestroy(b);
+		ck(hipStreamSynchronize(w.stream));
+		return SSLM_OK;
+	});
+	return st == SSLM_OK ? n : -1;
+}
+
 // ---- profiling ----
 void sslm_hip_profile_enable(int on) { g_prof.on = on != 0; }
 void sslm_hip_profile_reset(void) {
+	prof_collect();
 	for (int i = 0; i < SSLM_HIP_PROFILE_CLASSES; ++i) {
 		g_prof.ms[i] = 0;
 		g_prof.launches[i] = g_prof.bytes[i] = g_prof.ops[i] = 0;
 	}
+	g_prof.shapes.clear();
+}
+int sslm_hip_profile_shapes(int64_t* keys, double* ms, int64_t* launches, int64_t* bytes, int64_t* ops, int cap) {
+	prof_collect();
+	int n = 0;
+	for (auto& kv : g_prof.shapes) {
+		if (n < cap) {
+			if (keys) keys[n] = kv.first;
+			if (ms) ms[n] = kv.second.ms;
+			if (launches) launches[n] = kv.second.launches;
+			if (bytes) bytes[n] = kv.second.bytes;
+			if (ops) ops[n] = kv.second.ops;
+		}
+		++n;
+	}
+	return n;
 }
 void sslm_hip_profile_read(double* ms, int64_t* launches, int64_t* bytes, int64_t* ops, int classes) {
 	prof_collect();

@@ -29,6 +29,10 @@ class Device:
     def zeros(self, shape, dtype) -> "DeviceArray":
         return self.upload(np.zeros(shape, dtype=dtype))
 
+    def copy_device(self, dst: "DeviceArray", src: "DeviceArray"):
+        n = min(dst.nbytes, src.nbytes)
+        self.lib.check("copy d2d", self.lib.lib.sslm_hip_copy(dst.ptr, src.ptr, n, 2))
+
 
 class DeviceArray:
     def __init__(self, dev: Device, shape, dtype):
