@@ -195,7 +195,8 @@ int sslm_hip_profile_shapes(int64_t* keys, double* ms, int64_t* launches, int64_
  * `site_m/site_e` (reference src/matmul.cpp:466-509 + forward_sites.cpp:461-470 +
  * checked_chain_funnel.cpp:257-364).  Writes int8 codes [m, n] and per-row scales
  * out_me[2*t] = m, out_me[2*t+1] = e, and per-row status (0 = Ok, else the reference's
- * SslmForwardStatus value).  All pointers are device pointers; synchronous. */
+ * SslmForwardStatus value).  All pointers are device pointers; synchronous.  Requires
+ * 1 <= m <= 512, k and n multiples of 16, n <= 8192 (else SSLM_INVALID_ARGUMENT). */
 sslm_status sslm_hip_gemm_requant(const int8_t* a, const int8_t* w, const int32_t* fold, int32_t m, int32_t n,
                                   int32_t k, int64_t in_m, int64_t in_e, int64_t site_m, int64_t site_e,
                                   int8_t* out_codes, int64_t* out_me, int32_t* out_status);

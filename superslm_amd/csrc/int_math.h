@@ -11,6 +11,9 @@
 #include <stdint.h>
 
 #define SSLM_HD __host__ __device__ __forceinline__
+// Rarely taken slow paths stay out of line: a kernel's latency-bound row code runs once per
+// launch from a cold instruction cache, so its size costs more than a call on the rare path.
+#define SSLM_COLD __host__ __device__ inline __attribute__((noinline))
 
 namespace sslm {
 
@@ -86,7 +89,7 @@ SSLM_HD int64_t normalize_scale(int64_t d_prime, int* s_out) {
 }
 
 // src/intmath.cpp:303-333 -- 3 Newton steps from a minimax seed, 2 correction steps.
-SSLM_HD int64_t reciprocal(int64_t dn) {
+SSLM_COLD int64_t reciprocal(int64_t dn) {
 	const int64_t c32 = (2 * ((int64_t)48 << 31) + 17) / 34;
 	const int64_t c32_2 = (2 * ((int64_t)32 << 31) + 17) / 34;
 	int64_t y = c32 - ((c32_2 * dn) >> 31);
@@ -109,9 +112,11 @@ SSLM_HD int64_t reciprocal(int64_t dn) {
 // Exact floor(n / d) for 0 <= n < 2^63, d >= 1: a double-precision estimate (off by at most one
 // for these magnitudes) corrected with exact 128-bit residue checks.  Replaces the long 64-bit
 // integer division sequence on the GPU; the result is the integer quotient bit for bit.
+SSLM_COLD int64_t div_i64_cold(int64_t n, int64_t d) { return n / d; }
+
 SSLM_HD int64_t div_floor_pos(int64_t n, int64_t d) {
 	int64_t q = (int64_t)((double)n / (double)d);
-	if (q >= ((int64_t)1 << 51)) return n / d;  // estimate no longer within one of the quotient
+	if (q >= ((int64_t)1 << 51)) return div_i64_cold(n, d);  // estimate no longer within one of the quotient
 	if (q < 0) q = 0;
 	s128 r = (s128)n - (s128)q * d;
 	if (r < 0) {
@@ -138,10 +143,12 @@ SSLM_HD int64_t reciprocal_fast(int64_t dn) {
 	if (dn < ((int64_t)1 << 30) || dn >= ((int64_t)1 << 31)) return reciprocal(dn);
 	int64_t y = (int64_t)(4611686018427387904.0 / (double)dn);
 	for (int i = 0; i < 2; ++i) {  // the reference's correction rule: -dn <= 2(2^62 - y dn) < dn
-		s128 res2 = ((s128)((int64_t)1 << 62) - (s128)y * (s128)dn) * 2;
-		if (res2 >= (s128)dn) {
+		// y is within a few units of 2^62 / dn < 2^32, so y * dn < 2^63 and the residue is small:
+		// 64-bit arithmetic is exact here
+		const int64_t res2 = (((int64_t)1 << 62) - y * dn) * 2;
+		if (res2 >= dn) {
 			y += 1;
-		} else if (res2 < -(s128)dn) {
+		} else if (res2 < -dn) {
 			y -= 1;
 		}
 	}
@@ -259,30 +266,57 @@ struct FunnelPlan {
 	Scale out;
 };
 
-SSLM_HD int32_t funnel_plan(uint64_t d_prime, const Scale* incoming, int n_in, Scale site, FunnelPlan* plan) {
-	for (int i = 0; i < n_in; ++i)
-		if (!fits_i32(incoming[i].m)) return kCarriedScaleMantissaOutOfDomain;
-	if (!fits_i32(site.m)) return kCarriedScaleMantissaOutOfDomain;
+struct FunnelOut {
+	int32_t st;
+	int32_t s;
+	int64_t r;
+	Scale out;
+};
+
+// By-value form with at most two incoming factors, kept out of line: every row kernel evaluates
+// two or three plans, and one shared copy is cheaper than inlined ones.
+SSLM_COLD FunnelOut funnel_plan_v(uint64_t d_prime, int n_in, Scale in0, Scale in1, Scale site) {
+	FunnelOut o{};
+	o.st = kCarriedScaleMantissaOutOfDomain;
+	if ((n_in > 0 && !fits_i32(in0.m)) || (n_in > 1 && !fits_i32(in1.m))) return o;
+	if (!fits_i32(site.m)) return o;
 	if (d_prime < 1) d_prime = 1;
-	if (d_prime > ((uint64_t)1 << 31)) return kChainInputOutOfDomain;
-	int s;
-	int64_t dn = normalize_scale((int64_t)d_prime, &s);
-	int64_t r = reciprocal_fast(dn);
-	Scale run;
-	bool have = false;
-	for (int i = 0; i < n_in; ++i) {
-		run = have ? combine_scale(run, incoming[i]) : incoming[i];
-		have = true;
-		if (!fits_i32(run.m)) return kCarriedScaleMantissaOutOfDomain;
+	if (d_prime > ((uint64_t)1 << 31)) {
+		o.st = kChainInputOutOfDomain;
+		return o;
 	}
-	run = have ? combine_scale(run, site) : site;
-	if (!fits_i32(run.m)) return kCarriedScaleMantissaOutOfDomain;
+	int s;
+	const int64_t dn = normalize_scale((int64_t)d_prime, &s);
+	const int64_t r = reciprocal_fast(dn);
+	Scale run = site;
+	if (n_in > 0) {
+		run = in0;
+		if (n_in > 1) {
+			run = combine_scale(run, in1);
+			if (!fits_i32(run.m)) return o;
+		}
+		run = combine_scale(run, site);
+	}
+	if (!fits_i32(run.m)) return o;
 	run = combine_scale(run, Scale{dn, -(int64_t)s});
-	if (!fits_i32(run.m)) return kCarriedScaleMantissaOutOfDomain;
-	plan->r = r;
-	plan->s = s;
-	plan->out = run;
-	return kOk;
+	if (!fits_i32(run.m)) return o;
+	o.st = kOk;
+	o.s = s;
+	o.r = r;
+	o.out = run;
+	return o;
+}
+
+// n_in <= 2 (every site of the forward path)
+SSLM_HD int32_t funnel_plan(uint64_t d_prime, const Scale* incoming, int n_in, Scale site, FunnelPlan* plan) {
+	const Scale z{0, 0};
+	const FunnelOut o = funnel_plan_v(d_prime, n_in, n_in > 0 ? incoming[0] : z, n_in > 1 ? incoming[1] : z, site);
+	if (o.st == kOk) {
+		plan->r = o.r;
+		plan->s = o.s;
+		plan->out = o.out;
+	}
+	return o.st;
 }
 
 // forward_sites.cpp:389-395
@@ -296,8 +330,8 @@ SSLM_HD int64_t composed_exponent(int64_t e_a, int64_t e_t) {
 // forward_sites.cpp:513-653 -- round_away(branch*m_a*r_t / 2^k), k = 62-(e_a-e_t); a negative k
 // is an exact left shift.  *clamped: the saturation-counter predicate; *exceeded: the true
 // magnitude does not fit int64.
-SSLM_HD int64_t landing_rescale(int64_t branch, int64_t m_a, int64_t r_t, int64_t k, bool* clamped,
-                                 bool* exceeded) {
+SSLM_COLD int64_t landing_rescale(int64_t branch, int64_t m_a, int64_t r_t, int64_t k, bool* clamped,
+                                   bool* exceeded) {
 	bool neg = (branch < 0) != (m_a < 0);
 	uint64_t ab = branch < 0 ? (~(uint64_t)branch + 1u) : (uint64_t)branch;
 	uint64_t am = m_a < 0 ? (~(uint64_t)m_a + 1u) : (uint64_t)m_a;
@@ -483,7 +517,8 @@ SSLM_HD int64_t softmax_ceiling(int64_t q_b, int64_t q_c) {
 // src/intmath.cpp:381-418 + checked_chain_funnel.cpp:454-482: the bias term
 // round_away(b*r_a / 2^(30+62+e_a)); false when the exponent or the sum with `acc` is out of
 // domain.
-SSLM_HD bool bias_term(int64_t b, int64_t r_a, int64_t e_a, int64_t acc, int64_t* out) {
+// The general form on 128-bit products (any bias code).
+SSLM_COLD bool bias_term_wide(int64_t b, int64_t r_a, int64_t e_a, int64_t acc, int64_t* out) {
 	s128 sum = (s128)30 + 62 + (s128)e_a;
 	if (sum < 0 || sum > 63) return false;
 	int exponent = (int)sum;
@@ -495,6 +530,25 @@ SSLM_HD bool bias_term(int64_t b, int64_t r_a, int64_t e_a, int64_t acc, int64_t
 	if (rounded != (s128)(int64_t)rounded) return false;
 	int64_t term = (int64_t)rounded;
 	uint64_t s = (uint64_t)acc + (uint64_t)term;
+	if (((((uint64_t)acc ^ (uint64_t)term) >> 63) == 0) && ((((uint64_t)acc ^ s) >> 63) != 0)) return false;
+	*out = term;
+	return true;
+}
+
+// Same result; |b| < 2^30 with 0 <= r_a <= 2^33 (every bias of a real artifact against a
+// reciprocal of a canonical mantissa) keeps b * r_a inside int64, so the common case needs no
+// 128-bit arithmetic.
+SSLM_HD bool bias_term(int64_t b, int64_t r_a, int64_t e_a, int64_t acc, int64_t* out) {
+	const uint64_t ab = b < 0 ? (uint64_t)0 - (uint64_t)b : (uint64_t)b;
+	if (ab >= ((uint64_t)1 << 30) || r_a < 0 || r_a > ((int64_t)1 << 33)) return bias_term_wide(b, r_a, e_a, acc, out);
+	if (e_a < -92 || e_a > -29) return false;  // exponent 92 + e_a outside [0, 63]
+	const int exponent = (int)(92 + e_a);
+	const int64_t wide = b * r_a;
+	const uint64_t mask = ((uint64_t)1 << exponent) - 1u;
+	const uint64_t rem = (uint64_t)wide & mask;
+	const uint64_t thr = (mask >> 1) + (wide < 0 ? 1u : 0u);
+	const int64_t term = (wide >> exponent) + (rem > thr ? 1 : 0);
+	const uint64_t s = (uint64_t)acc + (uint64_t)term;
 	if (((((uint64_t)acc ^ (uint64_t)term) >> 63) == 0) && ((((uint64_t)acc ^ s) >> 63) != 0)) return false;
 	*out = term;
 	return true;

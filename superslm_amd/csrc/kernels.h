@@ -36,6 +36,7 @@ struct Segment {
 constexpr int kMaxRank = 64;
 constexpr int kPartLd = 512;  // token stride of the per-tile partial maxima (>= tokens per launch)
 constexpr int kMaxSeg = 3;
+constexpr int kFunnelMaxN = 8192;  // widest row the standalone funnel kernel covers
 
 struct Epilogue {
 	Segment seg[kMaxSeg];

@@ -7,6 +7,8 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cstdio>
+#include <cstdlib>
 
 #include "kernels.h"
 
@@ -77,6 +79,25 @@ struct EpiResult {
 	bool ok;
 };
 
+// LoRA delta of channel jj for token t (forward_sites.cpp:1114-1141): the adapter's B row
+// against the token's intermediate codes, amplified by the delta fold.  Out of line: adapters
+// are optional and the loop would otherwise be inlined into every epilogue element.  Plain
+// values only: a reference into the kernel arguments would make the compiler copy them to
+// scratch memory.
+__device__ __attribute__((noinline)) int64_t lora_delta_v(const int8_t* lora_b, const int8_t* lora_u,
+                                                          const int32_t* dfold, int rank, int t, int jj) {
+	const int8_t* br = lora_b + (size_t)jj * rank;
+	const int8_t* ur = lora_u + (size_t)t * kMaxRank;
+	int64_t d = 0;
+	for (int r = 0; r < rank; ++r) d += (int32_t)br[r] * (int32_t)ur[r];
+	const int32_t* df = dfold + 3 * jj;
+	return apply_amp_fold(d, df[0], df[1], df[2]);
+}
+
+__device__ __forceinline__ int64_t lora_delta(const Segment& sg, int rank, int t, int jj) {
+	return lora_delta_v(sg.lora_b, sg.lora_u, sg.lora_dfold, rank, t, jj);
+}
+
 __device__ __forceinline__ EpiResult epi_value(const Epilogue& e, int t, int j, int32_t acc) {
 	int si = 0;
 	while (si + 1 < e.nseg && j >= e.seg[si].n_end) ++si;
@@ -85,12 +106,7 @@ __device__ __forceinline__ EpiResult epi_value(const Epilogue& e, int t, int j, 
 	const int32_t* f = sg.fold + 3 * jj;
 	int64_t v = apply_fold((int64_t)acc, f[0], f[1], f[2]);
 	if (sg.lora_b) {
-		const int8_t* br = sg.lora_b + (size_t)jj * e.rank;
-		const int8_t* ur = sg.lora_u + (size_t)t * kMaxRank;
-		int64_t d = 0;
-		for (int r = 0; r < e.rank; ++r) d += (int32_t)br[r] * (int32_t)ur[r];
-		const int32_t* df = sg.lora_dfold + 3 * jj;
-		v += apply_amp_fold(d, df[0], df[1], df[2]);
+		v += lora_delta(sg, e.rank, t, jj);
 	}
 	bool ok = true;
 	if (sg.bias) {
@@ -163,6 +179,44 @@ __device__ __forceinline__ void epi_publish(const Epilogue& e, int tile, int t, 
 // epilogue; with several, each split stores its raw partial plane and the consumer adds them
 // (no cross-block synchronisation inside the kernel).
 // ------------------------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t dpp_max16(uint32_t v) {
+	// row_ror:8, 4, 2, 1 -- every lane of the 16-lane row ends with the row maximum
+	uint32_t w = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x128, 0xf, 0xf, false);
+	v = w > v ? w : v;
+	w = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x124, 0xf, 0xf, false);
+	v = w > v ? w : v;
+	w = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x122, 0xf, 0xf, false);
+	v = w > v ? w : v;
+	w = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x121, 0xf, 0xf, false);
+	return w > v ? w : v;
+}
+
+// Refused bias reconciles in the decode GEMV epilogue (rare; out of line): bit v of `mask` marks
+// token t0 + v.
+__device__ __attribute__((noinline)) void set_status_rows(int32_t* status, const TokenInfo* tok, int32_t layer, int t0,
+                                                         uint32_t mask) {
+	for (int v = 0; v < 4; ++v)
+		if (mask >> v & 1) set_status(status, tok[t0 + v].slot, layer, kBiasReconcileProductOutOfDomain);
+}
+
+// The fields of segment `si` (wave-uniform) that the decode GEMV epilogue uses, selected with
+// constant indices so they stay scalar kernel-argument loads.
+struct SegView {
+	int32_t n_begin, mode, ld_out;
+	void* out;
+	uint32_t* maxpart;
+	const int32_t* fold;
+	const int64_t* bias;
+	const int8_t* lora_b;
+	const int32_t* lora_dfold;
+	const int8_t* lora_u;
+};
+
+__device__ __forceinline__ SegView seg_view(const Epilogue& e, int si) {
+	const Segment& s = si == 0 ? e.seg[0] : (si == 1 ? e.seg[1] : e.seg[2]);
+	return SegView{s.n_begin, s.mode, s.ld_out, s.out, s.maxpart, s.fold, s.bias, s.lora_b, s.lora_dfold, s.lora_u};
+}
+
 constexpr int kGemvWaves = 4;
 
 template <int MB, int TPW, int CPW>
@@ -181,7 +235,7 @@ __global__ __launch_bounds__(64 * kGemvWaves) void k_gemv(GemmArgs g, int cps) {
 	for (int tt = 0; tt < TPW; ++tt) {
 		const int col = (tile0 + tt) * 16 + ri;
 		col_ok[tt] = col < g.N;
-		wrow[tt] = g.w + (size_t)(col_ok[tt] ? col : 0) * g.K + grp * 32;
+		wrow[tt] = g.w + (size_t)(col_ok[tt] ? col : g.N - 1) * g.K + grp * 32;
 	}
 	const int8_t* arow[MB];
 	bool row_ok[MB];
@@ -189,7 +243,33 @@ __global__ __launch_bounds__(64 * kGemvWaves) void k_gemv(GemmArgs g, int cps) {
 	for (int mb = 0; mb < MB; ++mb) {
 		const int r = mb * 16 + ri;
 		row_ok[mb] = r < g.M;
-		arow[mb] = g.a + (size_t)(row_ok[mb] ? r : 0) * g.lda + grp * 32;
+		arow[mb] = g.a + (size_t)(row_ok[mb] ? r : g.M - 1) * g.lda + grp * 32;
+	}
+	// The projection epilogue's parameters for the tile this wave finishes (MB * TPW <=
+	// kGemvWaves: one (mb, tile) per wave) are fetched now, so they arrive with the weights.
+	// Segment bounds are multiples of 16, so the segment is uniform over the tile and is chosen
+	// with wave-uniform values; the loads are unconditional, from always-valid addresses (the
+	// weights stand in for unused values), so no branch join waits on them before the loop.
+	const Epilogue& e = g.epi;
+	const int o_mine = __builtin_amdgcn_readfirstlane(wave);
+	const bool proj = g.splits <= 1 && !e.raw_out && !e.argmax_key && o_mine < MB * TPW;
+	int si = 0;
+	if (proj) {
+		const int jt = (tile0 + o_mine % TPW) * 16;
+		while (si + 1 < e.nseg && jt >= e.seg[si].n_end) ++si;
+	}
+	const SegView sg = seg_view(e, si);
+	const bool p_lora = proj && sg.lora_b != nullptr, p_bias = proj && sg.bias != nullptr;
+	const int jj0 = min((tile0 + o_mine % TPW) * 16 + ri, g.N - 1) - (proj ? sg.n_begin : 0);
+	const int32_t* fp = proj ? sg.fold + 3 * jj0 : (const int32_t*)g.w;
+	const int32_t p_f0 = fp[0], p_f1 = fp[1], p_f2 = fp[2];
+	const int64_t p_b = *(p_bias ? sg.bias + jj0 : (const int64_t*)g.w);
+	int64_t p_rcp[4], p_ein[4];
+#pragma unroll
+	for (int v = 0; v < 4; ++v) {
+		const int t = min((o_mine / TPW) * 16 + grp * 4 + v, g.M - 1);
+		p_rcp[v] = *(p_bias ? e.in_recip + t : (const int64_t*)g.w);
+		p_ein[v] = (p_bias ? e.in_scale + t : (const Scale*)g.w)->e;
 	}
 	v4i acc[MB][TPW];
 #pragma unroll
@@ -199,65 +279,104 @@ __global__ __launch_bounds__(64 * kGemvWaves) void k_gemv(GemmArgs g, int cps) {
 	for (int base = c_begin + wave; base < c_end; base += kGemvWaves * CPW) {
 		v4i b[CPW][TPW][2], x[CPW][MB][2];
 #pragma unroll
-		for (int i = 0; i < CPW; ++i) {
-			const int c = base + i * kGemvWaves;
-			const bool ok = c < c_end;
+		for (int i = 0; i < CPW; ++i) {  // clamped, unconditional loads; out-of-range chunks add 0
+			const int c = min(base + i * kGemvWaves, c_end - 1);
 #pragma unroll
 			for (int tt = 0; tt < TPW; ++tt) {
-				b[i][tt][0] = ok && col_ok[tt] ? load16(wrow[tt] + (size_t)c * 128) : z;
-				b[i][tt][1] = ok && col_ok[tt] ? load16(wrow[tt] + (size_t)c * 128 + 16) : z;
+				b[i][tt][0] = load16(wrow[tt] + (size_t)c * 128);
+				b[i][tt][1] = load16(wrow[tt] + (size_t)c * 128 + 16);
 			}
 #pragma unroll
 			for (int mb = 0; mb < MB; ++mb) {
-				x[i][mb][0] = ok && row_ok[mb] ? load16(arow[mb] + (size_t)c * 128) : z;
-				x[i][mb][1] = ok && row_ok[mb] ? load16(arow[mb] + (size_t)c * 128 + 16) : z;
+				x[i][mb][0] = load16(arow[mb] + (size_t)c * 128);
+				x[i][mb][1] = load16(arow[mb] + (size_t)c * 128 + 16);
 			}
 		}
 #pragma unroll
-		for (int i = 0; i < CPW; ++i)
+		for (int i = 0; i < CPW; ++i) {
+			const bool ok = base + i * kGemvWaves < c_end;
 #pragma unroll
-			for (int mb = 0; mb < MB; ++mb)
+			for (int mb = 0; mb < MB; ++mb) {
+				const v4i x0 = ok && row_ok[mb] ? x[i][mb][0] : z, x1 = ok && row_ok[mb] ? x[i][mb][1] : z;
 #pragma unroll
 				for (int tt = 0; tt < TPW; ++tt) {
-					acc[mb][tt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(x[i][mb][0], b[i][tt][0], acc[mb][tt], 0, 0, 0);
-					acc[mb][tt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(x[i][mb][1], b[i][tt][1], acc[mb][tt], 0, 0, 0);
+					acc[mb][tt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(x0, b[i][tt][0], acc[mb][tt], 0, 0, 0);
+					acc[mb][tt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(x1, b[i][tt][1], acc[mb][tt], 0, 0, 0);
 				}
+			}
+		}
 	}
 #pragma unroll
 	for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
 		for (int tt = 0; tt < TPW; ++tt) red[wave][mb * TPW + tt][lane] = acc[mb][tt];
+	// Drain this wave's loads here (a wave that ran the loop has none left; one that ran no
+	// chunk still holds its prologue loads).  Without it the wait counts in the epilogue --
+	// which on this target also count stores -- are derived from the no-chunk path and end up
+	// waiting for the epilogue's own stores to be acknowledged.
+	__builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0), expcnt and lgkmcnt unconstrained
 	__syncthreads();
-	const Epilogue& e = g.epi;
-	for (int o = wave; o < MB * TPW; o += kGemvWaves) {
-		const int mb = o / TPW, tile = tile0 + o % TPW;
-		v4i tot = red[0][o][lane];
+	if (o_mine >= MB * TPW) return;
+	const int mb = o_mine / TPW, tile = tile0 + o_mine % TPW;
+	v4i tot = red[0][o_mine][lane];
 #pragma unroll
-		for (int w = 1; w < kGemvWaves; ++w) {
-			const v4i y = red[w][o][lane];
-			tot[0] += y[0];
-			tot[1] += y[1];
-			tot[2] += y[2];
-			tot[3] += y[3];
-		}
-		const int j = tile * 16 + ri;
-		if (g.splits > 1) {
+	for (int w = 1; w < kGemvWaves; ++w) {
+		const v4i y = red[w][o_mine][lane];
+		tot[0] += y[0];
+		tot[1] += y[1];
+		tot[2] += y[2];
+		tot[3] += y[3];
+	}
+	const int j = tile * 16 + ri;
+	const int t0 = mb * 16 + grp * 4;  // this lane's tokens: t0 .. t0 + 3
+	if (g.splits > 1 || e.raw_out) {
+		// raw accumulators: a split-K plane, or the whole sum for a consumer that applies the
+		// epilogue on the row
+		int32_t* dst = g.splits > 1 ? g.split_part + (size_t)split * g.M * g.N : e.raw_out;
 #pragma unroll
-			for (int v = 0; v < 4; ++v) {
-				const int t = mb * 16 + grp * 4 + v;
-				if (t < g.M && j < g.N) g.split_part[((size_t)split * g.M + t) * g.N + j] = tot[v];
+		for (int v = 0; v < 4; ++v)
+			if (t0 + v < g.M && j < g.N) dst[(size_t)(t0 + v) * g.N + j] = tot[v];
+	} else if (e.argmax_key) {
+		// per (token, 16-column tile) greedy keys: the larger logit, then the smaller index
+#pragma unroll
+		for (int v = 0; v < 4; ++v) {
+			uint64_t key = j < g.N ? ((uint64_t)((uint32_t)tot[v] ^ 0x80000000u) << 32) | (0xffffffffu - (uint32_t)j) : 0;
+			for (int o = 8; o > 0; o >>= 1) {
+				const uint64_t k2 = __shfl_xor(key, o, 16);
+				key = k2 > key ? k2 : key;
 			}
-			continue;
+			if (ri == 0 && t0 + v < g.M && tile * 16 < g.N) e.argmax_key[(size_t)(t0 + v) * e.key_ld + tile] = key;
+		}
+	} else {
+		// projection epilogue (forward_sites.cpp:1114-1141): WSC1 fold -> LoRA delta -> bias
+		// reconcile; every value first, then the stores
+		const int jj = j - sg.n_begin;
+		const int32_t mode = sg.mode;
+		int64_t val[4];
+		uint32_t mabs[4];
+		uint32_t bad = 0;
+#pragma unroll
+		for (int v = 0; v < 4; ++v) {
+			const bool live = t0 + v < g.M && j < g.N;
+			val[v] = apply_fold((int64_t)tot[v], p_f0, p_f1, p_f2);
+			if (p_lora && live) val[v] += lora_delta_v(sg.lora_b, sg.lora_u, sg.lora_dfold, e.rank, t0 + v, jj);
+			if (p_bias) {
+				int64_t term;
+				if (bias_term(p_b, p_rcp[v], p_ein[v], val[v], &term)) val[v] += term;
+				else bad |= live ? 1u << v : 0u;
+			}
+			mabs[v] = dpp_max16(live && mode == kSegFunnel ? sat_abs_u32(val[v]) : 0u);  // tile max
 		}
 #pragma unroll
 		for (int v = 0; v < 4; ++v) {
-			const int t = mb * 16 + grp * 4 + v;
-			uint64_t key = 0;
-			uint32_t mabs = 0;
-			int seg = 0;
-			if (t < g.M && j < g.N) epi_element(e, g.N, t, j, tot[v], &key, &mabs, &seg);
-			epi_publish(e, tile, t, t < g.M && tile * 16 < g.N, key, mabs, seg);
+			if (t0 + v < g.M && j < g.N) {
+				if (mode == kSegWide) ((int64_t*)sg.out)[(size_t)(t0 + v) * sg.ld_out + jj] = val[v];
+				else ((int32_t*)sg.out)[(size_t)(t0 + v) * sg.ld_out + jj] = sat_i32(val[v]);
+			}
+			if (mode == kSegFunnel && sg.maxpart && ri == 0 && t0 + v < g.M)
+				sg.maxpart[(size_t)tile * kPartLd + t0 + v] = mabs[v];
 		}
+		if (bad) set_status_rows(e.status, e.tok, e.layer, t0, bad);  // refused bias reconciles (values left unbiased)
 	}
 }
 
@@ -372,18 +491,6 @@ constexpr int kPBN = 128, kPBK = 64, kPStride = kPBK;
 // rows written whole (the global-load pattern) both spread over distinct banks, for 32- and
 // 64-bank LDS alike.
 __device__ __forceinline__ int lds_chunk(int row, int q) { return row * kPStride + ((q ^ (((row >> 1) ^ (row >> 3)) & 3)) << 4); }
-
-__device__ __forceinline__ uint32_t dpp_max16(uint32_t v) {
-	// row_ror:8, 4, 2, 1 -- every lane of the 16-lane row ends with the row maximum
-	uint32_t w = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x128, 0xf, 0xf, false);
-	v = w > v ? w : v;
-	w = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x124, 0xf, 0xf, false);
-	v = w > v ? w : v;
-	w = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x122, 0xf, 0xf, false);
-	v = w > v ? w : v;
-	w = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x121, 0xf, 0xf, false);
-	return w > v ? w : v;
-}
 
 // WSC1 fold without a branch on the identity flag (same value as apply_fold)
 __device__ __forceinline__ int64_t fold_select(int32_t acc, int32_t identity, int32_t mult, int32_t shift) {
@@ -620,6 +727,15 @@ __global__ __launch_bounds__(kRowBlock) void k_embed(const int32_t* tokens, cons
 // A slot's status is read once by thread 0 and tested after the first barrier, so the whole
 // block leaves together.
 // ------------------------------------------------------------------------------------------
+// A block reduction's result is the same in every lane; saying so (readfirstlane) lets the
+// compiler keep it, and the scalar scale plans computed from it, in scalar registers.
+__device__ __forceinline__ uint64_t uni_u64(uint64_t v) {
+	const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+	const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+	return ((uint64_t)hi << 32) | lo;
+}
+__device__ __forceinline__ int64_t uni_i64(int64_t v) { return (int64_t)uni_u64((uint64_t)v); }
+
 template <int BS>
 __device__ __forceinline__ uint64_t blk_max(uint64_t v, uint64_t* slots) {
 	v = wave_max_u64(v);
@@ -628,7 +744,7 @@ __device__ __forceinline__ uint64_t blk_max(uint64_t v, uint64_t* slots) {
 	uint64_t r = slots[0];
 #pragma unroll
 	for (int i = 1; i < BS / 64; ++i) r = slots[i] > r ? slots[i] : r;
-	return r;
+	return uni_u64(r);
 }
 
 // two maxima, one barrier; `slots` holds 2 * BS / 64 entries
@@ -648,6 +764,8 @@ __device__ __forceinline__ void blk_max2(uint64_t& x, uint64_t& y, uint64_t* slo
 		x = slots[i] > x ? slots[i] : x;
 		y = slots[BS / 64 + i] > y ? slots[BS / 64 + i] : y;
 	}
+	x = uni_u64(x);
+	y = uni_u64(y);
 }
 
 template <int BS>
@@ -658,7 +776,7 @@ __device__ __forceinline__ int64_t blk_sum(int64_t v, int64_t* slots) {
 	int64_t r = 0;
 #pragma unroll
 	for (int i = 0; i < BS / 64; ++i) r += slots[i];
-	return r;
+	return uni_i64(r);
 }
 
 template <int BS>
@@ -669,7 +787,7 @@ __device__ __forceinline__ int64_t blk_max_i64(int64_t v, int64_t* slots) {
 	int64_t r = slots[0];
 #pragma unroll
 	for (int i = 1; i < BS / 64; ++i) r = slots[i] > r ? slots[i] : r;
-	return r;
+	return uni_i64(r);
 }
 
 // this thread's share of the max over tiles [tile0, tile0 + ntiles) of a per-(tile, token)
@@ -691,7 +809,7 @@ __device__ __forceinline__ uint64_t abs_u64(int64_t v) { return v < 0 ? (uint64_
 // -- is issued before the first use, in straight-line code, so the row pays one memory round
 // trip.  Columns with live[k] false read a valid column and return 0.  Returns false when a bias
 // reconcile refused its product (epi_value's rule).
-template <int N>
+template <int N, int S>
 __device__ __forceinline__ bool raw_row(const RawIn& r, int si, int M, int t, const int (&j)[N], const bool (&live)[N],
                                         int64_t (&v)[N]) {
 	const Segment& sg = r.epi.seg[si];
@@ -706,9 +824,9 @@ __device__ __forceinline__ bool raw_row(const RawIn& r, int si, int M, int t, co
 		jj[k] = jc - sg.n_begin;
 		acc[k] = 0;
 #pragma unroll
-		for (int s2 = 0; s2 < kMaxRawSplits; ++s2) {  // clamped plane index: no branch, no extra round trip
-			const uint32_t x = (uint32_t)row[(size_t)min(s2, r.splits - 1) * plane + jc];
-			acc[k] += s2 < r.splits ? x : 0u;  // the true sum fits int32; partials wrap harmlessly
+		for (int s2 = 0; s2 < S; ++s2) {  // clamped plane index: no branch, no extra round trip
+			const uint32_t x = (uint32_t)row[(size_t)(S == 1 ? 0 : min(s2, r.splits - 1)) * plane + jc];
+			acc[k] += (S == 1 || s2 < r.splits) ? x : 0u;  // the true sum fits int32; partials wrap harmlessly
 		}
 		const int32_t* f = sg.fold + 3 * jj[k];
 		f0[k] = f[0];
@@ -728,12 +846,7 @@ __device__ __forceinline__ bool raw_row(const RawIn& r, int si, int M, int t, co
 	for (int k = 0; k < N; ++k) {
 		v[k] = apply_fold((int64_t)(int32_t)acc[k], f0[k], f1[k], f2[k]);
 		if (sg.lora_b) {
-			const int8_t* br = sg.lora_b + (size_t)jj[k] * r.epi.rank;
-			const int8_t* ur = sg.lora_u + (size_t)t * kMaxRank;
-			int64_t d = 0;
-			for (int q = 0; q < r.epi.rank; ++q) d += (int32_t)br[q] * (int32_t)ur[q];
-			const int32_t* df = sg.lora_dfold + 3 * jj[k];
-			v[k] += apply_amp_fold(d, df[0], df[1], df[2]);
+			v[k] += lora_delta(sg, r.epi.rank, t, jj[k]);
 		}
 		if (sg.bias) {
 			int64_t term;
@@ -817,7 +930,7 @@ __global__ __launch_bounds__(BS) void k_rmsnorm(sslm_launch::RowNormArgs a, int 
 // q funnel + RoPE(q); K/V landing, RoPE(K), KV write (forward_sites.cpp:1281-1418, :1748-1787).
 // The K/V landing does not depend on the q funnel, so it is computed while the q maximum is
 // reduced.  Up to 2 K (and 2 V) pairs per thread: NKV * D <= 4 * BS.
-template <int BS, int EQ, bool RAW>
+template <int BS, int EQ, int RS>
 __global__ __launch_bounds__(BS) void k_qkv_post(sslm_launch::QkvPostArgs a) {
 	__shared__ uint64_t s_red[BS / 64];
 	__shared__ int32_t s_st;
@@ -833,7 +946,7 @@ __global__ __launch_bounds__(BS) void k_qkv_post(sslm_launch::QkvPostArgs a) {
 	// q pair values
 	int2 qv[EQ];
 	uint64_t qmx = 0;
-	if (RAW) {
+	if (RS > 0) {
 		int j[2 * EQ];
 		bool live[2 * EQ];
 		int64_t v[2 * EQ];
@@ -844,7 +957,7 @@ __global__ __launch_bounds__(BS) void k_qkv_post(sslm_launch::QkvPostArgs a) {
 			j[2 * k + 1] = 2 * p + 1;
 			live[2 * k] = live[2 * k + 1] = p < H / 2;
 		}
-		const bool ok = raw_row<2 * EQ>(a.raw, 0, a.M, t, j, live, v);
+		const bool ok = raw_row<2 * EQ, RS>(a.raw, 0, a.M, t, j, live, v);
 #pragma unroll
 		for (int k = 0; k < EQ; ++k) {
 			qv[k] = make_int2(sat_i32(v[2 * k]), sat_i32(v[2 * k + 1]));
@@ -862,11 +975,11 @@ __global__ __launch_bounds__(BS) void k_qkv_post(sslm_launch::QkvPostArgs a) {
 	}
 	if (threadIdx.x == 0) s_st = a.status[ti.slot];
 	// K/V landing (LandingRescale at the normed scale, per kv head) and RoPE(K)
-	const int64_t* kv = RAW ? nullptr : a.kv_f + (size_t)t * 2 * KVH;
+	const int64_t* kv = RS > 0 ? nullptr : a.kv_f + (size_t)t * 2 * KVH;
 	int8_t kq[2][2], vq[2][2];
 	uint64_t sat = 0;
 	int64_t rk[4], rv[4];
-	if (RAW) {
+	if (RS > 0) {
 		int jk[4], jv[4];
 		bool live[4];
 #pragma unroll
@@ -878,8 +991,8 @@ __global__ __launch_bounds__(BS) void k_qkv_post(sslm_launch::QkvPostArgs a) {
 			jv[2 * k + 1] = H + KVH + 2 * p + 1;
 			live[2 * k] = live[2 * k + 1] = p < KVH / 2;
 		}
-		const bool okk = raw_row<4>(a.raw, 1, a.M, t, jk, live, rk);
-		const bool okv = raw_row<4>(a.raw, 2, a.M, t, jv, live, rv);
+		const bool okk = raw_row<4, RS>(a.raw, 1, a.M, t, jk, live, rk);
+		const bool okv = raw_row<4, RS>(a.raw, 2, a.M, t, jv, live, rv);
 		if (!(okk && okv)) qmx = kBad;
 	}
 #pragma unroll
@@ -889,7 +1002,7 @@ __global__ __launch_bounds__(BS) void k_qkv_post(sslm_launch::QkvPostArgs a) {
 			const int hd = (2 * p) / D;
 			const int i = p % pairs;
 			longlong2 kk, vv;
-			if (RAW) {
+			if (RS > 0) {
 				kk = make_longlong2(rk[2 * k], rk[2 * k + 1]);
 				vv = make_longlong2(rv[2 * k], rv[2 * k + 1]);
 			} else {
@@ -991,7 +1104,7 @@ __global__ __launch_bounds__(BS) void k_funnel(sslm_launch::FunnelArgs a) {
 
 // projection funnel -> residual reconcile -> (optional) RMSNorm, all on one token's row
 // (forward_sites.cpp:871-989 residual; :410-459 norm).  `out_stream` never aliases `stream`.
-template <int BS, int EPT, bool RAW>
+template <int BS, int EPT, int RS>
 __global__ __launch_bounds__(BS) void k_residual_norm(sslm_launch::ResidualArgs a) {
 	__shared__ uint64_t s_b[BS / 64], s_r[BS / 64], s_n[BS / 64];
 	__shared__ int64_t s_ss[BS / 64];
@@ -1006,7 +1119,7 @@ __global__ __launch_bounds__(BS) void k_residual_norm(sslm_launch::ResidualArgs 
 	const int8_t* srow = a.stream + (size_t)sidx * H;
 	int32_t bf[EPT], g[EPT], sv[EPT];
 	uint64_t bmx = 0;
-	if (RAW) {
+	if (RS > 0) {
 		int j[EPT];
 		bool live[EPT];
 		int64_t v[EPT];
@@ -1015,7 +1128,7 @@ __global__ __launch_bounds__(BS) void k_residual_norm(sslm_launch::ResidualArgs 
 			j[k] = threadIdx.x + k * BS;
 			live[k] = j[k] < H;
 		}
-		const bool ok = raw_row<EPT>(a.raw, 0, a.M, t, j, live, v);
+		const bool ok = raw_row<EPT, RS>(a.raw, 0, a.M, t, j, live, v);
 #pragma unroll
 		for (int k = 0; k < EPT; ++k) {
 			bf[k] = sat_i32(v[k]);
@@ -1026,11 +1139,11 @@ __global__ __launch_bounds__(BS) void k_residual_norm(sslm_launch::ResidualArgs 
 #pragma unroll
 	for (int k = 0; k < EPT; ++k) {
 		const int i = threadIdx.x + k * BS;
-		if (!RAW) bf[k] = i < H ? bfr[i] : 0;
+		if (RS == 0) bf[k] = i < H ? bfr[i] : 0;
 		sv[k] = i < H ? srow[i] : 0;
 		g[k] = (a.gain && i < H) ? a.gain[i] : 0;
 	}
-	if (!RAW) bmx = part_max<BS>(a.branch_maxpart, 0, H / 16, t);
+	if (RS == 0) bmx = part_max<BS>(a.branch_maxpart, 0, H / 16, t);
 	const Scale ss = a.stream_scale[sidx];
 	if (threadIdx.x == 0) s_st = a.status[slot];
 	bmx = blk_max<BS>(bmx, s_b);
@@ -1099,7 +1212,7 @@ __global__ __launch_bounds__(BS) void k_residual_norm(sslm_launch::ResidualArgs 
 // gate/up funnels -> MlpActSite (forward_sites.cpp:796-864) -> act funnel.  The sigmoid of a
 // gate code depends only on the code and the token's gate scale, so the 256 possible values
 // are tabulated per block once the gate plan is known.
-template <int BS, int EPT, bool RAW>
+template <int BS, int EPT, int RS>
 __global__ __launch_bounds__(BS) void k_mlp_act(sslm_launch::ActArgs a) {
 	__shared__ uint64_t s_gu[2 * BS / 64], s_a[BS / 64];
 	__shared__ int32_t sig[256];
@@ -1110,7 +1223,7 @@ __global__ __launch_bounds__(BS) void k_mlp_act(sslm_launch::ActArgs a) {
 	const int32_t* ufr = gfr + I;
 	int32_t gf[EPT], uf[EPT];
 	uint64_t gm = 0, um = 0;
-	if (RAW) {
+	if (RS > 0) {
 		int jg[EPT], ju[EPT];
 		bool live[EPT];
 		int64_t vg[EPT], vu[EPT];
@@ -1120,8 +1233,8 @@ __global__ __launch_bounds__(BS) void k_mlp_act(sslm_launch::ActArgs a) {
 			ju[k] = I + jg[k];
 			live[k] = jg[k] < I;
 		}
-		const bool okg = raw_row<EPT>(a.raw, 0, a.M, t, jg, live, vg);
-		const bool oku = raw_row<EPT>(a.raw, 1, a.M, t, ju, live, vu);
+		const bool okg = raw_row<EPT, RS>(a.raw, 0, a.M, t, jg, live, vg);
+		const bool oku = raw_row<EPT, RS>(a.raw, 1, a.M, t, ju, live, vu);
 #pragma unroll
 		for (int k = 0; k < EPT; ++k) {
 			gf[k] = sat_i32(vg[k]);
@@ -1138,7 +1251,7 @@ __global__ __launch_bounds__(BS) void k_mlp_act(sslm_launch::ActArgs a) {
 			uf[k] = i < I ? ufr[i] : 0;
 		}
 	}
-	if (!RAW) {
+	if (RS == 0) {
 		gm = part_max<BS>(a.gu_maxpart, 0, I / 16, t);
 		um = part_max<BS>(a.gu_maxpart, I / 16, I / 16, t);
 	}
@@ -1467,38 +1580,48 @@ void embed(const int32_t* tokens, int M, const int8_t* embed_w, int H, int vocab
 
 // Row kernels are instantiated for a set of per-thread element counts; the smallest one that
 // covers the row is launched.
-constexpr int kRowBS = 512;   // rmsnorm, qkv_post, funnel, residual
-constexpr int kActBS = 1024;  // mlp_act (rows of I elements)
+constexpr int kRowBS = 512;     // qkv_post, residual (decode rows of H elements)
+constexpr int kActBS = 1024;    // mlp_act (rows of I elements)
+constexpr int kFunnelBS = 512;  // funnel, rmsnorm
+static_assert(16 * kFunnelBS >= kFunnelMaxN, "funnel instances must cover kFunnelMaxN");
 
 #define SSLM_EPT_CASES(X) X(1) X(2) X(3) X(4) X(6) X(8) X(12) X(16)
 #define SSLM_ACT_EPT_CASES(X) X(1) X(2) X(4) X(9) X(12) X(20)
 
 static int row_ept(int n, int bs) { return (n + bs - 1) / bs; }
 
+// Geometry is validated before any launch (row_geometry_ok at model map, argument checks at the
+// test entry points); a row no instance covers is a bug, not a case to skip silently.
+[[noreturn]] static void no_instance(const char* kernel, int n) {
+	fprintf(stderr, "sslm_hip: no %s instance for a row of %d elements\n", kernel, n);
+	abort();
+}
+
 void rmsnorm(const RowNormArgs& a, int M, int H, const TokenInfo* tok, int32_t* status, int32_t layer,
              hipStream_t s) {
-	const int need = row_ept(H, kRowBS);
+	const int need = row_ept(H, kFunnelBS);
 #define X(E)                                                                                               \
 	if (need <= E) {                                                                                       \
-		hipLaunchKernelGGL((k_rmsnorm<kRowBS, E>), dim3(M), dim3(kRowBS), 0, s, a, H, tok, status, layer); \
+		hipLaunchKernelGGL((k_rmsnorm<kFunnelBS, E>), dim3(M), dim3(kFunnelBS), 0, s, a, H, tok, status, layer); \
 		return;                                                                                            \
 	}
 	SSLM_EPT_CASES(X)
 #undef X
+	no_instance("rmsnorm", H);
 }
 
 void qkv_post(const QkvPostArgs& a, hipStream_t s) {
 	const int need = row_ept(a.H / 2, kRowBS);
 #define X(E)                                                                                          \
 	if (need <= E) {                                                                                  \
-		if (a.raw.part)                                                                               \
-			hipLaunchKernelGGL((k_qkv_post<kRowBS, E, true>), dim3(a.M), dim3(kRowBS), 0, s, a);  \
-		else                                                                                          \
-			hipLaunchKernelGGL((k_qkv_post<kRowBS, E, false>), dim3(a.M), dim3(kRowBS), 0, s, a); \
+		if (!a.raw.part) hipLaunchKernelGGL((k_qkv_post<kRowBS, E, 0>), dim3(a.M), dim3(kRowBS), 0, s, a); \
+		else if (a.raw.splits == 1) hipLaunchKernelGGL((k_qkv_post<kRowBS, E, 1>), dim3(a.M), dim3(kRowBS), 0, s, a); \
+		else hipLaunchKernelGGL((k_qkv_post<kRowBS, E, kMaxRawSplits>), dim3(a.M), dim3(kRowBS), 0, s, a); \
 		return;                                                                                       \
 	}
 	X(1) X(2) X(4) X(8)
 #undef X
+	no_instance("qkv_post", a.H);
 }
 
 void attention(const AttnArgs& a, hipStream_t s) {
@@ -1514,46 +1637,47 @@ void attention(const AttnArgs& a, hipStream_t s) {
 }
 
 void funnel(const FunnelArgs& a, hipStream_t s) {
-	const int need = row_ept(a.N, kRowBS);
+	const int need = row_ept(a.N, kFunnelBS);
 #define X(E)                                                                               \
 	if (need <= E) {                                                                       \
-		hipLaunchKernelGGL((k_funnel<kRowBS, E>), dim3(a.M), dim3(kRowBS), 0, s, a); \
+		hipLaunchKernelGGL((k_funnel<kFunnelBS, E>), dim3(a.M), dim3(kFunnelBS), 0, s, a); \
 		return;                                                                            \
 	}
 	SSLM_EPT_CASES(X)
 #undef X
+	no_instance("funnel", a.N);
 }
 
 void residual_norm(const ResidualArgs& a, hipStream_t s) {
 	const int need = row_ept(a.H, kRowBS);
 #define X(E)                                                                                               \
 	if (need <= E) {                                                                                       \
-		if (a.raw.part)                                                                                    \
-			hipLaunchKernelGGL((k_residual_norm<kRowBS, E, true>), dim3(a.M), dim3(kRowBS), 0, s, a);  \
-		else                                                                                               \
-			hipLaunchKernelGGL((k_residual_norm<kRowBS, E, false>), dim3(a.M), dim3(kRowBS), 0, s, a); \
+		if (!a.raw.part) hipLaunchKernelGGL((k_residual_norm<kRowBS, E, 0>), dim3(a.M), dim3(kRowBS), 0, s, a); \
+		else if (a.raw.splits == 1) hipLaunchKernelGGL((k_residual_norm<kRowBS, E, 1>), dim3(a.M), dim3(kRowBS), 0, s, a); \
+		else hipLaunchKernelGGL((k_residual_norm<kRowBS, E, kMaxRawSplits>), dim3(a.M), dim3(kRowBS), 0, s, a); \
 		return;                                                                                            \
 	}
 	SSLM_EPT_CASES(X)
 #undef X
+	no_instance("residual_norm", a.H);
 }
 
 void mlp_act(const ActArgs& a, hipStream_t s) {
 	const int need = row_ept(a.I, kActBS);
 #define X(E)                                                                                         \
 	if (need <= E) {                                                                                 \
-		if (a.raw.part)                                                                              \
-			hipLaunchKernelGGL((k_mlp_act<kActBS, E, true>), dim3(a.M), dim3(kActBS), 0, s, a);  \
-		else                                                                                         \
-			hipLaunchKernelGGL((k_mlp_act<kActBS, E, false>), dim3(a.M), dim3(kActBS), 0, s, a); \
+		if (!a.raw.part) hipLaunchKernelGGL((k_mlp_act<kActBS, E, 0>), dim3(a.M), dim3(kActBS), 0, s, a); \
+		else if (a.raw.splits == 1) hipLaunchKernelGGL((k_mlp_act<kActBS, E, 1>), dim3(a.M), dim3(kActBS), 0, s, a); \
+		else hipLaunchKernelGGL((k_mlp_act<kActBS, E, kMaxRawSplits>), dim3(a.M), dim3(kActBS), 0, s, a); \
 		return;                                                                                      \
 	}
 	SSLM_ACT_EPT_CASES(X)
 #undef X
+	no_instance("mlp_act", a.I);
 }
 
 bool row_geometry_ok(int H, int I, int NKV, int D) {
-	return H <= 16 * kRowBS && I <= 20 * kActBS && NKV * D <= 4 * kRowBS && H / 2 <= 8 * kRowBS &&
+	return H <= 16 * kRowBS && H <= 16 * kFunnelBS && I <= 20 * kActBS && NKV * D <= 4 * kRowBS && H / 2 <= 8 * kRowBS &&
 	       (D == 32 || D == 64 || D == 128 || D == 256);
 }
 

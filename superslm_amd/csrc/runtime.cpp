@@ -296,24 +296,38 @@ void run_gemm(sslm_model m, Track& w, const GemmArgs& g, int cls) {
 	ck(hipGetLastError());
 }
 
-// Decode projections whose GEMV splits K hand their raw partial planes to the next row kernel,
-// which applies the epilogue; call once g.epi is complete.  Returns a null RawIn otherwise.
-// `allow`: the consumer's raw variant holds its row in registers without spilling.
-RawIn split_raw(sslm_model m, Track& w, GemmArgs& g, bool allow) {
+// Decode projections (and prefill GEMMs that split K) hand their raw partial planes to the next
+// row kernel, which applies the epilogue; call once g.epi is complete.  Returns a null RawIn
+// otherwise.  `allow_multi` / `allow_single`: the consumer's raw variant for several planes /
+// one plane holds its row in registers without (much) spilling.
+RawIn split_raw(sslm_model m, Track& w, GemmArgs& g, bool allow_multi, bool allow_single) {
 	RawIn r{};
-	if (!allow || !w.raw_part) return r;
+	if (!w.raw_part) return r;
 	bool lora = false;
 	for (int i = 0; i < g.epi.nseg; ++i) lora = lora || g.epi.seg[i].lora_b;
 	int splits = 1;
-	if (sslm_launch::gemv_eligible(g.M, g.K)) splits = sslm_launch::gemv_plan(g.M, g.N, g.K, true).splits;
-	else if (!lora && g.K % 64 == 0) splits = sslm_launch::prefill_plan(g.M, g.N, g.K, true).splits;
-	if (splits <= 1) return r;
-	g.splits = splits;
-	g.split_part = w.raw_part;
+	// A decode GEMV always hands its raw accumulators to the consumer, which applies the
+	// epilogue on the row: in the GEMV the epilogue's stores and waits sit behind the weight
+	// stream.  A prefill GEMM keeps its own epilogue unless it splits K.  The flags say which
+	// raw consumers fit their register budget (several planes / one plane).
+	if (sslm_launch::gemv_eligible(g.M, g.K)) {
+		splits = allow_multi ? sslm_launch::gemv_plan(g.M, g.N, g.K, true).splits : 1;
+		if (splits == 1 && !allow_single) return r;
+	} else {
+		if (!allow_multi || lora || g.K % 64 != 0) return r;
+		splits = sslm_launch::prefill_plan(g.M, g.N, g.K, true).splits;
+		if (splits <= 1) return r;
+	}
 	r.part = w.raw_part;
 	r.splits = splits;
 	r.ld = g.N;
 	r.epi = g.epi;
+	if (splits > 1) {
+		g.splits = splits;
+		g.split_part = w.raw_part;
+	} else {
+		g.epi.raw_out = w.raw_part;  // plane 0 of [splits][M][N]
+	}
 	return r;
 }
 
@@ -387,7 +401,7 @@ ProjArgs qkv_args(sslm_model m, Track& w, int l, int M, sslm_adapter ad) {
 	attach_lora(m, w, ad, l, 1, &g.epi.seg[1], 1);
 	attach_lora(m, w, ad, l, 2, &g.epi.seg[2], 2);
 	ProjArgs pa{g, RawIn{}};
-	pa.raw = split_raw(m, w, pa.g, H <= 4096);
+	pa.raw = split_raw(m, w, pa.g, H <= 4096, true);
 	return pa;
 }
 
@@ -401,7 +415,7 @@ ProjArgs o_args(sslm_model m, Track& w, int l, int M, sslm_adapter ad) {
 	g.epi.seg[0] = funnel_seg(0, H, w.o_f, H, w.mx_o, lw.f_o, nullptr);
 	attach_lora(m, w, ad, l, 3, &g.epi.seg[0], 0);
 	ProjArgs pa{g, RawIn{}};
-	pa.raw = split_raw(m, w, pa.g, H <= 6144);
+	pa.raw = split_raw(m, w, pa.g, H <= 6144, true);
 	return pa;
 }
 
@@ -417,7 +431,7 @@ ProjArgs gu_args(sslm_model m, Track& w, int l, int M, sslm_adapter ad) {
 	attach_lora(m, w, ad, l, 4, &g.epi.seg[0], 0);
 	attach_lora(m, w, ad, l, 5, &g.epi.seg[1], 1);
 	ProjArgs pa{g, RawIn{}};
-	pa.raw = split_raw(m, w, pa.g, I <= 4096);
+	pa.raw = split_raw(m, w, pa.g, I <= 4096, false);
 	return pa;
 }
 
@@ -431,7 +445,7 @@ ProjArgs down_args(sslm_model m, Track& w, int l, int M, sslm_adapter ad) {
 	g.epi.seg[0] = funnel_seg(0, H, w.down_f, H, w.mx_down, lw.f_down, nullptr);
 	attach_lora(m, w, ad, l, 6, &g.epi.seg[0], 0);
 	ProjArgs pa{g, RawIn{}};
-	pa.raw = split_raw(m, w, pa.g, H <= 6144);
+	pa.raw = split_raw(m, w, pa.g, H <= 6144, true);
 	return pa;
 }
 
@@ -773,9 +787,10 @@ void alloc_track(sslm_model m, Track& w, int T, bool head) {
 		for (auto& sh : shapes) {
 			for (int rows = 1; rows <= T; ++rows) {
 				int sp = 1;
-				if (sslm_launch::gemv_eligible(rows, sh[1])) sp = sslm_launch::gemv_plan(rows, sh[0], sh[1], true).splits;
+				const bool gemv = sslm_launch::gemv_eligible(rows, sh[1]);
+				if (gemv) sp = sslm_launch::gemv_plan(rows, sh[0], sh[1], true).splits;
 				else if (sh[1] % 64 == 0) sp = sslm_launch::prefill_plan(rows, sh[0], sh[1], true).splits;
-				if (sp > 1) elems = std::max(elems, (size_t)sp * rows * sh[0]);
+				if (sp > 1 || gemv) elems = std::max(elems, (size_t)sp * rows * sh[0]);  // a GEMV is always raw
 			}
 		}
 		w.raw_part = elems ? dalloc<int32_t>(elems, &own) : nullptr;
@@ -1751,7 +1766,7 @@ sslm_status sslm_hip_gemm_requant(const int8_t* a, const int8_t* w, const int32_
                                   int32_t k, int64_t in_m, int64_t in_e, int64_t site_m, int64_t site_e,
                                   int8_t* out_codes, int64_t* out_me, int32_t* out_status) {
 	if (!a || !w || !fold || !out_codes || !out_me || !out_status || m < 1 || m > kPartLd || n < 1 || k < 16 ||
-	    k % 16 || n % 16)
+	    k % 16 || n % 16 || n > kFunnelMaxN)
 		return SSLM_INVALID_ARGUMENT;
 	return guarded([&]() -> sslm_status {
 		std::lock_guard<std::mutex> lk(g_sa.mu);

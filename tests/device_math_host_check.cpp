@@ -158,7 +158,7 @@ int main(int argc, char** argv) {
 	std::vector<int32_t> table(1025);
 	for (int j = 0; j < 1025; ++j) table[j] = (int32_t)(j * 32);  // any monotone table exercises the lookup
 	for (long i = 0; i < N; ++i) {
-		const int64_t b = uni(-(1LL << 40), 1LL << 40), r_a = uni((1LL << 31) + 1, 1LL << 32), e_a = uni(-120, 10);
+		const int64_t b = (i & 1) ? uni(-(1LL << 40), 1LL << 40) : uni(-(1LL << 30) + 1, (1LL << 30) - 1), r_a = uni((1LL << 31) + 1, 1LL << 32), e_a = uni(-120, 10);
 		const int64_t acc = uni(-(1LL << 62), 1LL << 62);
 		int64_t t1 = 0, t2 = 0;
 		const bool k1 = bias_term(b, r_a, e_a, acc, &t1);
