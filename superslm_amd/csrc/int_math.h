@@ -273,9 +273,9 @@ struct FunnelOut {
 	Scale out;
 };
 
-// By-value form with at most two incoming factors, kept out of line: every row kernel evaluates
-// two or three plans, and one shared copy is cheaper than inlined ones.
-SSLM_COLD FunnelOut funnel_plan_v(uint64_t d_prime, int n_in, Scale in0, Scale in1, Scale site) {
+// By-value form with at most two incoming factors.  Inlined: in the row kernels its inputs are
+// wave-uniform, so it compiles to scalar code.
+SSLM_HD FunnelOut funnel_plan_v(uint64_t d_prime, int n_in, Scale in0, Scale in1, Scale site) {
 	FunnelOut o{};
 	o.st = kCarriedScaleMantissaOutOfDomain;
 	if ((n_in > 0 && !fits_i32(in0.m)) || (n_in > 1 && !fits_i32(in1.m))) return o;
@@ -330,8 +330,8 @@ SSLM_HD int64_t composed_exponent(int64_t e_a, int64_t e_t) {
 // forward_sites.cpp:513-653 -- round_away(branch*m_a*r_t / 2^k), k = 62-(e_a-e_t); a negative k
 // is an exact left shift.  *clamped: the saturation-counter predicate; *exceeded: the true
 // magnitude does not fit int64.
-SSLM_COLD int64_t landing_rescale(int64_t branch, int64_t m_a, int64_t r_t, int64_t k, bool* clamped,
-                                   bool* exceeded) {
+SSLM_HD int64_t landing_rescale(int64_t branch, int64_t m_a, int64_t r_t, int64_t k, bool* clamped,
+                                 bool* exceeded) {
 	bool neg = (branch < 0) != (m_a < 0);
 	uint64_t ab = branch < 0 ? (~(uint64_t)branch + 1u) : (uint64_t)branch;
 	uint64_t am = m_a < 0 ? (~(uint64_t)m_a + 1u) : (uint64_t)m_a;
@@ -366,6 +366,11 @@ SSLM_COLD int64_t landing_rescale(int64_t branch, int64_t m_a, int64_t r_t, int6
 	return raw;
 }
 
+SSLM_COLD int64_t landing_rescale_cold(int64_t branch, int64_t m_a, int64_t r_t, int64_t k, bool* clamped,
+                                        bool* exceeded) {
+	return landing_rescale(branch, m_a, r_t, k, clamped, exceeded);
+}
+
 // landing_rescale for the residual site's operands (|branch| <= 127 code, |m_a| < 2^31 + 1,
 // r_t < 2^33) on 64-bit halves when the composed exponent k is non-negative; every other case
 // takes the general 128-bit path above.  Same outputs bit for bit.
@@ -373,7 +378,7 @@ SSLM_HD int64_t landing_small(int64_t branch, int64_t m_a, int64_t r_t, int64_t 
 	const uint64_t ab = branch < 0 ? (uint64_t)0 - (uint64_t)branch : (uint64_t)branch;
 	const uint64_t am = m_a < 0 ? (uint64_t)0 - (uint64_t)m_a : (uint64_t)m_a;
 	if (k < 0 || ab > 127u || am > ((uint64_t)1 << 31) || (uint64_t)r_t >= ((uint64_t)1 << 33))
-		return landing_rescale(branch, m_a, r_t, k, clamped, exceeded);
+		return landing_rescale_cold(branch, m_a, r_t, k, clamped, exceeded);
 	const bool neg = (branch < 0) != (m_a < 0);
 	const uint64_t a = ab * am;  // < 2^39
 	const uint64_t lo = a * (uint64_t)r_t;

@@ -61,9 +61,14 @@ __device__ __forceinline__ uint64_t block_max_u64(uint64_t v, uint64_t* red) {
 	return r;
 }
 
+// Row maxima travel as 32-bit magnitudes: |v| saturated at 2^32 - 2, so that 2^32 - 1 (kBad32)
+// is free to mark a refusal somewhere in the row.  Every consumer rejects a maximum above 2^31
+// (the funnel's accepted domain), so the saturation changes no outcome.
+constexpr uint32_t kBad32 = 0xffffffffu;
+
 __device__ __forceinline__ uint32_t sat_abs_u32(int64_t v) {
 	uint64_t a = v < 0 ? (uint64_t)0 - (uint64_t)v : (uint64_t)v;
-	return a > 0xffffffffull ? 0xffffffffu : (uint32_t)a;
+	return a > 0xfffffffeull ? 0xfffffffeu : (uint32_t)a;
 }
 
 __device__ __forceinline__ int32_t sat_i32(int64_t v) {
@@ -736,22 +741,41 @@ __device__ __forceinline__ uint64_t uni_u64(uint64_t v) {
 }
 __device__ __forceinline__ int64_t uni_i64(int64_t v) { return (int64_t)uni_u64((uint64_t)v); }
 
+// 32-bit wave reductions: a 16-lane rotate butterfly (DPP) leaves every lane with its row's
+// result, and the four row results are read as scalars -- the value comes back wave-uniform.
+__device__ __forceinline__ uint32_t wave_max32(uint32_t v) {
+	v = dpp_max16(v);
+	const uint32_t a = __builtin_amdgcn_readlane(v, 0), b = __builtin_amdgcn_readlane(v, 16);
+	const uint32_t c = __builtin_amdgcn_readlane(v, 32), d = __builtin_amdgcn_readlane(v, 48);
+	return max(max(a, b), max(c, d));
+}
+
+__device__ __forceinline__ int32_t wave_sum32(int32_t v) {
+	v += __builtin_amdgcn_update_dpp(0, v, 0x128, 0xf, 0xf, false);  // row_ror:8
+	v += __builtin_amdgcn_update_dpp(0, v, 0x124, 0xf, 0xf, false);  // row_ror:4
+	v += __builtin_amdgcn_update_dpp(0, v, 0x122, 0xf, 0xf, false);  // row_ror:2
+	v += __builtin_amdgcn_update_dpp(0, v, 0x121, 0xf, 0xf, false);  // row_ror:1
+	return __builtin_amdgcn_readlane(v, 0) + __builtin_amdgcn_readlane(v, 16) + __builtin_amdgcn_readlane(v, 32) +
+	       __builtin_amdgcn_readlane(v, 48);
+}
+
+// block reductions with one barrier; each call site owns its LDS slots (BS / 64 entries)
 template <int BS>
-__device__ __forceinline__ uint64_t blk_max(uint64_t v, uint64_t* slots) {
-	v = wave_max_u64(v);
+__device__ __forceinline__ uint32_t blk_max32(uint32_t v, uint32_t* slots) {
+	v = wave_max32(v);
 	if ((threadIdx.x & 63) == 0) slots[threadIdx.x >> 6] = v;
 	__syncthreads();
-	uint64_t r = slots[0];
+	uint32_t r = slots[0];
 #pragma unroll
-	for (int i = 1; i < BS / 64; ++i) r = slots[i] > r ? slots[i] : r;
-	return uni_u64(r);
+	for (int i = 1; i < BS / 64; ++i) r = max(r, slots[i]);
+	return __builtin_amdgcn_readfirstlane(r);
 }
 
 // two maxima, one barrier; `slots` holds 2 * BS / 64 entries
 template <int BS>
-__device__ __forceinline__ void blk_max2(uint64_t& x, uint64_t& y, uint64_t* slots) {
-	x = wave_max_u64(x);
-	y = wave_max_u64(y);
+__device__ __forceinline__ void blk_max32x2(uint32_t& x, uint32_t& y, uint32_t* slots) {
+	x = wave_max32(x);
+	y = wave_max32(y);
 	if ((threadIdx.x & 63) == 0) {
 		slots[threadIdx.x >> 6] = x;
 		slots[BS / 64 + (threadIdx.x >> 6)] = y;
@@ -761,22 +785,42 @@ __device__ __forceinline__ void blk_max2(uint64_t& x, uint64_t& y, uint64_t* slo
 	y = slots[BS / 64];
 #pragma unroll
 	for (int i = 1; i < BS / 64; ++i) {
-		x = slots[i] > x ? slots[i] : x;
-		y = slots[BS / 64 + i] > y ? slots[BS / 64 + i] : y;
+		x = max(x, slots[i]);
+		y = max(y, slots[BS / 64 + i]);
 	}
-	x = uni_u64(x);
-	y = uni_u64(y);
+	x = __builtin_amdgcn_readfirstlane(x);
+	y = __builtin_amdgcn_readfirstlane(y);
 }
 
 template <int BS>
-__device__ __forceinline__ int64_t blk_sum(int64_t v, int64_t* slots) {
-	v = wave_sum_i64(v);
+__device__ __forceinline__ int32_t blk_sum32(int32_t v, int32_t* slots) {
+	v = wave_sum32(v);
 	if ((threadIdx.x & 63) == 0) slots[threadIdx.x >> 6] = v;
 	__syncthreads();
-	int64_t r = 0;
+	int32_t r = 0;
 #pragma unroll
 	for (int i = 0; i < BS / 64; ++i) r += slots[i];
-	return uni_i64(r);
+	return __builtin_amdgcn_readfirstlane(r);
+}
+
+// this thread's share of the max over tiles [tile0, tile0 + ntiles) of a per-(tile, token)
+// partial array (32-bit); combine across the block with blk_max32
+template <int BS>
+__device__ __forceinline__ uint32_t part_max32(const uint32_t* part, int tile0, int ntiles, int t) {
+	uint32_t m = 0;
+	for (int i = threadIdx.x; i < ntiles; i += BS) m = max(m, part[(size_t)(tile0 + i) * kPartLd + t]);
+	return m;
+}
+
+template <int BS>
+__device__ __forceinline__ uint64_t blk_max(uint64_t v, uint64_t* slots) {
+	v = wave_max_u64(v);
+	if ((threadIdx.x & 63) == 0) slots[threadIdx.x >> 6] = v;
+	__syncthreads();
+	uint64_t r = slots[0];
+#pragma unroll
+	for (int i = 1; i < BS / 64; ++i) r = slots[i] > r ? slots[i] : r;
+	return uni_u64(r);
 }
 
 template <int BS>
@@ -790,19 +834,6 @@ __device__ __forceinline__ int64_t blk_max_i64(int64_t v, int64_t* slots) {
 	return uni_i64(r);
 }
 
-// this thread's share of the max over tiles [tile0, tile0 + ntiles) of a per-(tile, token)
-// partial array; combine across the block with blk_max
-template <int BS>
-__device__ __forceinline__ uint64_t part_max(const uint32_t* part, int tile0, int ntiles, int t) {
-	uint64_t m = 0;
-	for (int i = threadIdx.x; i < ntiles; i += BS) {
-		const uint64_t v = part[(size_t)(tile0 + i) * kPartLd + t];
-		m = v > m ? v : m;
-	}
-	return m;
-}
-
-__device__ __forceinline__ uint64_t abs_u64(int64_t v) { return v < 0 ? (uint64_t)0 - (uint64_t)v : (uint64_t)v; }
 
 // N elements (columns j[k] of segment `si`) of token t of a raw split-K projection with the
 // segment's epilogue applied (RawIn).  Every load -- all split planes, fold triples and biases
@@ -858,8 +889,6 @@ __device__ __forceinline__ bool raw_row(const RawIn& r, int si, int M, int t, co
 	return ok;
 }
 
-constexpr uint64_t kBad = ~(uint64_t)0;  // max-reduction sentinel: a refusal somewhere in the row
-
 constexpr int32_t kSkipped = -1;  // the slot had already failed: nothing written, no status
 
 // forward_sites.cpp:410-459 -- the RMSNorm site body on a register-resident row of codes `h`
@@ -867,13 +896,13 @@ constexpr int32_t kSkipped = -1;  // the slot had already failed: nothing writte
 template <int BS, int EPT>
 __device__ __forceinline__ int32_t rmsnorm_regs(const int32_t (&h)[EPT], const int32_t (&g)[EPT], int H, Scale site,
                                                 int8_t* out, Scale* out_scale, int64_t* out_recip, int64_t* fd,
-                                                int64_t* s_sum, uint64_t* s_max, const int32_t* prior) {
-	int64_t ss = 0;
+                                                int32_t* s_sum, uint32_t* s_max, const int32_t* prior) {
+	int32_t ss = 0;  // sum of squared int8 codes: < 2^14 * H, exact in int32
 #pragma unroll
-	for (int k = 0; k < EPT; ++k) ss += (int64_t)(h[k] * h[k]);
-	ss = blk_sum<BS>(ss, s_sum);
+	for (int k = 0; k < EPT; ++k) ss += h[k] * h[k];
+	ss = blk_sum32<BS>(ss, s_sum);
 	if (prior && *prior != 0) return kSkipped;
-	int64_t root = isqrt_fast(div_floor_pos(ss << 32, (int64_t)H));
+	int64_t root = isqrt_fast(div_floor_pos((int64_t)ss << 32, (int64_t)H));
 	root = root > 1 ? root : 1;
 	if (threadIdx.x < 256) {  // floor((v << 32) / root) for every int8 v
 		const int64_t v = ((int64_t)threadIdx.x - 128) << 32;
@@ -881,14 +910,13 @@ __device__ __forceinline__ int32_t rmsnorm_regs(const int32_t (&h)[EPT], const i
 	}
 	__syncthreads();
 	int64_t w[EPT];
-	uint64_t mx = 0;
+	uint32_t mx = 0;
 #pragma unroll
 	for (int k = 0; k < EPT; ++k) {
 		w[k] = fd[h[k] + 128] * (int64_t)g[k];
-		const uint64_t ab = abs_u64(w[k]);
-		mx = ab > mx ? ab : mx;
+		mx = max(mx, sat_abs_u32(w[k]));
 	}
-	mx = blk_max<BS>(mx, s_max);
+	mx = blk_max32<BS>(mx, s_max);
 	FunnelPlan plan;
 	const int32_t st = funnel_plan(mx, nullptr, 0, site, &plan);
 	if (st != kOk) return st;
@@ -908,8 +936,8 @@ template <int BS, int EPT>
 __global__ __launch_bounds__(BS) void k_rmsnorm(sslm_launch::RowNormArgs a, int H, const TokenInfo* tok,
                                               int32_t* status, int32_t layer) {
 	__shared__ int64_t fd[256];
-	__shared__ int64_t s_sum[BS / 64];
-	__shared__ uint64_t s_max[BS / 64];
+	__shared__ int32_t s_sum[BS / 64];
+	__shared__ uint32_t s_max[BS / 64];
 	__shared__ int32_t s_st;
 	const int t = blockIdx.x;
 	const int slot = tok[t].slot;
@@ -932,7 +960,7 @@ __global__ __launch_bounds__(BS) void k_rmsnorm(sslm_launch::RowNormArgs a, int 
 // reduced.  Up to 2 K (and 2 V) pairs per thread: NKV * D <= 4 * BS.
 template <int BS, int EQ, int RS>
 __global__ __launch_bounds__(BS) void k_qkv_post(sslm_launch::QkvPostArgs a) {
-	__shared__ uint64_t s_red[BS / 64];
+	__shared__ uint32_t s_red[BS / 64];
 	__shared__ int32_t s_st;
 	const int t = blockIdx.x;
 	const TokenInfo ti = a.tok[t];
@@ -945,7 +973,7 @@ __global__ __launch_bounds__(BS) void k_qkv_post(sslm_launch::QkvPostArgs a) {
 	const int64_t* sn = a.rope_sin + (pos_ok ? pos : 0) * pairs;
 	// q pair values
 	int2 qv[EQ];
-	uint64_t qmx = 0;
+	uint32_t qmx = 0;
 	if (RS > 0) {
 		int j[2 * EQ];
 		bool live[2 * EQ];
@@ -961,9 +989,9 @@ __global__ __launch_bounds__(BS) void k_qkv_post(sslm_launch::QkvPostArgs a) {
 #pragma unroll
 		for (int k = 0; k < EQ; ++k) {
 			qv[k] = make_int2(sat_i32(v[2 * k]), sat_i32(v[2 * k + 1]));
-			qmx = std::max(qmx, (uint64_t)std::max(sat_abs_u32(v[2 * k]), sat_abs_u32(v[2 * k + 1])));
+			qmx = max(qmx, max(sat_abs_u32(v[2 * k]), sat_abs_u32(v[2 * k + 1])));
 		}
-		if (!ok) qmx = kBad;
+		if (!ok) qmx = kBad32;
 	} else {
 		const int2* qf = (const int2*)(a.q_f + (size_t)t * H);
 #pragma unroll
@@ -971,7 +999,7 @@ __global__ __launch_bounds__(BS) void k_qkv_post(sslm_launch::QkvPostArgs a) {
 			const int p = threadIdx.x + k * BS;
 			qv[k] = p < H / 2 ? qf[p] : make_int2(0, 0);
 		}
-		qmx = part_max<BS>(a.q_maxpart, 0, H / 16, t);
+		qmx = part_max32<BS>(a.q_maxpart, 0, H / 16, t);
 	}
 	if (threadIdx.x == 0) s_st = a.status[ti.slot];
 	// K/V landing (LandingRescale at the normed scale, per kv head) and RoPE(K)
@@ -993,7 +1021,7 @@ __global__ __launch_bounds__(BS) void k_qkv_post(sslm_launch::QkvPostArgs a) {
 		}
 		const bool okk = raw_row<4, RS>(a.raw, 1, a.M, t, jk, live, rk);
 		const bool okv = raw_row<4, RS>(a.raw, 2, a.M, t, jv, live, rv);
-		if (!(okk && okv)) qmx = kBad;
+		if (!(okk && okv)) qmx = kBad32;
 	}
 #pragma unroll
 	for (int k = 0; k < 2; ++k) {
@@ -1024,10 +1052,10 @@ __global__ __launch_bounds__(BS) void k_qkv_post(sslm_launch::QkvPostArgs a) {
 			sat += (uint64_t)c0 + (uint64_t)c1 + (uint64_t)c2 + (uint64_t)c3;
 		}
 	}
-	qmx = blk_max<BS>(qmx, s_red);
+	qmx = blk_max32<BS>(qmx, s_red);
 	if (s_st != 0) return;
 	FunnelPlan plan;
-	int32_t st = qmx == kBad ? kBiasReconcileProductOutOfDomain : funnel_plan(qmx, &ns, 1, a.q_site, &plan);
+	int32_t st = qmx == kBad32 ? kBiasReconcileProductOutOfDomain : funnel_plan(qmx, &ns, 1, a.q_site, &plan);
 	if (st == kOk && !pos_ok) st = kPositionOverCap;
 	if (st != kOk) {
 		if (threadIdx.x == 0) set_status(a.status, ti.slot, a.layer, st);
@@ -1070,7 +1098,7 @@ __global__ __launch_bounds__(BS) void k_qkv_post(sslm_launch::QkvPostArgs a) {
 // funnel over an int32 fold-output row (checked_chain_funnel.cpp:257-364)
 template <int BS, int EPT>
 __global__ __launch_bounds__(BS) void k_funnel(sslm_launch::FunnelArgs a) {
-	__shared__ uint64_t s_m[BS / 64];
+	__shared__ uint32_t s_m[BS / 64];
 	__shared__ int32_t s_st;
 	const int t = blockIdx.x, N = a.N;
 	const int slot = a.tok[t].slot;
@@ -1081,11 +1109,11 @@ __global__ __launch_bounds__(BS) void k_funnel(sslm_launch::FunnelArgs a) {
 		const int i = threadIdx.x + k * BS;
 		f[k] = i < N ? frow[i] : 0;
 	}
-	uint64_t mx = part_max<BS>(a.maxpart, 0, a.ntiles, t);
+	uint32_t mx = part_max32<BS>(a.maxpart, 0, a.ntiles, t);
 	Scale inc{0, 0};
 	if (a.incoming) inc = a.incoming[t];
 	if (threadIdx.x == 0) s_st = a.status[slot];
-	mx = blk_max<BS>(mx, s_m);
+	mx = blk_max32<BS>(mx, s_m);
 	if (s_st != 0) return;
 	FunnelPlan plan;
 	const int32_t st = funnel_plan(mx, a.incoming ? &inc : nullptr, a.incoming ? 1 : 0, a.site, &plan);
@@ -1106,9 +1134,10 @@ __global__ __launch_bounds__(BS) void k_funnel(sslm_launch::FunnelArgs a) {
 // (forward_sites.cpp:871-989 residual; :410-459 norm).  `out_stream` never aliases `stream`.
 template <int BS, int EPT, int RS>
 __global__ __launch_bounds__(BS) void k_residual_norm(sslm_launch::ResidualArgs a) {
-	__shared__ uint64_t s_b[BS / 64], s_r[BS / 64], s_n[BS / 64];
-	__shared__ int64_t s_ss[BS / 64];
+	__shared__ uint32_t s_b[BS / 64], s_r[BS / 64], s_n[BS / 64];
+	__shared__ int32_t s_ss[BS / 64];
 	__shared__ int64_t fd[256];
+	__shared__ int64_t land[256];  // landed branch value per branch code (code + 127)
 	__shared__ int32_t s_st;
 	const int t = blockIdx.x, H = a.H;
 	KT(0);
@@ -1118,7 +1147,7 @@ __global__ __launch_bounds__(BS) void k_residual_norm(sslm_launch::ResidualArgs 
 	const int32_t* bfr = a.branch_f + (size_t)t * H;
 	const int8_t* srow = a.stream + (size_t)sidx * H;
 	int32_t bf[EPT], g[EPT], sv[EPT];
-	uint64_t bmx = 0;
+	uint32_t bmx = 0;
 	if (RS > 0) {
 		int j[EPT];
 		bool live[EPT];
@@ -1132,9 +1161,9 @@ __global__ __launch_bounds__(BS) void k_residual_norm(sslm_launch::ResidualArgs 
 #pragma unroll
 		for (int k = 0; k < EPT; ++k) {
 			bf[k] = sat_i32(v[k]);
-			bmx = std::max(bmx, (uint64_t)sat_abs_u32(v[k]));
+			bmx = max(bmx, sat_abs_u32(v[k]));
 		}
-		if (!ok) bmx = kBad;
+		if (!ok) bmx = kBad32;
 	}
 #pragma unroll
 	for (int k = 0; k < EPT; ++k) {
@@ -1143,46 +1172,54 @@ __global__ __launch_bounds__(BS) void k_residual_norm(sslm_launch::ResidualArgs 
 		sv[k] = i < H ? srow[i] : 0;
 		g[k] = (a.gain && i < H) ? a.gain[i] : 0;
 	}
-	if (RS == 0) bmx = part_max<BS>(a.branch_maxpart, 0, H / 16, t);
+	if (RS == 0) bmx = part_max32<BS>(a.branch_maxpart, 0, H / 16, t);
 	const Scale ss = a.stream_scale[sidx];
 	if (threadIdx.x == 0) s_st = a.status[slot];
-	bmx = blk_max<BS>(bmx, s_b);
+	bmx = blk_max32<BS>(bmx, s_b);
 	KT(1);
 	if (s_st != 0) return;
 	FunnelPlan bplan;
-	int32_t st = bmx == kBad ? kBiasReconcileProductOutOfDomain : funnel_plan(bmx, &bin, 1, a.branch_site, &bplan);
+	int32_t st = bmx == kBad32 ? kBiasReconcileProductOutOfDomain : funnel_plan(bmx, &bin, 1, a.branch_site, &bplan);
 	if (st == kOk && !fits_i32(ss.m)) st = kCarriedScaleMantissaOutOfDomain;
 	if (st != kOk) {
 		if (threadIdx.x == 0) set_status(a.status, slot, a.layer, st);
 		return;
 	}
-	const int64_t r_h = reciprocal_fast(ss.m);
-	const Scale bs = bplan.out;
-	const int64_t kx = composed_exponent(bs.e, ss.e);
 	KT(2);
+	// The landed value depends on the branch code alone (forward_sites.cpp:513-653 with the
+	// row's scales fixed), so the 255 possible values are tabulated, one per thread;
+	// INT64_MIN marks a code whose landing exceeds int64.
+	int32_t code[EPT];
+#pragma unroll
+	for (int k = 0; k < EPT; ++k) code[k] = requant_code_small(bf[k], (uint64_t)bplan.r, bplan.s);
+	if (threadIdx.x < 255) {
+		const int64_t r_h = reciprocal_fast(ss.m);
+		const int64_t kx = composed_exponent(bplan.out.e, ss.e);
+		bool cl, ex;
+		const int64_t rec = landing_small((int64_t)threadIdx.x - 127, bplan.out.m, r_h, kx, &cl, &ex);
+		land[threadIdx.x] = ex ? kI64Min : rec;
+	}
+	__syncthreads();
 	int64_t w[EPT];
-	uint64_t mx = 0;
+	uint32_t mx = 0;
 #pragma unroll
 	for (int k = 0; k < EPT; ++k) {
 		const int i = threadIdx.x + k * BS;
 		w[k] = 0;
 		if (i < H) {
-			const int8_t code = requant_code_small(bf[k], (uint64_t)bplan.r, bplan.s);
-			bool cl, ex;
-			const int64_t rec = landing_small(code, bs.m, r_h, kx, &cl, &ex);
-			if (ex) {
-				mx = kBad;
+			const int64_t rec = land[code[k] + 127];
+			if (rec == kI64Min) {
+				mx = kBad32;
 			} else {
 				w[k] = rec + sv[k];
-				const uint64_t ab = abs_u64(w[k]);
-				mx = ab > mx ? ab : mx;
+				mx = max(mx, sat_abs_u32(w[k]));
 			}
 		}
 	}
-	mx = blk_max<BS>(mx, s_r);
+	mx = blk_max32<BS>(mx, s_r);
 	KT(3);
 	FunnelPlan rplan;
-	st = mx == kBad ? kResidualReconciliationMagnitudeOutOfDomain : funnel_plan(mx, &ss, 1, a.res_site, &rplan);
+	st = mx == kBad32 ? kResidualReconciliationMagnitudeOutOfDomain : funnel_plan(mx, &ss, 1, a.res_site, &rplan);
 	if (st != kOk) {
 		if (threadIdx.x == 0) set_status(a.status, slot, a.layer, st);
 		return;
@@ -1214,7 +1251,7 @@ __global__ __launch_bounds__(BS) void k_residual_norm(sslm_launch::ResidualArgs 
 // are tabulated per block once the gate plan is known.
 template <int BS, int EPT, int RS>
 __global__ __launch_bounds__(BS) void k_mlp_act(sslm_launch::ActArgs a) {
-	__shared__ uint64_t s_gu[2 * BS / 64], s_a[BS / 64];
+	__shared__ uint32_t s_gu[2 * BS / 64], s_a[BS / 64];
 	__shared__ int32_t sig[256];
 	__shared__ int32_t s_st;
 	const int t = blockIdx.x, I = a.I;
@@ -1222,7 +1259,7 @@ __global__ __launch_bounds__(BS) void k_mlp_act(sslm_launch::ActArgs a) {
 	const int32_t* gfr = a.gu_f + (size_t)t * 2 * I;
 	const int32_t* ufr = gfr + I;
 	int32_t gf[EPT], uf[EPT];
-	uint64_t gm = 0, um = 0;
+	uint32_t gm = 0, um = 0;
 	if (RS > 0) {
 		int jg[EPT], ju[EPT];
 		bool live[EPT];
@@ -1239,10 +1276,10 @@ __global__ __launch_bounds__(BS) void k_mlp_act(sslm_launch::ActArgs a) {
 		for (int k = 0; k < EPT; ++k) {
 			gf[k] = sat_i32(vg[k]);
 			uf[k] = sat_i32(vu[k]);
-			gm = std::max(gm, (uint64_t)sat_abs_u32(vg[k]));
-			um = std::max(um, (uint64_t)sat_abs_u32(vu[k]));
+			gm = max(gm, sat_abs_u32(vg[k]));
+			um = max(um, sat_abs_u32(vu[k]));
 		}
-		if (!(okg && oku)) gm = kBad;
+		if (!(okg && oku)) gm = kBad32;
 	} else {
 #pragma unroll
 		for (int k = 0; k < EPT; ++k) {
@@ -1252,15 +1289,15 @@ __global__ __launch_bounds__(BS) void k_mlp_act(sslm_launch::ActArgs a) {
 		}
 	}
 	if (RS == 0) {
-		gm = part_max<BS>(a.gu_maxpart, 0, I / 16, t);
-		um = part_max<BS>(a.gu_maxpart, I / 16, I / 16, t);
+		gm = part_max32<BS>(a.gu_maxpart, 0, I / 16, t);
+		um = part_max32<BS>(a.gu_maxpart, I / 16, I / 16, t);
 	}
 	const Scale inc = a.in_scale[t];
 	if (threadIdx.x == 0) s_st = a.status[slot];
-	blk_max2<BS>(gm, um, s_gu);
+	blk_max32x2<BS>(gm, um, s_gu);
 	if (s_st != 0) return;
 	FunnelPlan gp, up;
-	int32_t st = gm == kBad ? kBiasReconcileProductOutOfDomain : funnel_plan(gm, &inc, 1, a.gate_site, &gp);
+	int32_t st = gm == kBad32 ? kBiasReconcileProductOutOfDomain : funnel_plan(gm, &inc, 1, a.gate_site, &gp);
 	if (st == kOk) st = funnel_plan(um, &inc, 1, a.up_site, &up);
 	if (st == kOk) st = check_silu_scale(gp.out.m, gp.out.e);
 	if (st != kOk) {
@@ -1276,15 +1313,14 @@ __global__ __launch_bounds__(BS) void k_mlp_act(sslm_launch::ActArgs a) {
 		uc[k] = requant_code_small(uf[k], (uint64_t)up.r, up.s);
 	}
 	__syncthreads();
-	int64_t w[EPT];
-	uint64_t mx = 0;
+	int64_t w[EPT];  // the sigmoid table is artifact data: no bound is assumed on it
+	uint32_t mx = 0;
 #pragma unroll
 	for (int k = 0; k < EPT; ++k) {
 		w[k] = (int64_t)gc[k] * sig[gc[k] + 128] * (int64_t)uc[k];
-		const uint64_t ab = abs_u64(w[k]);
-		mx = ab > mx ? ab : mx;
+		mx = max(mx, sat_abs_u32(w[k]));
 	}
-	mx = blk_max<BS>(mx, s_a);
+	mx = blk_max32<BS>(mx, s_a);
 	const Scale inc2[2] = {gp.out, up.out};
 	FunnelPlan ap;
 	st = funnel_plan(mx, inc2, 2, a.act_site, &ap);
@@ -1312,7 +1348,8 @@ __global__ __launch_bounds__(BS) void k_attention(sslm_launch::AttnArgs a, int u
 	extern __shared__ int64_t dyn[];
 	__shared__ int64_t s_mx[BS / 64];
 	__shared__ int64_t s_sum[BS / 64];
-	__shared__ uint64_t s_ref[BS / 64], s_ab[BS / 64];
+	__shared__ uint64_t s_ref[BS / 64];
+	__shared__ uint32_t s_ab[BS / 64];
 	__shared__ int32_t s_ctx[BS * 4];
 	__shared__ int32_t s_st;
 	constexpr int TPR = D / 4, PG = BS / TPR;
@@ -1434,17 +1471,17 @@ __global__ __launch_bounds__(BS) void k_attention(sslm_launch::AttnArgs a, int u
 		sc[3] = acc3;
 	}
 	__syncthreads();
-	uint64_t mabs = 0;
+	uint32_t mabs = 0;
 	if (threadIdx.x < D) {
 		int32_t c = 0;
 #pragma unroll
 		for (int g2 = 0; g2 < PG; ++g2) c += s_ctx[g2 * D + threadIdx.x];
 		const int64_t f = apply_fold(c, f0, f1, f2);
 		a.ctx_f[(size_t)t * a.H + (size_t)h * D + threadIdx.x] = sat_i32(f);
-		mabs = abs_u64(f);
+		mabs = sat_abs_u32(f);
 	}
-	mabs = blk_max<BS>(mabs, s_ab);
-	if (threadIdx.x == 0) a.ctx_maxpart[(size_t)h * kPartLd + t] = mabs > 0xffffffffull ? 0xffffffffu : (uint32_t)mabs;
+	mabs = blk_max32<BS>(mabs, s_ab);
+	if (threadIdx.x == 0) a.ctx_maxpart[(size_t)h * kPartLd + t] = mabs;
 }
 
 // LoRA intermediate (forward_sites.cpp:1066-1086): u[k] = clamp(amp_fold(A[k] . x))
