@@ -96,6 +96,14 @@ __device__ __forceinline__ void set_status(int32_t* status, int32_t slot, int32_
 	if (st != kOk) atomicCAS(&status[slot], 0, (layer << 8) | st);
 }
 
+// Attention runs its heads in parallel, but the reference runs them in order and reports the
+// first refusing head: each refusal is recorded as (head << 8) | status with atomicMin, and the
+// context funnel that follows resolves the word into the status and resets it.
+constexpr int32_t kHeadStatusNone = 0x7fffffff;
+__device__ __forceinline__ void report_head(int32_t* head_status, int32_t slot, int32_t head, int32_t st) {
+	if (st != kOk) atomicMin(&head_status[slot], (head << 8) | st);
+}
+
 }  // namespace sslm
 
 // Host launch wrappers (kernels.hip).
@@ -157,12 +165,12 @@ struct AttnArgs {
 	int M, H, NH, NKV, D;
 	int64_t cap;
 	const TokenInfo* tok;
-	const int8_t* q_rot;      // [M, H]
+	const int8_t* q_rot;      // [M, H] (attention: rotated q codes from qkv_post)
 	const Scale* q_scale;     // [M]
 	const int64_t* khead_m;   // [NKV]
 	const int64_t* khead_e;
 	const int32_t* ctx_fold;  // [NH, 3]
-	const int8_t* kv_pool;
+	int8_t* kv_pool;
 	int64_t block_bytes;
 	int32_t layer;
 	int64_t ln2_q, b_q, ca_q;
@@ -170,8 +178,27 @@ struct AttnArgs {
 	uint32_t* ctx_maxpart;    // [NH * kPartLd]: one partial per query head
 	int64_t* scratch;         // [M, NH, cap] when rows exceed LDS
 	int32_t* status;
+	int32_t* head_status;     // [slots] attention-stage refusals, (head << 8) | status, min wins
+	// attention_decode only: the q|k|v post-processing inputs (funnel-epilogue outputs of the
+	// projection), in place of q_rot / q_scale
+	const int32_t* q_f;         // [M, H]
+	const uint32_t* q_maxpart;  // tiles [0, H/16)
+	const int64_t* kv_f;        // [M, 2*NKV*D] k then v
+	const Scale* in_scale;      // [M] normed scale
+	Scale q_site;
+	const int64_t* r_t_k;       // [NKV]
+	const int64_t* e_t_k;
+	const int64_t* r_t_v;
+	const int64_t* e_t_v;
+	const int64_t* rope_cos;    // [cap, D/2]
+	const int64_t* rope_sin;
+	unsigned long long* sat;    // [slots]
 };
 void attention(const AttnArgs& a, hipStream_t s);
+// Decode attention with the q|k|v post-processing fused in (one block per (query head, token)):
+// valid when every token of the launch belongs to a different sequence, so no token attends to
+// a position another block of the launch writes.
+void attention_decode(const AttnArgs& a, hipStream_t s);
 // the attention row (cap int64 values) lives in LDS up to this context capacity, else in
 // AttnArgs::scratch ([M, NH, cap] int64)
 constexpr int64_t kAttnLdsCap = 6144;
@@ -191,6 +218,7 @@ struct FunnelArgs {
 	Scale* out_scale;
 	int32_t layer;
 	int32_t* status;
+	int32_t* head_status;  // or null: attention-stage refusals to resolve into `status` first
 };
 void funnel(const FunnelArgs& a, hipStream_t s);
 

@@ -1112,7 +1112,16 @@ __global__ __launch_bounds__(BS) void k_funnel(sslm_launch::FunnelArgs a) {
 	uint32_t mx = part_max32<BS>(a.maxpart, 0, a.ntiles, t);
 	Scale inc{0, 0};
 	if (a.incoming) inc = a.incoming[t];
-	if (threadIdx.x == 0) s_st = a.status[slot];
+	if (threadIdx.x == 0) {
+		if (a.head_status) {  // the first refusing head of the attention that produced this row
+			const int32_t hs = a.head_status[slot];
+			if (hs != kHeadStatusNone) {
+				set_status(a.status, slot, a.layer, hs & 0xff);
+				a.head_status[slot] = kHeadStatusNone;
+			}
+		}
+		s_st = a.status[slot];
+	}
 	mx = blk_max32<BS>(mx, s_m);
 	if (s_st != 0) return;
 	FunnelPlan plan;
@@ -1343,32 +1352,107 @@ __global__ __launch_bounds__(BS) void k_mlp_act(sslm_launch::ActArgs a) {
 // positions p = threadIdx.x + k * BS through the score, exp and probability passes, so those
 // passes meet only at the row max and row sum.  PV: D / 4 threads cover one V row (4 channels
 // each); the position groups' int32 partials meet in LDS (exact: probabilities sum to <= 2^15).
-template <int BS, int D>
+//
+// FUSED (decode): the block first does the q|k|v post-processing of qkv_post for its head --
+// the q funnel from the projection's tile maxima, q codes and RoPE(q), and the K/V landing and
+// RoPE(K) of its KV group at the current position (forward_sites.cpp:1281-1418, :1748-1787).
+// The group's first head writes that K/V to the cache; every head reads position `pos` from its
+// own LDS copy, so no block reads what another block of the launch writes.
+template <int BS, int D, bool FUSED>
 __global__ __launch_bounds__(BS) void k_attention(sslm_launch::AttnArgs a, int use_lds) {
 	extern __shared__ int64_t dyn[];
 	__shared__ int64_t s_mx[BS / 64];
 	__shared__ int64_t s_sum[BS / 64];
 	__shared__ uint64_t s_ref[BS / 64];
-	__shared__ uint32_t s_ab[BS / 64];
+	__shared__ uint32_t s_ab[BS / 64], s_qm[BS / 64];
 	__shared__ int32_t s_ctx[BS * 4];
+	__shared__ __attribute__((aligned(16))) int8_t s_qc[D], s_kc[D], s_vc[D];
 	__shared__ int32_t s_st;
-	constexpr int TPR = D / 4, PG = BS / TPR;
+	constexpr int TPR = D / 4, PG = BS / TPR, PAIRS = D / 2;
+	static_assert(BS >= PAIRS, "one thread per RoPE pair");
 	const int h = blockIdx.x, t = blockIdx.y;
 	const int group = a.NH / a.NKV, kvh = h / group;
 	const TokenInfo ti = a.tok[t];
-	const Scale qs = a.q_scale[t];
 	const int64_t km = a.khead_m[kvh], ke = a.khead_e[kvh];
-	const int8_t* qrow = a.q_rot + (size_t)t * a.H + (size_t)h * D;
-	v4i q[D / 16];
-#pragma unroll
-	for (int j = 0; j < D / 16; ++j) q[j] = load16(qrow + 16 * j);
 	const int32_t* cf = a.ctx_fold + 3 * h;
 	const int32_t f0 = cf[0], f1 = cf[1], f2 = cf[2];
-	if (threadIdx.x == 0) s_st = a.status[ti.slot];
+	const int64_t pos = ti.pos;
+	const int8_t* blk = a.kv_pool + (int64_t)ti.block * a.block_bytes;
+	const int64_t half = a.cap * (int64_t)a.NKV * D;
+	int8_t* kstore = a.kv_pool + (int64_t)ti.block * a.block_bytes + (int64_t)a.layer * half * 2 + (int64_t)kvh * a.cap * D;
+	v4i q[D / 16];
+	Scale qs;
+	if (!FUSED) {
+		qs = a.q_scale[t];
+		const int8_t* qrow = a.q_rot + (size_t)t * a.H + (size_t)h * D;
+#pragma unroll
+		for (int j = 0; j < D / 16; ++j) q[j] = load16(qrow + 16 * j);
+		if (threadIdx.x == 0) s_st = a.status[ti.slot];
+	} else {
+		const int H = a.H, KVH = a.NKV * D, i = threadIdx.x;
+		const Scale ns = a.in_scale[t];
+		const bool pos_ok = pos >= 0 && pos < a.cap;
+		uint32_t qmx = part_max32<BS>(a.q_maxpart, 0, H / 16, t);
+		int2 qv = make_int2(0, 0);
+		longlong2 kk = make_longlong2(0, 0), vv = make_longlong2(0, 0);
+		int32_t c = 0, sn = 0;
+		if (i < PAIRS) {
+			qv = ((const int2*)(a.q_f + (size_t)t * H + (size_t)h * D))[i];
+			const int64_t* kvrow = a.kv_f + (size_t)t * 2 * KVH + (size_t)kvh * D;
+			kk = ((const longlong2*)kvrow)[i];
+			vv = ((const longlong2*)(kvrow + KVH))[i];
+			const int64_t pp = pos_ok ? pos : 0;
+			c = (int32_t)a.rope_cos[pp * PAIRS + i];
+			sn = (int32_t)a.rope_sin[pp * PAIRS + i];
+		}
+		const int64_t rtk = a.r_t_k[kvh], rtv = a.r_t_v[kvh];
+		const int64_t k_e = composed_exponent(ns.e, a.e_t_k[kvh]), v_e = composed_exponent(ns.e, a.e_t_v[kvh]);
+		if (threadIdx.x == 0) s_st = a.status[ti.slot];
+		qmx = blk_max32<BS>(qmx, s_qm);
+		if (s_st != 0) return;
+		FunnelPlan plan;
+		int32_t st = funnel_plan(qmx, &ns, 1, a.q_site, &plan);
+		if (st == kOk && !pos_ok) st = kPositionOverCap;
+		if (st != kOk) {  // the same for every head of the token
+			if (threadIdx.x == 0) set_status(a.status, ti.slot, a.layer, st);
+			return;
+		}
+		uint32_t sat = 0;
+		if (i < PAIRS) {
+			bool c0, c1, c2, c3, x0;
+			const int64_t k0 = clamp_code(landing_rescale(kk.x, ns.m, rtk, k_e, &c0, &x0));
+			const int64_t k1 = clamp_code(landing_rescale(kk.y, ns.m, rtk, k_e, &c1, &x0));
+			int64_t xr, yr;
+			rope_pair((int32_t)k0, (int32_t)k1, c, sn, &xr, &yr);
+			const char2 kc = make_char2((char)clamp_code(xr), (char)clamp_code(yr));
+			const char2 vc = make_char2((char)clamp_code(landing_rescale(vv.x, ns.m, rtv, v_e, &c2, &x0)),
+			                            (char)clamp_code(landing_rescale(vv.y, ns.m, rtv, v_e, &c3, &x0)));
+			sat = (uint32_t)c0 + (uint32_t)c1 + (uint32_t)c2 + (uint32_t)c3;
+			((char2*)s_kc)[i] = kc;
+			((char2*)s_vc)[i] = vc;
+			if (h % group == 0) {  // the group's writer
+				const int64_t off = pos * D + 2 * i;
+				*(char2*)(kstore + off) = kc;
+				*(char2*)(kstore + half + off) = vc;
+			}
+			const int32_t x = requant_code_small(qv.x, (uint64_t)plan.r, plan.s);
+			const int32_t y = requant_code_small(qv.y, (uint64_t)plan.r, plan.s);
+			rope_pair(x, y, c, sn, &xr, &yr);
+			((char2*)s_qc)[i] = make_char2((char)clamp_code(xr), (char)clamp_code(yr));
+		}
+		if (h % group == 0) {  // the writer counts the saturations of its landing
+			const int32_t ws = wave_sum32((int32_t)sat);
+			if ((threadIdx.x & 63) == 0 && ws) atomicAdd(&a.sat[ti.slot], (unsigned long long)ws);
+		}
+		__syncthreads();
+#pragma unroll
+		for (int j = 0; j < D / 16; ++j) q[j] = *(const v4i*)(s_qc + 16 * j);
+		qs = plan.out;
+	}
 	// i-exp constants of the row's scale (every thread, redundantly)
 	int32_t st = kOk;
 	int64_t c_qln2 = 0, c_qb = 0, c_qc = 0, c_M = 0;
-	const int64_t width = ti.pos + 1;
+	const int64_t width = pos + 1;
 	if (!fits_i32(qs.m) || !fits_i32(km)) {
 		st = kCarriedScaleMantissaOutOfDomain;
 	} else {
@@ -1384,8 +1468,6 @@ __global__ __launch_bounds__(BS) void k_attention(sslm_launch::AttnArgs a, int u
 	}
 	const bool live = st == kOk && width >= 1 && width <= a.cap;
 	int64_t* ex = use_lds ? dyn : a.scratch + ((int64_t)t * a.NH + h) * a.cap;
-	const int8_t* blk = a.kv_pool + (int64_t)ti.block * a.block_bytes;
-	const int64_t half = a.cap * (int64_t)a.NKV * D;
 	const int8_t* kbase = blk + (int64_t)a.layer * half * 2 + (int64_t)kvh * a.cap * D;
 	const int8_t* vbase = kbase + half;
 	// pass 1: scores (int32-exact dots) and the row max
@@ -1396,7 +1478,7 @@ __global__ __launch_bounds__(BS) void k_attention(sslm_launch::AttnArgs a, int u
 			int32_t acc = 0;
 #pragma unroll
 			for (int j = 0; j < D / 16; ++j) {
-				const v4i kw = load16(kr + 16 * j);
+				const v4i kw = FUSED && p == pos ? *(const v4i*)(s_kc + 16 * j) : load16(kr + 16 * j);
 				acc = __builtin_amdgcn_sdot4(q[j].x, kw.x, acc, false);
 				acc = __builtin_amdgcn_sdot4(q[j].y, kw.y, acc, false);
 				acc = __builtin_amdgcn_sdot4(q[j].z, kw.z, acc, false);
@@ -1407,13 +1489,13 @@ __global__ __launch_bounds__(BS) void k_attention(sslm_launch::AttnArgs a, int u
 		}
 	}
 	mx = blk_max_i64<BS>(mx, s_mx);
-	if (s_st != 0) return;
+	if (!FUSED && s_st != 0) return;
 	if (st != kOk) {
-		if (threadIdx.x == 0) set_status(a.status, ti.slot, a.layer, st);
+		if (threadIdx.x == 0) report_head(a.head_status, ti.slot, h, st);
 		return;
 	}
 	if (!live) {  // width outside [1, cap]: the KV landing of this position already refused it
-		if (threadIdx.x == 0) set_status(a.status, ti.slot, a.layer, kPositionOverCap);
+		if (threadIdx.x == 0) report_head(a.head_status, ti.slot, h, kPositionOverCap);
 		return;
 	}
 	// pass 2: i-exp values (SoftmaxRowQ15, intmath.cpp:853-889) and the row sum
@@ -1443,7 +1525,7 @@ __global__ __launch_bounds__(BS) void k_attention(sslm_launch::AttnArgs a, int u
 		refused |= s_ref[i];
 	}
 	if (refused) {
-		if (threadIdx.x == 0) set_status(a.status, ti.slot, a.layer, kSoftmaxKernelRefusedAfterGateAccepted);
+		if (threadIdx.x == 0) report_head(a.head_status, ti.slot, h, kSoftmaxKernelRefusedAfterGateAccepted);
 		return;
 	}
 	// pass 3: Q15 probabilities p = (e << 15) / max(total, 1)
@@ -1457,7 +1539,7 @@ __global__ __launch_bounds__(BS) void k_attention(sslm_launch::AttnArgs a, int u
 		const int8_t* vc = vbase + 4 * dq;
 #pragma unroll 4
 		for (int64_t p = pg; p < width; p += PG) {
-			const int32_t v = *(const int32_t*)(vc + p * D);
+			const int32_t v = FUSED && p == pos ? *(const int32_t*)(s_vc + 4 * dq) : *(const int32_t*)(vc + p * D);
 			const int32_t pr = (int32_t)ex[p];
 			acc0 += pr * (int32_t)(int8_t)(v & 0xff);
 			acc1 += pr * (int32_t)(int8_t)((v >> 8) & 0xff);
@@ -1661,17 +1743,23 @@ void qkv_post(const QkvPostArgs& a, hipStream_t s) {
 	no_instance("qkv_post", a.H);
 }
 
-void attention(const AttnArgs& a, hipStream_t s) {
+template <bool FUSED>
+static void launch_attention(const AttnArgs& a, hipStream_t s) {
 	const size_t lds = (size_t)a.cap * sizeof(int64_t);
 	const int use_lds = attention_in_lds(a.cap) ? 1 : 0;
 	const dim3 grid(a.NH, a.M);
+	const size_t dyn = use_lds ? lds : 0;
 	switch (a.D) {
-		case 32: hipLaunchKernelGGL((k_attention<kBlock, 32>), grid, dim3(kBlock), use_lds ? lds : 0, s, a, use_lds); break;
-		case 64: hipLaunchKernelGGL((k_attention<kBlock, 64>), grid, dim3(kBlock), use_lds ? lds : 0, s, a, use_lds); break;
-		case 128: hipLaunchKernelGGL((k_attention<kBlock, 128>), grid, dim3(kBlock), use_lds ? lds : 0, s, a, use_lds); break;
-		default: hipLaunchKernelGGL((k_attention<kBlock, 256>), grid, dim3(kBlock), use_lds ? lds : 0, s, a, use_lds); break;
+		case 32: hipLaunchKernelGGL((k_attention<kBlock, 32, FUSED>), grid, dim3(kBlock), dyn, s, a, use_lds); break;
+		case 64: hipLaunchKernelGGL((k_attention<kBlock, 64, FUSED>), grid, dim3(kBlock), dyn, s, a, use_lds); break;
+		case 128: hipLaunchKernelGGL((k_attention<kBlock, 128, FUSED>), grid, dim3(kBlock), dyn, s, a, use_lds); break;
+		case 256: hipLaunchKernelGGL((k_attention<kBlock, 256, FUSED>), grid, dim3(kBlock), dyn, s, a, use_lds); break;
+		default: no_instance("attention", a.D);
 	}
 }
+
+void attention(const AttnArgs& a, hipStream_t s) { launch_attention<false>(a, s); }
+void attention_decode(const AttnArgs& a, hipStream_t s) { launch_attention<true>(a, s); }
 
 void funnel(const FunnelArgs& a, hipStream_t s) {
 	const int need = row_ept(a.N, kFunnelBS);

@@ -215,6 +215,7 @@ struct sslm_model_s {
 	Scale* stream_scale;    // [kSlotCapacity]
 	unsigned long long* sat;  // [kSlotCapacity]
 	int32_t* status;        // [kSlotCapacity]
+	int32_t* head_status;   // [kSlotCapacity] attention-stage refusals awaiting the ctx funnel
 	std::vector<int> free_slots;
 	std::vector<Track> tracks;  // tracks[0]: prefill and head; all: decode token groups
 	std::map<std::string, hipGraphExec_t> graphs;  // captured decode submissions by shape
@@ -371,7 +372,7 @@ struct ProjArgs {
 	RawIn raw;
 };
 
-ProjArgs qkv_args(sslm_model m, Track& w, int l, int M, sslm_adapter ad) {
+ProjArgs qkv_args(sslm_model m, Track& w, int l, int M, sslm_adapter ad, bool fused) {
 	const DevLayer& lw = m->layers[l];
 	const int H = m->H, KVH = m->KVH;
 	GemmArgs g = gemm_args(m, w, w.normed, M, H, lw.w_qkv, H + 2 * KVH, H);
@@ -401,7 +402,8 @@ ProjArgs qkv_args(sslm_model m, Track& w, int l, int M, sslm_adapter ad) {
 	attach_lora(m, w, ad, l, 1, &g.epi.seg[1], 1);
 	attach_lora(m, w, ad, l, 2, &g.epi.seg[2], 2);
 	ProjArgs pa{g, RawIn{}};
-	pa.raw = split_raw(m, w, pa.g, H <= 4096, true);
+	// the fused decode attention reads the funnel epilogue's outputs (q tile maxima, K/V wide)
+	if (!fused) pa.raw = split_raw(m, w, pa.g, H <= 4096, true);
 	return pa;
 }
 
@@ -458,6 +460,42 @@ GemmArgs head_args(sslm_model m, Track& w, int M, const TokenInfo* tok) {
 	return g;
 }
 
+// Attention arguments shared by the fused (decode) and the two-kernel (prefill) paths.
+sslm_launch::AttnArgs attn_args(sslm_model m, Track& w, int l, int M) {
+	const DevLayer& lw = m->layers[l];
+	sslm_launch::AttnArgs a{};
+	a.M = M;
+	a.H = m->H;
+	a.NH = m->NH;
+	a.NKV = m->NKV;
+	a.D = m->D;
+	a.cap = m->cap;
+	a.tok = w.tok;
+	a.khead_m = lw.khead_m;
+	a.khead_e = lw.khead_e;
+	a.ctx_fold = lw.ctx_fold;
+	a.kv_pool = m->pool_dev;
+	a.block_bytes = (int64_t)m->block_bytes;
+	a.layer = l;
+	a.ln2_q = m->ln2_q;
+	a.b_q = m->b_q;
+	a.ca_q = m->ca_q;
+	a.ctx_f = w.ctx_f;
+	a.ctx_maxpart = w.mx_ctx;
+	a.scratch = w.attn_scratch;
+	a.status = m->status;
+	a.head_status = m->head_status;
+	return a;
+}
+
+bool fused_attention_enabled() {
+	static const bool on = [] {
+		const char* e = getenv("SSLM_HIP_FUSED_ATTN");
+		return !(e && e[0] == '0');
+	}();
+	return on;
+}
+
 // The stream (committed hidden state) a launch sequence reads and commits: decode batches use
 // the per-slot state, prefill chunks the chunk rows.
 struct StreamRef {
@@ -467,7 +505,9 @@ struct StreamRef {
 };
 
 // Layers [l0, l1) for M tokens whose TokenInfo is already on the device.
-void run_layers(sslm_model m, Track& w, int M, StreamRef st, int l0, int l1, sslm_adapter ad) {
+// `decode`: every token belongs to a different sequence (a decode step), so attention may take
+// the fused path.
+void run_layers(sslm_model m, Track& w, int M, StreamRef st, int l0, int l1, sslm_adapter ad, bool decode) {
 	const int H = m->H, I = m->I, KVH = m->KVH;
 	hipStream_t s = w.stream;
 	{
@@ -477,6 +517,7 @@ void run_layers(sslm_model m, Track& w, int M, StreamRef st, int l0, int l1, ssl
 		sslm_launch::rmsnorm(a, M, H, w.tok, m->status, l0, s);
 		ck(hipGetLastError());
 	}
+	const bool fused = decode && sslm_launch::gemv_eligible(M, H) && fused_attention_enabled();
 	for (int l = l0; l < l1; ++l) {
 		const DevLayer& lw = m->layers[l];
 		RawIn raw{};  // the last projection's split-K partials, when it split
@@ -484,11 +525,28 @@ void run_layers(sslm_model m, Track& w, int M, StreamRef st, int l0, int l1, ssl
 		{
 			const int pj[3] = {0, 1, 2};
 			run_lora_u(m, w, ad, l, pj, 3, w.normed, M, H);
-			ProjArgs pa = qkv_args(m, w, l, M, ad);
+			ProjArgs pa = qkv_args(m, w, l, M, ad, fused);
 			raw = pa.raw;
 			run_gemm(m, w, pa.g, kProfGemm);
 		}
-		{
+		if (fused) {
+			sslm_launch::AttnArgs a = attn_args(m, w, l, M);
+			a.q_f = w.q_f;
+			a.q_maxpart = w.mx_q;
+			a.kv_f = w.kv_f;
+			a.in_scale = w.normed_scale;
+			a.q_site = lw.q;
+			a.r_t_k = lw.r_t_k;
+			a.e_t_k = lw.e_t_k;
+			a.r_t_v = lw.r_t_v;
+			a.e_t_v = lw.e_t_v;
+			a.rope_cos = m->rope_cos;
+			a.rope_sin = m->rope_sin;
+			a.sat = m->sat;
+			ProfScope p(s, kProfAttn, 0, 0);
+			sslm_launch::attention_decode(a, s);
+			ck(hipGetLastError());
+		} else {
 			sslm_launch::QkvPostArgs a{};
 			a.M = M;
 			a.H = H;
@@ -516,36 +574,16 @@ void run_layers(sslm_model m, Track& w, int M, StreamRef st, int l0, int l1, ssl
 			a.status = m->status;
 			a.kv_pool = m->pool_dev;
 			a.raw = raw;
-			ProfScope p(s, kProfRow, 0, 0);
-			sslm_launch::qkv_post(a, s);
-			ck(hipGetLastError());
-		}
-		{
-			sslm_launch::AttnArgs a{};
-			a.M = M;
-			a.H = H;
-			a.NH = m->NH;
-			a.NKV = m->NKV;
-			a.D = m->D;
-			a.cap = m->cap;
-			a.tok = w.tok;
-			a.q_rot = w.q_rot;
-			a.q_scale = w.q_scale;
-			a.khead_m = lw.khead_m;
-			a.khead_e = lw.khead_e;
-			a.ctx_fold = lw.ctx_fold;
-			a.kv_pool = m->pool_dev;
-			a.block_bytes = (int64_t)m->block_bytes;
-			a.layer = l;
-			a.ln2_q = m->ln2_q;
-			a.b_q = m->b_q;
-			a.ca_q = m->ca_q;
-			a.ctx_f = w.ctx_f;
-			a.ctx_maxpart = w.mx_ctx;
-			a.scratch = w.attn_scratch;
-			a.status = m->status;
+			{
+				ProfScope p(s, kProfRow, 0, 0);
+				sslm_launch::qkv_post(a, s);
+				ck(hipGetLastError());
+			}
+			sslm_launch::AttnArgs aa = attn_args(m, w, l, M);
+			aa.q_rot = w.q_rot;
+			aa.q_scale = w.q_scale;
 			ProfScope p(s, kProfAttn, 0, 0);
-			sslm_launch::attention(a, s);
+			sslm_launch::attention(aa, s);
 			ck(hipGetLastError());
 		}
 		{
@@ -563,6 +601,7 @@ void run_layers(sslm_model m, Track& w, int M, StreamRef st, int l0, int l1, ssl
 			a.out_scale = w.ctx_scale;
 			a.layer = l;
 			a.status = m->status;
+			a.head_status = m->head_status;
 			ProfScope p(s, kProfRow, 0, 0);
 			sslm_launch::funnel(a, s);
 			ck(hipGetLastError());
@@ -982,6 +1021,11 @@ bool build_device_model(sslm_model m, std::string* err) {
 	m->stream_scale = dalloc<Scale>(kSlotCapacity, &own);
 	m->sat = dalloc<unsigned long long>(kSlotCapacity, &own);
 	m->status = dalloc<int32_t>(kSlotCapacity, &own);
+	m->head_status = dalloc<int32_t>(kSlotCapacity, &own);
+	{
+		const std::vector<int32_t> none(kSlotCapacity, kHeadStatusNone);
+		ck(hipMemcpy(m->head_status, none.data(), none.size() * sizeof(int32_t), hipMemcpyHostToDevice));
+	}
 	for (int i = kSlotCapacity - 1; i >= 0; --i) m->free_slots.push_back(i);
 	// tracks: track 0 carries prefill chunks and the LM head; the others run extra token groups
 	// of a decode step concurrently
@@ -1029,7 +1073,7 @@ sslm_status prefill_tokens(sslm_model m, sslm_seq s, const int32_t* tokens, int 
 			                   w.hid_chunk_scale, w.ident, w.tok, m->status, w.stream);
 			ck(hipGetLastError());
 		}
-		run_layers(m, w, T, StreamRef{w.hid_chunk, w.hid_chunk_scale, w.ident}, 0, m->L, s->adapter);
+		run_layers(m, w, T, StreamRef{w.hid_chunk, w.hid_chunk_scale, w.ident}, 0, m->L, s->adapter, false);
 		int32_t word = 0;
 		ck(hipMemcpyAsync(&word, m->status + s->slot, 4, hipMemcpyDeviceToHost, w.stream));
 		ck(hipStreamSynchronize(w.stream));
@@ -1422,7 +1466,7 @@ static sslm_status decode_batch(sslm_model m, sslm_seq* seqs, int32_t n, uint32_
 			                   m->stream_scale, w.slot_idx, w.tok, m->status, w.stream);
 			ck(hipGetLastError());
 		}
-		run_layers(m, w, M, StreamRef{m->stream_codes, m->stream_scale, w.slot_idx}, (int)un.l0, (int)un.l1, un.ad);
+		run_layers(m, w, M, StreamRef{m->stream_codes, m->stream_scale, w.slot_idx}, (int)un.l0, (int)un.l1, un.ad, true);
 	};
 	auto stage_logits = [&](size_t b, int M, hipStream_t s) {
 		h_tok.emplace_back(M);
@@ -1858,9 +1902,15 @@ int32_t sslm_hip_bench_decode_gemv(sslm_model model, int32_t M, int32_t iters, d
 		for (int t = 0; t < M; ++t) ti[t] = TokenInfo{0, t, 0};
 		ck(hipMemcpyAsync(w.tok, ti.data(), M * sizeof(TokenInfo), hipMemcpyHostToDevice, w.stream));
 		ck(hipMemcpyAsync(w.lg_tok, ti.data(), M * sizeof(TokenInfo), hipMemcpyHostToDevice, w.stream));
-		std::vector<GemmArgs> gs = {qkv_args(m, w, 0, M, nullptr).g, o_args(m, w, 0, M, nullptr).g,
+		std::vector<GemmArgs> gs = {qkv_args(m, w, 0, M, nullptr, fused_attention_enabled()).g, o_args(m, w, 0, M, nullptr).g,
 		                            gu_args(m, w, 0, M, nullptr).g, down_args(m, w, 0, M, nullptr).g,
 		                            head_args(m, w, M, w.lg_tok)};
+		// The timed launches run on whatever the workspaces hold: their epilogue refusals must not
+		// reach the sequences' status words, so they write a private array.
+		int32_t* scratch_status = nullptr;
+		ck(hipMalloc(&scratch_status, (size_t)kSlotCapacity * sizeof(int32_t)));
+		ck(hipMemsetAsync(scratch_status, 0, (size_t)kSlotCapacity * sizeof(int32_t), w.stream));
+		for (GemmArgs& g : gs) g.epi.status = scratch_status;
 		hipEvent_t a, b;
 		ck(hipEventCreate(&a));
 		ck(hipEventCreate(&b));
@@ -1881,6 +1931,7 @@ int32_t sslm_hip_bench_decode_gemv(sslm_model model, int32_t M, int32_t iters, d
 		(void)hipEventDestroy(a);
 		(void)hipEventDestroy(b);
 		ck(hipStreamSynchronize(w.stream));
+		ck(hipFree(scratch_status));
 		return SSLM_OK;
 	});
 	return st == SSLM_OK ? n : -1;
