@@ -103,37 +103,42 @@ def copy_calibration(hip):
 
 def traffic_from(fetch_csv, write_csv):
     """HBM bytes per decode-GEMV launch from two rocprofv3 --pmc runs of
-    `bench.py --phase decode --calibrate`: FETCH_SIZE and WRITE_SIZE (KiB per dispatch), each
-    scaled by what the counter reads for the calibration copy of known size."""
-    def per_kernel(path, counter):
-        vals = defaultdict(list)
+    `bench.py --phase decode --pmc-steps --calibrate` (decode steps only, so the dispatches are the
+    step's own mix): FETCH_SIZE and WRITE_SIZE (KiB per dispatch), each scaled by what the counter
+    reads for the calibration copy of known size, averaged per (kernel, grid) and over every
+    M <= 16 GEMV dispatch (the prompts' prefill runs M = 32 instances, k_gemv<2, ...>)."""
+    def per_dispatch(path, counter):
+        vals, meta = defaultdict(float), {}
         for r in csv.DictReader(open(path)):
             if r["Counter_Name"] != counter:
                 continue
-            vals[(r["Dispatch_Id"], r["Kernel_Name"])].append(float(r["Counter_Value"]))
-        agg = defaultdict(list)
-        for (d, name), v in vals.items():
-            agg[name].append(sum(v))
-        return agg
-    fetch = per_kernel(fetch_csv, "FETCH_SIZE")
-    write = per_kernel(write_csv, "WRITE_SIZE")
-    copy_name = next(n for n in fetch if "copyBuffer" in n)
-    f_scale = CALIBRATION_BYTES / (max(fetch[copy_name]) * 1024.0)
-    w_scale = CALIBRATION_BYTES / (max(write[copy_name]) * 1024.0)
-    kernels = {}
-    for name in fetch:
-        if "k_gemv<1," not in name:  # decode-step GEMVs (M <= 16); the prompts' prefill runs M = 32
+            d = r["Dispatch_Id"]
+            vals[d] += float(r["Counter_Value"])
+            meta[d] = (r["Kernel_Name"], int(r["Grid_Size"]) // int(r["Workgroup_Size"]))
+        groups = defaultdict(list)
+        for d, v in vals.items():
+            groups[meta[d]].append(v)
+        return groups
+    fetch = per_dispatch(fetch_csv, "FETCH_SIZE")
+    write = per_dispatch(write_csv, "WRITE_SIZE")
+    copy_key = next(k for k in fetch if "copyBuffer" in k[0])
+    f_scale = CALIBRATION_BYTES / (max(fetch[copy_key]) * 1024.0)
+    w_scale = CALIBRATION_BYTES / (max(write[copy_key]) * 1024.0)
+    kernels = []
+    for (name, blocks), fv in sorted(fetch.items(), key=lambda kv: kv[0][1]):
+        if "k_gemv<1," not in name:
             continue
-        f = np.mean(fetch[name]) * 1024.0 * f_scale
-        w = np.mean(write.get(name, [0.0])) * 1024.0 * w_scale
-        kernels[name] = {"dispatches": len(fetch[name]), "fetch_bytes": round(f), "write_bytes": round(w)}
-    total_d = sum(k["dispatches"] for k in kernels.values())
-    total_b = sum((k["fetch_bytes"] + k["write_bytes"]) * k["dispatches"] for k in kernels.values())
+        f = np.mean(fv) * 1024.0 * f_scale
+        w = np.mean(write.get((name, blocks), [0.0])) * 1024.0 * w_scale
+        kernels.append({"kernel": name, "blocks": blocks, "dispatches": len(fv), "fetch_bytes": round(f),
+                        "write_bytes": round(w)})
+    total_d = sum(k["dispatches"] for k in kernels)
+    total_b = sum((k["fetch_bytes"] + k["write_bytes"]) * k["dispatches"] for k in kernels)
     out = {"calibration": {"copy_bytes": CALIBRATION_BYTES, "fetch_scale": f_scale, "write_scale": w_scale},
            "kernels": kernels, "mean_traffic_bytes_per_launch": round(total_b / max(1, total_d)),
            "dispatches": total_d,
            "command": "rocprofv3 --pmc FETCH_SIZE (then WRITE_SIZE) --output-format csv -- "
-                      "python3 bench.py --phase decode --steps 5 --warmup 2 --no-cpu --calibrate"}
+                      "python3 bench.py --phase decode --pmc-steps --steps 3 --warmup 2 --no-cpu --calibrate"}
     os.makedirs(os.path.dirname(TRAFFIC_FILE), exist_ok=True)
     json.dump(out, open(TRAFFIC_FILE, "w"), indent=1)
     print(json.dumps(out, indent=1))
@@ -150,6 +155,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--phase", choices=["all", "decode", "prefill"], default="all")
     ap.add_argument("--calibrate", action="store_true", help="add the PMC calibration copy")
+    ap.add_argument("--pmc-steps", action="store_true",
+                    help="decode steps only (no profiled pass, GEMV timing or M = 1 decode): for --pmc runs")
     ap.add_argument("--traffic-from", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"))
     args = ap.parse_args()
     if args.traffic_from:
@@ -196,6 +203,8 @@ def main():
         tok_s = B * args.steps / dt
         ms_step = dt * 1000.0 / args.steps
         print(f"[bench] decode B={B}: {ms_step:.3f} ms/step, {tok_s:.1f} tok/s", file=sys.stderr, flush=True)
+        if args.pmc_steps:
+            return
 
         # profiled pass of the same steps: events around every launch, per class and per shape
         profile(hip, True)
