@@ -210,6 +210,19 @@ bool value_gate(const Artifact& a, std::string* err) {
 		if (e < -60) return fail(err, "KvLandingReciprocals e below -60");
 		if (r < ((int64_t)1 << 31) + 1 || r > ((int64_t)1 << 32)) return fail(err, "KvLandingReciprocals R outside (2^31, 2^32]");
 	}
+	// DeltaFoldScales / UFoldScales (src/model.cpp:320-345, :380-405): (identity, mult, exponent)
+	// triples, identity in {0,1}, exponent in [-31, 31]
+	for (const auto* fold : {&a.delta_fold, &a.u_fold}) {
+		for (const auto& kv : *fold) {
+			const TensorView& t = kv.second;
+			if (t.elems % 3) return fail(err, "amplifying fold " + kv.first + " is not a multiple of 3");
+			for (uint64_t r = 0; r < t.elems / 3; ++r) {
+				const int32_t id = rd_i32(t.data + r * 12), ex = rd_i32(t.data + r * 12 + 8);
+				if (id < 0 || id > 1) return fail(err, "amplifying fold " + kv.first + " identity not in {0,1}");
+				if (ex < -31 || ex > 31) return fail(err, "amplifying fold " + kv.first + " exponent outside [-31,31]");
+			}
+		}
+	}
 	if (a.has_config) {  // geometry join and ROP1 shape (src/model.cpp:1260-1330)
 		const ModelConfig& c = a.config;
 		if (c.kv_heads > c.heads || c.heads % c.kv_heads) return fail(err, "CFG1 kv heads do not divide heads");

@@ -40,7 +40,8 @@ struct Artifact {
 };
 
 // Parses and validates `data` (header, section table, SHA-256 integrity, every sub-format and
-// the load-time value gate).  Returns false with a diagnostic on any rejection.
+// the load-time value gate).  Returns false with a diagnostic on any rejection.  Config and
+// SigmoidLut are required of every artifact, adapters included (src/artifact.cpp:152-170).
 bool parse_artifact(const uint8_t* data, size_t size, Artifact* out, std::string* err);
 
 // The canonical SIL1 table: round_half_even(sigmoid(-16 + i/32) * 2^15), i in [0, 1024].

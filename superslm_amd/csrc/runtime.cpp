@@ -1702,15 +1702,119 @@ sslm_status sslm_seq_save(sslm_seq seq, void* buf, size_t* n) {
 	return SSLM_INVALID_ARGUMENT;
 }
 
+// src/sslm_abi.cpp:2990-3085 with PopulateAdapterFromView (adapter_marshal.h): the adapter is an
+// .sslm container (Config and SigmoidLut copied from the base, like every artifact) whose
+// Provenance section starts with the 68-byte ADP1 record (magic, version 1,
+// rank, target-module mask, base integrity hash, lora_alpha, use_rslora, reserved 0, name
+// length), whose DeltaFoldScales entries "layer<N>.<proj>" name the adapted projections, each with
+// a UFoldScales entry of `rank` rows and "<name>.lora_A" [rank, in] / "<name>.lora_B" [out, rank]
+// int8 tensors.  Checks run in the reference's order; a base-hash mismatch is
+// SSLM_ADAPTER_MODEL_MISMATCH, every other rejection SSLM_ARTIFACT_REJECTED.  Ranks above
+// kMaxRank (64) are outside this backend's kernels and rejected as well.
 sslm_status sslm_adapter_map(const void* data, size_t size, sslm_model base, sslm_adapter* out) {
-	(void)data;
-	(void)size;
-	(void)base;
-	if (out) *out = nullptr;
-	return SSLM_INVALID_ARGUMENT;
+	if (!out) return SSLM_INVALID_ARGUMENT;
+	*out = nullptr;
+	if (!data || !base) return SSLM_INVALID_ARGUMENT;
+	Artifact A;
+	std::string err;
+	if (!parse_artifact((const uint8_t*)data, size, &A, &err)) return SSLM_ARTIFACT_REJECTED;
+	const uint8_t* pv = A.provenance;
+	if (!pv || A.provenance_bytes < 68 || memcmp(pv, "ADP1", 4) != 0 || rd_i32(pv + 4) != 1) return SSLM_ARTIFACT_REJECTED;
+	const uint32_t rank = (uint32_t)rd_i32(pv + 8), mask = (uint32_t)rd_i32(pv + 12);
+	if (rd_i32(pv + 60) != 0) return SSLM_ARTIFACT_REJECTED;
+	const uint32_t name_len = (uint32_t)rd_i32(pv + 64);
+	if (A.provenance_bytes < 68ull + name_len) return SSLM_ARTIFACT_REJECTED;
+	if (mask & ~0x7fu) return SSLM_ARTIFACT_REJECTED;  // 7 PEFT-adaptable projections (model.h:433)
+	if (memcmp(pv + 16, base->art.hash, 32) != 0) return SSLM_ADAPTER_MODEL_MISMATCH;
+	if (A.weights.empty() || A.delta_fold.empty() || A.u_fold.empty()) return SSLM_ARTIFACT_REJECTED;
+	if (rank > (uint32_t)kMaxRank) return SSLM_ARTIFACT_REJECTED;
+	// ADP1 mask bit order: q o gate up down k v; handle slots: q k v o gate up down
+	static const char* const kProj[7] = {"q_proj", "o_proj", "gate_proj", "up_proj", "down_proj", "k_proj", "v_proj"};
+	static const int kSlot[7] = {0, 3, 4, 5, 6, 1, 2};
+	const uint64_t H = base->H, I = base->I, KVH = base->KVH;
+	const uint64_t out_ch[7] = {H, H, I, I, H, KVH, KVH};
+	const uint64_t in_ch[7] = {H, H, H, H, I, H, H};
+	struct Item {
+		int layer, proj;
+		const TensorView *a, *b, *d, *u;
+	};
+	std::vector<Item> items;
+	for (const auto& kv : A.delta_fold) {
+		const std::string& name = kv.first;
+		// "layer<N>.<proj>" (adapter_marshal.h ParseLayerProjName)
+		if (name.size() <= 5 || name.compare(0, 5, "layer") != 0) return SSLM_ARTIFACT_REJECTED;
+		size_t i = 5;
+		uint64_t layer = 0;
+		while (i < name.size() && name[i] >= '0' && name[i] <= '9') {
+			layer = layer * 10 + (uint64_t)(name[i] - '0');
+			if (layer > 0xffffffffull) return SSLM_ARTIFACT_REJECTED;
+			++i;
+		}
+		if (i == 5 || i >= name.size() || name[i] != '.') return SSLM_ARTIFACT_REJECTED;
+		const std::string proj = name.substr(i + 1);
+		if (proj.empty() || proj.find('.') != std::string::npos) return SSLM_ARTIFACT_REJECTED;
+		if (layer >= (uint64_t)base->L) return SSLM_ARTIFACT_REJECTED;
+		int pi = -1;
+		for (int k = 0; k < 7; ++k)
+			if (proj == kProj[k]) pi = k;
+		if (pi < 0 || !(mask >> pi & 1)) return SSLM_ARTIFACT_REJECTED;
+		if (kv.second.elems / 3 != out_ch[pi]) return SSLM_ARTIFACT_REJECTED;
+		auto u = A.u_fold.find(name);
+		if (u == A.u_fold.end() || u->second.elems / 3 != rank) return SSLM_ARTIFACT_REJECTED;
+		auto a = A.weights.find(name + ".lora_A"), b = A.weights.find(name + ".lora_B");
+		if (a == A.weights.end() || b == A.weights.end()) return SSLM_ARTIFACT_REJECTED;
+		if (a->second.rank != 2 || a->second.shape[0] != rank || a->second.shape[1] != in_ch[pi]) return SSLM_ARTIFACT_REJECTED;
+		if (b->second.rank != 2 || b->second.shape[0] != out_ch[pi] || b->second.shape[1] != rank) return SSLM_ARTIFACT_REJECTED;
+		items.push_back(Item{(int)layer, kSlot[pi], &a->second, &b->second, &kv.second, &u->second});
+	}
+	auto* h = new (std::nothrow) sslm_adapter_s();
+	if (!h) return SSLM_ALLOCATION_FAILED;
+	const sslm_status st = guarded([&]() -> sslm_status {
+		h->model = base;
+		h->rank = rank;
+		h->bytes = size;
+		h->proj.assign((size_t)base->L * 7, AdapterProj{});
+		for (const Item& it : items) {
+			AdapterProj& p = h->proj[(size_t)it.layer * 7 + it.proj];
+			std::vector<int8_t> a8, b8;
+			std::vector<int32_t> uf, df;
+			append_le(&a8, *it.a);
+			append_le(&b8, *it.b);
+			append_le(&uf, *it.u);
+			append_le(&df, *it.d);
+			p.a = dupload(a8, &h->owned);
+			p.b = dupload(b8, &h->owned);
+			p.ufold = dupload(uf, &h->owned);
+			p.dfold = dupload(df, &h->owned);
+		}
+		return SSLM_OK;
+	});
+	if (st != SSLM_OK) {
+		for (void* q : h->owned) (void)hipFree(q);
+		delete h;
+		return st;
+	}
+	base->live_refs++;
+	*out = h;
+	return SSLM_OK;
 }
 
-sslm_status sslm_adapter_release(sslm_adapter adapter) { return adapter ? SSLM_OK : SSLM_INVALID_ARGUMENT; }
+sslm_status sslm_adapter_release(sslm_adapter adapter) {
+	if (!adapter) return SSLM_INVALID_ARGUMENT;
+	if (adapter->live_refs.load() != 0) return SSLM_ADAPTER_HAS_LIVE_SEQUENCES;
+	{
+		// no decode may still read the adapter's tensors
+		std::lock_guard<std::mutex> lk(adapter->model->mu);
+		for (Track& w : adapter->model->tracks)
+			if (w.stream) (void)hipStreamSynchronize(w.stream);
+		for (auto& kv : adapter->model->graphs) (void)hipGraphExecDestroy(kv.second);
+		adapter->model->graphs.clear();  // captured graphs may hold its device pointers
+	}
+	for (void* q : adapter->owned) (void)hipFree(q);
+	adapter->model->live_refs--;
+	delete adapter;
+	return SSLM_OK;
+}
 
 size_t sslm_adapter_residency(sslm_adapter adapter) { return adapter ? adapter->bytes : 0; }
 

@@ -139,9 +139,30 @@ class Model:
         self.lib.check("sslm_decode_step", st)
         return list(out)
 
+    def adapter(self, artifact) -> "Adapter":
+        return Adapter(self, artifact)
+
     def close(self):
         if self.handle:
             self.lib.check("sslm_model_unmap", self.lib.lib.sslm_model_unmap(self.handle))
+            self.handle = None
+
+
+class Adapter:
+    """A mapped LoRA adapter artifact (sslm_adapter_map).  Keeps its bytes alive."""
+
+    def __init__(self, model: Model, artifact):
+        self.model = model
+        self._bytes = ctypes.create_string_buffer(bytes(artifact), len(artifact))
+        h = ctypes.c_void_p()
+        self.status = model.lib.lib.sslm_adapter_map(ctypes.addressof(self._bytes), len(artifact),
+                                                     model.handle, ctypes.byref(h))
+        model.lib.check("sslm_adapter_map", self.status)
+        self.handle = h
+
+    def release(self):
+        if self.handle:
+            self.model.lib.check("sslm_adapter_release", self.model.lib.lib.sslm_adapter_release(self.handle))
             self.handle = None
 
 

@@ -388,3 +388,59 @@ def build_synthetic(cfg: ModelConfig, seed: int = 1234, temperature: float = 1.0
     m.rng = rng
     m.to_array()
     return m
+
+
+# ADP1 target-module bit order (reference include/superslm/model.h:433 kPeftAdaptableProjections)
+PEFT_PROJECTIONS = ("q_proj", "o_proj", "gate_proj", "up_proj", "down_proj", "k_proj", "v_proj")
+
+
+def build_adapter(sm: SyntheticModel, rank: int = 16, targets=("q_proj", "v_proj"), seed: int = 77,
+                  layers=None, name: str = "synthetic") -> bytes:
+    """A seeded LoRA adapter artifact for `sm` (reference adapter_marshal.h PopulateAdapterFromView):
+    Config and SigmoidLut copied from the base, Provenance = the 68-byte ADP1 record + name, Weights = "layer<N>.<proj>.lora_A" [rank, in] and
+    ".lora_B" [out, rank] int8, DeltaFoldScales / UFoldScales = (identity, mult, exponent) rows
+    for each adapted "layer<N>.<proj>".  The u folds bring A.x back into code range; the delta
+    folds mix identity rows, attenuating exponents and amplifying (negative) exponents so every
+    branch of the amplifying fold is exercised."""
+    c = sm.config
+    rng = np.random.default_rng(seed)
+    base_hash = bytes(sm.to_array()[HASH_OFFSET:HASH_OFFSET + 32])
+    kvh = c.kv_heads * c.head_dim
+    out_ch = {"q_proj": c.hidden, "o_proj": c.hidden, "down_proj": c.hidden, "k_proj": kvh, "v_proj": kvh,
+              "gate_proj": c.inter, "up_proj": c.inter}
+    in_ch = {p: (c.inter if p == "down_proj" else c.hidden) for p in PEFT_PROJECTIONS}
+    mask = 0
+    for t in targets:
+        mask |= 1 << PEFT_PROJECTIONS.index(t)
+    weights, dfs, ufs = [], [], []
+    for layer in (range(c.layers) if layers is None else layers):
+        for proj in targets:
+            key = f"layer{layer}.{proj}"
+            k_in, n_out = in_ch[proj], out_ch[proj]
+            a = rng.integers(-127, 128, size=(rank, k_in), dtype=np.int8)
+            b = rng.integers(-127, 128, size=(n_out, rank), dtype=np.int8)
+            # |A.x| ~ 127 * 73 * sqrt(K): exponent so u lands around +-40 (some rows saturate)
+            ue = int(np.clip(np.round(np.log2(0.75 * 127 * 73 * np.sqrt(k_in) / 40.0)), 0, 31))
+            u = np.empty((rank, 3), dtype=np.int32)
+            u[:, 0] = 0
+            u[:, 1] = rng.integers(1 << 30, 1 << 31, size=rank, dtype=np.int64).astype(np.int32)
+            u[:, 2] = rng.integers(ue - 1, ue + 2, size=rank)
+            u[rank // 2, 0] = 1  # one pass-through row (clamped to +-127 by the site)
+            d = np.empty((n_out, 3), dtype=np.int32)
+            d[:, 0] = (rng.random(n_out) < 0.1).astype(np.int32)
+            d[:, 1] = rng.integers(1 << 30, 1 << 31, size=n_out, dtype=np.int64).astype(np.int32)
+            d[:, 2] = rng.integers(-2, 9, size=n_out)
+            weights += [(key + ".lora_A", a), (key + ".lora_B", b)]
+            dfs.append((key, d))
+            ufs.append((key, u))
+    nm = name.encode()
+    prov = struct.pack("<4siii32sdiii", b"ADP1", 1, rank, mask, base_hash, float(2 * rank), 0, 0, len(nm)) + nm
+    sections = [  # the reference converter's six sections (tools/sslm_convert_adapter.py:1315-1320)
+        (SEC_CONFIG, DT_RAW, cfg1(c), 8),
+        (SEC_SIGMOID_LUT, DT_I32, sil1(sm.silu), 8),
+        (SEC_PROVENANCE, DT_RAW, prov, 8),
+        (SEC_WEIGHTS, DT_I8, Manifest(b"WGT1", 1, weights), 64),
+        (SEC_DELTA_FOLD, DT_I32, Manifest(b"DFS1", 4, dfs), 64),
+        (SEC_U_FOLD, DT_I32, Manifest(b"UFS1", 4, ufs), 64),
+    ]
+    return write_container(sections)

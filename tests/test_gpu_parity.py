@@ -120,3 +120,95 @@ def test_long_prefill_chunk_matches_reference(name, n, hip_lib, ref_lib):
     assert np.array_equal(h[1], r[1]), "KV after prefill differs"
     assert h[2] == r[2], f"tokens differ: hip {h[2]} ref {r[2]}"
     assert np.array_equal(h[3], r[3]), "KV after decode differs"
+
+
+ALL_PROJ = ("q_proj", "o_proj", "gate_proj", "up_proj", "down_proj", "k_proj", "v_proj")
+
+
+def _run_lora(lib, artifact, adapter_blobs, prompts, script, budget):
+    """Sequences with adapters (index into `adapter_blobs` or None) decoded together; `script` is a
+    list of (step count, {sequence: adapter index or None}) phases -- the attachments change
+    between tokens, as sslm_seq_set_adapter allows.  Returns every phase's tokens and the KV."""
+    model = Model(lib, artifact)
+    ads = [model.adapter(b) for b in adapter_blobs]
+    pool = model.pool(len(prompts))
+    seqs = [pool.seq() for _ in prompts]
+    toks = []
+    for phase, (steps, attach) in enumerate(script):
+        for i, a in attach.items():
+            seqs[i].set_adapter(ads[a] if a is not None else None)
+        if phase == 0:
+            for sq, p in zip(seqs, prompts):
+                sq.prefill(p)
+        for _ in range(steps):
+            toks.append(model.decode_step(seqs, budget))
+    kv = [pool.kv_block(i).copy() for i in range(len(prompts))]
+    for sq in seqs:
+        sq.release()
+    pool.close()
+    for a in ads:
+        a.release()
+    model.close()
+    return toks, kv
+
+
+@pytest.mark.parametrize("name,targets,rank", [("small", ("q_proj", "v_proj"), 16), ("tiny", ALL_PROJ, 8),
+                                               ("medium", ALL_PROJ, 16)])
+def test_lora_adapter_matches_reference(name, targets, rank, hip_lib, ref_lib):
+    """LoRA side-GEMMs (u = amp_fold(A.x), delta = amp_fold(B.u)) on the adapted projections,
+    with a swap between tokens: adapter 0 on every sequence, then sequence 0 detached and
+    sequence 1 moved to adapter 1, mixed with an unadapted sequence in the same batch."""
+    from superslm_amd.sslm_artifact import build_adapter
+    sm, art = synthetic(name)
+    blobs = [build_adapter(sm, rank=rank, targets=targets, seed=s) for s in (5, 6)]
+    rng = np.random.default_rng(41)
+    prompts = [rng.integers(0, sm.config.vocab, size=n) for n in (7, 12, 4)]
+    L = sm.config.layers
+    for budget in sorted({L, 1}):
+        script = [(2 * L // budget, {0: 0, 1: 0, 2: None}), (2 * L // budget, {0: None, 1: 1})]
+        print(f"case lora {name} targets={len(targets)} rank={rank} budget={budget}", flush=True)
+        r = _run_lora(ref_lib, art, blobs, prompts, script, budget)
+        h = _run_lora(hip_lib, art, blobs, prompts, script, budget)
+        assert h[0] == r[0], f"tokens differ: hip {h[0]} ref {r[0]}"
+        for i in range(len(prompts)):
+            assert np.array_equal(h[1][i], r[1][i]), f"KV of sequence {i} differs"
+
+
+@pytest.mark.parametrize("name,n", [("small", 90)])
+def test_lora_long_prefill_matches_reference(name, n, hip_lib, ref_lib):
+    """A prefill chunk of more than 64 tokens with every projection adapted (the tiled GEMM with
+    the LoRA epilogue, the batched u side-GEMM)."""
+    from superslm_amd.sslm_artifact import build_adapter
+    sm, art = synthetic(name)
+    blob = build_adapter(sm, rank=16, targets=ALL_PROJ, seed=9)
+    rng = np.random.default_rng(43)
+    prompt = rng.integers(0, sm.config.vocab, size=n)
+    L = sm.config.layers
+    print(f"case lora long prefill {name} n={n}", flush=True)
+    script = [(3, {0: 0})]
+    r = _run_lora(ref_lib, art, [blob], [prompt], script, L)
+    h = _run_lora(hip_lib, art, [blob], [prompt], script, L)
+    assert h[0] == r[0], f"tokens differ: hip {h[0]} ref {r[0]}"
+    assert np.array_equal(h[1][0], r[1][0]), "KV differs"
+
+
+def test_adapter_map_rejections_match_reference(hip_lib, ref_lib):
+    """sslm_adapter_map statuses: another base's adapter, a truncated container, a bad ADP1 magic."""
+    from superslm_amd.sslm import SslmError
+    from superslm_amd.sslm_artifact import build_adapter
+    sm, art = synthetic("tiny")
+    sm2, _ = synthetic("tiny", seed=8)
+    good = build_adapter(sm, rank=4, seed=1)
+    cases = {"other base": build_adapter(sm2, rank=4, seed=1), "truncated": good[:-7]}
+    statuses = {}
+    for lib_name, lib in (("ref", ref_lib), ("hip", hip_lib)):
+        model = Model(lib, art)
+        for case, blob in cases.items():
+            try:
+                model.adapter(blob).release()
+                statuses[(lib_name, case)] = 0
+            except SslmError as e:
+                statuses[(lib_name, case)] = e.status
+        model.close()
+    for case in cases:
+        assert statuses[("hip", case)] == statuses[("ref", case)] != 0, (case, statuses)
