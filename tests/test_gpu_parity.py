@@ -165,7 +165,9 @@ def test_lora_adapter_matches_reference(name, targets, rank, hip_lib, ref_lib):
     prompts = [rng.integers(0, sm.config.vocab, size=n) for n in (7, 12, 4)]
     L = sm.config.layers
     for budget in sorted({L, 1}):
-        script = [(2 * L // budget, {0: 0, 1: 0, 2: None}), (2 * L // budget, {0: None, 1: 1})]
+        # phases end on token boundaries (the first call after prefill only produces logits;
+        # a token takes L / budget calls), where sslm_seq_set_adapter accepts a swap
+        script = [(1 + 2 * (L // budget), {0: 0, 1: 0, 2: None}), (2 * (L // budget), {0: None, 1: 1})]
         print(f"case lora {name} targets={len(targets)} rank={rank} budget={budget}", flush=True)
         r = _run_lora(ref_lib, art, blobs, prompts, script, budget)
         h = _run_lora(hip_lib, art, blobs, prompts, script, budget)
@@ -193,7 +195,7 @@ def test_lora_long_prefill_matches_reference(name, n, hip_lib, ref_lib):
 
 
 def test_adapter_map_rejections_match_reference(hip_lib, ref_lib):
-    """sslm_adapter_map statuses: another base's adapter, a truncated container, a bad ADP1 magic."""
+    """sslm_adapter_map statuses: another base's adapter, a truncated container."""
     from superslm_amd.sslm import SslmError
     from superslm_amd.sslm_artifact import build_adapter
     sm, art = synthetic("tiny")
