@@ -366,9 +366,15 @@ SSLM_HD int64_t landing_rescale(int64_t branch, int64_t m_a, int64_t r_t, int64_
 	return raw;
 }
 
-SSLM_COLD int64_t landing_rescale_cold(int64_t branch, int64_t m_a, int64_t r_t, int64_t k, bool* clamped,
-                                        bool* exceeded) {
-	return landing_rescale(branch, m_a, r_t, k, clamped, exceeded);
+struct Landing {
+	int64_t raw;
+	bool clamped, exceeded;
+};
+
+SSLM_COLD Landing landing_rescale_cold(int64_t branch, int64_t m_a, int64_t r_t, int64_t k) {
+	Landing l;
+	l.raw = landing_rescale(branch, m_a, r_t, k, &l.clamped, &l.exceeded);
+	return l;
 }
 
 // landing_rescale for the residual site's operands (|branch| <= 127 code, |m_a| < 2^31 + 1,
@@ -378,7 +384,12 @@ SSLM_HD int64_t landing_small(int64_t branch, int64_t m_a, int64_t r_t, int64_t 
 	const uint64_t ab = branch < 0 ? (uint64_t)0 - (uint64_t)branch : (uint64_t)branch;
 	const uint64_t am = m_a < 0 ? (uint64_t)0 - (uint64_t)m_a : (uint64_t)m_a;
 	if (k < 0 || ab > 127u || am > ((uint64_t)1 << 31) || (uint64_t)r_t >= ((uint64_t)1 << 33))
-		return landing_rescale_cold(branch, m_a, r_t, k, clamped, exceeded);
+	{
+		const Landing l = landing_rescale_cold(branch, m_a, r_t, k);
+		*clamped = l.clamped;
+		*exceeded = l.exceeded;
+		return l.raw;
+	}
 	const bool neg = (branch < 0) != (m_a < 0);
 	const uint64_t a = ab * am;  // < 2^39
 	const uint64_t lo = a * (uint64_t)r_t;
@@ -522,22 +533,30 @@ SSLM_HD int64_t softmax_ceiling(int64_t q_b, int64_t q_c) {
 // src/intmath.cpp:381-418 + checked_chain_funnel.cpp:454-482: the bias term
 // round_away(b*r_a / 2^(30+62+e_a)); false when the exponent or the sum with `acc` is out of
 // domain.
-// The general form on 128-bit products (any bias code).
-SSLM_COLD bool bias_term_wide(int64_t b, int64_t r_a, int64_t e_a, int64_t acc, int64_t* out) {
+// The general form on 128-bit products (any bias code).  Returns its result by value (an
+// out-of-line call given a pointer would keep the caller's variable in scratch memory).
+struct BiasTerm {
+	int64_t term;
+	bool ok;
+};
+
+SSLM_COLD BiasTerm bias_term_wide(int64_t b, int64_t r_a, int64_t e_a, int64_t acc) {
+	BiasTerm r{0, false};
 	s128 sum = (s128)30 + 62 + (s128)e_a;
-	if (sum < 0 || sum > 63) return false;
+	if (sum < 0 || sum > 63) return r;
 	int exponent = (int)sum;
 	s128 wide = (s128)b * (s128)r_a;
 	uint64_t mask = ((uint64_t)1 << exponent) - 1u;
 	uint64_t rem = (uint64_t)wide & mask;
 	uint64_t thr = (mask >> 1) + (wide < 0 ? 1u : 0u);
 	s128 rounded = (wide >> exponent) + (rem > thr ? 1 : 0);
-	if (rounded != (s128)(int64_t)rounded) return false;
+	if (rounded != (s128)(int64_t)rounded) return r;
 	int64_t term = (int64_t)rounded;
 	uint64_t s = (uint64_t)acc + (uint64_t)term;
-	if (((((uint64_t)acc ^ (uint64_t)term) >> 63) == 0) && ((((uint64_t)acc ^ s) >> 63) != 0)) return false;
-	*out = term;
-	return true;
+	if (((((uint64_t)acc ^ (uint64_t)term) >> 63) == 0) && ((((uint64_t)acc ^ s) >> 63) != 0)) return r;
+	r.term = term;
+	r.ok = true;
+	return r;
 }
 
 // Same result; |b| < 2^30 with 0 <= r_a <= 2^33 (every bias of a real artifact against a
@@ -545,7 +564,11 @@ SSLM_COLD bool bias_term_wide(int64_t b, int64_t r_a, int64_t e_a, int64_t acc, 
 // 128-bit arithmetic.
 SSLM_HD bool bias_term(int64_t b, int64_t r_a, int64_t e_a, int64_t acc, int64_t* out) {
 	const uint64_t ab = b < 0 ? (uint64_t)0 - (uint64_t)b : (uint64_t)b;
-	if (ab >= ((uint64_t)1 << 30) || r_a < 0 || r_a > ((int64_t)1 << 33)) return bias_term_wide(b, r_a, e_a, acc, out);
+	if (ab >= ((uint64_t)1 << 30) || r_a < 0 || r_a > ((int64_t)1 << 33)) {
+		const BiasTerm w = bias_term_wide(b, r_a, e_a, acc);
+		if (w.ok) *out = w.term;
+		return w.ok;
+	}
 	if (e_a < -92 || e_a > -29) return false;  // exponent 92 + e_a outside [0, 63]
 	const int exponent = (int)(92 + e_a);
 	const int64_t wide = b * r_a;

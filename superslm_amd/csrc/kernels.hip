@@ -503,6 +503,20 @@ __device__ __forceinline__ int64_t fold_select(int32_t acc, int32_t identity, in
 	return identity != 0 ? (int64_t)acc : folded;
 }
 
+// The same fold as straight-line int32 arithmetic (apply_fold on an int32 accumulator; the
+// result is int32 either way): srdhm as one 64-bit product, rdbpot32 as mask / threshold, the
+// identity flag as a final select.
+__device__ __forceinline__ int32_t fold32(int32_t acc, int32_t identity, int32_t mult, int32_t shift) {
+	const int64_t ab = (int64_t)acc * (int64_t)mult + ((int64_t)1 << 30);
+	const int64_t hi64 = ab >> 31;
+	const int32_t hi = hi64 > kI32Max ? kI32Max : (int32_t)hi64;
+	const uint32_t mask = ((uint32_t)1 << shift) - 1u;
+	const uint32_t rem = (uint32_t)hi & mask;
+	const uint32_t thr = (mask >> 1) + (hi < 0 ? 1u : 0u);
+	const int32_t folded = (hi >> shift) + (rem > thr ? 1 : 0);
+	return identity != 0 ? acc : folded;
+}
+
 template <int BM>
 __global__ __launch_bounds__(BM / 128 * 2 * 64, 2) void k_gemm_mfma(GemmArgs g, int kspan) {
 	constexpr int WAVES = BM / 128 * 2, NT = WAVES * 64;
@@ -607,27 +621,52 @@ __global__ __launch_bounds__(BM / 128 * 2 * 64, 2) void k_gemm_mfma(GemmArgs g, 
 	int32_t* fout = nullptr;
 	int64_t* wout = nullptr;
 	uint32_t* mpart = nullptr;
+	// the block's per-row bias operands (reciprocal and exponent of the input scale), staged in
+	// LDS after the slabs, so the store loop does not wait on a global load per row
+	int64_t* s_rcp = (int64_t*)(smem + WAVES * 32 * 64 * 4);
+	int64_t* s_ein = s_rcp + BM;
+	static_assert(WAVES * 32 * 64 * 4 + BM * 16 <= 2 * ROWS * kPStride, "epilogue LDS");
 	if (!raw) {
-		int s2 = 0;
-		while (s2 + 1 < e.nseg && col0 >= e.seg[s2].n_end) ++s2;
-		const Segment sg = e.seg[s2];  // segment bounds are multiples of 16: one per lane
-		const int jc = (col_ok ? col0 : sg.n_begin) - sg.n_begin;
-		const int32_t* f = sg.fold + 3 * jc;
+		// the lane's segment (bounds are multiples of 16: one per lane), every field read with a
+		// constant index -- a lane-dependent index into the kernel arguments would copy them to
+		// scratch memory
+		int si = 0;
+		if (e.nseg > 1 && col0 >= e.seg[0].n_end) si = 1;
+		if (e.nseg > 2 && col0 >= e.seg[1].n_end) si = 2;
+#define SSLM_SEG_FIELD(f) (si == 0 ? e.seg[0].f : (si == 1 ? e.seg[1].f : e.seg[2].f))
+		const int32_t n_begin = SSLM_SEG_FIELD(n_begin), mode = SSLM_SEG_FIELD(mode);
+		const int32_t* fold = SSLM_SEG_FIELD(fold);
+		const int64_t* sb = SSLM_SEG_FIELD(bias);
+		void* sout = SSLM_SEG_FIELD(out);
+		uint32_t* smax = SSLM_SEG_FIELD(maxpart);
+		ldc = SSLM_SEG_FIELD(ld_out);
+#undef SSLM_SEG_FIELD
+		const int jc = (col_ok ? col0 : n_begin) - n_begin;
+		const int32_t* f = fold + 3 * jc;
 #pragma unroll
 		for (int q = 0; q < 4; ++q) {
 			f0[q] = f[3 * q];
 			f1[q] = f[3 * q + 1];
 			f2[q] = f[3 * q + 2];
-			bias[q] = sg.bias ? sg.bias[jc + q] : 0;
+			bias[q] = sb ? sb[jc + q] : 0;
 		}
-		has_bias = sg.bias != nullptr;
-		wide = sg.mode == kSegWide;
-		ldc = sg.ld_out;
-		fout = (int32_t*)sg.out + jc;
-		wout = (int64_t*)sg.out + jc;
-		mpart = sg.maxpart ? sg.maxpart + (size_t)(col0 >> 4) * kPartLd : nullptr;
+		has_bias = sb != nullptr;
+		wide = mode == kSegWide;
+		fout = (int32_t*)sout + jc;
+		wout = (int64_t*)sout + jc;
+		mpart = smax ? smax + (size_t)(col0 >> 4) * kPartLd : nullptr;
 	}
+	bool any_bias = false;  // block-uniform: every segment's bias pointer
+	for (int i = 0; i < e.nseg; ++i) any_bias = any_bias || (!raw && e.seg[i].bias != nullptr);
 	__syncthreads();  // every wave is done reading the last LDS stage
+	if (any_bias) {
+		for (int r = threadIdx.x; r < BM; r += NT) {
+			const int t = min(m0 + r, g.M - 1);
+			s_rcp[r] = e.in_recip[t];
+			s_ein[r] = e.in_scale[t].e;
+		}
+		__syncthreads();
+	}
 #pragma unroll
 	for (int mt = 0; mt < 4; ++mt) {
 		// 32x32 accumulator layout: lane holds column lane % 32 of the sub-tile, rows
@@ -651,6 +690,25 @@ __global__ __launch_bounds__(BM / 128 * 2 * 64, 2) void k_gemm_mfma(GemmArgs g, 
 				}
 				continue;
 			}
+			if (!any_bias && !wide) {
+				// no bias anywhere in the launch (o, gate|up, down): straight-line int32 fold,
+				// int32 store, tile maximum -- no branch per element
+				v4i o;
+				uint32_t mx = 0;
+#pragma unroll
+				for (int q = 0; q < 4; ++q) {
+					o[q] = fold32(a[q], f0[q], f1[q], f2[q]);
+					mx = max(mx, o[q] < 0 ? 0u - (uint32_t)o[q] : (uint32_t)o[q]);
+				}
+				if (ok) *(v4i*)(fout + (size_t)t * ldc) = o;
+				if (!ok) mx = 0;
+				uint32_t w2 = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)mx, 0xb1, 0xf, 0xf, false);
+				mx = max(mx, w2);
+				w2 = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)mx, 0x4e, 0xf, 0xf, false);
+				mx = max(mx, w2);
+				if ((lane & 3) == 0 && t < g.M && col_ok && mpart) mpart[t] = mx;
+				continue;
+			}
 			int64_t val[4];
 			uint32_t mx = 0;
 #pragma unroll
@@ -658,8 +716,9 @@ __global__ __launch_bounds__(BM / 128 * 2 * 64, 2) void k_gemm_mfma(GemmArgs g, 
 				val[q] = f0[q] != 0 ? (int64_t)a[q] : (int64_t)rdbpot32(srdhm(a[q], f1[q]), f2[q]);
 				if (has_bias && ok) {
 					int64_t term;
-					if (bias_term(bias[q], e.in_recip[t], e.in_scale[t].e, val[q], &term)) val[q] += term;
-					else set_status(e.status, e.tok[t].slot, e.layer, kBiasReconcileProductOutOfDomain);
+					const int rr = wm + mt * 32 + r;
+					if (bias_term(bias[q], s_rcp[rr], s_ein[rr], val[q], &term)) val[q] += term;
+					else set_status_rows(e.status, e.tok, e.layer, t, 1u);
 				}
 				const uint32_t m1 = sat_abs_u32(val[q]);
 				mx = m1 > mx ? m1 : mx;
