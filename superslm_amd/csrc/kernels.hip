@@ -1321,6 +1321,7 @@ template <int BS, int EPT, int RS>
 __global__ __launch_bounds__(BS) void k_mlp_act(sslm_launch::ActArgs a) {
 	__shared__ uint32_t s_gu[2 * BS / 64], s_a[BS / 64];
 	__shared__ int32_t sig[256];
+	__shared__ int32_t s_silu[1025];  // the SiLU node table, loaded with the row
 	__shared__ int32_t s_st;
 	const int t = blockIdx.x, I = a.I;
 	const int slot = a.tok[t].slot;
@@ -1361,6 +1362,7 @@ __global__ __launch_bounds__(BS) void k_mlp_act(sslm_launch::ActArgs a) {
 		um = part_max32<BS>(a.gu_maxpart, I / 16, I / 16, t);
 	}
 	const Scale inc = a.in_scale[t];
+	for (int i = threadIdx.x; i < 1025; i += BS) s_silu[i] = a.silu[i];
 	if (threadIdx.x == 0) s_st = a.status[slot];
 	blk_max32x2<BS>(gm, um, s_gu);
 	if (s_st != 0) return;
@@ -1373,7 +1375,7 @@ __global__ __launch_bounds__(BS) void k_mlp_act(sslm_launch::ActArgs a) {
 		return;
 	}
 	const Scale gs = gp.out;
-	if (threadIdx.x < 256) sig[threadIdx.x] = silu_sigmoid_q15(a.silu, (int8_t)(threadIdx.x - 128), gs.m, (int)gs.e);
+	if (threadIdx.x < 256) sig[threadIdx.x] = silu_sigmoid_q15(s_silu, (int8_t)(threadIdx.x - 128), gs.m, (int)gs.e);
 	int32_t gc[EPT], uc[EPT];
 #pragma unroll
 	for (int k = 0; k < EPT; ++k) {
