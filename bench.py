@@ -144,6 +144,71 @@ def traffic_from(fetch_csv, write_csv):
     print(json.dumps(out, indent=1))
 
 
+def extras(hip, model, pool, cfg, sm, rng, args, line):
+    """BASELINE configurations 0 and 3 beside the headline: the standalone GEMM + requant
+    (sslm_hip_gemm_requant, M 32 x K 896 x N 4864) and the 16-sequence decode with a rank-16
+    LoRA adapter on q and v."""
+    from superslm_amd.device import Device
+    from superslm_amd.sslm_artifact import build_adapter
+    out = {}
+    # configuration 0
+    L = hip.lib
+    L.sslm_hip_gemm_requant.restype = ctypes.c_int
+    L.sslm_hip_gemm_requant.argtypes = ([ctypes.c_void_p] * 3 + [ctypes.c_int32] * 3 + [ctypes.c_int64] * 4 +
+                                        [ctypes.c_void_p] * 3)
+    M0, K0, N0 = 32, 896, 4864
+    g = np.random.default_rng(20260101)
+    a = g.integers(-127, 128, size=(M0, K0), dtype=np.int8)
+    w = g.integers(-127, 128, size=(N0, K0), dtype=np.int8)
+    fold = np.zeros((N0, 3), dtype=np.int32)
+    fold[:, 1] = g.integers(1 << 30, 1 << 31, size=N0, dtype=np.int64).astype(np.int32)
+    fold[:, 2] = g.integers(8, 21, size=N0, dtype=np.int32)
+    dev = Device(hip)
+    da, dw, df = dev.upload(a), dev.upload(w), dev.upload(fold)
+    codes, me, st = dev.zeros((M0, N0), np.int8), dev.zeros((M0, 2), np.int64), dev.zeros((M0,), np.int32)
+    args0 = (da.ptr, dw.ptr, df.ptr, M0, N0, K0, 1 << 30, -37, 1518500250, -45, codes.ptr, me.ptr, st.ptr)
+    for _ in range(3):
+        assert L.sslm_hip_gemm_requant(*args0) == 0
+    n0 = 50
+    profile(hip, True)
+    t0 = time.perf_counter()
+    for _ in range(n0):
+        L.sslm_hip_gemm_requant(*args0)
+    wall = (time.perf_counter() - t0) / n0
+    ms, la, by, op = profile_read(hip)
+    profile(hip, False)
+    gemm_us, funnel_us = ms[0] * 1e3 / n0, ms[3] * 1e3 / n0
+    c0_bytes = N0 * K0 + M0 * K0 + M0 * N0 + 12 * N0  # the algorithmic bytes of the fused op
+    out["config0_gemm_requant"] = {
+        "shape": "M 32 x K 896 x N 4864", "gemm_us": round(gemm_us, 3), "funnel_us": round(funnel_us, 3),
+        "kernels_us": round(gemm_us + funnel_us, 3), "call_us_incl_sync": round(wall * 1e6, 2),
+        "gbs": round(c0_bytes / ((gemm_us + funnel_us) * 1e-6) / 1e9, 1),
+        "tops": round(2.0 * M0 * N0 * K0 / ((gemm_us + funnel_us) * 1e-6) / 1e12, 2)}
+    print(f"[bench] config0: GEMM {gemm_us:.2f} us + funnel {funnel_us:.2f} us", file=sys.stderr, flush=True)
+    # configuration 3: LoRA rank 16 on q and v, every sequence of the batch adapted
+    blob = build_adapter(sm, rank=16, targets=("q_proj", "v_proj"), seed=3)
+    ad = model.adapter(blob)
+    B = args.batch
+    seqs = [pool.seq() for _ in range(B)]
+    for s, p in zip(seqs, [rng.integers(0, cfg.vocab, size=args.prompt) for _ in range(B)]):
+        s.set_adapter(ad)
+        s.prefill(p)
+    for _ in range(3):
+        model.decode_step(seqs, cfg.layers)
+    hip.lib.sslm_hip_synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        model.decode_step(seqs, cfg.layers)
+    hip.lib.sslm_hip_synchronize()
+    dt = time.perf_counter() - t0
+    out["config3_lora_decode_tok_s"] = round(B * args.steps / dt, 2)
+    print(f"[bench] config3 (LoRA r16 q,v): {out['config3_lora_decode_tok_s']} tok/s", file=sys.stderr, flush=True)
+    for s in seqs:
+        s.release()
+    ad.release()
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -179,7 +244,7 @@ def main():
         copy_calibration(hip)
     model = Model(hip, image)
     B = args.batch
-    pool = model.pool(B + 1)
+    pool = model.pool(2 * B + 1)  # decode batch, prefill chunk, configuration-3 batch
     rng = np.random.default_rng(99)
     prompts = [rng.integers(0, cfg.vocab, size=args.prompt) for _ in range(B)]
     line = None
@@ -306,6 +371,9 @@ def main():
                     "scaling": "weak", "vs_baseline": None, "dtype": "int8", "data": "synthetic",
                     "config": {"workload": "config2 prefill: one 512-token chunk through 28 layers, 1.5B shape"}}
         line.update(pre)
+
+    if args.phase == "all":
+        line.update(extras(hip, model, pool, cfg, sm, rng, args, line))
 
     # CPU baseline: the reference compiled from its sources, same artifact, bounded sample
     ref_so = os.path.join(ROOT, "oracle", "_ref", "libsuperslm_ref.so")

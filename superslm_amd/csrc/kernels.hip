@@ -84,23 +84,42 @@ struct EpiResult {
 	bool ok;
 };
 
-// LoRA delta of channel jj for token t (forward_sites.cpp:1114-1141): the adapter's B row
-// against the token's intermediate codes, amplified by the delta fold.  Out of line: adapters
-// are optional and the loop would otherwise be inlined into every epilogue element.  Plain
-// values only: a reference into the kernel arguments would make the compiler copy them to
-// scratch memory.
-__device__ __attribute__((noinline)) int64_t lora_delta_v(const int8_t* lora_b, const int8_t* lora_u,
-                                                          const int32_t* dfold, int rank, int t, int jj) {
+// LoRA delta of channel jj for token t (forward_sites.cpp:1051-1112): the adapter's B row
+// against the token's intermediate codes, amplified by the delta fold.  |B.u| <= 127^2 * rank
+// < 2^31, so packed int8 dot products (sdot4) accumulate it exactly in int32; a rank that is not
+// a multiple of 4 takes the byte loop out of line.  Plain values only: a reference into the
+// kernel arguments would make the compiler copy them to scratch memory.
+__device__ __attribute__((noinline)) int32_t lora_dot_bytes(const int8_t* br, const int8_t* ur, int rank) {
+	int32_t d = 0;
+	for (int r = 0; r < rank; ++r) d += (int32_t)br[r] * (int32_t)ur[r];
+	return d;
+}
+
+__device__ __forceinline__ int64_t lora_delta_v(const int8_t* lora_b, const int8_t* lora_u, const int32_t* dfold,
+                                                int rank, int t, int jj) {
 	const int8_t* br = lora_b + (size_t)jj * rank;
 	const int8_t* ur = lora_u + (size_t)t * kMaxRank;
-	int64_t d = 0;
-	for (int r = 0; r < rank; ++r) d += (int32_t)br[r] * (int32_t)ur[r];
+	int32_t d = 0;
+	if ((rank & 3) == 0) {
+		for (int r = 0; r < rank; r += 4)
+			d = __builtin_amdgcn_sdot4(*(const int32_t*)(br + r), *(const int32_t*)(ur + r), d, false);
+	} else {
+		d = lora_dot_bytes(br, ur, rank);
+	}
 	const int32_t* df = dfold + 3 * jj;
-	return apply_amp_fold(d, df[0], df[1], df[2]);
+	return apply_amp_fold((int64_t)d, df[0], df[1], df[2]);
+}
+
+// Called out of line: adapters are optional, and inlined into an epilogue the delta costs the
+// common path registers (the decode GEMV must stay within 128 VGPRs for 4 waves per SIMD) and,
+// unrolled per element, code size in the row kernels.
+__device__ __attribute__((noinline)) int64_t lora_delta_cold(const int8_t* lora_b, const int8_t* lora_u,
+                                                             const int32_t* dfold, int rank, int t, int jj) {
+	return lora_delta_v(lora_b, lora_u, dfold, rank, t, jj);
 }
 
 __device__ __forceinline__ int64_t lora_delta(const Segment& sg, int rank, int t, int jj) {
-	return lora_delta_v(sg.lora_b, sg.lora_u, sg.lora_dfold, rank, t, jj);
+	return lora_delta_cold(sg.lora_b, sg.lora_u, sg.lora_dfold, rank, t, jj);
 }
 
 __device__ __forceinline__ EpiResult epi_value(const Epilogue& e, int t, int j, int32_t acc) {
@@ -364,7 +383,7 @@ __global__ __launch_bounds__(64 * kGemvWaves) void k_gemv(GemmArgs g, int cps) {
 		for (int v = 0; v < 4; ++v) {
 			const bool live = t0 + v < g.M && j < g.N;
 			val[v] = apply_fold((int64_t)tot[v], p_f0, p_f1, p_f2);
-			if (p_lora && live) val[v] += lora_delta_v(sg.lora_b, sg.lora_u, sg.lora_dfold, e.rank, t0 + v, jj);
+			if (p_lora && live) val[v] += lora_delta_cold(sg.lora_b, sg.lora_u, sg.lora_dfold, e.rank, t0 + v, jj);
 			if (p_bias) {
 				int64_t term;
 				if (bias_term(p_b, p_rcp[v], p_ein[v], val[v], &term)) val[v] += term;
@@ -1629,18 +1648,38 @@ __global__ __launch_bounds__(BS) void k_attention(sslm_launch::AttnArgs a, int u
 
 // LoRA intermediate (forward_sites.cpp:1066-1086): u[k] = clamp(amp_fold(A[k] . x))
 __global__ __launch_bounds__(kBlock) void k_lora_u(sslm_launch::LoraUArgs a) {
-	const int t = blockIdx.x;
+	// one block per (token, adapted projection); wave w computes ranks w, w + 4, ...: each lane
+	// covers 16-byte chunks of K with sdot4 (|A.x| <= 127^2 * K < 2^31, exact in int32), the
+	// wave reduces with DPP, lane 0 applies the u fold (UFS1) and clamps to +-127
+	const int t = blockIdx.x, p = blockIdx.y;
 	const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+	const int chunks = a.K >> 4;  // K is a multiple of 64
 	const int8_t* x = a.x + (size_t)t * a.K;
-	for (int task = wave; task < a.nproj * a.rank; task += kBlock / 64) {
-		const int p = task / a.rank, r = task % a.rank;
+	constexpr int kMaxChunks = 20480 / 16 / 64;  // K <= 20480: at most 20 chunks per lane
+	v4i xc[kMaxChunks];
+#pragma unroll
+	for (int i = 0; i < kMaxChunks; ++i) {
+		const int c = lane + 64 * i;
+		xc[i] = c < chunks ? load16(x + 16 * c) : v4i{0, 0, 0, 0};
+	}
+	for (int r = wave; r < a.rank; r += kBlock / 64) {
 		const int8_t* arow = a.a[p] + (size_t)r * a.K;
-		int64_t acc = 0;
-		for (int k = lane; k < a.K; k += 64) acc += (int32_t)arow[k] * (int32_t)x[k];
-		acc = wave_sum_i64(acc);
+		int32_t acc = 0;
+#pragma unroll
+		for (int i = 0; i < kMaxChunks; ++i) {
+			const int c = lane + 64 * i;
+			if (64 * i < chunks) {  // wave-uniform bound
+				const v4i w = c < chunks ? load16(arow + 16 * c) : v4i{0, 0, 0, 0};
+				acc = __builtin_amdgcn_sdot4(w.x, xc[i].x, acc, false);
+				acc = __builtin_amdgcn_sdot4(w.y, xc[i].y, acc, false);
+				acc = __builtin_amdgcn_sdot4(w.z, xc[i].z, acc, false);
+				acc = __builtin_amdgcn_sdot4(w.w, xc[i].w, acc, false);
+			}
+		}
+		acc = wave_sum32(acc);
 		if (lane == 0) {
 			const int32_t* f = a.ufold[p] + 3 * r;
-			a.u[p][(size_t)t * kMaxRank + r] = (int8_t)clamp_code(apply_amp_fold(acc, f[0], f[1], f[2]));
+			a.u[p][(size_t)t * kMaxRank + r] = (int8_t)clamp_code(apply_amp_fold((int64_t)acc, f[0], f[1], f[2]));
 		}
 	}
 }
@@ -1867,7 +1906,7 @@ bool row_geometry_ok(int H, int I, int NKV, int D) {
 	       (D == 32 || D == 64 || D == 128 || D == 256);
 }
 
-void lora_u(const LoraUArgs& a, hipStream_t s) { hipLaunchKernelGGL(k_lora_u, dim3(a.M), dim3(kBlock), 0, s, a); }
+void lora_u(const LoraUArgs& a, hipStream_t s) { hipLaunchKernelGGL(k_lora_u, dim3(a.M, a.nproj), dim3(kBlock), 0, s, a); }
 
 void argmax_finalize(const unsigned long long* keys, int ntiles, int M, int32_t* out_tokens, hipStream_t s) {
 	hipLaunchKernelGGL(k_argmax_finalize, dim3(M), dim3(kRowBlock), 0, s, keys, ntiles, out_tokens);
