@@ -209,6 +209,51 @@ def extras(hip, model, pool, cfg, sm, rng, args, line):
     return out
 
 
+def config4(args):
+    """BASELINE configuration 4 on one GPU: the 7B shape (H 3584, I 18944, 28 layers, 28 / 4
+    heads, context cap 4608), 32 sequences each prefilled with 2048 tokens in 512-token chunks,
+    then greedy decode steps over all 32 at context ~2048 (one GPU's share; no CPU leg -- the
+    reference needs minutes per token at this shape)."""
+    cfg = CONFIGS["qwen7b"]
+    t0 = time.time()
+    sm = build_synthetic(cfg, seed=7007)
+    image = sm.to_array()
+    print(f"[bench] synthetic 7B artifact {image.nbytes / 1e9:.2f} GB in {time.time() - t0:.1f}s",
+          file=sys.stderr, flush=True)
+    hip = SslmLib(os.path.join(ROOT, "superslm_amd", "libsslm_hip.so"))
+    model = Model(hip, image)
+    B, ctx = 32, 2048
+    pool = model.pool(B)
+    rng = np.random.default_rng(4)
+    seqs = [pool.seq() for _ in range(B)]
+    t0 = time.perf_counter()
+    for s in seqs:
+        p = rng.integers(0, cfg.vocab, size=ctx)
+        done = 0
+        while done < ctx:
+            done += s.prefill(p[done:], chunk_budget=512)
+    hip.lib.sslm_hip_synchronize()
+    pre_s = time.perf_counter() - t0
+    print(f"[bench] config4 prefill {B} x {ctx}: {pre_s:.2f} s, {B * ctx / pre_s:.0f} tok/s", file=sys.stderr, flush=True)
+    for _ in range(max(2, args.warmup)):
+        model.decode_step(seqs, cfg.layers)
+    hip.lib.sslm_hip_synchronize()
+    steps = max(4, min(args.steps, 32))
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        model.decode_step(seqs, cfg.layers)
+    hip.lib.sslm_hip_synchronize()
+    dt = time.perf_counter() - t0
+    line = {"metric": "config4 7B decode tok/s (32 sequences at context ~2048)", "value": round(B * steps / dt, 2),
+            "unit": "tok/s", "n_gpus": 1, "steps": steps, "warmup": max(2, args.warmup),
+            "ms_per_step": round(dt * 1e3 / steps, 3), "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": "int8", "data": "synthetic",
+            "config": {"workload": "config4: Qwen2.5-7B shape, 32 sequences x 2048-token chunked prefill, then "
+                                   "greedy decode", "batch": B, "context": ctx},
+            "prefill_tok_s": round(B * ctx / pre_s, 1)}
+    print(json.dumps(line))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -218,7 +263,7 @@ def main():
     ap.add_argument("--prompt", type=int, default=32)
     ap.add_argument("--cpu-seqs", type=int, default=2)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--phase", choices=["all", "decode", "prefill"], default="all")
+    ap.add_argument("--phase", choices=["all", "decode", "prefill", "config4"], default="all")
     ap.add_argument("--calibrate", action="store_true", help="add the PMC calibration copy")
     ap.add_argument("--pmc-steps", action="store_true",
                     help="decode steps only (no profiled pass, GEMV timing or M = 1 decode): for --pmc runs")
@@ -232,6 +277,9 @@ def main():
               "(sequences shard across GPUs with no exchange; see DESIGN.md)", file=sys.stderr)
         sys.exit(2)
 
+    if args.phase == "config4":
+        config4(args)
+        return
     cfg = CONFIGS["qwen1.5b"]
     t0 = time.time()
     sm = build_synthetic(cfg, seed=1515)

@@ -1450,8 +1450,19 @@ __global__ __launch_bounds__(BS) void k_attention(sslm_launch::AttnArgs a, int u
 	__shared__ int32_t s_st;
 	constexpr int TPR = D / 4, PG = BS / TPR, PAIRS = D / 2;
 	static_assert(BS >= PAIRS, "one thread per RoPE pair");
-	const int h = blockIdx.x, t = blockIdx.y;
-	const int group = a.NH / a.NKV, kvh = h / group;
+	// XCD-aware order: workgroups go round-robin to the 8 XCDs (block id mod 8), so the R query
+	// heads of one (kv head, token) group are numbered id = (i * R + r) * 8 + x -- all on XCD x,
+	// sharing that XCD's L2 copy of the group's K/V.  Ids past the last group exit at once.
+	const int group = a.NH / a.NKV;
+	int h, t;
+	{
+		const int id = blockIdx.x, x = id & 7, k = id >> 3;
+		const int gi = x + 8 * (k / group);  // group index: (token, kv head) = (gi / NKV, gi % NKV)
+		if (gi >= a.M * a.NKV) return;
+		t = gi / a.NKV;
+		h = (gi % a.NKV) * group + k % group;
+	}
+	const int kvh = h / group;
 	const TokenInfo ti = a.tok[t];
 	const int64_t km = a.khead_m[kvh], ke = a.khead_e[kvh];
 	const int32_t* cf = a.ctx_fold + 3 * h;
@@ -1847,7 +1858,8 @@ template <bool FUSED>
 static void launch_attention(const AttnArgs& a, hipStream_t s) {
 	const size_t lds = (size_t)a.cap * sizeof(int64_t);
 	const int use_lds = attention_in_lds(a.cap) ? 1 : 0;
-	const dim3 grid(a.NH, a.M);
+	const int groups = a.M * a.NKV, per_xcd = (groups + 7) / 8;
+	const dim3 grid(per_xcd * 8 * (a.NH / a.NKV));  // see the XCD-aware order in k_attention
 	const size_t dyn = use_lds ? lds : 0;
 	switch (a.D) {
 		case 32: hipLaunchKernelGGL((k_attention<kBlock, 32, FUSED>), grid, dim3(kBlock), dyn, s, a, use_lds); break;
