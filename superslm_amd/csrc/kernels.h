@@ -77,8 +77,9 @@ constexpr int kGemvTargetBlocks = 512;
 // prefill GEMM launch shape (M > 64)
 struct PrefillPlan {
 	int bm;      // block rows (256 or 128); block columns are 128
-	int splits;  // K splits over gridDim.z
-	int kspan;   // K per split (multiple of 64)
+	int splits;  // K splits over gridDim.z (raw partial planes)
+	int kspan;   // K per split (multiple of 128)
+	int blocks;  // gridDim.x: one tile per block
 };
 constexpr int kPrefillTargetBlocks = 256;
 constexpr int kMaxRawSplits = 8;  // split planes a raw consumer adds
@@ -117,6 +118,8 @@ GemvPlan gemv_plan(int M, int N, int K, bool split_ok);
 bool gemv_eligible(int M, int K);
 // launch shape of the prefill GEMM; `split_ok` as for gemv_plan
 PrefillPlan prefill_plan(int M, int N, int K, bool split_ok);
+// the MFMA prefill GEMM takes K in multiples of its 128-deep step; other K use the tiled kernel
+bool prefill_mfma_k(int K);
 
 struct RowNormArgs {
 	// input stream codes: in_codes[idx[t] * ld_in], input scale ignored (norm kills it)

@@ -497,24 +497,29 @@ __global__ __launch_bounds__(kBlock) void k_gemm_tiled(GemmArgs g) {
 }
 
 // ------------------------------------------------------------------------------------------
-// Prefill GEMM (M > 64): block tile BM x 128 (BM = 256: 4 waves, BM = 128: 2 waves), each wave a
-// 128x64 tile of v_mfma_i32_32x32x32_i8 (4x2; the larger wave tile halves LDS reads per MAC
-// against 64x64), BK = 64.  Global tiles travel through two register stages (the loads of
-// K-step t + 2 are issued before step t's MFMAs) into two LDS stages with XOR-swizzled 16-byte
-// chunks (lds_chunk: conflict-free for both the operand reads and the row writes; 48 KB per
-// block at BM = 256, so up to three blocks share a CU), one barrier per K-step.  Loads are unconditional: rows past M or N read a
-// clamped valid row whose products land only in discarded outputs, and K is a multiple of 64.
+// Prefill GEMM (M > 64): block tile BM x 128 with BK = 128.  The tile is cut into 128x64 wave
+// tiles of v_mfma_i32_32x32x32_i8 (4x2), TW = BM / 64 of them, and each wave tile is shared by
+// two waves that take the two 64-deep halves of every K step (2 TW waves: 8 at BM = 256); the
+// pair's accumulators are summed in the epilogue.  Two waves per SIMD let one issue MFMAs
+// while the other waits at the barrier or on load issue.
+// Operands go global -> LDS directly (global_load_lds_dwordx4, 1 KB per wave instruction: 8 full
+// 128-byte rows) through NS = 3 stages; the loads of K step t + 3 are issued between step t's
+// MFMAs (the per-CU load rate is the other limit of this loop, so its issue is spread out),
+// and the operand fragments of step t + 1 are read while step t's MFMAs run.  Rows of a stage
+// hold XOR-swizzled 16-byte chunks (lds_chunk).  One barrier per K step.  Loads are
+// unconditional: rows past M or N read a clamped valid row whose products land only in
+// discarded outputs, and K is a multiple of 128.
 // gridDim.z splits K; with several splits each stores its raw int32 partial plane and the
 // consumer applies the epilogue (RawIn), as for the decode GEMV.  With one split the block runs
 // the epilogue (see below).
 // ------------------------------------------------------------------------------------------
-constexpr int kPBN = 128, kPBK = 64, kPStride = kPBK;
+constexpr int kPBN = 128, kPBK = 128, kPStride = kPBK, kPrefillStages = 3;
 
-// LDS placement of the 16-byte chunk `q` (0..3) of tile row `row`: the chunk index is XORed with
-// bits of the row so that 16 consecutive rows read at one chunk (the MFMA operand pattern) and 4
-// rows written whole (the global-load pattern) both spread over distinct banks, for 32- and
-// 64-bank LDS alike.
-__device__ __forceinline__ int lds_chunk(int row, int q) { return row * kPStride + ((q ^ (((row >> 1) ^ (row >> 3)) & 3)) << 4); }
+// LDS placement of the 16-byte chunk `q` (0..7) of tile row `row` (128 bytes a row): the chunk
+// index is XORed with row bits 1..3, so 16 consecutive rows read at one chunk (the MFMA
+// operand pattern: even and odd rows fall in the two 128-byte halves of the 64 banks, and the
+// 8 even rows in 8 distinct chunks) are conflict-free; the direct loads write whole rows.
+__device__ __forceinline__ int lds_chunk(int row, int q) { return row * kPStride + ((q ^ ((row >> 1) & 7)) << 4); }
 
 // WSC1 fold without a branch on the identity flag (same value as apply_fold)
 __device__ __forceinline__ int64_t fold_select(int32_t acc, int32_t identity, int32_t mult, int32_t shift) {
@@ -536,43 +541,75 @@ __device__ __forceinline__ int32_t fold32(int32_t acc, int32_t identity, int32_t
 	return identity != 0 ? acc : folded;
 }
 
-template <int BM>
-__global__ __launch_bounds__(BM / 128 * 2 * 64, 2) void k_gemm_mfma(GemmArgs g, int kspan) {
-	constexpr int WAVES = BM / 128 * 2, NT = WAVES * 64;
-	constexpr int ROWS = BM + kPBN;
-	constexpr int CPR = kPBK / 16;         // 16-byte chunks per row and stage
-	constexpr int CPT = ROWS * CPR / NT;   // per thread
-	static_assert(CPT * NT == ROWS * CPR, "stage must split evenly over the block");
-	__shared__ __attribute__((aligned(16))) int8_t smem[2 * ROWS * kPStride];
-	const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-	const int m0 = blockIdx.y * BM, n0 = blockIdx.x * kPBN;
-	const int split = blockIdx.z;
-	const int k_begin = split * kspan;
-	const int ntile = (min(g.K, k_begin + kspan) - k_begin) / kPBK;
-	const int wm = (wave >> 1) * 128, wn = (wave & 1) * 64;
+// s_waitcnt with vmcnt(n), expcnt and lgkmcnt unconstrained (gfx9 encoding: vmcnt in bits
+// 3:0 and 15:14)
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+	static_assert(N >= 0 && N < 64, "vmcnt range");
+	__builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0f70);
+}
 
-	// per-thread chunk sources (A rows first, then B rows), rows clamped into the operands
+// LDS read of 16 bytes at byte address `base + OFF` of the shared segment, issued from inline
+// assembly: the compiler's wait insertion would otherwise treat every pending direct-to-LDS
+// load as a possible writer and drain them all before the read.  The caller waits on lgkmcnt
+// itself (lgkm_wait) before using the result.
+template <int OFF>
+__device__ __forceinline__ v4i lds_read16(uint32_t base) {
+	v4i r;
+	asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(base), "i"(OFF));
+	return r;
+}
+
+// lgkmcnt(N) wait that the fragments pass through, so nothing reading them moves above it
+template <int N>
+__device__ __forceinline__ void lgkm_wait(v4i (&a)[4], v4i (&b)[2]) {
+	asm volatile("s_waitcnt lgkmcnt(%6)"
+	             : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]), "+v"(b[0]), "+v"(b[1])
+	             : "i"(N));
+}
+
+template <int BM, int NS>
+__global__ __launch_bounds__(BM / 32 * 64, 1) void k_gemm_mfma(GemmArgs g, PrefillPlan pp) {
+	constexpr int TW = BM / 64;           // wave tiles (128x64) per block tile
+	constexpr int WAVES = 2 * TW, NT = WAVES * 64;
+	constexpr int ROWS = BM + kPBN;
+	constexpr int STAGE = ROWS * kPStride;  // bytes of one 128-deep K step of A and W rows
+	constexpr int INSTS = STAGE / 1024;     // 1 KB direct-to-LDS wave loads per stage
+	constexpr int CPT = INSTS / WAVES;      // per wave
+	constexpr int CH = kPStride / 16;       // 16-byte chunks per row
+	static_assert(CPT * WAVES == INSTS, "stage must split evenly over the waves");
+	static_assert(NS >= 2 && (NS - 1) * CPT < 64, "stages in flight must fit vmcnt");
+	__shared__ __attribute__((aligned(1024))) int8_t smem[NS * STAGE];
+	const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+	const int wt = wave % TW, kh = wave / TW;  // wave tile, K half
+	const int wm = (wt >> 1) * 128, wn = (wt & 1) * 64;
+
+	const int tiles_m = (g.M + BM - 1) / BM;  // tile t: rows (t % tiles_m) * BM, columns (t / tiles_m) * 128
+	v16i acc[4][2];
+	// K steps [ks0, ks1) of tile `tile` into acc
+	auto run_tile = [&](int tile, int ks0, int ks1) {
+	const int m0 = (tile % tiles_m) * BM, n0 = (tile / tiles_m) * kPBN;
+	const int k_begin = ks0 * kPBK, ntile = ks1 - ks0;
+	// Each wave load instruction writes 1 KB of LDS in lane order (16 bytes per lane): lane l
+	// of instruction i fills slot 64 i + l, i.e. row slot / 8 at physical chunk slot % 8, so it
+	// fetches the logical chunk that lds_chunk() places there (rows clamped into the operands).
 	const int8_t* src[CPT];
-	int lds_off[CPT];
 #pragma unroll
 	for (int j = 0; j < CPT; ++j) {
-		const int c = threadIdx.x + j * NT;
-		const int row = c / CPR, kc = (c % CPR) * 16;
-		lds_off[j] = lds_chunk(row, c % CPR);
-		if (row < BM) src[j] = g.a + (size_t)min(m0 + row, g.M - 1) * g.lda + k_begin + kc;
-		else src[j] = g.w + (size_t)min(n0 + row - BM, g.N - 1) * g.K + k_begin + kc;
+		const int slot = (wave * CPT + j) * 64 + lane;
+		const int row = slot / CH, pc = slot % CH;
+		const int q = pc ^ ((row >> 1) & 7);
+		if (row < BM) src[j] = g.a + (size_t)min(m0 + row, g.M - 1) * g.lda + k_begin + q * 16;
+		else src[j] = g.w + (size_t)min(n0 + row - BM, g.N - 1) * g.K + k_begin + q * 16;
 	}
-	auto gload = [&](v4i (&r)[CPT], int t) {
+	// load j of tile t into stage st (clamped: past the last tile the last is fetched again,
+	// into a stage no step reads, so every step waits for the same count)
+	auto issue_one = [&](int st, int t, int j) {
 		const size_t kb = (size_t)min(t, ntile - 1) * kPBK;
-#pragma unroll
-		for (int j = 0; j < CPT; ++j) r[j] = load16(src[j] + kb);
+		__builtin_amdgcn_global_load_lds((const void*)(src[j] + kb),
+		                                 (__attribute__((address_space(3))) void*)(smem + st * STAGE + (wave * CPT + j) * 1024),
+		                                 16, 0, 0);
 	};
-	auto sstore = [&](const v4i (&r)[CPT], int buf) {
-		int8_t* sm = smem + buf * ROWS * kPStride;
-#pragma unroll
-		for (int j = 0; j < CPT; ++j) *(v4i*)&sm[lds_off[j]] = r[j];
-	};
-	v16i acc[4][2];
 #pragma unroll
 	for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -580,53 +617,91 @@ __global__ __launch_bounds__(BM / 128 * 2 * 64, 2) void k_gemm_mfma(GemmArgs g, 
 #pragma unroll
 			for (int v = 0; v < 16; ++v) acc[i][j][v] = 0;
 	// operand addresses: row wm + lane % 32 (+ 32 i) of A, wn + lane % 32 (+ 32 j) of B, chunk
-	// 2 ks + lane / 32; the swizzle depends only on the row's low bits, so +32 rows keep it
+	// 2 (2 kh + ks) + lane / 32; the swizzle depends only on the row's low bits, so +32 rows
+	// keep it
+	const uint32_t lds0 = (uint32_t)(size_t)(__attribute__((address_space(3))) int8_t*)smem;
 	const int arow = wm + (lane & 31), brow = BM + wn + (lane & 31);
-	int aoff[2], boff[2];
+	uint32_t aoff[2], boff[2];
 #pragma unroll
 	for (int ks = 0; ks < 2; ++ks) {
-		aoff[ks] = lds_chunk(arow, 2 * ks + (lane >> 5));
-		boff[ks] = lds_chunk(brow, 2 * ks + (lane >> 5));
+		aoff[ks] = lds0 + lds_chunk(arow, 2 * (2 * kh + ks) + (lane >> 5));
+		boff[ks] = lds0 + lds_chunk(brow, 2 * (2 * kh + ks) + (lane >> 5));
 	}
-	auto compute = [&](int buf) {
-		const int8_t* sm = smem + buf * ROWS * kPStride;
+	constexpr int R32 = 32 * kPStride;
+	// the wave's operand fragments of one stage: A rows +0/32/64/96 and B rows +0/32 for its two
+	// 32-deep steps
+	auto frags = [&](v4i (&a)[8], v4i (&b)[4], int st) {
 #pragma unroll
-		for (int ks = 0; ks < kPBK / 32; ++ks) {
-			v4i a[4], b[2];
+		for (int ks = 0; ks < 2; ++ks) {
+			const uint32_t ab = aoff[ks] + st * STAGE, bb = boff[ks] + st * STAGE;
+			a[4 * ks] = lds_read16<0>(ab);
+			a[4 * ks + 1] = lds_read16<R32>(ab);
+			a[4 * ks + 2] = lds_read16<2 * R32>(ab);
+			a[4 * ks + 3] = lds_read16<3 * R32>(ab);
+			b[2 * ks] = lds_read16<0>(bb);
+			b[2 * ks + 1] = lds_read16<R32>(bb);
+		}
+	};
+	auto frags_wait = [&](v4i (&a)[8], v4i (&b)[4]) {
+		lgkm_wait<0>(*(v4i(*)[4])&a[0], *(v4i(*)[2])&b[0]);
+		lgkm_wait<0>(*(v4i(*)[4])&a[4], *(v4i(*)[2])&b[2]);
+	};
+	// step t: x holds tile t's fragments (read during step t - 1), y receives tile t + 1's.
+	// Every wave's reads of tile t are complete before the barrier, so its stage takes the loads
+	// of tile t + NS, spread between the MFMAs.
+	auto step = [&](v4i (&xa)[8], v4i (&xb)[4], v4i (&ya)[8], v4i (&yb)[4], int t) {
+		frags_wait(xa, xb);
+		wait_vmcnt<(NS - 2) * CPT>();  // own loads of tile t + 1 have landed
+		// a bare s_barrier: __syncthreads() adds a workgroup release fence, which would drain
+		// every direct-to-LDS load still in flight
+		__builtin_amdgcn_s_barrier();
+		frags(ya, yb, (t + 1) % NS);
+		int li = 0, m = 0;
 #pragma unroll
-			for (int i = 0; i < 4; ++i) a[i] = *(const v4i*)&sm[aoff[ks] + i * 32 * kPStride];
-#pragma unroll
-			for (int j = 0; j < 2; ++j) b[j] = *(const v4i*)&sm[boff[ks] + j * 32 * kPStride];
+		for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
 			for (int i = 0; i < 4; ++i)
 #pragma unroll
-				for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], b[j], acc[i][j], 0, 0, 0);
-		}
+				for (int j = 0; j < 2; ++j) {
+					if (li < CPT && m == li * 16 / CPT) {
+						__builtin_amdgcn_sched_barrier(0);
+						issue_one(t % NS, t + NS, li);
+						++li;
+						__builtin_amdgcn_sched_barrier(0);
+					}
+					acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(xa[4 * ks + i], xb[2 * ks + j], acc[i][j], 0, 0, 0);
+					++m;
+				}
 	};
-	v4i ra[CPT], rb[CPT];
-	gload(ra, 0);
-	gload(rb, 1);
-	sstore(ra, 0);
-	__syncthreads();
-	// step t: tile t in LDS stage t & 1; tile t + 1 in flight in the other register set; the
-	// loads of tile t + 2 go out before step t's MFMAs
+	v4i ca[8], cb[4], na[8], nb[4];
+#pragma unroll
+	for (int i = 0; i < NS; ++i)
+#pragma unroll
+		for (int j = 0; j < CPT; ++j) issue_one(i, i, j);
+	wait_vmcnt<(NS - 1) * CPT>();
+	__builtin_amdgcn_s_barrier();
+	frags(ca, cb, 0);
 	for (int t = 0; t < ntile; t += 2) {
-		gload(ra, t + 2);
-		compute(0);
-		sstore(rb, 1);
-		__syncthreads();
-		gload(rb, t + 3);
-		if (t + 1 < ntile) compute(1);
-		sstore(ra, 0);
-		__syncthreads();
+		step(ca, cb, na, nb, t);
+		if (t + 1 < ntile) step(na, nb, ca, cb, t + 1);
 	}
+	frags_wait(ca, cb);
+	frags_wait(na, nb);
+	wait_vmcnt<0>();  // the trailing (clamped) loads land before the stages are reused
+	__syncthreads();
 
+	};
+	// epilogue of tile `tile` on acc (raw split plane `split` when gridDim.z > 1)
+	auto epilogue = [&](int tile, int split) {
+	const int m0 = (tile % tiles_m) * BM, n0 = (tile / tiles_m) * kPBN;
 	// Epilogue, 32 rows at a time: each wave parks a 32x64 slice of its accumulators in its own
-	// 8 KB of LDS (the main loop's stages are free now); then lane l owns the 4 columns
-	// wn + 4 (l % 16) .. +3 and rows l / 16 + 4 p of the slice -- 16-byte loads and stores,
-	// per-column parameters in registers, each 16-column tile's partial maximum reduced over a
-	// lane quad with DPP.
+	// 8 KB of LDS (the main loop's stages are free now); the two waves of a wave tile then sum
+	// their slices, lane l owning the 4 columns wn + 4 (l % 16) .. +3 and rows l / 16 + 4 p
+	// (p in 4 kh .. 4 kh + 3) of the slice -- 16-byte loads and stores, per-column parameters
+	// in registers, each 16-column tile's partial maximum reduced over a lane quad with DPP.
 	int32_t* slab = (int32_t*)smem + wave * 32 * 64;
+	const int32_t* slab0 = (const int32_t*)smem + wt * 32 * 64;
+	const int32_t* slab1 = (const int32_t*)smem + (wt + TW) * 32 * 64;
 	const int c4 = (lane & 15) * 4, rsub = lane >> 4;
 	const int col0 = n0 + wn + c4;  // first of this lane's 4 columns (with an epilogue N % 16 == 0)
 	const bool col_ok = col0 < g.N;
@@ -644,7 +719,7 @@ __global__ __launch_bounds__(BM / 128 * 2 * 64, 2) void k_gemm_mfma(GemmArgs g, 
 	// LDS after the slabs, so the store loop does not wait on a global load per row
 	int64_t* s_rcp = (int64_t*)(smem + WAVES * 32 * 64 * 4);
 	int64_t* s_ein = s_rcp + BM;
-	static_assert(WAVES * 32 * 64 * 4 + BM * 16 <= 2 * ROWS * kPStride, "epilogue LDS");
+	static_assert(WAVES * 32 * 64 * 4 + BM * 16 <= NS * STAGE, "epilogue LDS");
 	if (!raw) {
 		// the lane's segment (bounds are multiples of 16: one per lane), every field read with a
 		// constant index -- a lane-dependent index into the kernel arguments would copy them to
@@ -695,12 +770,12 @@ __global__ __launch_bounds__(BM / 128 * 2 * 64, 2) void k_gemm_mfma(GemmArgs g, 
 #pragma unroll
 			for (int v = 0; v < 16; ++v)
 				slab[(8 * (v >> 2) + 4 * (lane >> 5) + (v & 3)) * 64 + nt * 32 + (lane & 31)] = acc[mt][nt][v];
-		__builtin_amdgcn_wave_barrier();
-		for (int p = 0; p < 8; ++p) {
+		__syncthreads();
+		for (int p = 4 * kh; p < 4 * kh + 4; ++p) {
 			const int r = 4 * p + rsub;
 			const int t = m0 + wm + mt * 32 + r;
 			const bool ok = t < g.M && col_ok;
-			const v4i a = *(const v4i*)&slab[r * 64 + c4];
+			const v4i a = *(const v4i*)&slab0[r * 64 + c4] + *(const v4i*)&slab1[r * 64 + c4];
 			if (raw) {
 				if (ok && col0 + 4 <= g.N) {
 					*(v4i*)&raw_out[(size_t)t * g.N + col0] = a;
@@ -759,8 +834,20 @@ __global__ __launch_bounds__(BM / 128 * 2 * 64, 2) void k_gemm_mfma(GemmArgs g, 
 			mx = w2 > mx ? w2 : mx;
 			if ((lane & 3) == 0 && t < g.M && col_ok && mpart && !wide) mpart[t] = mx;
 		}
-		__builtin_amdgcn_wave_barrier();
+		__syncthreads();  // the slabs are rewritten for the next 32 rows
 	}
+	};
+
+	const int S = g.K / kPBK;  // K steps
+	// XCD-aware order: workgroups are dispatched round-robin over the 8 XCDs, so the virtual
+	// block vb = (b % 8) * (B / 8) + b / 8 puts neighbouring tiles (which share A or W rows) in
+	// one XCD's L2
+	const int B = gridDim.x;
+	const int vb = B % 8 == 0 ? (int)(blockIdx.x % 8) * (B / 8) + (int)(blockIdx.x / 8) : (int)blockIdx.x;
+	// one tile per block; gridDim.z splits K into raw partial planes
+	const int ks0 = blockIdx.z * pp.kspan / kPBK;
+	run_tile(vb, ks0, min(S, ks0 + pp.kspan / kPBK));
+	epilogue(vb, blockIdx.z);
 }
 
 // ------------------------------------------------------------------------------------------
@@ -1775,17 +1862,19 @@ void gemm(const GemmArgs& g, hipStream_t s) {
 	}
 	bool lora = false;
 	for (int i = 0; i < g.epi.nseg; ++i) lora = lora || g.epi.seg[i].lora_b;
-	if (!lora && !g.epi.argmax_key && g.K % kPBK == 0 && (g.epi.raw_out || g.N % 16 == 0)) {
+	if (!lora && !g.epi.argmax_key && prefill_mfma_k(g.K) && (g.epi.raw_out || g.N % 16 == 0)) {
 		// g.splits > 1 only as prefill_plan(M, N, K, true).splits, sized by the caller
 		const PrefillPlan p = prefill_plan(g.M, g.N, g.K, g.splits > 1);
-		const dim3 grid((g.N + kPBN - 1) / kPBN, (g.M + p.bm - 1) / p.bm, p.splits);
-		if (p.bm == 256) hipLaunchKernelGGL(k_gemm_mfma<256>, grid, dim3(256), 0, s, g, p.kspan);
-		else hipLaunchKernelGGL(k_gemm_mfma<128>, grid, dim3(128), 0, s, g, p.kspan);
+		const dim3 grid(p.blocks, 1, p.splits);
+		if (p.bm == 256) hipLaunchKernelGGL((k_gemm_mfma<256, kPrefillStages>), grid, dim3(512), 0, s, g, p);
+		else hipLaunchKernelGGL((k_gemm_mfma<128, kPrefillStages>), grid, dim3(256), 0, s, g, p);
 		return;
 	}
 	dim3 grid((g.N + kBN - 1) / kBN, (g.M + kBM - 1) / kBM);
 	hipLaunchKernelGGL(k_gemm_tiled, grid, dim3(kBlock), 0, s, g);
 }
+
+bool prefill_mfma_k(int K) { return K > 0 && K % kPBK == 0; }
 
 PrefillPlan prefill_plan(int M, int N, int K, bool split_ok) {
 	PrefillPlan p{};
@@ -1794,10 +1883,11 @@ PrefillPlan prefill_plan(int M, int N, int K, bool split_ok) {
 	const int steps = (K + kPBK - 1) / kPBK;
 	p.splits = 1;
 	if (split_ok && tiles < kPrefillTargetBlocks)
-		p.splits = std::max(1, std::min({(kPrefillTargetBlocks + tiles - 1) / tiles, steps / 3, kMaxRawSplits}));
+		p.splits = std::max(1, std::min({(kPrefillTargetBlocks + tiles - 1) / tiles, steps / 2, kMaxRawSplits}));
 	const int steps_per = (steps + p.splits - 1) / p.splits;
 	p.kspan = steps_per * kPBK;
 	p.splits = (K + p.kspan - 1) / p.kspan;
+	p.blocks = tiles;
 	return p;
 }
 

@@ -315,7 +315,7 @@ RawIn split_raw(sslm_model m, Track& w, GemmArgs& g, bool allow_multi, bool allo
 		splits = allow_multi ? sslm_launch::gemv_plan(g.M, g.N, g.K, true).splits : 1;
 		if (splits == 1 && !allow_single) return r;
 	} else {
-		if (!allow_multi || lora || g.K % 64 != 0) return r;
+		if (!allow_multi || lora || !sslm_launch::prefill_mfma_k(g.K)) return r;
 		splits = sslm_launch::prefill_plan(g.M, g.N, g.K, true).splits;
 		if (splits <= 1) return r;
 	}
@@ -828,7 +828,7 @@ void alloc_track(sslm_model m, Track& w, int T, bool head) {
 				int sp = 1;
 				const bool gemv = sslm_launch::gemv_eligible(rows, sh[1]);
 				if (gemv) sp = sslm_launch::gemv_plan(rows, sh[0], sh[1], true).splits;
-				else if (sh[1] % 64 == 0) sp = sslm_launch::prefill_plan(rows, sh[0], sh[1], true).splits;
+				else if (sslm_launch::prefill_mfma_k(sh[1])) sp = sslm_launch::prefill_plan(rows, sh[0], sh[1], true).splits;
 				if (sp > 1 || gemv) elems = std::max(elems, (size_t)sp * rows * sh[0]);  // a GEMV is always raw
 			}
 		}

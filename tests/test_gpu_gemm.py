@@ -20,7 +20,9 @@ def _lib(hip_lib):
 
 @pytest.mark.parametrize("m,n,k", [(1, 256, 128), (3, 320, 1536), (16, 512, 896), (37, 4864, 896),
                                    (64, 1536, 8960), (1, 1536, 8960), (16, 2048, 1536), (16, 1536, 65536),
-                                   (48, 96, 4096), (65, 384, 256), (200, 640, 1536), (512, 256, 128)])
+                                   (48, 96, 4096), (65, 384, 256), (200, 640, 1536), (512, 256, 128),
+                                   # ragged row and column tiles at several K steps
+                                   (300, 16512, 256), (257, 4224, 384)])
 def test_gemm_i32_exact(m, n, k, hip_lib):
     L = _lib(hip_lib)
     dev = Device(hip_lib)
@@ -54,7 +56,7 @@ IN_SCALE = (1 << 30, -37)
 SITE = (1518500250, -45)
 
 
-@pytest.mark.parametrize("m", [32, 1, 128])
+@pytest.mark.parametrize("m", [32, 1, 128, 300])
 def test_config0_requant_matches_oracle(m, hip_lib, oracle_lib):
     from oracle_bind import project_rows
     L = _lib(hip_lib)
