@@ -124,7 +124,13 @@ sslm_status sslm_workspace_destroy(sslm_workspace ws);                          
 sslm_status sslm_seq_create(sslm_model model, sslm_kv_pool* pool, sslm_seq* out);    /* :38 */
 sslm_status sslm_seq_release(sslm_seq seq);                                          /* :39 */
 sslm_status sslm_seq_reset(sslm_seq seq);                                            /* :40 */
+/* SSB3 sequence blob, byte-identical to the reference's (src/sslm_abi.cpp:2585-2720); the
+ * two-call sizing form (buf NULL) sets *n and returns SSLM_BUFFER_TOO_SMALL */
 sslm_status sslm_seq_save(sslm_seq seq, void* buf, size_t* n);                       /* :42 */
+/* SSB3 or SSB2 blob into a block of `pool`, checked in the reference's order
+ * (src/sslm_abi.cpp:2722-2987) */
+sslm_status sslm_seq_restore(sslm_model model, sslm_kv_pool* pool, const void* buf, size_t n,
+                             sslm_seq* out);                                         /* :43 */
 sslm_status sslm_seq_set_adapter(sslm_seq seq, sslm_adapter adapter);                /* :45 */
 sslm_status sslm_adapter_map(const void* data, size_t size, sslm_model base, sslm_adapter* out); /* :46 */
 sslm_status sslm_adapter_release(sslm_adapter adapter);                              /* :47 */
@@ -158,7 +164,6 @@ sslm_status sslm_prefix_prefill(sslm_model model, sslm_prefix prefix, const int3
 sslm_status sslm_prefix_freeze(sslm_prefix prefix);
 sslm_status sslm_prefix_release(sslm_prefix prefix);
 sslm_status sslm_seq_adopt_prefix(sslm_seq seq, sslm_prefix prefix);
-sslm_status sslm_seq_restore(sslm_model model, sslm_kv_pool* pool, const void* buf, size_t n, sslm_seq* out);
 sslm_status sslm_tokenize(sslm_model model, const char* utf8, int32_t* tokens, int32_t* n);
 sslm_status sslm_schema_lookup(sslm_model model, const char* name, sslm_schema* out);
 size_t sslm_schema_count(sslm_model model);

@@ -1066,6 +1066,7 @@ __device__ __forceinline__ int32_t rmsnorm_regs(const int32_t (&h)[EPT], const i
 #pragma unroll
 	for (int k = 0; k < EPT; ++k) ss += h[k] * h[k];
 	ss = blk_sum32<BS>(ss, s_sum);
+	KT(10);
 	if (prior && *prior != 0) return kSkipped;
 	int64_t root = isqrt_fast(div_floor_pos((int64_t)ss << 32, (int64_t)H));
 	root = root > 1 ? root : 1;
@@ -1074,6 +1075,7 @@ __device__ __forceinline__ int32_t rmsnorm_regs(const int32_t (&h)[EPT], const i
 		fd[threadIdx.x] = v >= 0 ? div_floor_pos(v, root) : -div_floor_pos(-v + root - 1, root);
 	}
 	__syncthreads();
+	KT(11);
 	int64_t w[EPT];
 	uint32_t mx = 0;
 #pragma unroll
@@ -1082,9 +1084,11 @@ __device__ __forceinline__ int32_t rmsnorm_regs(const int32_t (&h)[EPT], const i
 		mx = max(mx, sat_abs_u32(w[k]));
 	}
 	mx = blk_max32<BS>(mx, s_max);
+	KT(12);
 	FunnelPlan plan;
 	const int32_t st = funnel_plan(mx, nullptr, 0, site, &plan);
 	if (st != kOk) return st;
+	KT(13);
 #pragma unroll
 	for (int k = 0; k < EPT; ++k) {
 		const int i = threadIdx.x + k * BS;

@@ -246,6 +246,10 @@ struct sslm_seq_s {
 	int32_t current_token = -1;
 	bool ready_for_logits = false;
 	sslm_adapter adapter = nullptr;
+	int64_t forced_token_count = 0;
+	// damped-greedy anti-LM state carried through save/restore (order 0: none)
+	int32_t anti_lm_order = 0;
+	std::vector<int32_t> anti_lm_history;
 	std::mutex mu;
 };
 
@@ -259,6 +263,29 @@ namespace {
 
 std::mutex g_registry_mu;
 std::set<sslm_seq_s*> g_live_seqs;
+
+// sequence blob constants (src/sslm_abi.cpp:102, :2585-2618)
+constexpr uint8_t kBlobMagic[4] = {'S', 'S', 'B', '3'};
+constexpr uint8_t kBlobMagicV2[4] = {'S', 'S', 'B', '2'};
+constexpr size_t kBlobHeader = 120, kBlobHeaderV2 = 108;
+constexpr uint32_t kWalkUnused = 0xFFFFFFFFu;  // DFA walk state of a sequence with no schema bound
+
+void put32(uint8_t* p, uint32_t v) {
+	for (int i = 0; i < 4; ++i) p[i] = (uint8_t)(v >> (8 * i));
+}
+void put64(uint8_t* p, uint64_t v) {
+	for (int i = 0; i < 8; ++i) p[i] = (uint8_t)(v >> (8 * i));
+}
+uint32_t get32(const uint8_t* p) {
+	uint32_t v = 0;
+	for (int i = 0; i < 4; ++i) v |= (uint32_t)p[i] << (8 * i);
+	return v;
+}
+uint64_t get64(const uint8_t* p) {
+	uint64_t v = 0;
+	for (int i = 0; i < 8; ++i) v |= (uint64_t)p[i] << (8 * i);
+	return v;
+}
 
 // ------------------------------------------------------------------------------------------
 // launch helpers
@@ -1298,6 +1325,9 @@ sslm_status sslm_seq_reset(sslm_seq seq) {
 		seq->layer_index = 0;
 		seq->current_token = -1;
 		seq->ready_for_logits = false;
+		seq->forced_token_count = 0;
+		seq->anti_lm_order = 0;
+		seq->anti_lm_history.clear();
 		return SSLM_OK;
 	});
 }
@@ -1679,6 +1709,10 @@ sslm_status sslm_decode_params_init(sslm_model model, int32_t mode, int32_t laye
 sslm_status sslm_stats(sslm_model model, sslm_seq seq, sslm_stats_out* out) {
 	if (!model || !seq || !out) return SSLM_INVALID_ARGUMENT;
 	memset(out, 0, sizeof(*out));
+	// src/sslm_abi.cpp:2506-2534
+	out->decode_step_ceiling = model->L;
+	out->decode_step_actual = model->L;
+	out->forced_token_count = seq->forced_token_count;
 	out->kv_blocks_resident = 1;
 	return SSLM_OK;
 }
@@ -1695,11 +1729,61 @@ sslm_status sslm_g5_test_only_peek_kv_block_bytes(sslm_kv_pool pool, uint32_t bl
 	});
 }
 
+// Sequence blob, SSB3 (src/sslm_abi.cpp:2585-2618 layout, :2620-2720 save): 120-byte header --
+// magic, model integrity hash, kv_precision, schema name hash (0: none), DFA walk state,
+// adapter binding id (0), context_length, layer_index, current_token (-1 unless resting between
+// decode steps), hidden scale (m, e), KV saturation count, forced-token count, anti-LM order and
+// history count -- then the residual codes (H bytes, mid-token only), the anti-LM history, the
+// KV block count (1) and the sequence's KV block in the reference layout.  All fields little
+// endian.  The residual and KV block are read back from the device.
 sslm_status sslm_seq_save(sslm_seq seq, void* buf, size_t* n) {
-	(void)seq;
-	(void)buf;
-	if (n) *n = 0;
-	return SSLM_INVALID_ARGUMENT;
+	if (!n || !seq) return SSLM_INVALID_ARGUMENT;
+	sslm_model m = seq->model;
+	const bool mid_token = seq->layer_index != 0;
+	const size_t residual = mid_token ? (size_t)m->H : 0;
+	const size_t history = seq->anti_lm_history.size();
+	if (seq->context_length < 0 || history > (size_t)seq->context_length) return SSLM_INVALID_ARGUMENT;
+	const size_t required = kBlobHeader + residual + 4 * history + 4 + seq->pool->block_size;
+	if (!buf || *n < required) {
+		*n = required;
+		return SSLM_BUFFER_TOO_SMALL;
+	}
+	return guarded([&]() -> sslm_status {
+		std::lock_guard<std::mutex> lk(m->mu);
+		for (auto& t : m->tracks) ck(hipStreamSynchronize(t.stream));
+		uint8_t* p = (uint8_t*)buf;
+		Scale hs{};
+		unsigned long long sat = 0;
+		ck(hipMemcpy(&hs, m->stream_scale + seq->slot, sizeof(Scale), hipMemcpyDeviceToHost));
+		ck(hipMemcpy(&sat, m->sat + seq->slot, 8, hipMemcpyDeviceToHost));
+		memcpy(p, kBlobMagic, 4);
+		memcpy(p + 4, m->art.hash, 32);
+		put32(p + 36, m->c.kv_precision);
+		put64(p + 40, 0);             // schema name hash: no schema bound
+		put32(p + 48, kWalkUnused);   // DFA walk state
+		put64(p + 52, 0);             // adapter binding id (the reference always writes 0)
+		put64(p + 60, (uint64_t)seq->context_length);
+		put32(p + 68, seq->layer_index);
+		const bool pending_embed = seq->layer_index == 0 && !seq->ready_for_logits;
+		put32(p + 72, (uint32_t)(pending_embed ? seq->current_token : -1));
+		put64(p + 76, (uint64_t)hs.m);
+		put64(p + 84, (uint64_t)hs.e);
+		put64(p + 92, (uint64_t)sat);
+		put64(p + 100, (uint64_t)seq->forced_token_count);
+		put32(p + 108, (uint32_t)seq->anti_lm_order);
+		put64(p + 112, (uint64_t)history);
+		size_t off = kBlobHeader;
+		if (residual) ck(hipMemcpy(p + off, m->stream_codes + (size_t)seq->slot * m->H, residual, hipMemcpyDeviceToHost));
+		off += residual;
+		for (size_t i = 0; i < history; ++i, off += 4) put32(p + off, (uint32_t)seq->anti_lm_history[i]);
+		put32(p + off, 1);  // KV block count
+		off += 4;
+		ck(hipMemcpy(p + off, seq->pool->dev + (size_t)seq->block * seq->pool->block_size, seq->pool->block_size,
+		             hipMemcpyDeviceToHost));
+		off += seq->pool->block_size;
+		*n = off;
+		return SSLM_OK;
+	});
 }
 
 // src/sslm_abi.cpp:2990-3085 with PopulateAdapterFromView (adapter_marshal.h): the adapter is an
@@ -1841,9 +1925,99 @@ sslm_status sslm_prefix_prefill(sslm_model, sslm_prefix, const int32_t*, int32_t
 sslm_status sslm_prefix_freeze(sslm_prefix) { return SSLM_INVALID_ARGUMENT; }
 sslm_status sslm_prefix_release(sslm_prefix) { return SSLM_INVALID_ARGUMENT; }
 sslm_status sslm_seq_adopt_prefix(sslm_seq, sslm_prefix) { return SSLM_INVALID_ARGUMENT; }
-sslm_status sslm_seq_restore(sslm_model, sslm_kv_pool*, const void*, size_t, sslm_seq* out) {
-	if (out) *out = nullptr;
-	return SSLM_INVALID_ARGUMENT;
+// src/sslm_abi.cpp:2722-2987: checks in the reference's order (magic SSB3 or SSB2, sizes, model
+// hash, kv precision, schema binding -- none can resolve here, as no schema is ever bound --
+// field domains, exact size, KV block count, pool identity), then a block is drawn, the KV
+// block and residual uploaded and the resting state rebuilt: current_token >= 0 resumes with
+// the embed of that token; otherwise a whole-token state with context ready for logits (its
+// residual codes are not in the blob, so they restart from zero, as in the reference).
+sslm_status sslm_seq_restore(sslm_model model, sslm_kv_pool* pool, const void* buf, size_t n, sslm_seq* out) {
+	if (!out) return SSLM_INVALID_ARGUMENT;
+	*out = nullptr;
+	if (!model || !pool || !*pool || !buf) return SSLM_INVALID_ARGUMENT;
+	if (n < 4) return SSLM_INVALID_ARGUMENT;
+	const uint8_t* p = (const uint8_t*)buf;
+	const bool v3 = memcmp(p, kBlobMagic, 4) == 0, v2 = memcmp(p, kBlobMagicV2, 4) == 0;
+	if (!v3 && !v2) return SSLM_INVALID_ARGUMENT;
+	const size_t header = v3 ? kBlobHeader : kBlobHeaderV2;
+	if (n < header + 4) return SSLM_INVALID_ARGUMENT;
+	if (memcmp(p + 4, model->art.hash, 32) != 0) return SSLM_RESTORE_MODEL_MISMATCH;
+	if (get32(p + 36) != model->c.kv_precision) return SSLM_RESTORE_KV_MISMATCH;
+	if (get64(p + 40) != 0) return SSLM_RESTORE_SCHEMA_MISMATCH;
+	if (get32(p + 48) != kWalkUnused) return SSLM_RESTORE_SCHEMA_MISMATCH;
+	const int64_t context_length = (int64_t)get64(p + 60);
+	const uint32_t layer_index = get32(p + 68);
+	const int32_t current_token = (int32_t)get32(p + 72);
+	const Scale hs{(int64_t)get64(p + 76), (int64_t)get64(p + 84)};
+	const uint64_t sat = get64(p + 92);
+	const int64_t forced = (int64_t)get64(p + 100);
+	const int32_t order = v3 ? (int32_t)get32(p + 108) : 0;
+	const uint64_t history = v3 ? get64(p + 112) : 0;
+	if ((order == 0 && history != 0) || order < 0 || history > (uint64_t)SIZE_MAX) return SSLM_INVALID_ARGUMENT;
+	if (context_length < 0 || context_length > (int64_t)model->c.context_cap || layer_index > (uint32_t)model->L ||
+	    history > (uint64_t)context_length || history > (uint64_t)model->c.context_cap)
+		return SSLM_INVALID_ARGUMENT;
+	const size_t residual = layer_index != 0 ? (size_t)model->H : 0;
+	const size_t tail = header + residual + 4 * (size_t)history + 4;
+	if (n < tail) return SSLM_INVALID_ARGUMENT;
+	const uint8_t* residual_ptr = p + header;
+	const uint8_t* history_ptr = residual_ptr + residual;
+	if (get32(history_ptr + 4 * history) != 1) return SSLM_INVALID_ARGUMENT;  // KV block count
+	const size_t block_size = model->block_bytes;
+	if (block_size == 0) return SSLM_ARTIFACT_REJECTED;
+	if (n < tail + block_size) return SSLM_INVALID_ARGUMENT;
+	const uint8_t* kv_ptr = p + tail;
+	sslm_kv_pool pl = *pool;
+	if (pl->model != model) return SSLM_INVALID_ARGUMENT;
+	return guarded([&]() -> sslm_status {
+		std::lock_guard<std::mutex> lk(model->mu);
+		uint32_t block;
+		{
+			std::lock_guard<std::mutex> g(pl->mu);
+			if (pl->free_list.empty()) return SSLM_KV_POOL_EXHAUSTED;
+			if (model->free_slots.empty()) return SSLM_ALLOCATION_FAILED;
+			block = pl->free_list.back();  // src/sslm_abi.cpp:1308-1331
+			pl->free_list.pop_back();
+			pl->live_refs++;
+		}
+		const int slot = model->free_slots.back();
+		model->free_slots.pop_back();
+		hipStream_t st = model->tracks[0].stream;
+		ck(hipStreamSynchronize(st));
+		ck(hipMemcpy(pl->dev + (size_t)block * pl->block_size, kv_ptr, block_size, hipMemcpyHostToDevice));
+		std::vector<int8_t> codes(model->H, 0);
+		if (residual) memcpy(codes.data(), residual_ptr, residual);
+		ck(hipMemcpy(model->stream_codes + (size_t)slot * model->H, codes.data(), model->H, hipMemcpyHostToDevice));
+		ck(hipMemcpy(model->stream_scale + slot, &hs, sizeof(Scale), hipMemcpyHostToDevice));
+		const unsigned long long sat_v = sat;
+		ck(hipMemcpy(model->sat + slot, &sat_v, 8, hipMemcpyHostToDevice));
+		const int32_t zero = 0;
+		ck(hipMemcpy(model->status + slot, &zero, 4, hipMemcpyHostToDevice));
+		sslm_seq_s* s = new sslm_seq_s();
+		s->model = model;
+		s->pool = pl;
+		s->block = block;
+		s->slot = slot;
+		s->layer_index = layer_index;
+		s->context_length = context_length;
+		s->forced_token_count = forced;
+		s->anti_lm_order = order;
+		for (uint64_t i = 0; i < history; ++i) s->anti_lm_history.push_back((int32_t)get32(history_ptr + 4 * i));
+		if (current_token >= 0) {
+			s->current_token = current_token;
+			s->ready_for_logits = false;
+		} else {
+			s->current_token = -1;
+			s->ready_for_logits = layer_index == 0 && context_length > 0;
+		}
+		model->live_refs++;
+		{
+			std::lock_guard<std::mutex> rl(g_registry_mu);
+			g_live_seqs.insert(s);
+		}
+		*out = s;
+		return SSLM_OK;
+	});
 }
 sslm_status sslm_tokenize(sslm_model, const char*, int32_t*, int32_t*) { return SSLM_INVALID_ARGUMENT; }
 sslm_status sslm_schema_lookup(sslm_model, const char*, sslm_schema* out) {

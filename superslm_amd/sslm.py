@@ -93,6 +93,7 @@ class SslmLib:
         sig("sslm_adapter_map", ctypes.c_int, vp, sz, vp, pvp)
         sig("sslm_adapter_release", ctypes.c_int, vp)
         sig("sslm_seq_save", ctypes.c_int, vp, vp, ctypes.POINTER(sz))
+        sig("sslm_seq_restore", ctypes.c_int, vp, pvp, vp, sz, pvp)
         self.has_peek = hasattr(L, "sslm_g5_test_only_peek_kv_block_bytes")
         if self.has_peek:
             sig("sslm_g5_test_only_peek_kv_block_bytes", ctypes.c_int, vp, u32, vp, sz)
@@ -189,6 +190,19 @@ class KvPool:
     def seq(self) -> "Seq":
         return Seq(self)
 
+    def restore(self, blob: bytes, raw: bool = False):
+        """sslm_seq_restore of a saved sequence blob into this pool: a Seq, or with `raw` the
+        status and the Seq (None unless the status is SSLM_OK)."""
+        m = self.model
+        buf = ctypes.create_string_buffer(bytes(blob), len(blob))
+        h = ctypes.c_void_p()
+        st = m.lib.lib.sslm_seq_restore(m.handle, ctypes.byref(self.handle), buf, len(blob), ctypes.byref(h))
+        seq = Seq(self, handle=h) if st == SSLM_OK else None
+        if raw:
+            return st, seq
+        m.lib.check("sslm_seq_restore", st)
+        return seq
+
     def close(self):
         if self.handle:
             self.model.lib.check("sslm_kv_pool_destroy", self.model.lib.lib.sslm_kv_pool_destroy(self.handle))
@@ -196,9 +210,12 @@ class KvPool:
 
 
 class Seq:
-    def __init__(self, pool: KvPool):
+    def __init__(self, pool: KvPool, handle=None):
         lib = pool.model.lib
         self.pool = pool
+        if handle is not None:  # a restored sequence
+            self.handle = handle
+            return
         h = ctypes.c_void_p()
         lib.check("sslm_seq_create", lib.lib.sslm_seq_create(pool.model.handle, ctypes.byref(pool.handle),
                                                               ctypes.byref(h)))
@@ -220,6 +237,12 @@ class Seq:
         m = self.pool.model
         m.lib.check("sslm_seq_set_adapter",
                     m.lib.lib.sslm_seq_set_adapter(self.handle, adapter.handle if adapter else None))
+
+    def save_size(self):
+        """The two-call sizing form: (status, required size) of sslm_seq_save with no buffer."""
+        n = ctypes.c_size_t(0)
+        st = self.pool.model.lib.lib.sslm_seq_save(self.handle, None, ctypes.byref(n))
+        return st, n.value
 
     def save(self) -> bytes:
         lib = self.pool.model.lib
