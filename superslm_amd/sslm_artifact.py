@@ -54,6 +54,16 @@ def write_container(sections, flags: int = 0) -> bytes:
     return bytes(write_container_array(sections, flags))
 
 
+def with_flags(image: bytes, flags: int) -> bytes:
+    """The container `image` with header flags `flags` (bit 0: Option-G fused K landing, bit 1:
+    damped-greedy constants; src/artifact.cpp:254-270, :511-518) and its integrity SHA-256
+    recomputed (over the file with the hash field zeroed)."""
+    b = bytearray(image)
+    struct.pack_into("<I", b, 16, flags)
+    b[32:64] = hashlib.sha256(bytes(b[:32]) + bytes(32) + bytes(b[64:])).digest()
+    return bytes(b)
+
+
 def write_container_array(sections, flags: int = 0) -> np.ndarray:
     """Same as write_container, returning the file image as a uint8 array (no extra copy)."""
     count = len(sections)

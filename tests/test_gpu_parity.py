@@ -214,3 +214,27 @@ def test_adapter_map_rejections_match_reference(hip_lib, ref_lib):
         model.close()
     for case in cases:
         assert statuses[("hip", case)] == statuses[("ref", case)] != 0, (case, statuses)
+
+
+def test_option_g_flag_matches_reference(hip_lib, ref_lib):
+    """Artifact flag bit 0 (Option-G fused K landing, src/artifact.cpp:511-513).  The reference's
+    C ABI never enables it: prefill passes option_g_fused_k_landing = false
+    (src/sslm_abi.cpp:1535-1540) and decode runs the RunLayerLoop overload that fixes it to false
+    (forward_sites.cpp:2018-2031).  Both libraries accept the flagged artifact and run the
+    plain landing; tokens and KV must agree."""
+    from superslm_amd.sslm_artifact import with_flags
+    sm, plain = synthetic("tiny")
+    art = with_flags(plain, 1)
+    assert art[16] == 1 and art[32:64] != plain[32:64]
+    prompt = np.random.default_rng(12).integers(0, sm.config.vocab, size=11)
+    L = sm.config.layers
+    for budget in sorted({1, L}):
+        print(f"case option-g budget={budget}", flush=True)
+        r = _run(ref_lib, art, prompt, 5, budget)
+        h = _run(hip_lib, art, prompt, 5, budget)
+        p = _run(hip_lib, plain, prompt, 5, budget)
+        assert h[0] == r[0]
+        assert np.array_equal(h[1], r[1]), "KV after prefill differs"
+        assert h[2] == r[2], f"tokens differ: hip {h[2]} ref {r[2]}"
+        assert np.array_equal(h[3], r[3]), "KV after decode differs"
+        assert h[2] == p[2] and np.array_equal(h[3], p[3])  # the flag changes nothing at the ABI
