@@ -84,6 +84,10 @@ typedef enum sslm_span_kind { SSLM_SPAN_PROMPT = 0, SSLM_SPAN_SCHEMA_CONTENT = 1
 
 #define SSLM_DECODE_MODE_GREEDY 0
 #define SSLM_DECODE_MODE_DAMPED_GREEDY 1
+/* reference sslm_abi.h:194-196: sslm_decode_params_init's damped-greedy defaults */
+#define SSLM_DAMPED_GREEDY_DEFAULT_ALPHA_Q15 65536
+#define SSLM_DAMPED_GREEDY_DEFAULT_ANTI_LM_ORDER 2
+#define SSLM_DAMPED_GREEDY_DEFAULT_TOP_K 6
 
 /* reference sslm_abi.h:207-224 */
 typedef struct sslm_decode_params {

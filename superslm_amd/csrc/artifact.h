@@ -37,6 +37,9 @@ struct Artifact {
 	std::vector<int32_t> sigmoid_lut;
 	const uint8_t* provenance = nullptr;
 	uint64_t provenance_bytes = 0;
+	// DampedGreedyConstants section (raw bytes; read only when header flag bit 1 is set)
+	const uint8_t* damped = nullptr;
+	uint64_t damped_bytes = 0;
 };
 
 // Parses and validates `data` (header, section table, SHA-256 integrity, every sub-format and

@@ -210,6 +210,10 @@ struct sslm_model_s {
 	int64_t *rope_cos, *rope_sin;
 	Scale embed_site, final_site;
 	int64_t ln2_q, b_q, ca_q;
+	// damped greedy: i-exp triple of the artifact's logit scale (src/sslm_abi.cpp:1172-1185)
+	bool dg_available = false;
+	int64_t dg_q_ln2 = 0, dg_q_b = 0, dg_q_c = 0;
+	int32_t* logits = nullptr;  // [kMaxTokens, V] raw head rows, allocated on first damped use
 	// per-slot sequence state
 	int8_t* stream_codes;   // [kSlotCapacity, H]
 	Scale* stream_scale;    // [kSlotCapacity]
@@ -222,6 +226,79 @@ struct sslm_model_s {
 	int8_t* pool_dev = nullptr;  // KV pool of the launch sequence being recorded
 	std::atomic<int> live_refs{0};
 	std::mutex mu;  // serializes GPU submission on this model
+};
+
+// Damped-greedy anti-LM (src/damped_greedy_antilm.cpp): for each order n in 1..max_order, the
+// counts of tokens that followed each (n-1)-token context of the generated history, and the
+// history itself.  Only lookups by context are made, so an ordered map serves (no iteration
+// order reaches any result).
+struct AntiLm {
+	struct Entry {
+		std::map<int32_t, int64_t> counts;
+		int64_t total = 0;
+	};
+	int order = 0;
+	std::vector<std::map<std::vector<int32_t>, Entry>> tables;
+	std::vector<int32_t> history;
+
+	void reset(int max_order) {
+		order = max_order;
+		tables.assign(max_order > 0 ? max_order : 0, {});
+		history.clear();
+	}
+	const Entry* context(int n) const {  // the table entry of order n's current context
+		const size_t len = (size_t)n - 1;
+		if (len > history.size()) return nullptr;
+		const std::vector<int32_t> ctx(history.end() - (long)len, history.end());
+		auto it = tables[n - 1].find(ctx);
+		return it == tables[n - 1].end() ? nullptr : &it->second;
+	}
+	// AntiLmUpdate, :129-152
+	void update(int32_t token) {
+		for (int n = 1; n <= order; ++n) {
+			const size_t len = (size_t)n - 1;
+			if (len > history.size()) continue;
+			Entry& e = tables[n - 1][std::vector<int32_t>(history.end() - (long)len, history.end())];
+			e.counts[token] += 1;
+			e.total += 1;
+		}
+		history.push_back(token);
+	}
+	// AntiLmPenalize, :160-228: p_omega in Q15 per candidate, a beta^(max_order - n) weighted
+	// mix over the orders whose context was seen (weights normalized, the last takes the rest)
+	void penalize(const int32_t* cand, size_t k, int64_t* out) const {
+		constexpr int64_t kBetaQ15 = 29491;  // round(0.9 * 2^15)
+		auto pow_q15 = [](int64_t b, int ex) {
+			int64_t r = (int64_t)1 << 15;
+			for (int i = 0; i < ex; ++i) r = (r * b) >> 15;
+			return r;
+		};
+		for (size_t c = 0; c < k; ++c) out[c] = 0;
+		int active = 0;
+		int64_t raw_sum = 0;
+		for (int n = 1; n <= order; ++n)
+			if (context(n)) {
+				++active;
+				raw_sum += pow_q15(kBetaQ15, order - n);
+			}
+		if (active == 0) return;
+		int idx = 0;
+		int64_t norm_sum = 0;
+		for (int n = 1; n <= order; ++n) {
+			const Entry* e = context(n);
+			if (!e) continue;
+			++idx;
+			const int64_t w = idx == active ? ((int64_t)1 << 15) - norm_sum
+			                                : (pow_q15(kBetaQ15, order - n) << 15) / raw_sum;
+			norm_sum += w;
+			for (size_t c = 0; c < k; ++c) {
+				auto f = e->counts.find(cand[c]);
+				const int64_t count = f == e->counts.end() ? 0 : f->second;
+				out[c] += (w * ((count << 15) / e->total)) >> 15;
+			}
+		}
+		for (size_t c = 0; c < k; ++c) out[c] = std::min<int64_t>(std::max<int64_t>(out[c], 0), (int64_t)1 << 15);
+	}
 };
 
 struct sslm_kv_pool_s {
@@ -247,9 +324,7 @@ struct sslm_seq_s {
 	bool ready_for_logits = false;
 	sslm_adapter adapter = nullptr;
 	int64_t forced_token_count = 0;
-	// damped-greedy anti-LM state carried through save/restore (order 0: none)
-	int32_t anti_lm_order = 0;
-	std::vector<int32_t> anti_lm_history;
+	AntiLm anti_lm;  // damped-greedy n-gram state (order 0: none)
 	std::mutex mu;
 };
 
@@ -754,6 +829,52 @@ void run_logits(sslm_model m, Track& w, int M, StreamRef st, const TokenInfo* to
 	ck(hipGetLastError());
 }
 
+// Damped-greedy selection over one logit row (src/damped_greedy_topk.cpp:1-461, free text: every
+// token legal).  Top-k by (logit desc, index asc); q_theta = the k i-exp values renormalized to
+// Q15 (TopKRenormalizeQ15: each against the row-max peak, refused when any is out of domain);
+// p_omega from the anti-LM; winner = max of q_theta - (alpha * p_omega >> 15), lowest index on
+// ties.  Returns false when refused.
+bool damped_pick(const int32_t* row, int V, const sslm_decode_params& p, const AntiLm& lm, int32_t* token) {
+	const int k = p.top_k;
+	std::vector<int32_t> idx(V);
+	for (int i = 0; i < V; ++i) idx[i] = i;
+	auto before = [&](int32_t a, int32_t b) { return row[a] != row[b] ? row[a] > row[b] : a < b; };
+	std::partial_sort(idx.begin(), idx.begin() + k, idx.end(), before);
+	if (check_softmax_width(p.q_b, p.q_c, k) != kOk) return false;
+	int64_t row_max = row[idx[0]];
+	for (int i = 1; i < k; ++i) row_max = std::max<int64_t>(row_max, row[idx[i]]);
+	const int64_t peak = iexp_element(0, p.q_ln2, p.q_b, p.q_c, kI64Max);
+	const bool peak_ok = peak >= 1 && peak <= kSoftmaxMaxSafe;
+	std::vector<int64_t> q(k, 0);
+	bool well_formed = peak_ok;
+	int64_t total = 0;
+	for (int i = 0; i < k; ++i) {
+		const int64_t v = iexp_element((int64_t)row[idx[i]] - row_max, p.q_ln2, p.q_b, p.q_c, kI64Max);
+		if (v < 0 || !peak_ok || v > peak) {  // refused construction, or outside [0, peak]
+			well_formed = false;
+			continue;
+		}
+		q[i] = v;
+		total += v;
+	}
+	if (!well_formed) return false;
+	const int64_t denom = total > 1 ? total : 1;
+	for (int i = 0; i < k; ++i) q[i] = (q[i] << 15) / denom;
+	std::vector<int64_t> omega(k, 0);
+	lm.penalize(idx.data(), k, omega.data());
+	int64_t best = 0;
+	int32_t best_tok = -1;
+	for (int i = 0; i < k; ++i) {
+		const int64_t score = q[i] - (int32_t)(((int64_t)p.alpha_q15 * omega[i]) >> 15);
+		if (best_tok < 0 || score > best || (score == best && idx[i] < best_tok)) {
+			best = score;
+			best_tok = idx[i];
+		}
+	}
+	*token = best_tok;
+	return true;
+}
+
 sslm_status map_forward_status(int32_t word) {
 	const int32_t st = word & 0xff;
 	if (st == 0) return SSLM_OK;
@@ -1043,6 +1164,26 @@ bool build_device_model(sslm_model m, std::string* err) {
 		m->b_q = (int64_t)(1.353 * (double)((int64_t)1 << 30));
 		m->ca_q = (int64_t)((0.344 / 0.3585) * (double)((int64_t)1 << 30));
 	}
+	if (A.flags & 2u) {  // damped-greedy constants (src/damped_greedy_phaseD.cpp, src/sslm_abi.cpp:1172-1185)
+		if (!A.damped || A.damped_bytes != 12) {
+			*err = "damped-greedy constants section missing or malformed";
+			return false;
+		}
+		const int64_t dm = (int64_t)get64(A.damped);
+		const int64_t de = (int32_t)get32(A.damped + 8);
+		int64_t ql = 0, qb = 0, qc = 0;
+		// in domain: the i-exp triple derives, and a softmax over the real vocabulary (151,936
+		// entries) passes the row-width gate
+		if (iexp_scale_constants(dm, de, m->ln2_q, m->b_q, m->ca_q, &ql, &qb, &qc) != 0 ||
+		    check_softmax_width(qb, qc, 151936) != kOk) {
+			*err = "damped-greedy constants out of domain";
+			return false;
+		}
+		m->dg_available = true;
+		m->dg_q_ln2 = ql;
+		m->dg_q_b = qb;
+		m->dg_q_c = qc;
+	}
 	// slots
 	m->stream_codes = dalloc<int8_t>((size_t)kSlotCapacity * H, &own);
 	m->stream_scale = dalloc<Scale>(kSlotCapacity, &own);
@@ -1326,8 +1467,7 @@ sslm_status sslm_seq_reset(sslm_seq seq) {
 		seq->current_token = -1;
 		seq->ready_for_logits = false;
 		seq->forced_token_count = 0;
-		seq->anti_lm_order = 0;
-		seq->anti_lm_history.clear();
+		seq->anti_lm.reset(0);
 		return SSLM_OK;
 	});
 }
@@ -1400,8 +1540,11 @@ int track_min() {
 	return v;
 }
 
-static sslm_status decode_batch(sslm_model m, sslm_seq* seqs, int32_t n, uint32_t budget, int32_t* out_tokens,
-                                bool* stop_cap) {
+static sslm_status decode_batch(sslm_model m, sslm_seq* seqs, int32_t n, const sslm_decode_params& params,
+                                int32_t* out_tokens, bool* stop_cap) {
+	const uint32_t budget = (uint32_t)params.layer_budget;
+	const bool damped = params.mode == SSLM_DECODE_MODE_DAMPED_GREEDY;
+	if (damped && !m->logits) m->logits = dalloc<int32_t>((size_t)kMaxTokens * m->V, &m->owned);
 	// Partition: sequences needing layers, grouped by their current layer; sequences needing logits.
 	std::vector<int> need_logits;
 	std::vector<std::pair<uint32_t, std::vector<int>>> groups;
@@ -1513,7 +1656,14 @@ static sslm_status decode_batch(sslm_model m, sslm_seq* seqs, int32_t n, uint32_
 	};
 	auto launch_logits = [&](int M) {
 		run_logits(m, t0, M, StreamRef{m->stream_codes, m->stream_scale, t0.lg_slot}, t0.lg_tok);
+		if (damped) {  // the whole logit rows as well: the head's raw int32 accumulators
+			GemmArgs g = head_args(m, t0, M, t0.lg_tok);
+			g.epi.argmax_key = nullptr;
+			g.epi.raw_out = m->logits;
+			run_gemm(m, t0, g, kProfHead);
+		}
 	};
+	std::vector<int32_t> rows(damped ? lg.size() * (size_t)m->V : 0);
 	// every sequence of one call shares the pool of the first (checked by the caller)
 	m->pool_dev = seqs[0]->pool->dev;
 	std::vector<int32_t> toks(lg.size());
@@ -1562,10 +1712,14 @@ static sslm_status decode_batch(sslm_model m, sslm_seq* seqs, int32_t n, uint32_
 		}
 		if (!lg.empty()) {
 			const int M = (int)lg.size();
-			if (use_graph) ck(hipGraphLaunch(graph_of("lg|" + std::to_string(M), t0.stream, [&] { launch_logits(M); }), t0.stream));
+			if (use_graph)
+				ck(hipGraphLaunch(graph_of("lg|" + std::to_string(M) + (damped ? "|d" : ""), t0.stream, [&] { launch_logits(M); }),
+				                  t0.stream));
 			else launch_logits(M);
 		}
 		if (!lg.empty()) ck(hipMemcpyAsync(toks.data(), t0.out_tokens, lg.size() * 4, hipMemcpyDeviceToHost, t0.stream));
+		if (damped && !lg.empty())
+			ck(hipMemcpyAsync(rows.data(), m->logits, rows.size() * 4, hipMemcpyDeviceToHost, t0.stream));
 	} else {
 		std::vector<bool> used(ntr, false);
 		for (size_t u = 0; u < units.size(); ++u) {
@@ -1583,6 +1737,9 @@ static sslm_status decode_batch(sslm_model m, sslm_seq* seqs, int32_t n, uint32_
 			stage_logits(b, M, t0.stream);
 			launch_logits(M);
 			ck(hipMemcpyAsync(toks.data() + b, t0.out_tokens, M * 4, hipMemcpyDeviceToHost, t0.stream));
+			if (damped)
+				ck(hipMemcpyAsync(rows.data() + b * (size_t)m->V, m->logits, (size_t)M * m->V * 4, hipMemcpyDeviceToHost,
+				                  t0.stream));
 		}
 	}
 	std::vector<int32_t> words(kSlotCapacity);
@@ -1621,9 +1778,26 @@ static sslm_status decode_batch(sslm_model m, sslm_seq* seqs, int32_t n, uint32_
 		if (failed_layers[i]) continue;
 		sslm_seq s = seqs[i];
 		s->ready_for_logits = false;
-		s->current_token = toks[k];
+		if (failed_head[i]) {
+			s->current_token = toks[k];
+			s->layer_index = 0;
+			out_tokens[i] = -1;
+			continue;
+		}
+		int32_t tok = toks[k];
+		if (damped) {  // src/sslm_abi.cpp:2301-2384
+			if (s->anti_lm.order == 0 || s->anti_lm.order != params.anti_lm_max_order)
+				s->anti_lm.reset(params.anti_lm_max_order);
+			if (!damped_pick(rows.data() + k * (size_t)m->V, m->V, params, s->anti_lm, &tok)) {
+				out_tokens[i] = -1;  // refused: no token this call; the sequence keeps its layer index
+				if (first_err == SSLM_OK) first_err = map_forward_status(kSoftmaxKernelRefusedAfterGateAccepted);
+				continue;
+			}
+			s->anti_lm.update(tok);
+		}
+		s->current_token = tok;
 		s->layer_index = 0;
-		out_tokens[i] = failed_head[i] ? -1 : toks[k];
+		out_tokens[i] = tok;
 	}
 	ck(hipStreamSynchronize(t0.stream));
 	return first_err;
@@ -1635,7 +1809,19 @@ static sslm_status decode_impl(sslm_model model, sslm_seq* seqs, int32_t n, cons
 	if (n < 1) return SSLM_INVALID_ARGUMENT;
 	if (params->struct_size != sizeof(sslm_decode_params)) return SSLM_INVALID_ARGUMENT;
 	if (params->layer_budget < 1 || params->layer_budget > model->L) return SSLM_INVALID_ARGUMENT;
-	if (params->mode != SSLM_DECODE_MODE_GREEDY) return SSLM_INVALID_ARGUMENT;
+	// src/sslm_abi.cpp:2004-2035: the mode and, for damped greedy, alpha in [0, 2^20), anti-LM
+	// order >= 1, 1 <= top_k <= vocab, the artifact's constants, the top-k softmax width and a
+	// constructible i-exp peak
+	if (params->mode != SSLM_DECODE_MODE_GREEDY && params->mode != SSLM_DECODE_MODE_DAMPED_GREEDY)
+		return SSLM_INVALID_ARGUMENT;
+	if (params->mode == SSLM_DECODE_MODE_DAMPED_GREEDY) {
+		if (params->alpha_q15 < 0 || params->alpha_q15 >= (1 << 20) || params->anti_lm_max_order < 1 ||
+		    params->top_k < 1 || params->top_k > model->V)
+			return SSLM_INVALID_ARGUMENT;
+		if (!model->dg_available) return SSLM_ARTIFACT_REJECTED;
+		if (check_softmax_width(params->q_b, params->q_c, params->top_k) != kOk) return SSLM_INVALID_ARGUMENT;
+		if (params->q_ln2 < 1 || params->q_ln2 > kI64Max / 30) return SSLM_INVALID_ARGUMENT;  // the peak's construction
+	}
 	for (int32_t i = 0; i < n; ++i)
 		if (!seqs[i]) return SSLM_INVALID_ARGUMENT;
 	return guarded([&]() -> sslm_status {
@@ -1671,8 +1857,7 @@ static sslm_status decode_impl(sslm_model model, sslm_seq* seqs, int32_t n, cons
 			}
 			std::vector<int32_t> out(run.size(), -1);
 			bool stop_cap = false;
-			const sslm_status st = decode_batch(model, run.data(), (int32_t)run.size(), (uint32_t)params->layer_budget,
-			                                    out.data(), &stop_cap);
+			const sslm_status st = decode_batch(model, run.data(), (int32_t)run.size(), *params, out.data(), &stop_cap);
 			for (size_t k = 0; k < run.size(); ++k) out_tokens[idx[k]] = out[k];
 			if (st != SSLM_OK) return st;
 			if (stop_cap) return SSLM_CONTEXT_CAP_EXCEEDED;
@@ -1682,10 +1867,17 @@ static sslm_status decode_impl(sslm_model model, sslm_seq* seqs, int32_t n, cons
 	});
 }
 
+// src/sslm_abi.cpp:2436-2449: the v1.1 verb reads only the layer budget (its struct was one
+// int32_t) and decodes greedily; sslm_decode_step_v2 takes the whole struct.
 sslm_status sslm_decode_step(sslm_model model, sslm_seq* seqs, int32_t n, const sslm_decode_params* params,
                              sslm_workspace ws, int32_t* out_tokens) {
 	(void)ws;
-	return decode_impl(model, seqs, n, params, out_tokens);
+	if (!params) return SSLM_INVALID_ARGUMENT;
+	sslm_decode_params legacy{};
+	legacy.layer_budget = params->layer_budget;
+	legacy.struct_size = sizeof(legacy);
+	legacy.mode = SSLM_DECODE_MODE_GREEDY;
+	return decode_impl(model, seqs, n, &legacy, out_tokens);
 }
 
 sslm_status sslm_decode_step_v2(sslm_model model, sslm_seq* seqs, int32_t n, const sslm_decode_params* params,
@@ -1697,11 +1889,19 @@ sslm_status sslm_decode_step_v2(sslm_model model, sslm_seq* seqs, int32_t n, con
 sslm_status sslm_decode_params_init(sslm_model model, int32_t mode, int32_t layer_budget, sslm_decode_params* out) {
 	if (!model || !out || layer_budget < 1 || layer_budget > model->L) return SSLM_INVALID_ARGUMENT;
 	if (mode != SSLM_DECODE_MODE_GREEDY && mode != SSLM_DECODE_MODE_DAMPED_GREEDY) return SSLM_INVALID_ARGUMENT;
-	if (mode == SSLM_DECODE_MODE_DAMPED_GREEDY) return SSLM_ARTIFACT_REJECTED;  // no damped-greedy constants
 	sslm_decode_params p{};
 	p.layer_budget = layer_budget;
 	p.struct_size = sizeof(p);
 	p.mode = mode;
+	if (mode == SSLM_DECODE_MODE_DAMPED_GREEDY) {  // src/sslm_abi.cpp:2473-2484
+		if (!model->dg_available) return SSLM_ARTIFACT_REJECTED;
+		p.alpha_q15 = SSLM_DAMPED_GREEDY_DEFAULT_ALPHA_Q15;
+		p.anti_lm_max_order = SSLM_DAMPED_GREEDY_DEFAULT_ANTI_LM_ORDER;
+		p.top_k = std::min<int32_t>(SSLM_DAMPED_GREEDY_DEFAULT_TOP_K, model->V);
+		p.q_ln2 = model->dg_q_ln2;
+		p.q_b = model->dg_q_b;
+		p.q_c = model->dg_q_c;
+	}
 	*out = p;
 	return SSLM_OK;
 }
@@ -1741,7 +1941,7 @@ sslm_status sslm_seq_save(sslm_seq seq, void* buf, size_t* n) {
 	sslm_model m = seq->model;
 	const bool mid_token = seq->layer_index != 0;
 	const size_t residual = mid_token ? (size_t)m->H : 0;
-	const size_t history = seq->anti_lm_history.size();
+	const size_t history = seq->anti_lm.history.size();
 	if (seq->context_length < 0 || history > (size_t)seq->context_length) return SSLM_INVALID_ARGUMENT;
 	const size_t required = kBlobHeader + residual + 4 * history + 4 + seq->pool->block_size;
 	if (!buf || *n < required) {
@@ -1770,12 +1970,12 @@ sslm_status sslm_seq_save(sslm_seq seq, void* buf, size_t* n) {
 		put64(p + 84, (uint64_t)hs.e);
 		put64(p + 92, (uint64_t)sat);
 		put64(p + 100, (uint64_t)seq->forced_token_count);
-		put32(p + 108, (uint32_t)seq->anti_lm_order);
+		put32(p + 108, (uint32_t)seq->anti_lm.order);
 		put64(p + 112, (uint64_t)history);
 		size_t off = kBlobHeader;
 		if (residual) ck(hipMemcpy(p + off, m->stream_codes + (size_t)seq->slot * m->H, residual, hipMemcpyDeviceToHost));
 		off += residual;
-		for (size_t i = 0; i < history; ++i, off += 4) put32(p + off, (uint32_t)seq->anti_lm_history[i]);
+		for (size_t i = 0; i < history; ++i, off += 4) put32(p + off, (uint32_t)seq->anti_lm.history[i]);
 		put32(p + off, 1);  // KV block count
 		off += 4;
 		ck(hipMemcpy(p + off, seq->pool->dev + (size_t)seq->block * seq->pool->block_size, seq->pool->block_size,
@@ -2001,8 +2201,10 @@ sslm_status sslm_seq_restore(sslm_model model, sslm_kv_pool* pool, const void* b
 		s->layer_index = layer_index;
 		s->context_length = context_length;
 		s->forced_token_count = forced;
-		s->anti_lm_order = order;
-		for (uint64_t i = 0; i < history; ++i) s->anti_lm_history.push_back((int32_t)get32(history_ptr + 4 * i));
+		if (order > 0) {  // the counts are rebuilt by replaying the history (src/sslm_abi.cpp:2905-2925)
+			s->anti_lm.reset(order);
+			for (uint64_t i = 0; i < history; ++i) s->anti_lm.update((int32_t)get32(history_ptr + 4 * i));
+		}
 		if (current_token >= 0) {
 			s->current_token = current_token;
 			s->ready_for_logits = false;

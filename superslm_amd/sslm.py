@@ -88,6 +88,7 @@ class SslmLib:
         sig("sslm_seq_reset", ctypes.c_int, vp)
         sig("sslm_prefill", ctypes.c_int, vp, vp, pi32, i32, i32, ctypes.c_int, vp, pi32)
         sig("sslm_decode_step", ctypes.c_int, vp, pvp, i32, ctypes.POINTER(DecodeParams), vp, pi32)
+        sig("sslm_decode_step_v2", ctypes.c_int, vp, pvp, i32, ctypes.POINTER(DecodeParams), vp, pi32)
         sig("sslm_decode_params_init", ctypes.c_int, vp, i32, i32, ctypes.POINTER(DecodeParams))
         sig("sslm_seq_set_adapter", ctypes.c_int, vp, vp)
         sig("sslm_adapter_map", ctypes.c_int, vp, sz, vp, pvp)
@@ -123,18 +124,25 @@ class Model:
     def pool(self, blocks: int) -> "KvPool":
         return KvPool(self, blocks)
 
-    def decode_params(self, layer_budget: int) -> DecodeParams:
+    def decode_params(self, layer_budget: int, mode: int = 0, raw: bool = False):
+        """sslm_decode_params_init (mode 0 greedy, 1 damped greedy); with `raw` the status too."""
         p = DecodeParams()
-        self.lib.check("sslm_decode_params_init",
-                       self.lib.lib.sslm_decode_params_init(self.handle, 0, layer_budget, ctypes.byref(p)))
+        st = self.lib.lib.sslm_decode_params_init(self.handle, mode, layer_budget, ctypes.byref(p))
+        if raw:
+            return st, p
+        self.lib.check("sslm_decode_params_init", st)
         return p
 
-    def decode_step(self, seqs, layer_budget: int, raw: bool = False):
+    def decode_step(self, seqs, layer_budget: int, raw: bool = False, params: DecodeParams | None = None,
+                    v2: bool = False):
+        """One sslm_decode_step, or sslm_decode_step_v2 when `params` (or `v2`) is given."""
         n = len(seqs)
         arr = (ctypes.c_void_p * n)(*[s.handle.value for s in seqs])
         out = (ctypes.c_int32 * n)()
-        p = self.decode_params(layer_budget)
-        st = self.lib.lib.sslm_decode_step(self.handle, arr, n, ctypes.byref(p), None, out)
+        p = params if params is not None else self.decode_params(layer_budget)
+        # sslm_decode_step_v2 reads the whole struct (the v1 verb reads only layer_budget)
+        verb = self.lib.lib.sslm_decode_step_v2 if v2 or params is not None else self.lib.lib.sslm_decode_step
+        st = verb(self.handle, arr, n, ctypes.byref(p), None, out)
         if raw:
             return st, list(out)
         self.lib.check("sslm_decode_step", st)

@@ -33,6 +33,7 @@ SEC_KV_LANDING_RECIPROCALS = 9
 SEC_SIGMOID_LUT = 12
 SEC_DELTA_FOLD = 40
 SEC_U_FOLD = 41
+SEC_DAMPED_GREEDY = 42
 
 DT_RAW, DT_I8, DT_I32, DT_I64 = 0, 1, 2, 3
 _DT_SIZE = {DT_RAW: 1, DT_I8: 1, DT_I32: 4, DT_I64: 8}
@@ -280,6 +281,9 @@ class SyntheticModel:
 
     image: np.ndarray = None
     rng: object = None
+    # damped-greedy logit scale (m, e): written as a DampedGreedyConstants section with header
+    # flag bit 1 (src/damped_greedy_phaseD.cpp: 12 raw bytes, int64 m then int32 e)
+    damped: tuple = None
 
     def to_bytes(self) -> bytes:
         return bytes(self.to_array())
@@ -312,7 +316,11 @@ class SyntheticModel:
         ]
         if self.biases:
             sections.append((SEC_BIASES, DT_I64, Manifest(b"BIA1", 8, list(self.biases.items())), 64))
-        img = write_container_array(sections)
+        flags = 0
+        if self.damped is not None:
+            sections.append((SEC_DAMPED_GREEDY, DT_RAW, struct.pack("<qi", *self.damped), 8))
+            flags |= 2
+        img = write_container_array(sections, flags)
         base = int.from_bytes(img[HEADER_BYTES + SECTION_DESC_BYTES + 8:HEADER_BYTES + SECTION_DESC_BYTES + 16].tobytes(),
                               "little")  # offset of the Weights section (second in the table)
         self.weights.update(wgt.views(img, base))
@@ -331,7 +339,8 @@ def _codes(rng, shape):
     return RandI8(shape)
 
 
-def build_synthetic(cfg: ModelConfig, seed: int = 1234, temperature: float = 1.0) -> SyntheticModel:
+def build_synthetic(cfg: ModelConfig, seed: int = 1234, temperature: float = 1.0,
+                    damped_logit_scale: float | None = None) -> SyntheticModel:
     """Seeded synthetic integer model whose constants follow one real-scale model.
 
     Real value of a code = code * (m * 2^e).  Each projection's WSC1 fold F = acc * mult / 2^(31+s)
@@ -339,10 +348,13 @@ def build_synthetic(cfg: ModelConfig, seed: int = 1234, temperature: float = 1.0
     spread act as per-channel weight-scale variation), so the projection site constant is c_f/127;
     norms use g_s / (2^16 * 127); residuals 1/127; the SiLU product 2^-15/127 (it already carries
     both incoming scales).  K/V land at a fixed code scale, and softmax_khead folds the k code
-    scale with 1/sqrt(head_dim) so the derived i-exp q_ln2 sits near 5e4 score units."""
+    scale with 1/sqrt(head_dim) so the derived i-exp q_ln2 sits near 5e4 score units.
+    `damped_logit_scale` (the real value of one logit unit) adds the damped-greedy constants."""
     rng = np.random.Generator(np.random.PCG64(seed))
     c = cfg
     m = SyntheticModel(config=c)
+    if damped_logit_scale is not None:
+        m.damped = scale_me(damped_logit_scale)
     H, I, D, NH, NKV = c.hidden, c.inter, c.head_dim, c.heads, c.kv_heads
     KVH = NKV * D
     g_s = 1.0 / 127.0
