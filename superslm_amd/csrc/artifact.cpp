@@ -320,6 +320,10 @@ bool parse_artifact(const uint8_t* data, size_t size, Artifact* out, std::string
 				out->provenance = b;
 				out->provenance_bytes = p.size;
 				break;
+			case kSchemaMasks:
+				out->schemas = b;
+				out->schemas_bytes = p.size;
+				break;
 			case kDampedGreedy:
 				out->damped = b;
 				out->damped_bytes = p.size;

@@ -37,6 +37,9 @@ struct Artifact {
 	std::vector<int32_t> sigmoid_lut;
 	const uint8_t* provenance = nullptr;
 	uint64_t provenance_bytes = 0;
+	// SchemaMasks (SCM1) section, parsed by the runtime
+	const uint8_t* schemas = nullptr;
+	uint64_t schemas_bytes = 0;
 	// DampedGreedyConstants section (raw bytes; read only when header flag bit 1 is set)
 	const uint8_t* damped = nullptr;
 	uint64_t damped_bytes = 0;

@@ -197,37 +197,6 @@ struct Track {
 	hipEvent_t fork = nullptr;
 };
 
-struct sslm_model_s {
-	Artifact art;
-	ModelConfig c;
-	int H, L, NH, NKV, D, I, V, KVH;
-	int64_t cap;
-	size_t block_bytes;
-	std::vector<void*> owned;
-	std::vector<DevLayer> layers;
-	int8_t *embed, *head;
-	int32_t *final_gain, *silu;
-	int64_t *rope_cos, *rope_sin;
-	Scale embed_site, final_site;
-	int64_t ln2_q, b_q, ca_q;
-	// damped greedy: i-exp triple of the artifact's logit scale (src/sslm_abi.cpp:1172-1185)
-	bool dg_available = false;
-	int64_t dg_q_ln2 = 0, dg_q_b = 0, dg_q_c = 0;
-	int32_t* logits = nullptr;  // [kMaxTokens, V] raw head rows, allocated on first damped use
-	// per-slot sequence state
-	int8_t* stream_codes;   // [kSlotCapacity, H]
-	Scale* stream_scale;    // [kSlotCapacity]
-	unsigned long long* sat;  // [kSlotCapacity]
-	int32_t* status;        // [kSlotCapacity]
-	int32_t* head_status;   // [kSlotCapacity] attention-stage refusals awaiting the ctx funnel
-	std::vector<int> free_slots;
-	std::vector<Track> tracks;  // tracks[0]: prefill and head; all: decode token groups
-	std::map<std::string, hipGraphExec_t> graphs;  // captured decode submissions by shape
-	int8_t* pool_dev = nullptr;  // KV pool of the launch sequence being recorded
-	std::atomic<int> live_refs{0};
-	std::mutex mu;  // serializes GPU submission on this model
-};
-
 // Damped-greedy anti-LM (src/damped_greedy_antilm.cpp): for each order n in 1..max_order, the
 // counts of tokens that followed each (n-1)-token context of the generated history, and the
 // history itself.  Only lookups by context are made, so an ordered map serves (no iteration
@@ -301,6 +270,59 @@ struct AntiLm {
 	}
 };
 
+// SCM1 schema masks (include/superslm/schema_masks.h): per schema a DFA over token ids -- one
+// vocabulary bitmask page per state (bit t set iff the state has a transition on token t), the
+// CSR transition rows (token ascending) and the sorted accepting set.  The tables point into the
+// artifact bytes, which outlive the model.
+struct SchemaEntry {
+	std::string name;
+	uint64_t name_hash = 0;  // FNV-1a 64 of the name
+	uint32_t states = 0, accepting_count = 0, transitions = 0;
+	const uint8_t* pages = nullptr;    // states x page_bytes
+	const uint8_t* offsets = nullptr;  // states + 1 LE u32
+	const uint8_t* accepting = nullptr;
+	const uint8_t* trans = nullptr;    // (token, next) LE u32 pairs
+};
+
+struct sslm_schema_s {
+	sslm_model model = nullptr;
+	uint32_t index = 0;
+};
+
+struct sslm_model_s {
+	Artifact art;
+	ModelConfig c;
+	int H, L, NH, NKV, D, I, V, KVH;
+	int64_t cap;
+	size_t block_bytes;
+	std::vector<void*> owned;
+	std::vector<DevLayer> layers;
+	int8_t *embed, *head;
+	int32_t *final_gain, *silu;
+	int64_t *rope_cos, *rope_sin;
+	Scale embed_site, final_site;
+	int64_t ln2_q, b_q, ca_q;
+	// damped greedy: i-exp triple of the artifact's logit scale (src/sslm_abi.cpp:1172-1185)
+	bool dg_available = false;
+	int64_t dg_q_ln2 = 0, dg_q_b = 0, dg_q_c = 0;
+	int32_t* logits = nullptr;  // [kMaxTokens, V] raw head rows, allocated on first use
+	std::vector<SchemaEntry> schemas;
+	std::vector<sslm_schema_s> schema_handles;
+	uint32_t page_bytes = 0;  // (V + 7) / 8
+	// per-slot sequence state
+	int8_t* stream_codes;   // [kSlotCapacity, H]
+	Scale* stream_scale;    // [kSlotCapacity]
+	unsigned long long* sat;  // [kSlotCapacity]
+	int32_t* status;        // [kSlotCapacity]
+	int32_t* head_status;   // [kSlotCapacity] attention-stage refusals awaiting the ctx funnel
+	std::vector<int> free_slots;
+	std::vector<Track> tracks;  // tracks[0]: prefill and head; all: decode token groups
+	std::map<std::string, hipGraphExec_t> graphs;  // captured decode submissions by shape
+	int8_t* pool_dev = nullptr;  // KV pool of the launch sequence being recorded
+	std::atomic<int> live_refs{0};
+	std::mutex mu;  // serializes GPU submission on this model
+};
+
 struct sslm_kv_pool_s {
 	sslm_model model = nullptr;
 	void* buf = nullptr;
@@ -325,6 +347,8 @@ struct sslm_seq_s {
 	sslm_adapter adapter = nullptr;
 	int64_t forced_token_count = 0;
 	AntiLm anti_lm;  // damped-greedy n-gram state (order 0: none)
+	sslm_schema schema = nullptr;       // bound schema
+	uint32_t walk = 0xFFFFFFFFu;        // DFA walk state (0xFFFFFFFF: no schema bound)
 	std::mutex mu;
 };
 
@@ -360,6 +384,129 @@ uint64_t get64(const uint8_t* p) {
 	uint64_t v = 0;
 	for (int i = 0; i < 8; ++i) v |= (uint64_t)p[i] << (8 * i);
 	return v;
+}
+
+uint64_t fnv1a64(const char* p, size_t n) {
+	uint64_t h = 14695981039346656037ull;
+	for (size_t i = 0; i < n; ++i) {
+		h ^= (uint8_t)p[i];
+		h *= 1099511628211ull;
+	}
+	return h;
+}
+
+// SchemaMasksTable::Parse (include/superslm/schema_masks.h): 24-byte header ("SCM1", version 1,
+// schema count in [1, 65536], vocab = the config's, name blob length, reserved 0), 56-byte
+// descriptors, the name blob, then per schema four non-overlapping blocks after the manifest
+// (mask pages, state offsets, accepting set, transitions) with: offsets[0] = 0, nondecreasing,
+// offsets[states] = transitions; accepting strictly ascending below `states`; each CSR row's
+// tokens strictly ascending, tokens < vocab, next states < states; and every mask bit equal to
+// the existence of the transition.  Returns false on any violation.
+bool parse_schemas(const uint8_t* d, uint64_t size, uint32_t vocab, std::vector<SchemaEntry>* out) {
+	out->clear();
+	if (size < 24 || memcmp(d, "SCM1", 4) != 0 || get32(d + 4) != 1) return false;
+	const uint32_t count = get32(d + 8), v = get32(d + 12), blob = get32(d + 16);
+	if (get32(d + 20) != 0 || count == 0 || count > 65536 || v == 0 || v != vocab) return false;
+	const uint64_t manifest_end = 24 + (uint64_t)count * 56 + blob;
+	if (manifest_end > size) return false;
+	const uint64_t blob_off = manifest_end - blob, page = ((uint64_t)v + 7) / 8;
+	struct Span {
+		uint64_t off, len;
+	};
+	std::vector<Span> used;
+	auto overlaps = [](const Span& a, const Span& b) { return a.off < b.off + b.len && b.off < a.off + a.len; };
+	for (uint32_t i = 0; i < count; ++i) {
+		const uint8_t* e = d + 24 + (uint64_t)i * 56;
+		const uint32_t name_off = get32(e), name_len = get32(e + 4), states = get32(e + 8), acc = get32(e + 12),
+		               trans = get32(e + 16);
+		if (get32(e + 20) != 0) return false;
+		if (name_len == 0 || (uint64_t)name_off + name_len > blob) return false;
+		SchemaEntry se;
+		se.name.assign((const char*)d + blob_off + name_off, name_len);
+		for (auto& o : *out)
+			if (o.name == se.name) return false;
+		if (states == 0 || states > 1048576 || acc > states || trans > 16777216) return false;
+		const Span blocks[4] = {{get64(e + 24), (uint64_t)states * page},
+		                        {get64(e + 32), ((uint64_t)states + 1) * 4},
+		                        {get64(e + 40), (uint64_t)acc * 4},
+		                        {get64(e + 48), (uint64_t)trans * 8}};
+		for (const Span& b : blocks)
+			if (b.off > UINT64_MAX - b.len || b.off < manifest_end || b.off + b.len > size) return false;
+		for (const Span& b : blocks)
+			for (const Span& u : used)
+				if (overlaps(b, u)) return false;
+		for (int a = 0; a < 4; ++a)
+			for (int b = a + 1; b < 4; ++b)
+				if (overlaps(blocks[a], blocks[b])) return false;
+		for (const Span& b : blocks) used.push_back(b);
+		const uint8_t* offs = d + blocks[1].off;
+		if (get32(offs) != 0 || get32(offs + (size_t)states * 4) != trans) return false;
+		for (uint32_t st = 0; st < states; ++st)
+			if (get32(offs + (size_t)st * 4) > get32(offs + (size_t)(st + 1) * 4)) return false;
+		const uint8_t* accp = d + blocks[2].off;
+		for (uint32_t a = 0; a < acc; ++a) {
+			const uint32_t x = get32(accp + (size_t)a * 4);
+			if (x >= states || (a > 0 && x <= get32(accp + (size_t)(a - 1) * 4))) return false;
+		}
+		const uint8_t* tr = d + blocks[3].off;
+		const uint8_t* pages = d + blocks[0].off;
+		for (uint32_t st = 0; st < states; ++st) {
+			const uint32_t r0 = get32(offs + (size_t)st * 4), r1 = get32(offs + (size_t)(st + 1) * 4);
+			for (uint32_t k = r0; k < r1; ++k) {
+				const uint32_t tok = get32(tr + (size_t)k * 8), nx = get32(tr + (size_t)k * 8 + 4);
+				if (tok >= v || nx >= states || (k > r0 && tok <= get32(tr + (size_t)(k - 1) * 8))) return false;
+			}
+			const uint8_t* pg = pages + (size_t)st * page;
+			uint32_t cur = r0;
+			for (uint32_t t = 0; t < v; ++t) {
+				const bool bit = (pg[t >> 3] >> (t & 7)) & 1u;
+				bool in_row = false;
+				if (cur < r1 && get32(tr + (size_t)cur * 8) == t) {
+					in_row = true;
+					++cur;
+				}
+				if (bit != in_row) return false;
+			}
+		}
+		se.name_hash = fnv1a64(se.name.data(), se.name.size());
+		se.states = states;
+		se.accepting_count = acc;
+		se.transitions = trans;
+		se.pages = pages;
+		se.offsets = offs;
+		se.accepting = accp;
+		se.trans = tr;
+		out->push_back(std::move(se));
+	}
+	return true;
+}
+
+// SchemaMasksTable::Transition: binary search of state's CSR row
+bool schema_next(const SchemaEntry& e, uint32_t state, uint32_t token, uint32_t* next) {
+	uint32_t lo = get32(e.offsets + (size_t)state * 4), hi = get32(e.offsets + (size_t)(state + 1) * 4);
+	while (lo < hi) {
+		const uint32_t mid = lo + (hi - lo) / 2;
+		const uint32_t t = get32(e.trans + (size_t)mid * 8);
+		if (t == token) {
+			*next = get32(e.trans + (size_t)mid * 8 + 4);
+			return true;
+		}
+		if (t < token) lo = mid + 1;
+		else hi = mid;
+	}
+	return false;
+}
+
+bool schema_accepting(const SchemaEntry& e, uint32_t state) {  // src/sslm_abi.cpp:2488-2503
+	uint32_t lo = 0, hi = e.accepting_count;
+	while (lo < hi) {
+		const uint32_t mid = lo + (hi - lo) / 2;
+		const uint32_t v = get32(e.accepting + (size_t)mid * 4);
+		if (v == state) return true;
+		if (v < state) lo = mid + 1;
+		else hi = mid;
+	}
+	return false;
 }
 
 // ------------------------------------------------------------------------------------------
@@ -829,16 +976,23 @@ void run_logits(sslm_model m, Track& w, int M, StreamRef st, const TokenInfo* to
 	ck(hipGetLastError());
 }
 
-// Damped-greedy selection over one logit row (src/damped_greedy_topk.cpp:1-461, free text: every
-// token legal).  Top-k by (logit desc, index asc); q_theta = the k i-exp values renormalized to
+// Damped-greedy selection over one logit row (src/damped_greedy_topk.cpp:1-461); `page` is the
+// bound schema's mask page (masked logits already INT32_MIN), null for free text.  Top-k by (logit desc, index asc); q_theta = the k i-exp values renormalized to
 // Q15 (TopKRenormalizeQ15: each against the row-max peak, refused when any is out of domain);
 // p_omega from the anti-LM; winner = max of q_theta - (alpha * p_omega >> 15), lowest index on
 // ties.  Returns false when refused.
-bool damped_pick(const int32_t* row, int V, const sslm_decode_params& p, const AntiLm& lm, int32_t* token) {
+bool damped_pick(const int32_t* row, int V, const sslm_decode_params& p, const AntiLm& lm, const uint8_t* page,
+                 int32_t* token) {
 	const int k = p.top_k;
+	auto legal = [&](int32_t t) { return !page || ((page[t >> 3] >> (t & 7)) & 1u); };
 	std::vector<int32_t> idx(V);
 	for (int i = 0; i < V; ++i) idx[i] = i;
-	auto before = [&](int32_t a, int32_t b) { return row[a] != row[b] ? row[a] > row[b] : a < b; };
+	// FsdTopK order: logit desc, then legal before masked, then index asc
+	auto before = [&](int32_t a, int32_t b) {
+		if (row[a] != row[b]) return row[a] > row[b];
+		if (legal(a) != legal(b)) return legal(a);
+		return a < b;
+	};
 	std::partial_sort(idx.begin(), idx.begin() + k, idx.end(), before);
 	if (check_softmax_width(p.q_b, p.q_c, k) != kOk) return false;
 	int64_t row_max = row[idx[0]];
@@ -865,7 +1019,7 @@ bool damped_pick(const int32_t* row, int V, const sslm_decode_params& p, const A
 	int64_t best = 0;
 	int32_t best_tok = -1;
 	for (int i = 0; i < k; ++i) {
-		const int64_t score = q[i] - (int32_t)(((int64_t)p.alpha_q15 * omega[i]) >> 15);
+		const int64_t score = legal(idx[i]) ? q[i] - (int32_t)(((int64_t)p.alpha_q15 * omega[i]) >> 15) : kI64Min;
 		if (best_tok < 0 || score > best || (score == best && idx[i] < best_tok)) {
 			best = score;
 			best_tok = idx[i];
@@ -1184,6 +1338,15 @@ bool build_device_model(sslm_model m, std::string* err) {
 		m->dg_q_b = qb;
 		m->dg_q_c = qc;
 	}
+	m->page_bytes = (uint32_t)((m->V + 7) / 8);
+	if (A.schemas) {  // src/sslm_abi.cpp:1193-1215
+		if (!parse_schemas(A.schemas, A.schemas_bytes, (uint32_t)m->V, &m->schemas)) {
+			*err = "SchemaMasks section rejected";
+			return false;
+		}
+		m->schema_handles.resize(m->schemas.size());
+		for (size_t i = 0; i < m->schemas.size(); ++i) m->schema_handles[i] = sslm_schema_s{m, (uint32_t)i};
+	}
 	// slots
 	m->stream_codes = dalloc<int8_t>((size_t)kSlotCapacity * H, &own);
 	m->stream_scale = dalloc<Scale>(kSlotCapacity, &own);
@@ -1468,6 +1631,7 @@ sslm_status sslm_seq_reset(sslm_seq seq) {
 		seq->ready_for_logits = false;
 		seq->forced_token_count = 0;
 		seq->anti_lm.reset(0);
+		seq->walk = seq->schema ? 0u : kWalkUnused;
 		return SSLM_OK;
 	});
 }
@@ -1479,7 +1643,7 @@ sslm_status sslm_prefill(sslm_model model, sslm_seq seq, const int32_t* tokens, 
 	*consumed = 0;
 	if (!model || !seq) return SSLM_INVALID_ARGUMENT;
 	if (count < 0 || chunk_budget < 1 || (count > 0 && !tokens)) return SSLM_INVALID_ARGUMENT;
-	if (kind == SSLM_SPAN_SCHEMA_CONTENT) return SSLM_SCHEMA_SPAN_UNBOUND;  // no schema can be bound
+	if (kind == SSLM_SPAN_SCHEMA_CONTENT && !seq->schema) return SSLM_SCHEMA_SPAN_UNBOUND;
 	if (seq->model != model) return SSLM_INVALID_ARGUMENT;
 	return guarded([&]() -> sslm_status {
 		std::lock_guard<std::mutex> lk(model->mu);
@@ -1495,12 +1659,36 @@ sslm_status sslm_prefill(sslm_model model, sslm_seq seq, const int32_t* tokens, 
 			}
 		const int64_t head = model->cap - seq->context_length;
 		const int32_t admit_cap = head <= 0 ? 0 : (head >= n ? n : (int32_t)head);
-		const int32_t admit = std::min(admit_id, admit_cap);
+		const int32_t admit_idcap = std::min(admit_id, admit_cap);
+		// a schema-content span walks the bound schema's DFA; the first token without a
+		// transition ends the admitted prefix (src/sslm_abi.cpp:1480-1510)
+		const SchemaEntry* se = kind == SSLM_SPAN_SCHEMA_CONTENT ? &model->schemas[seq->schema->index] : nullptr;
+		int32_t admit = admit_idcap;
+		uint32_t walk_after = seq->walk;
+		if (se) {
+			uint32_t w = seq->walk;
+			for (int32_t i = 0; i < admit_idcap; ++i) {
+				uint32_t nx = 0;
+				if (!schema_next(*se, w, (uint32_t)tokens[i], &nx)) {
+					admit = i;
+					break;
+				}
+				w = nx;
+			}
+			walk_after = w;
+		}
 		sslm_status stop = SSLM_OK;
-		if (admit < n) stop = admit_id <= admit_cap ? SSLM_TOKEN_ID_OUT_OF_RANGE : SSLM_CONTEXT_CAP_EXCEEDED;
+		if (admit < n) {
+			if (admit < admit_idcap) stop = SSLM_SCHEMA_SPAN_UNREACHABLE;
+			else stop = admit_id <= admit_cap ? SSLM_TOKEN_ID_OUT_OF_RANGE : SSLM_CONTEXT_CAP_EXCEEDED;
+		}
 		if (admit > 0) {
 			const sslm_status st = prefill_tokens(model, seq, tokens, admit);
 			if (st != SSLM_OK) return st;
+			if (se) {
+				seq->walk = walk_after;
+				seq->forced_token_count += admit;
+			}
 			seq->current_token = tokens[admit - 1];
 			*consumed = admit;
 			seq->ready_for_logits = true;  // src/sslm_abi.cpp:1969-1972
@@ -1541,10 +1729,9 @@ int track_min() {
 }
 
 static sslm_status decode_batch(sslm_model m, sslm_seq* seqs, int32_t n, const sslm_decode_params& params,
-                                int32_t* out_tokens, bool* stop_cap) {
+                                int32_t* out_tokens, sslm_status* stop) {
 	const uint32_t budget = (uint32_t)params.layer_budget;
 	const bool damped = params.mode == SSLM_DECODE_MODE_DAMPED_GREEDY;
-	if (damped && !m->logits) m->logits = dalloc<int32_t>((size_t)kMaxTokens * m->V, &m->owned);
 	// Partition: sequences needing layers, grouped by their current layer; sequences needing logits.
 	std::vector<int> need_logits;
 	std::vector<std::pair<uint32_t, std::vector<int>>> groups;
@@ -1555,8 +1742,16 @@ static sslm_status decode_batch(sslm_model m, sslm_seq* seqs, int32_t n, const s
 			continue;
 		}
 		if (s->layer_index == 0 && s->context_length >= m->cap) {  // src/sslm_abi.cpp:2233-2236
-			*stop_cap = true;
+			*stop = SSLM_CONTEXT_CAP_EXCEEDED;
 			out_tokens[i] = -1;
+			n = i;
+			break;
+		}
+		if (s->layer_index >= (uint32_t)m->L) {
+			// a whole token whose schema walk had no transition (-2) rests at the last layer; the
+			// reference's layer loop then refuses the next call (its layer_index < L guard), mapped
+			// to SSLM_ARTIFACT_REJECTED, after the sequences before it in the call
+			*stop = SSLM_ARTIFACT_REJECTED;
 			n = i;
 			break;
 		}
@@ -1598,6 +1793,10 @@ static sslm_status decode_batch(sslm_model m, sslm_seq* seqs, int32_t n, const s
 	}
 	std::vector<int> lg = need_logits;
 	lg.insert(lg.end(), finished.begin(), finished.end());
+	// whole logit rows come back to the host for damped greedy and for schema-masked argmax
+	bool rows_needed = damped;
+	for (int i : lg) rows_needed = rows_needed || seqs[i]->schema;
+	if (rows_needed && !m->logits) m->logits = dalloc<int32_t>((size_t)kMaxTokens * m->V, &m->owned);
 
 	// Host staging, uploaded before the kernels (kept alive until the sync below).  The common
 	// shape -- at most one unit per track and one head chunk -- stages every unit's tokens in its
@@ -1656,14 +1855,14 @@ static sslm_status decode_batch(sslm_model m, sslm_seq* seqs, int32_t n, const s
 	};
 	auto launch_logits = [&](int M) {
 		run_logits(m, t0, M, StreamRef{m->stream_codes, m->stream_scale, t0.lg_slot}, t0.lg_tok);
-		if (damped) {  // the whole logit rows as well: the head's raw int32 accumulators
+		if (rows_needed) {  // the whole logit rows as well: the head's raw int32 accumulators
 			GemmArgs g = head_args(m, t0, M, t0.lg_tok);
 			g.epi.argmax_key = nullptr;
 			g.epi.raw_out = m->logits;
 			run_gemm(m, t0, g, kProfHead);
 		}
 	};
-	std::vector<int32_t> rows(damped ? lg.size() * (size_t)m->V : 0);
+	std::vector<int32_t> rows(rows_needed ? lg.size() * (size_t)m->V : 0);
 	// every sequence of one call shares the pool of the first (checked by the caller)
 	m->pool_dev = seqs[0]->pool->dev;
 	std::vector<int32_t> toks(lg.size());
@@ -1713,12 +1912,12 @@ static sslm_status decode_batch(sslm_model m, sslm_seq* seqs, int32_t n, const s
 		if (!lg.empty()) {
 			const int M = (int)lg.size();
 			if (use_graph)
-				ck(hipGraphLaunch(graph_of("lg|" + std::to_string(M) + (damped ? "|d" : ""), t0.stream, [&] { launch_logits(M); }),
+				ck(hipGraphLaunch(graph_of("lg|" + std::to_string(M) + (rows_needed ? "|r" : ""), t0.stream, [&] { launch_logits(M); }),
 				                  t0.stream));
 			else launch_logits(M);
 		}
 		if (!lg.empty()) ck(hipMemcpyAsync(toks.data(), t0.out_tokens, lg.size() * 4, hipMemcpyDeviceToHost, t0.stream));
-		if (damped && !lg.empty())
+		if (rows_needed && !lg.empty())
 			ck(hipMemcpyAsync(rows.data(), m->logits, rows.size() * 4, hipMemcpyDeviceToHost, t0.stream));
 	} else {
 		std::vector<bool> used(ntr, false);
@@ -1737,7 +1936,7 @@ static sslm_status decode_batch(sslm_model m, sslm_seq* seqs, int32_t n, const s
 			stage_logits(b, M, t0.stream);
 			launch_logits(M);
 			ck(hipMemcpyAsync(toks.data() + b, t0.out_tokens, M * 4, hipMemcpyDeviceToHost, t0.stream));
-			if (damped)
+			if (rows_needed)
 				ck(hipMemcpyAsync(rows.data() + b * (size_t)m->V, m->logits, (size_t)M * m->V * 4, hipMemcpyDeviceToHost,
 				                  t0.stream));
 		}
@@ -1785,16 +1984,34 @@ static sslm_status decode_batch(sslm_model m, sslm_seq* seqs, int32_t n, const s
 			continue;
 		}
 		int32_t tok = toks[k];
+		const SchemaEntry* se = s->schema ? &m->schemas[s->schema->index] : nullptr;
+		const uint8_t* page = se ? se->pages + (size_t)s->walk * m->page_bytes : nullptr;
+		int32_t* row = rows_needed ? rows.data() + k * (size_t)m->V : nullptr;
+		if (se)  // the mask first: masked logits become INT32_MIN (forward_sites.cpp:2443-2449)
+			for (int t = 0; t < m->V; ++t)
+				if (!((page[t >> 3] >> (t & 7)) & 1u)) row[t] = INT32_MIN;
 		if (damped) {  // src/sslm_abi.cpp:2301-2384
 			if (s->anti_lm.order == 0 || s->anti_lm.order != params.anti_lm_max_order)
 				s->anti_lm.reset(params.anti_lm_max_order);
-			if (!damped_pick(rows.data() + k * (size_t)m->V, m->V, params, s->anti_lm, &tok)) {
+			if (!damped_pick(row, m->V, params, s->anti_lm, page, &tok)) {
 				out_tokens[i] = -1;  // refused: no token this call; the sequence keeps its layer index
 				if (first_err == SSLM_OK) first_err = map_forward_status(kSoftmaxKernelRefusedAfterGateAccepted);
 				continue;
 			}
-			s->anti_lm.update(tok);
+		} else if (se) {  // masked argmax, lowest index on ties
+			tok = 0;
+			for (int t = 1; t < m->V; ++t)
+				if (row[t] > row[tok]) tok = t;
 		}
+		if (se) {  // the walk advances only along an existing transition; none is a dead end (-2)
+			uint32_t nx = 0;
+			if (!schema_next(*se, s->walk, (uint32_t)tok, &nx)) {
+				out_tokens[i] = -2;
+				continue;
+			}
+			s->walk = nx;
+		}
+		if (damped) s->anti_lm.update(tok);
 		s->current_token = tok;
 		s->layer_index = 0;
 		out_tokens[i] = tok;
@@ -1855,12 +2072,15 @@ static sslm_status decode_impl(sslm_model model, sslm_seq* seqs, int32_t n, cons
 				idx.push_back(j);
 				++j;
 			}
-			std::vector<int32_t> out(run.size(), -1);
-			bool stop_cap = false;
-			const sslm_status st = decode_batch(model, run.data(), (int32_t)run.size(), *params, out.data(), &stop_cap);
-			for (size_t k = 0; k < run.size(); ++k) out_tokens[idx[k]] = out[k];
+			// entries the call never reaches keep the caller's values, as in the reference
+			constexpr int32_t kUntouched = INT32_MIN;
+			std::vector<int32_t> out(run.size(), kUntouched);
+			sslm_status stop = SSLM_OK;
+			const sslm_status st = decode_batch(model, run.data(), (int32_t)run.size(), *params, out.data(), &stop);
+			for (size_t k = 0; k < run.size(); ++k)
+				if (out[k] != kUntouched) out_tokens[idx[k]] = out[k];
 			if (st != SSLM_OK) return st;
-			if (stop_cap) return SSLM_CONTEXT_CAP_EXCEEDED;
+			if (stop != SSLM_OK) return stop;
 			i = j;
 		}
 		return SSLM_OK;
@@ -1914,6 +2134,7 @@ sslm_status sslm_stats(sslm_model model, sslm_seq seq, sslm_stats_out* out) {
 	out->decode_step_actual = model->L;
 	out->forced_token_count = seq->forced_token_count;
 	out->kv_blocks_resident = 1;
+	out->schema_accepting = seq->schema && schema_accepting(model->schemas[seq->schema->index], seq->walk) ? 1 : 0;
 	return SSLM_OK;
 }
 
@@ -1959,8 +2180,8 @@ sslm_status sslm_seq_save(sslm_seq seq, void* buf, size_t* n) {
 		memcpy(p, kBlobMagic, 4);
 		memcpy(p + 4, m->art.hash, 32);
 		put32(p + 36, m->c.kv_precision);
-		put64(p + 40, 0);             // schema name hash: no schema bound
-		put32(p + 48, kWalkUnused);   // DFA walk state
+		put64(p + 40, seq->schema ? m->schemas[seq->schema->index].name_hash : 0);  // 0: no schema bound
+		put32(p + 48, seq->walk);                                                     // DFA walk state
 		put64(p + 52, 0);             // adapter binding id (the reference always writes 0)
 		put64(p + 60, (uint64_t)seq->context_length);
 		put32(p + 68, seq->layer_index);
@@ -2143,8 +2364,18 @@ sslm_status sslm_seq_restore(sslm_model model, sslm_kv_pool* pool, const void* b
 	if (n < header + 4) return SSLM_INVALID_ARGUMENT;
 	if (memcmp(p + 4, model->art.hash, 32) != 0) return SSLM_RESTORE_MODEL_MISMATCH;
 	if (get32(p + 36) != model->c.kv_precision) return SSLM_RESTORE_KV_MISMATCH;
-	if (get64(p + 40) != 0) return SSLM_RESTORE_SCHEMA_MISMATCH;
-	if (get32(p + 48) != kWalkUnused) return SSLM_RESTORE_SCHEMA_MISMATCH;
+	// the schema binding resolves by name hash against this model's schemas, its walk state
+	// inside the schema (src/sslm_abi.cpp:2755-2800)
+	const uint64_t schema_hash = get64(p + 40);
+	const uint32_t walk = get32(p + 48);
+	sslm_schema schema = nullptr;
+	if (schema_hash != 0) {
+		for (size_t i = 0; i < model->schemas.size() && !schema; ++i)
+			if (model->schemas[i].name_hash == schema_hash) schema = &model->schema_handles[i];
+		if (!schema || walk >= model->schemas[schema->index].states) return SSLM_RESTORE_SCHEMA_MISMATCH;
+	} else if (walk != kWalkUnused) {
+		return SSLM_RESTORE_SCHEMA_MISMATCH;
+	}
 	const int64_t context_length = (int64_t)get64(p + 60);
 	const uint32_t layer_index = get32(p + 68);
 	const int32_t current_token = (int32_t)get32(p + 72);
@@ -2201,6 +2432,8 @@ sslm_status sslm_seq_restore(sslm_model model, sslm_kv_pool* pool, const void* b
 		s->layer_index = layer_index;
 		s->context_length = context_length;
 		s->forced_token_count = forced;
+		s->schema = schema;
+		s->walk = walk;
 		if (order > 0) {  // the counts are rebuilt by replaying the history (src/sslm_abi.cpp:2905-2925)
 			s->anti_lm.reset(order);
 			for (uint64_t i = 0; i < history; ++i) s->anti_lm.update((int32_t)get32(history_ptr + 4 * i));
@@ -2222,13 +2455,41 @@ sslm_status sslm_seq_restore(sslm_model model, sslm_kv_pool* pool, const void* b
 	});
 }
 sslm_status sslm_tokenize(sslm_model, const char*, int32_t*, int32_t*) { return SSLM_INVALID_ARGUMENT; }
-sslm_status sslm_schema_lookup(sslm_model, const char*, sslm_schema* out) {
-	if (out) *out = nullptr;
+// src/sslm_abi.cpp:1236-1264
+sslm_status sslm_schema_lookup(sslm_model model, const char* name, sslm_schema* out) {
+	if (!out) return SSLM_INVALID_ARGUMENT;
+	*out = nullptr;
+	if (!model || !name) return SSLM_INVALID_ARGUMENT;
+	for (size_t i = 0; i < model->schemas.size(); ++i)
+		if (model->schemas[i].name == name) {
+			*out = &model->schema_handles[i];
+			return SSLM_OK;
+		}
 	return SSLM_SCHEMA_NOT_FOUND;
 }
-size_t sslm_schema_count(sslm_model) { return 0; }
-sslm_status sslm_schema_name(sslm_model, int32_t, char*, size_t*) { return SSLM_INVALID_ARGUMENT; }
-sslm_status sslm_seq_set_schema(sslm_seq, sslm_schema) { return SSLM_INVALID_ARGUMENT; }
+size_t sslm_schema_count(sslm_model model) { return model ? model->schemas.size() : 0; }
+sslm_status sslm_schema_name(sslm_model model, int32_t index, char* buf, size_t* n) {
+	if (!n) return SSLM_INVALID_ARGUMENT;
+	if (!model || index < 0 || (size_t)index >= model->schemas.size()) return SSLM_INVALID_ARGUMENT;
+	const std::string& nm = model->schemas[index].name;
+	if (!buf || *n < nm.size()) {
+		*n = nm.size();
+		return SSLM_BUFFER_TOO_SMALL;
+	}
+	memcpy(buf, nm.data(), nm.size());
+	*n = nm.size();
+	return SSLM_OK;
+}
+// src/sslm_abi.cpp:1791-1818: only a sequence that has taken no token yet, at its walk's start
+sslm_status sslm_seq_set_schema(sslm_seq seq, sslm_schema schema) {
+	if (!seq) return SSLM_INVALID_ARGUMENT;
+	if (seq->current_token != -1) return SSLM_SCHEMA_BIND_REJECTED;
+	if (seq->walk != kWalkUnused && seq->walk != 0) return SSLM_SCHEMA_BIND_REJECTED;
+	if (schema && schema->model != seq->model) return SSLM_INVALID_ARGUMENT;
+	seq->schema = schema;
+	seq->walk = schema ? 0u : kWalkUnused;
+	return SSLM_OK;
+}
 sslm_status sslm_prefix_set_schema(sslm_prefix, sslm_schema) { return SSLM_INVALID_ARGUMENT; }
 sslm_status sslm_detokenize_stream(sslm_model, sslm_detok_state*, const int32_t*, int32_t, char*, int32_t* out_n) {
 	if (out_n) *out_n = 0;

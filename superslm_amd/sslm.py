@@ -27,6 +27,7 @@ STATUS_NAMES = [
 ]
 ABI_ALIGNMENT = 64
 SPAN_PROMPT = 0
+SPAN_SCHEMA_CONTENT = 1
 
 
 class SslmError(RuntimeError):
@@ -42,6 +43,13 @@ class DecodeParams(ctypes.Structure):
                 ("mode", ctypes.c_int32), ("alpha_q15", ctypes.c_int32),
                 ("anti_lm_max_order", ctypes.c_int32), ("top_k", ctypes.c_int32),
                 ("q_ln2", ctypes.c_int64), ("q_b", ctypes.c_int64), ("q_c", ctypes.c_int64)]
+
+
+class StatsOut(ctypes.Structure):
+    """sslm_stats_out (sslm_abi.h:232-238)."""
+    _fields_ = [("decode_step_ceiling", ctypes.c_int64), ("decode_step_actual", ctypes.c_int64),
+                ("forced_token_count", ctypes.c_int64), ("kv_blocks_resident", ctypes.c_int32),
+                ("schema_accepting", ctypes.c_int32)]
 
 
 class Config(ctypes.Structure):
@@ -95,6 +103,11 @@ class SslmLib:
         sig("sslm_adapter_release", ctypes.c_int, vp)
         sig("sslm_seq_save", ctypes.c_int, vp, vp, ctypes.POINTER(sz))
         sig("sslm_seq_restore", ctypes.c_int, vp, pvp, vp, sz, pvp)
+        sig("sslm_schema_lookup", ctypes.c_int, vp, ctypes.c_char_p, pvp)
+        sig("sslm_schema_count", sz, vp)
+        sig("sslm_schema_name", ctypes.c_int, vp, i32, vp, ctypes.POINTER(sz))
+        sig("sslm_seq_set_schema", ctypes.c_int, vp, vp)
+        sig("sslm_stats", ctypes.c_int, vp, vp, ctypes.POINTER(StatsOut))
         self.has_peek = hasattr(L, "sslm_g5_test_only_peek_kv_block_bytes")
         if self.has_peek:
             sig("sslm_g5_test_only_peek_kv_block_bytes", ctypes.c_int, vp, u32, vp, sz)
@@ -150,6 +163,32 @@ class Model:
 
     def adapter(self, artifact) -> "Adapter":
         return Adapter(self, artifact)
+
+    def schema_count(self) -> int:
+        return self.lib.lib.sslm_schema_count(self.handle)
+
+    def schema(self, name):
+        """sslm_schema_lookup: (status, handle or None)."""
+        h = ctypes.c_void_p()
+        st = self.lib.lib.sslm_schema_lookup(self.handle, name if name is None else name.encode(), ctypes.byref(h))
+        return st, (h if st == SSLM_OK else None)
+
+    def schema_name(self, index: int, size: int | None = None):
+        """sslm_schema_name with a buffer of `size` bytes (None: the sizing call): (status, name
+        bytes or the required size)."""
+        n = ctypes.c_size_t(size or 0)
+        if size is None:
+            st = self.lib.lib.sslm_schema_name(self.handle, index, None, ctypes.byref(n))
+            return st, n.value
+        buf = ctypes.create_string_buffer(size)
+        st = self.lib.lib.sslm_schema_name(self.handle, index, buf, ctypes.byref(n))
+        return st, buf.raw[:n.value] if st == SSLM_OK else n.value
+
+    def stats(self, seq) -> tuple:
+        out = StatsOut()
+        st = self.lib.lib.sslm_stats(self.handle, seq.handle, ctypes.byref(out))
+        return st, (out.decode_step_ceiling, out.decode_step_actual, out.forced_token_count,
+                    out.kv_blocks_resident, out.schema_accepting)
 
     def close(self):
         if self.handle:
@@ -229,13 +268,17 @@ class Seq:
                                                               ctypes.byref(h)))
         self.handle = h
 
-    def prefill(self, tokens, chunk_budget: int | None = None, raw: bool = False):
+    def set_schema(self, schema) -> int:
+        """sslm_seq_set_schema (None unbinds); returns the status."""
+        return self.pool.model.lib.lib.sslm_seq_set_schema(self.handle, schema)
+
+    def prefill(self, tokens, chunk_budget: int | None = None, raw: bool = False, kind: int = SPAN_PROMPT):
         m = self.pool.model
         arr = np.ascontiguousarray(np.asarray(tokens, dtype=np.int32))
         consumed = ctypes.c_int32(0)
         budget = chunk_budget if chunk_budget is not None else max(1, len(arr))
         st = m.lib.lib.sslm_prefill(m.handle, self.handle, arr.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)),
-                                    len(arr), budget, SPAN_PROMPT, None, ctypes.byref(consumed))
+                                    len(arr), budget, kind, None, ctypes.byref(consumed))
         if raw:
             return st, consumed.value
         m.lib.check("sslm_prefill", st)

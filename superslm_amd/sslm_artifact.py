@@ -34,6 +34,7 @@ SEC_SIGMOID_LUT = 12
 SEC_DELTA_FOLD = 40
 SEC_U_FOLD = 41
 SEC_DAMPED_GREEDY = 42
+SEC_SCHEMA_MASKS = 30
 
 DT_RAW, DT_I8, DT_I32, DT_I64 = 0, 1, 2, 3
 _DT_SIZE = {DT_RAW: 1, DT_I8: 1, DT_I32: 4, DT_I64: 8}
@@ -63,6 +64,46 @@ def with_flags(image: bytes, flags: int) -> bytes:
     struct.pack_into("<I", b, 16, flags)
     b[32:64] = hashlib.sha256(bytes(b[:32]) + bytes(32) + bytes(b[64:])).digest()
     return bytes(b)
+
+
+def scm1(vocab: int, schemas) -> bytes:
+    """SchemaMasks section (include/superslm/schema_masks.h): header "SCM1", version 1, count,
+    vocab, name-blob length, 0; 56-byte descriptors (name offset/length, state, accepting and
+    transition counts, 0, then u64 offsets of the mask pages, state offsets, accepting set and
+    transitions, relative to the section); the name blob; the blocks.  `schemas`: (name,
+    {state: {token: next}}, accepting) with states 0..n-1; mask bits follow the transitions."""
+    page = (vocab + 7) // 8
+    names = b"".join(n.encode() for n, _, _ in schemas)
+    head = 24 + 56 * len(schemas) + len(names)
+    cursor = (head + 7) // 8 * 8
+    descs, blocks, name_off = [], [], 0
+    for name, table, accepting in schemas:
+        n = max(table) + 1 if table else 1
+        n = max(n, max((max(r.values()) for r in table.values() if r), default=0) + 1,
+                max(accepting, default=0) + 1)
+        pages = bytearray(n * page)
+        offsets, trans = [0], []
+        for st in range(n):
+            for tok in sorted(table.get(st, {})):
+                pages[st * page + tok // 8] |= 1 << (tok % 8)
+                trans.append(struct.pack("<II", tok, table[st][tok]))
+            offsets.append(len(trans))
+        parts = [bytes(pages), struct.pack(f"<{n + 1}I", *offsets),
+                 struct.pack(f"<{len(accepting)}I", *sorted(accepting)), b"".join(trans)]
+        offs = []
+        for part in parts:
+            offs.append(cursor)
+            blocks.append((cursor, part))
+            cursor = (cursor + len(part) + 7) // 8 * 8
+        descs.append(struct.pack("<6I4Q", name_off, len(name.encode()), n, len(accepting), len(trans), 0, *offs))
+        name_off += len(name.encode())
+    out = bytearray(cursor)
+    out[:24] = struct.pack("<4s5I", b"SCM1", 1, len(schemas), vocab, len(names), 0)
+    out[24:24 + 56 * len(schemas)] = b"".join(descs)
+    out[24 + 56 * len(schemas):head] = names
+    for off, part in blocks:
+        out[off:off + len(part)] = part
+    return bytes(out)
 
 
 def write_container_array(sections, flags: int = 0) -> np.ndarray:
@@ -284,6 +325,8 @@ class SyntheticModel:
     # damped-greedy logit scale (m, e): written as a DampedGreedyConstants section with header
     # flag bit 1 (src/damped_greedy_phaseD.cpp: 12 raw bytes, int64 m then int32 e)
     damped: tuple = None
+    # SCM1 schemas: [(name, {state: {token: next_state}}, accepting states)]
+    schemas: list = None
 
     def to_bytes(self) -> bytes:
         return bytes(self.to_array())
@@ -317,6 +360,8 @@ class SyntheticModel:
         if self.biases:
             sections.append((SEC_BIASES, DT_I64, Manifest(b"BIA1", 8, list(self.biases.items())), 64))
         flags = 0
+        if self.schemas:
+            sections.append((SEC_SCHEMA_MASKS, DT_RAW, scm1(c.vocab, self.schemas), 8))
         if self.damped is not None:
             sections.append((SEC_DAMPED_GREEDY, DT_RAW, struct.pack("<qi", *self.damped), 8))
             flags |= 2
@@ -340,7 +385,7 @@ def _codes(rng, shape):
 
 
 def build_synthetic(cfg: ModelConfig, seed: int = 1234, temperature: float = 1.0,
-                    damped_logit_scale: float | None = None) -> SyntheticModel:
+                    damped_logit_scale: float | None = None, schemas=None) -> SyntheticModel:
     """Seeded synthetic integer model whose constants follow one real-scale model.
 
     Real value of a code = code * (m * 2^e).  Each projection's WSC1 fold F = acc * mult / 2^(31+s)
@@ -349,12 +394,14 @@ def build_synthetic(cfg: ModelConfig, seed: int = 1234, temperature: float = 1.0
     norms use g_s / (2^16 * 127); residuals 1/127; the SiLU product 2^-15/127 (it already carries
     both incoming scales).  K/V land at a fixed code scale, and softmax_khead folds the k code
     scale with 1/sqrt(head_dim) so the derived i-exp q_ln2 sits near 5e4 score units.
-    `damped_logit_scale` (the real value of one logit unit) adds the damped-greedy constants."""
+    `damped_logit_scale` (the real value of one logit unit) adds the damped-greedy constants;
+    `schemas` (see scm1) adds a SchemaMasks section."""
     rng = np.random.Generator(np.random.PCG64(seed))
     c = cfg
     m = SyntheticModel(config=c)
     if damped_logit_scale is not None:
         m.damped = scale_me(damped_logit_scale)
+    m.schemas = schemas
     H, I, D, NH, NKV = c.hidden, c.inter, c.head_dim, c.heads, c.kv_heads
     KVH = NKV * D
     g_s = 1.0 / 127.0
