@@ -10,9 +10,8 @@
  * The caller-owned KV-pool and workspace buffers are still required and validated exactly as the
  * reference validates them (size, 64-byte alignment) and hold only host bookkeeping.
  *
- * Verbs outside the integer forward path (tokenizer, schema-constrained decoding, prefixes,
- * sequence restore, damped greedy) are exported with their reference signatures and return
- * SSLM_INVALID_ARGUMENT.
+ * Verbs outside the integer forward path (tokenizer, prefixes, detokenize) are exported with
+ * their reference signatures and return SSLM_INVALID_ARGUMENT.
  */
 #ifndef SSLM_HIP_H
 #define SSLM_HIP_H
@@ -140,6 +139,12 @@ sslm_status sslm_adapter_map(const void* data, size_t size, sslm_model base, ssl
 sslm_status sslm_adapter_release(sslm_adapter adapter);                              /* :47 */
 size_t sslm_adapter_residency(sslm_adapter adapter);                                 /* :48 */
 
+/* ---- SCM1 schemas (src/sslm_abi.cpp:1236-1264, 1791-1818) ---- */
+sslm_status sslm_schema_lookup(sslm_model model, const char* name, sslm_schema* out);
+size_t sslm_schema_count(sslm_model model);
+sslm_status sslm_schema_name(sslm_model model, int32_t index, char* buf, size_t* n);
+sslm_status sslm_seq_set_schema(sslm_seq seq, sslm_schema schema);
+
 /* ---- the hot path ---- */
 sslm_status sslm_prefill(sslm_model model, sslm_seq seq, const int32_t* tokens, int32_t count,
                          int32_t chunk_budget, sslm_span_kind kind, sslm_workspace ws,
@@ -169,10 +174,6 @@ sslm_status sslm_prefix_freeze(sslm_prefix prefix);
 sslm_status sslm_prefix_release(sslm_prefix prefix);
 sslm_status sslm_seq_adopt_prefix(sslm_seq seq, sslm_prefix prefix);
 sslm_status sslm_tokenize(sslm_model model, const char* utf8, int32_t* tokens, int32_t* n);
-sslm_status sslm_schema_lookup(sslm_model model, const char* name, sslm_schema* out);
-size_t sslm_schema_count(sslm_model model);
-sslm_status sslm_schema_name(sslm_model model, int32_t index, char* buf, size_t* n);
-sslm_status sslm_seq_set_schema(sslm_seq seq, sslm_schema schema);
 sslm_status sslm_prefix_set_schema(sslm_prefix prefix, sslm_schema schema);
 sslm_status sslm_detokenize_stream(sslm_model model, sslm_detok_state* state, const int32_t* tokens, int32_t n,
                                    char* utf8, int32_t* out_n);
