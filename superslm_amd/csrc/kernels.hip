@@ -1536,10 +1536,10 @@ __global__ __launch_bounds__(BS) void k_attention(sslm_launch::AttnArgs a, int u
 	__shared__ int64_t s_sum[BS / 64];
 	__shared__ uint64_t s_ref[BS / 64];
 	__shared__ uint32_t s_ab[BS / 64], s_qm[BS / 64];
-	__shared__ int32_t s_ctx[BS * 4];
+	__shared__ int32_t s_ctx[BS * 16];  // pass 4 partial sums: PG position groups x D
 	__shared__ __attribute__((aligned(16))) int8_t s_qc[D], s_kc[D], s_vc[D];
 	__shared__ int32_t s_st;
-	constexpr int TPR = D / 4, PG = BS / TPR, PAIRS = D / 2;
+	constexpr int TPR = D / 16, PG = BS / TPR, PAIRS = D / 2;  // pass 4: threads per row, row groups
 	static_assert(BS >= PAIRS, "one thread per RoPE pair");
 	// XCD-aware order: workgroups go round-robin to the 8 XCDs (block id mod 8), so the R query
 	// heads of one (kv head, token) group are numbered id = (i * R + r) * 8 + x -- all on XCD x,
@@ -1655,6 +1655,7 @@ __global__ __launch_bounds__(BS) void k_attention(sslm_launch::AttnArgs a, int u
 	// pass 1: scores (int32-exact dots) and the row max
 	int64_t mx = INT64_MIN;
 	if (live) {
+#pragma unroll 2
 		for (int64_t p = threadIdx.x; p < width; p += BS) {
 			const int8_t* kr = kbase + p * D;
 			int32_t acc = 0;
@@ -1714,31 +1715,37 @@ __global__ __launch_bounds__(BS) void k_attention(sslm_launch::AttnArgs a, int u
 	const int64_t denom = sum > 1 ? sum : 1;
 	for (int64_t p = threadIdx.x; p < width; p += BS) ex[p] = div_floor_pos(ex[p] << 15, denom);
 	__syncthreads();
-	// pass 4: context = sum_p prob * V[p]
+	// pass 4: context = sum_p prob * V[p].  A thread owns 16 dimensions (one 16-byte load per
+	// row) of every PG-th position; the loop is unrolled so several rows are in flight.  The sums
+	// are exact in int32: the probabilities of a row add up to at most 2^15.
 	const int dq = threadIdx.x % TPR, pg = threadIdx.x / TPR;
-	int32_t acc0 = 0, acc1 = 0, acc2 = 0, acc3 = 0;
-	if (pg < PG) {
-		const int8_t* vc = vbase + 4 * dq;
+	int32_t acc[16];
+#pragma unroll
+	for (int j = 0; j < 16; ++j) acc[j] = 0;
+	{
+		const int8_t* vc = vbase + 16 * dq;
 #pragma unroll 4
 		for (int64_t p = pg; p < width; p += PG) {
-			const int32_t v = FUSED && p == pos ? *(const int32_t*)(s_vc + 4 * dq) : *(const int32_t*)(vc + p * D);
+			const v4i v = FUSED && p == pos ? *(const v4i*)(s_vc + 16 * dq) : load16(vc + p * D);
 			const int32_t pr = (int32_t)ex[p];
-			acc0 += pr * (int32_t)(int8_t)(v & 0xff);
-			acc1 += pr * (int32_t)(int8_t)((v >> 8) & 0xff);
-			acc2 += pr * (int32_t)(int8_t)((v >> 16) & 0xff);
-			acc3 += pr * (v >> 24);
+#pragma unroll
+			for (int w = 0; w < 4; ++w) {
+				const int32_t x = v[w];
+				acc[4 * w] += pr * (int32_t)(int8_t)(x & 0xff);
+				acc[4 * w + 1] += pr * (int32_t)(int8_t)((x >> 8) & 0xff);
+				acc[4 * w + 2] += pr * (int32_t)(int8_t)((x >> 16) & 0xff);
+				acc[4 * w + 3] += pr * (x >> 24);
+			}
 		}
-		int32_t* sc = s_ctx + pg * D + 4 * dq;
-		sc[0] = acc0;
-		sc[1] = acc1;
-		sc[2] = acc2;
-		sc[3] = acc3;
+		int32_t* sc = s_ctx + pg * D + 16 * dq;
+#pragma unroll
+		for (int j = 0; j < 16; ++j) sc[j] = acc[j];
 	}
 	__syncthreads();
 	uint32_t mabs = 0;
 	if (threadIdx.x < D) {
 		int32_t c = 0;
-#pragma unroll
+#pragma unroll 8
 		for (int g2 = 0; g2 < PG; ++g2) c += s_ctx[g2 * D + threadIdx.x];
 		const int64_t f = apply_fold(c, f0, f1, f2);
 		a.ctx_f[(size_t)t * a.H + (size_t)h * D + threadIdx.x] = sat_i32(f);
