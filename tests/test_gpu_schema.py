@@ -150,3 +150,36 @@ def test_malformed_schema_tables_rejected_like_reference(hip_lib, ref_lib):
     print(statuses[ref_lib.path], flush=True)
     assert statuses[hip_lib.path] == statuses[ref_lib.path]
     assert statuses[ref_lib.path]["good"] == 0
+
+
+def _mixed(lib, art, L, budget, mode):
+    """One decode batch: a sequence bound to "cycle", an unbound one, one bound to "wide"."""
+    m = Model(lib, art)
+    pool = m.pool(3)
+    seqs = [pool.seq() for _ in range(3)]
+    for sq, name in zip(seqs, ("cycle", None, "wide")):
+        if name:
+            assert sq.set_schema(m.schema(name)[1]) == 0
+    for sq, prompt in zip(seqs, ([11, 12], [13, 14, 15], [16])):
+        sq.prefill(prompt)
+    p = m.decode_params(budget, mode)
+    toks = [m.decode_step(seqs, budget, raw=True, params=p) for _ in range(6 * L // budget)]
+    out = (toks, [m.stats(sq) for sq in seqs], [sq.save() for sq in seqs],
+           [pool.kv_block(i).tobytes() for i in range(3)])
+    for sq in seqs:
+        sq.release()
+    pool.close()
+    m.close()
+    return out
+
+
+def test_mixed_schema_batch_matches_reference(hip_lib, ref_lib):
+    sm, art = schema_artifact()
+    L = sm.config.layers
+    for mode in (0, 1):
+        for budget in sorted({1, L}):
+            print(f"case mixed mode={mode} budget={budget}", flush=True)
+            r = _mixed(ref_lib, art, L, budget, mode)
+            h = _mixed(hip_lib, art, L, budget, mode)
+            assert h[0] == r[0], f"tokens differ: hip {h[0]} ref {r[0]}"
+            assert h[1] == r[1] and h[2] == r[2] and h[3] == r[3]
