@@ -1521,7 +1521,7 @@ __global__ __launch_bounds__(BS) void k_mlp_act(sslm_launch::ActArgs a) {
 // (forward_sites.cpp:1791-1905).  Scores, i-exp values and Q15 probabilities of the row live in
 // LDS when the context fits (else in the per-launch global scratch); each thread owns the
 // positions p = threadIdx.x + k * BS through the score, exp and probability passes, so those
-// passes meet only at the row max and row sum.  PV: D / 4 threads cover one V row (4 channels
+// passes meet only at the row max and row sum.  PV: D / 16 threads cover one V row (16 channels
 // each); the position groups' int32 partials meet in LDS (exact: probabilities sum to <= 2^15).
 //
 // FUSED (decode): the block first does the q|k|v post-processing of qkv_post for its head --
