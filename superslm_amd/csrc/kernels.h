@@ -50,6 +50,9 @@ struct Epilogue {
 	// logits mode: per (16-column tile, token) argmax keys instead of segments
 	unsigned long long* argmax_key;  // [M][key_ld] per (token, 16-column tile) keys, or null
 	int32_t key_ld;
+	// logits mode: per token a schema mask page (bit j set: token j legal) or null; masked
+	// logits count as INT32_MIN (forward_sites.cpp:2443-2449).  Null: no token masked.
+	const uint8_t* const* mask_page;
 	// raw mode: the int32 accumulator itself, [M, N]
 	int32_t* raw_out;
 };

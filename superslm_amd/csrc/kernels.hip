@@ -160,7 +160,9 @@ __device__ __forceinline__ void epi_element(const Epilogue& e, int N, int t, int
 	if (e.raw_out) {
 		e.raw_out[(size_t)t * N + j] = acc;
 	} else if (e.argmax_key) {
-		const uint32_t logit = (uint32_t)acc ^ 0x80000000u;
+		const uint8_t* pg = e.mask_page ? e.mask_page[t] : nullptr;
+		const int32_t v = pg && !((pg[j >> 3] >> (j & 7)) & 1u) ? INT32_MIN : acc;
+		const uint32_t logit = (uint32_t)v ^ 0x80000000u;
 		*key = ((uint64_t)logit << 32) | (uint64_t)(0xffffffffu - (uint32_t)j);
 	} else {
 		EpiResult r = epi_value(e, t, j, acc);
@@ -364,7 +366,10 @@ __global__ __launch_bounds__(64 * kGemvWaves) void k_gemv(GemmArgs g, int cps) {
 		// per (token, 16-column tile) greedy keys: the larger logit, then the smaller index
 #pragma unroll
 		for (int v = 0; v < 4; ++v) {
-			uint64_t key = j < g.N ? ((uint64_t)((uint32_t)tot[v] ^ 0x80000000u) << 32) | (0xffffffffu - (uint32_t)j) : 0;
+			// a schema-masked token's logit counts as INT32_MIN
+			const uint8_t* pg = e.mask_page && t0 + v < g.M ? e.mask_page[t0 + v] : nullptr;
+			const int32_t lv = pg && j < g.N && !((pg[j >> 3] >> (j & 7)) & 1u) ? INT32_MIN : tot[v];
+			uint64_t key = j < g.N ? ((uint64_t)((uint32_t)lv ^ 0x80000000u) << 32) | (0xffffffffu - (uint32_t)j) : 0;
 			for (int o = 8; o > 0; o >>= 1) {
 				const uint64_t k2 = __shfl_xor(key, o, 16);
 				key = k2 > key ? k2 : key;

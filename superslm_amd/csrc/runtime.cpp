@@ -193,6 +193,7 @@ struct Track {
 	int8_t* lora_u[3];
 	TokenInfo* lg_tok;    // head tracks: tokens of the joined final norm + head
 	int32_t* lg_slot;
+	const uint8_t** lg_mask;  // head tracks: per token its schema mask page in HBM, or null
 	hipEvent_t done = nullptr;
 	hipEvent_t fork = nullptr;
 };
@@ -309,6 +310,8 @@ struct sslm_model_s {
 	std::vector<SchemaEntry> schemas;
 	std::vector<sslm_schema_s> schema_handles;
 	uint32_t page_bytes = 0;  // (V + 7) / 8
+	uint8_t* d_pages = nullptr;     // every schema's mask pages, in HBM
+	std::vector<size_t> page_off;   // per schema: offset of its pages in d_pages
 	// per-slot sequence state
 	int8_t* stream_codes;   // [kSlotCapacity, H]
 	Scale* stream_scale;    // [kSlotCapacity]
@@ -961,7 +964,8 @@ void run_layers(sslm_model m, Track& w, int M, StreamRef st, int l0, int l1, ssl
 
 // final norm + LM head + lowest-index argmax for M tokens whose stream rows are st.idx
 // (src/sslm_abi.cpp:2280-2289, forward_sites.cpp:2412-2441)
-void run_logits(sslm_model m, Track& w, int M, StreamRef st, const TokenInfo* tok) {
+void run_logits(sslm_model m, Track& w, int M, StreamRef st, const TokenInfo* tok,
+                const uint8_t* const* mask = nullptr) {
 	hipStream_t s = w.stream;
 	{
 		ProfScope p(s, kProfRow, 0, 0);
@@ -971,6 +975,7 @@ void run_logits(sslm_model m, Track& w, int M, StreamRef st, const TokenInfo* to
 		ck(hipGetLastError());
 	}
 	GemmArgs g = head_args(m, w, M, tok);
+	g.epi.mask_page = mask;
 	run_gemm(m, w, g, kProfHead);
 	sslm_launch::argmax_finalize(w.argmax_key, (m->V + 15) / 16, M, w.out_tokens, s);
 	ck(hipGetLastError());
@@ -1140,6 +1145,7 @@ void alloc_track(sslm_model m, Track& w, int T, bool head) {
 	w.attn_scratch = sslm_launch::attention_in_lds(m->cap) ? nullptr : dalloc<int64_t>((size_t)T * m->NH * m->cap, &own);
 	w.lg_tok = head ? dalloc<TokenInfo>(T, &own) : nullptr;
 	w.lg_slot = head ? dalloc<int32_t>(T, &own) : nullptr;
+	w.lg_mask = head ? (const uint8_t**)dalloc<uintptr_t>(T, &own) : nullptr;
 	ck(hipStreamCreate(&w.stream));
 	ck(hipEventCreateWithFlags(&w.done, hipEventDisableTiming));
 	ck(hipEventCreateWithFlags(&w.fork, hipEventDisableTiming));
@@ -1346,6 +1352,16 @@ bool build_device_model(sslm_model m, std::string* err) {
 		}
 		m->schema_handles.resize(m->schemas.size());
 		for (size_t i = 0; i < m->schemas.size(); ++i) m->schema_handles[i] = sslm_schema_s{m, (uint32_t)i};
+		// the mask pages go to HBM, so masked greedy decoding takes its argmax on the device
+		size_t total = 0;
+		for (const SchemaEntry& e : m->schemas) {
+			m->page_off.push_back(total);
+			total += (size_t)e.states * m->page_bytes;
+		}
+		std::vector<uint8_t> pages(total);
+		for (size_t i = 0; i < m->schemas.size(); ++i)
+			memcpy(pages.data() + m->page_off[i], m->schemas[i].pages, (size_t)m->schemas[i].states * m->page_bytes);
+		m->d_pages = dupload(pages, &own);
 	}
 	// slots
 	m->stream_codes = dalloc<int8_t>((size_t)kSlotCapacity * H, &own);
@@ -1793,9 +1809,11 @@ static sslm_status decode_batch(sslm_model m, sslm_seq* seqs, int32_t n, const s
 	}
 	std::vector<int> lg = need_logits;
 	lg.insert(lg.end(), finished.begin(), finished.end());
-	// whole logit rows come back to the host for damped greedy and for schema-masked argmax
-	bool rows_needed = damped;
-	for (int i : lg) rows_needed = rows_needed || seqs[i]->schema;
+	// whole logit rows come back to the host for damped greedy; a schema-bound sequence's greedy
+	// argmax is masked on the device (its mask page per token)
+	const bool rows_needed = damped;
+	bool masked = false;
+	for (int i : lg) masked = masked || seqs[i]->schema;
 	if (rows_needed && !m->logits) m->logits = dalloc<int32_t>((size_t)kMaxTokens * m->V, &m->owned);
 
 	// Host staging, uploaded before the kernels (kept alive until the sync below).  The common
@@ -1808,6 +1826,7 @@ static sslm_status decode_batch(sslm_model m, sslm_seq* seqs, int32_t n, const s
 	const bool use_graph = one_per_track && graphs_enabled() && !prof_enabled();
 	std::deque<std::vector<TokenInfo>> h_tok;  // deque: references to earlier entries stay valid
 	std::deque<std::vector<int32_t>> h_i32;
+	std::deque<std::vector<const uint8_t*>> h_ptr;
 	auto stage_unit = [&](size_t u, hipStream_t s) {
 		const Unit& un = units[u];
 		Track& w = m->tracks[u % ntr];
@@ -1852,9 +1871,20 @@ static sslm_status decode_batch(sslm_model m, sslm_seq* seqs, int32_t n, const s
 		}
 		ck(hipMemcpyAsync(t0.lg_tok, ti.data(), M * sizeof(TokenInfo), hipMemcpyHostToDevice, s));
 		ck(hipMemcpyAsync(t0.lg_slot, slots.data(), M * 4, hipMemcpyHostToDevice, s));
+		if (masked) {
+			h_ptr.emplace_back(M, nullptr);
+			std::vector<const uint8_t*>& pg = h_ptr.back();
+			for (int t = 0; t < M; ++t) {
+				sslm_seq q = seqs[lg[b + t]];
+				if (q->schema)
+					pg[t] = m->d_pages + m->page_off[q->schema->index] + (size_t)q->walk * m->page_bytes;
+			}
+			ck(hipMemcpyAsync(t0.lg_mask, pg.data(), M * sizeof(void*), hipMemcpyHostToDevice, s));
+		}
 	};
 	auto launch_logits = [&](int M) {
-		run_logits(m, t0, M, StreamRef{m->stream_codes, m->stream_scale, t0.lg_slot}, t0.lg_tok);
+		run_logits(m, t0, M, StreamRef{m->stream_codes, m->stream_scale, t0.lg_slot}, t0.lg_tok,
+		           masked ? t0.lg_mask : nullptr);
 		if (rows_needed) {  // the whole logit rows as well: the head's raw int32 accumulators
 			GemmArgs g = head_args(m, t0, M, t0.lg_tok);
 			g.epi.argmax_key = nullptr;
@@ -1912,7 +1942,8 @@ static sslm_status decode_batch(sslm_model m, sslm_seq* seqs, int32_t n, const s
 		if (!lg.empty()) {
 			const int M = (int)lg.size();
 			if (use_graph)
-				ck(hipGraphLaunch(graph_of("lg|" + std::to_string(M) + (rows_needed ? "|r" : ""), t0.stream, [&] { launch_logits(M); }),
+				ck(hipGraphLaunch(graph_of("lg|" + std::to_string(M) + (rows_needed ? "|r" : "") + (masked ? "|m" : ""), t0.stream,
+				                           [&] { launch_logits(M); }),
 				                  t0.stream));
 			else launch_logits(M);
 		}
@@ -1987,7 +2018,7 @@ static sslm_status decode_batch(sslm_model m, sslm_seq* seqs, int32_t n, const s
 		const SchemaEntry* se = s->schema ? &m->schemas[s->schema->index] : nullptr;
 		const uint8_t* page = se ? se->pages + (size_t)s->walk * m->page_bytes : nullptr;
 		int32_t* row = rows_needed ? rows.data() + k * (size_t)m->V : nullptr;
-		if (se)  // the mask first: masked logits become INT32_MIN (forward_sites.cpp:2443-2449)
+		if (se && row)  // damped: the mask first, masked logits INT32_MIN (forward_sites.cpp:2443-2449)
 			for (int t = 0; t < m->V; ++t)
 				if (!((page[t >> 3] >> (t & 7)) & 1u)) row[t] = INT32_MIN;
 		if (damped) {  // src/sslm_abi.cpp:2301-2384
@@ -1998,11 +2029,7 @@ static sslm_status decode_batch(sslm_model m, sslm_seq* seqs, int32_t n, const s
 				if (first_err == SSLM_OK) first_err = map_forward_status(kSoftmaxKernelRefusedAfterGateAccepted);
 				continue;
 			}
-		} else if (se) {  // masked argmax, lowest index on ties
-			tok = 0;
-			for (int t = 1; t < m->V; ++t)
-				if (row[t] > row[tok]) tok = t;
-		}
+		}  // greedy: tok is the device's argmax, masked for a schema-bound sequence
 		if (se) {  // the walk advances only along an existing transition; none is a dead end (-2)
 			uint32_t nx = 0;
 			if (!schema_next(*se, s->walk, (uint32_t)tok, &nx)) {

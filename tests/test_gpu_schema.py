@@ -152,20 +152,22 @@ def test_malformed_schema_tables_rejected_like_reference(hip_lib, ref_lib):
     assert statuses[ref_lib.path]["good"] == 0
 
 
-def _mixed(lib, art, L, budget, mode):
-    """One decode batch: a sequence bound to "cycle", an unbound one, one bound to "wide"."""
+def _mixed(lib, art, L, budget, mode, n=3):
+    """One decode batch of `n` sequences cycling through: bound to "cycle", unbound, bound to
+    "wide"."""
     m = Model(lib, art)
-    pool = m.pool(3)
-    seqs = [pool.seq() for _ in range(3)]
-    for sq, name in zip(seqs, ("cycle", None, "wide")):
-        if name:
-            assert sq.set_schema(m.schema(name)[1]) == 0
-    for sq, prompt in zip(seqs, ([11, 12], [13, 14, 15], [16])):
-        sq.prefill(prompt)
+    pool = m.pool(n)
+    seqs = [pool.seq() for _ in range(n)]
+    names = ("cycle", None, "wide")
+    prompts = ([11, 12], [13, 14, 15], [16])
+    for i, sq in enumerate(seqs):
+        if names[i % 3]:
+            assert sq.set_schema(m.schema(names[i % 3])[1]) == 0
+        sq.prefill([t + i for t in prompts[i % 3]])
     p = m.decode_params(budget, mode)
     toks = [m.decode_step(seqs, budget, raw=True, params=p) for _ in range(6 * L // budget)]
     out = (toks, [m.stats(sq) for sq in seqs], [sq.save() for sq in seqs],
-           [pool.kv_block(i).tobytes() for i in range(3)])
+           [pool.kv_block(i).tobytes() for i in range(n)])
     for sq in seqs:
         sq.release()
     pool.close()
@@ -183,3 +185,16 @@ def test_mixed_schema_batch_matches_reference(hip_lib, ref_lib):
             h = _mixed(hip_lib, art, L, budget, mode)
             assert h[0] == r[0], f"tokens differ: hip {h[0]} ref {r[0]}"
             assert h[1] == r[1] and h[2] == r[2] and h[3] == r[3]
+
+
+def test_wide_mixed_schema_batch_matches_reference(hip_lib, ref_lib):
+    """72 sequences in one call: the LM head runs as a tiled GEMM (more than 64 tokens) with the
+    schema masks applied in its argmax epilogue."""
+    sm, art = schema_artifact()
+    L = sm.config.layers
+    for mode in (0, 1):
+        print(f"case wide mixed mode={mode}", flush=True)
+        r = _mixed(ref_lib, art, L, L, mode, n=72)
+        h = _mixed(hip_lib, art, L, L, mode, n=72)
+        assert h[0] == r[0], "tokens differ"
+        assert h[1] == r[1] and h[2] == r[2] and h[3] == r[3]
