@@ -523,6 +523,52 @@ SSLM_HD int64_t iexp_element(int64_t shifted, int64_t q_ln2, int64_t q_b, int64_
 	return value;
 }
 
+// floor(n / d) for 0 <= n, 1 <= d, given inv = 1.0 / d and that the true quotient lies in
+// [0, qmax] with qmax * d + d < 2^63: the double estimate is exact to within one for quotients
+// far below 2^50 and is corrected with exact 64-bit remainders.
+SSLM_HD int64_t div_rcp(int64_t n, int64_t d, double inv, int64_t qmax) {
+	int64_t q = (int64_t)((double)n * inv);
+	q = q < 0 ? 0 : (q > qmax ? qmax : q);
+	int64_t r = n - q * d;
+	while (r < 0) {
+		--q;
+		r += d;
+	}
+	while (r >= d) {
+		++q;
+		r -= d;
+	}
+	return q;
+}
+
+// iexp_element (intmath.cpp:580-668) for a row whose constants passed check_softmax_width
+// (q_c >= 0, q_b^2 + q_c <= kSoftmaxMaxSafe) and shifted <= 0:
+// the quotient z in [0, 30] from a reciprocal, and the square in 64 bits when |base| < 2^31
+// (then base^2 + q_c < 2^63); the 128-bit form otherwise.  Same value, or -1 when refused.
+SSLM_HD int64_t iexp_fast(int64_t shifted, int64_t q_ln2, double inv_ln2, int64_t q_b,
+                                             int64_t q_c, int64_t m_ceiling) {
+	if (q_ln2 < 1 || q_ln2 > kI64Max / 30) return -1;
+	const int64_t x = shifted < -30 * q_ln2 ? 30 * q_ln2 : -shifted;
+	int64_t z = (int64_t)((double)x * inv_ln2);
+	z = z < 0 ? 0 : (z > 30 ? 30 : z);
+	int64_t r = x - z * q_ln2;  // q_p = -r
+	while (r < 0) {
+		--z;
+		r += q_ln2;
+	}
+	while (r >= q_ln2) {
+		++z;
+		r -= q_ln2;
+	}
+	if (q_b < kI64Min + r) return -1;
+	const int64_t base = q_b - r;
+	int64_t value;
+	if (base > -(int64_t(1) << 31) && base < (int64_t(1) << 31)) value = (base * base + q_c) >> z;
+	else value = (int64_t)((((s128)base * base) + (s128)q_c) >> z);
+	if (m_ceiling <= 0 || value < 0 || value > m_ceiling) return -1;
+	return value;
+}
+
 // The softmax's per-element ceiling M = q_b^2 + q_c when usable (intmath.cpp:831-851), else 0.
 SSLM_HD int64_t softmax_ceiling(int64_t q_b, int64_t q_c) {
 	s128 m128 = (s128)q_b * q_b + (s128)q_c;

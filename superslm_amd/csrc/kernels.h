@@ -200,7 +200,10 @@ struct AttnArgs {
 	const int64_t* rope_sin;
 	unsigned long long* sat;    // [slots]
 };
-void attention(const AttnArgs& a, hipStream_t s);
+// `one_sequence`: the launch holds one sequence's consecutive positions (a prefill chunk), so
+// the query-tiled kernel may run (unless SSLM_HIP_TILED_ATTN=0).
+void attention(const AttnArgs& a, hipStream_t s, bool one_sequence = false);
+bool tiled_attention_enabled();
 // Decode attention with the q|k|v post-processing fused in (one block per (query head, token)):
 // valid when every token of the launch belongs to a different sequence, so no token attends to
 // a position another block of the launch writes.

@@ -1760,6 +1760,264 @@ __global__ __launch_bounds__(BS) void k_attention(sslm_launch::AttnArgs a, int u
 	if (threadIdx.x == 0) a.ctx_maxpart[(size_t)h * kPartLd + t] = mabs;
 }
 
+// Prefill attention over query tiles: one block per (query head, 16 consecutive tokens of one
+// sequence), the same arithmetic as k_attention (forward_sites.cpp:1791-1905) with each K and V
+// row read once per tile instead of once per token.  Scores Q.K^T are int32-exact on
+// v_mfma_i32_16x16x64_i8 (A = the tile's 16 query rows, B = 16 key rows; any k order shared by
+// both operands gives the same integer sum).  The softmax stays exact without keeping the row:
+// pass 1 takes each token's row max, pass 2 recomputes the scores for the i-exp values and their
+// sum, pass 3 recomputes them once more for the Q15 probabilities and multiplies by V.  P.V runs
+// on the same MFMA: a probability (0 .. 2^15) is split into three 7-bit parts p = a*2^14 + b*2^7
+// + c, each an int8 operand, and the three int32 products recombine exactly (the true sum is
+// below 2^22 in magnitude).  V is staged transposed in LDS ([dim][position], 4x4 byte blocks
+// transposed in registers) so a lane's 16 B operand holds 16 positions of one dimension.
+// The launch must hold one sequence's consecutive positions (a prefill chunk).
+template <int D>
+__global__ __launch_bounds__(256) void k_attention_tiled(sslm_launch::AttnArgs a) {
+	constexpr int TQ = 16, KB = 64, NC = (D + 63) / 64, DT = D / 16, PS = KB + 16, VS = KB + 16;
+	__shared__ __attribute__((aligned(16))) int8_t s_p[3][TQ][PS];  // probability parts [part][token][pos]
+	__shared__ __attribute__((aligned(16))) int8_t s_vt[D][VS];     // V^T of the current 64 positions
+	__shared__ int64_t s_c[TQ][4];                                   // per token: q_ln2, q_b, q_c, ceiling
+	__shared__ double s_inv[TQ];                                     // per token: 1 / q_ln2
+	__shared__ int64_t s_red[4][TQ];
+	__shared__ int32_t s_pos[TQ], s_ok[TQ];
+	__shared__ uint32_t s_mab[TQ], s_rf[TQ];  // per token: |context| maximum, softmax refused
+	__shared__ int32_t s_st;
+	const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, ri = lane & 15, g = lane >> 4;
+	const int group = a.NH / a.NKV, ntiles = (a.M + TQ - 1) / TQ;
+	int h, tile;
+	{  // XCD-aware order as in k_attention: the R heads of one (tile, kv head) share an XCD
+		const int id = blockIdx.x, x = id & 7, k = id >> 3;
+		const int gi = x + 8 * (k / group);
+		if (gi >= ntiles * a.NKV) return;
+		tile = ntiles - 1 - gi / a.NKV;  // the longest causal rows start first
+		h = (gi % a.NKV) * group + k % group;
+	}
+	const int t0 = tile * TQ, nt = min(TQ, a.M - t0);
+	const int kvh = h / group;
+	const TokenInfo ti0 = a.tok[t0];
+	if (threadIdx.x == 0) s_st = a.status[ti0.slot];
+	if (threadIdx.x < TQ) {
+		// the token's i-exp constants and width, as k_attention derives them
+		const int tq = threadIdx.x;
+		int32_t st = kOk;
+		int64_t c0 = 0, c1 = 0, c2 = 0, cm = 0, pos = -1;
+		if (tq < nt) {
+			const Scale qs = a.q_scale[t0 + tq];
+			pos = a.tok[t0 + tq].pos;
+			const int64_t km = a.khead_m[kvh], ke = a.khead_e[kvh];
+			if (!fits_i32(qs.m) || !fits_i32(km)) {
+				st = kCarriedScaleMantissaOutOfDomain;
+			} else {
+				const Scale sm = combine_scale(qs, Scale{km, ke});
+				if (!fits_i32(sm.m)) st = kCarriedScaleMantissaOutOfDomain;
+				else if (iexp_scale_constants(sm.m, sm.e, a.ln2_q, a.b_q, a.ca_q, &c0, &c1, &c2) != 0)
+					st = kIExpScaleDerivationOutOfDomain;
+				else {
+					st = check_softmax_width(c1, c2, pos + 1);
+					cm = softmax_ceiling(c1, c2);
+				}
+			}
+			if (st == kOk && !(pos + 1 >= 1 && pos + 1 <= a.cap)) st = -1;
+		} else {
+			st = -2;  // past the launch's last token
+		}
+		s_c[tq][0] = c0;
+		s_c[tq][1] = c1;
+		s_c[tq][2] = c2;
+		s_c[tq][3] = cm;
+		s_inv[tq] = st == kOk && c0 >= 1 ? 1.0 / (double)c0 : 0.0;
+		s_pos[tq] = (int32_t)pos;
+		s_ok[tq] = st;
+		s_mab[tq] = 0;
+		s_rf[tq] = 0;
+	}
+	__syncthreads();
+	if (s_st != 0) return;
+	if (threadIdx.x < nt && s_ok[threadIdx.x] != kOk)
+		report_head(a.head_status, ti0.slot, h, s_ok[threadIdx.x] == -1 ? kPositionOverCap : s_ok[threadIdx.x]);
+	int wmax = 0;  // positions [0, wmax) cover every live token's row
+	for (int tq = 0; tq < nt; ++tq)
+		if (s_ok[tq] == kOk) wmax = max(wmax, s_pos[tq] + 1);
+	if (wmax == 0) return;
+	const int8_t* kbase = a.kv_pool + (int64_t)ti0.block * a.block_bytes + (int64_t)a.layer * a.cap * a.NKV * D * 2 +
+	                      (int64_t)kvh * a.cap * D;
+	const int8_t* vbase = kbase + a.cap * (int64_t)a.NKV * D;
+	// this lane's A operand: query row ri, bytes c*64 + g*16 of chunk c
+	v4i qa[NC];
+#pragma unroll
+	for (int c = 0; c < NC; ++c) {
+		const int off = c * 64 + g * 16;
+		qa[c] = ri < nt && off < D ? load16(a.q_rot + (size_t)(t0 + ri) * a.H + (size_t)h * D + off) : v4i{0, 0, 0, 0};
+	}
+	// the output tokens of this lane: g*4 + v
+	int32_t tpos[4];
+	bool tok_ok[4];
+#pragma unroll
+	for (int v = 0; v < 4; ++v) {
+		tpos[v] = s_pos[g * 4 + v];
+		tok_ok[v] = s_ok[g * 4 + v] == kOk;
+	}
+	const int nblk = (wmax + KB - 1) / KB;
+	auto scores = [&](int blk, int* p_out) {
+		const int p = blk * KB + wave * 16 + ri;
+		const int8_t* kr = kbase + (int64_t)min(p, (int)a.cap - 1) * D;
+		v4i acc = v4i{0, 0, 0, 0};
+#pragma unroll
+		for (int c = 0; c < NC; ++c) {
+			const int off = c * 64 + g * 16;
+			const v4i kb = off < D ? load16(kr + off) : v4i{0, 0, 0, 0};
+			acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(qa[c], kb, acc, 0, 0, 0);
+		}
+		*p_out = p;
+		return acc;
+	};
+	// pass 1: row maxima
+	int32_t mx[4] = {INT32_MIN, INT32_MIN, INT32_MIN, INT32_MIN};
+	for (int blk = 0; blk < nblk; ++blk) {
+		int p;
+		const v4i s = scores(blk, &p);
+#pragma unroll
+		for (int v = 0; v < 4; ++v)
+			if (tok_ok[v] && p <= tpos[v]) mx[v] = max(mx[v], s[v]);
+	}
+#pragma unroll
+	for (int v = 0; v < 4; ++v) {
+		for (int o = 8; o > 0; o >>= 1) mx[v] = max(mx[v], __shfl_xor(mx[v], o, 16));
+		if (ri == 0) s_red[wave][g * 4 + v] = mx[v];
+	}
+	__syncthreads();
+	int64_t rmx[4];
+#pragma unroll
+	for (int v = 0; v < 4; ++v) {
+		const int tq = g * 4 + v;
+		rmx[v] = max(max(s_red[0][tq], s_red[1][tq]), max(s_red[2][tq], s_red[3][tq]));
+	}
+	int64_t cq[4][4];
+	double inv[4];
+#pragma unroll
+	for (int v = 0; v < 4; ++v) {
+#pragma unroll
+		for (int i = 0; i < 4; ++i) cq[v][i] = s_c[g * 4 + v][i];
+		inv[v] = s_inv[g * 4 + v];
+	}
+	__syncthreads();
+	// pass 2: i-exp values (SoftmaxRowQ15, intmath.cpp:853-889) and the row sums
+	int64_t sum[4] = {0, 0, 0, 0};
+	uint32_t refused = 0;
+	for (int blk = 0; blk < nblk; ++blk) {
+		int p;
+		const v4i s = scores(blk, &p);
+#pragma unroll
+		for (int v = 0; v < 4; ++v) {
+			if (tok_ok[v] && p <= tpos[v]) {
+				const int64_t e = iexp_fast((int64_t)s[v] - rmx[v], cq[v][0], inv[v], cq[v][1], cq[v][2], cq[v][3]);
+				if (e < 0) refused |= 1u << v;
+				else sum[v] += e;
+			}
+		}
+	}
+#pragma unroll
+	for (int v = 0; v < 4; ++v) {
+		for (int o = 8; o > 0; o >>= 1) sum[v] += __shfl_xor(sum[v], o, 16);
+		if (ri == 0) s_red[wave][g * 4 + v] = sum[v];
+	}
+	for (int o = 8; o > 0; o >>= 1) refused |= __shfl_xor(refused, o, 16);
+	if (ri == 0 && refused)
+		for (int v = 0; v < 4; ++v)
+			if (refused >> v & 1) s_rf[g * 4 + v] = 1;
+	__syncthreads();
+	int64_t denom[4];
+	double dinv[4];
+#pragma unroll
+	for (int v = 0; v < 4; ++v) {
+		const int tq = g * 4 + v;
+		const int64_t tot = s_red[0][tq] + s_red[1][tq] + s_red[2][tq] + s_red[3][tq];
+		denom[v] = tot > 1 ? tot : 1;
+		dinv[v] = 1.0 / (double)denom[v];
+		tok_ok[v] = tok_ok[v] && s_rf[tq] == 0;
+	}
+	if (threadIdx.x < nt && s_ok[threadIdx.x] == kOk && s_rf[threadIdx.x] != 0)
+		report_head(a.head_status, ti0.slot, h, kSoftmaxKernelRefusedAfterGateAccepted);
+	// pass 3: Q15 probabilities p = (e << 15) / max(total, 1), then context += P . V
+	constexpr int DTW = (DT + 3) / 4;  // dimension tiles per wave
+	v4i cacc[DTW][3];
+#pragma unroll
+	for (int i = 0; i < DTW; ++i)
+#pragma unroll
+		for (int k = 0; k < 3; ++k) cacc[i][k] = v4i{0, 0, 0, 0};
+	for (int blk = 0; blk < nblk; ++blk) {
+		int p;
+		const v4i s = scores(blk, &p);
+		const int pl = wave * 16 + ri;
+#pragma unroll
+		for (int v = 0; v < 4; ++v) {
+			int32_t pr = 0;
+			if (tok_ok[v] && p <= tpos[v]) {
+				// e <= total, so the quotient is at most 2^15
+				const int64_t e = iexp_fast((int64_t)s[v] - rmx[v], cq[v][0], inv[v], cq[v][1], cq[v][2], cq[v][3]);
+				pr = e == 0 ? 0 : (int32_t)div_rcp(e << 15, denom[v], dinv[v], 32768);
+			}
+			s_p[0][g * 4 + v][pl] = (int8_t)(pr >> 14);
+			s_p[1][g * 4 + v][pl] = (int8_t)((pr >> 7) & 127);
+			s_p[2][g * 4 + v][pl] = (int8_t)(pr & 127);
+		}
+		// V rows [blk*64, blk*64 + 64) transposed into s_vt: a 4x4 byte block per item
+		for (int it = threadIdx.x; it < (KB / 4) * (D / 4); it += 256) {
+			const int p4 = it / (D / 4), d4 = it % (D / 4);
+			uint32_t r[4];
+#pragma unroll
+			for (int i = 0; i < 4; ++i) {
+				const int pr = min(blk * KB + p4 * 4 + i, (int)a.cap - 1);
+				r[i] = *(const uint32_t*)(vbase + (int64_t)pr * D + d4 * 4);
+			}
+#pragma unroll
+			for (int j = 0; j < 4; ++j) {
+				const uint32_t c = ((r[0] >> (8 * j)) & 0xffu) | (((r[1] >> (8 * j)) & 0xffu) << 8) |
+				                   (((r[2] >> (8 * j)) & 0xffu) << 16) | (((r[3] >> (8 * j)) & 0xffu) << 24);
+				*(uint32_t*)&s_vt[d4 * 4 + j][p4 * 4] = c;
+			}
+		}
+		__syncthreads();
+#pragma unroll
+		for (int i = 0; i < DTW; ++i) {
+			const int dt = wave + 4 * i;
+			if (dt < DT) {
+				const v4i b = *(const v4i*)&s_vt[dt * 16 + ri][g * 16];
+#pragma unroll
+				for (int k = 0; k < 3; ++k) {
+					const v4i pa = *(const v4i*)&s_p[k][ri][g * 16];
+					cacc[i][k] = __builtin_amdgcn_mfma_i32_16x16x64_i8(pa, b, cacc[i][k], 0, 0, 0);
+				}
+			}
+		}
+		__syncthreads();
+	}
+	// epilogue: recombine the parts, fold, store; the per-token maximum over the head's dims
+	const int32_t* cf = a.ctx_fold + 3 * h;
+	const int32_t f0 = cf[0], f1 = cf[1], f2 = cf[2];
+#pragma unroll
+	for (int i = 0; i < DTW; ++i) {
+		const int dt = wave + 4 * i;
+		if (dt < DT) {
+			const int d = dt * 16 + ri;
+#pragma unroll
+			for (int v = 0; v < 4; ++v) {
+				const int32_t c = (int32_t)(((uint32_t)cacc[i][0][v] << 14) + ((uint32_t)cacc[i][1][v] << 7) +
+				                            (uint32_t)cacc[i][2][v]);
+				const int64_t f = apply_fold(c, f0, f1, f2);
+				const int tq = g * 4 + v;
+				if (tok_ok[v]) a.ctx_f[(size_t)(t0 + tq) * a.H + (size_t)h * D + d] = sat_i32(f);
+				const uint32_t m = dpp_max16(tok_ok[v] ? sat_abs_u32(f) : 0u);
+				if (ri == 0 && tok_ok[v]) atomicMax(&s_mab[tq], m);
+			}
+		}
+	}
+	__syncthreads();
+	if (threadIdx.x < nt && s_ok[threadIdx.x] == kOk && s_rf[threadIdx.x] == 0)
+		a.ctx_maxpart[(size_t)h * kPartLd + t0 + threadIdx.x] = s_mab[threadIdx.x];
+}
+
 // LoRA intermediate (forward_sites.cpp:1066-1086): u[k] = clamp(amp_fold(A[k] . x))
 __global__ __launch_bounds__(kBlock) void k_lora_u(sslm_launch::LoraUArgs a) {
 	// one block per (token, adapted projection); wave w computes ranks w, w + 4, ...: each lane
@@ -1976,7 +2234,29 @@ static void launch_attention(const AttnArgs& a, hipStream_t s) {
 	}
 }
 
-void attention(const AttnArgs& a, hipStream_t s) { launch_attention<false>(a, s); }
+void attention(const AttnArgs& a, hipStream_t s, bool one_sequence) {
+	if (!one_sequence || !tiled_attention_enabled()) {
+		launch_attention<false>(a, s);
+		return;
+	}
+	const int groups = ((a.M + 15) / 16) * a.NKV, per_xcd = (groups + 7) / 8;
+	const dim3 grid(per_xcd * 8 * (a.NH / a.NKV));  // see the XCD-aware order in k_attention_tiled
+	switch (a.D) {
+		case 32: hipLaunchKernelGGL((k_attention_tiled<32>), grid, dim3(256), 0, s, a); break;
+		case 64: hipLaunchKernelGGL((k_attention_tiled<64>), grid, dim3(256), 0, s, a); break;
+		case 128: hipLaunchKernelGGL((k_attention_tiled<128>), grid, dim3(256), 0, s, a); break;
+		case 256: hipLaunchKernelGGL((k_attention_tiled<256>), grid, dim3(256), 0, s, a); break;
+		default: no_instance("attention", a.D);
+	}
+}
+
+bool tiled_attention_enabled() {
+	static const bool on = [] {
+		const char* e = getenv("SSLM_HIP_TILED_ATTN");
+		return !(e && e[0] == '0');
+	}();
+	return on;
+}
 void attention_decode(const AttnArgs& a, hipStream_t s) { launch_attention<true>(a, s); }
 
 void funnel(const FunnelArgs& a, hipStream_t s) {

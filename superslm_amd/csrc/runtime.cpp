@@ -835,7 +835,7 @@ void run_layers(sslm_model m, Track& w, int M, StreamRef st, int l0, int l1, ssl
 			aa.q_rot = w.q_rot;
 			aa.q_scale = w.q_scale;
 			ProfScope p(s, kProfAttn, 0, 0);
-			sslm_launch::attention(aa, s);
+			sslm_launch::attention(aa, s, !decode);  // prefill chunks: one sequence, consecutive positions
 			ck(hipGetLastError());
 		}
 		{
