@@ -1772,14 +1772,14 @@ __global__ __launch_bounds__(BS) void k_attention(sslm_launch::AttnArgs a, int u
 // below 2^22 in magnitude).  V is staged transposed in LDS ([dim][position], 4x4 byte blocks
 // transposed in registers) so a lane's 16 B operand holds 16 positions of one dimension.
 // The launch must hold one sequence's consecutive positions (a prefill chunk).
-template <int D>
-__global__ __launch_bounds__(256) void k_attention_tiled(sslm_launch::AttnArgs a) {
-	constexpr int TQ = 16, KB = 64, NC = (D + 63) / 64, DT = D / 16, PS = KB + 16, VS = KB + 16;
+template <int D, int NW>
+__global__ __launch_bounds__(64 * NW) void k_attention_tiled(sslm_launch::AttnArgs a) {
+	constexpr int TQ = 16, KB = 16 * NW, NC = (D + 63) / 64, DT = D / 16, PS = KB + 16, VS = KB + 16;
 	__shared__ __attribute__((aligned(16))) int8_t s_p[3][TQ][PS];  // probability parts [part][token][pos]
-	__shared__ __attribute__((aligned(16))) int8_t s_vt[D][VS];     // V^T of the current 64 positions
+	__shared__ __attribute__((aligned(16))) int8_t s_vt[D][VS];     // V^T of the current step's positions
 	__shared__ int64_t s_c[TQ][4];                                   // per token: q_ln2, q_b, q_c, ceiling
 	__shared__ double s_inv[TQ];                                     // per token: 1 / q_ln2
-	__shared__ int64_t s_red[4][TQ];
+	__shared__ int64_t s_red[NW][TQ];
 	__shared__ int32_t s_pos[TQ], s_ok[TQ];
 	__shared__ uint32_t s_mab[TQ], s_rf[TQ];  // per token: |context| maximum, softmax refused
 	__shared__ int32_t s_st;
@@ -1891,7 +1891,9 @@ __global__ __launch_bounds__(256) void k_attention_tiled(sslm_launch::AttnArgs a
 #pragma unroll
 	for (int v = 0; v < 4; ++v) {
 		const int tq = g * 4 + v;
-		rmx[v] = max(max(s_red[0][tq], s_red[1][tq]), max(s_red[2][tq], s_red[3][tq]));
+		rmx[v] = s_red[0][tq];
+#pragma unroll
+		for (int w = 1; w < NW; ++w) rmx[v] = max(rmx[v], s_red[w][tq]);
 	}
 	int64_t cq[4][4];
 	double inv[4];
@@ -1932,7 +1934,9 @@ __global__ __launch_bounds__(256) void k_attention_tiled(sslm_launch::AttnArgs a
 #pragma unroll
 	for (int v = 0; v < 4; ++v) {
 		const int tq = g * 4 + v;
-		const int64_t tot = s_red[0][tq] + s_red[1][tq] + s_red[2][tq] + s_red[3][tq];
+		int64_t tot = 0;
+#pragma unroll
+		for (int w = 0; w < NW; ++w) tot += s_red[w][tq];
 		denom[v] = tot > 1 ? tot : 1;
 		dinv[v] = 1.0 / (double)denom[v];
 		tok_ok[v] = tok_ok[v] && s_rf[tq] == 0;
@@ -1940,7 +1944,7 @@ __global__ __launch_bounds__(256) void k_attention_tiled(sslm_launch::AttnArgs a
 	if (threadIdx.x < nt && s_ok[threadIdx.x] == kOk && s_rf[threadIdx.x] != 0)
 		report_head(a.head_status, ti0.slot, h, kSoftmaxKernelRefusedAfterGateAccepted);
 	// pass 3: Q15 probabilities p = (e << 15) / max(total, 1), then context += P . V
-	constexpr int DTW = (DT + 3) / 4;  // dimension tiles per wave
+	constexpr int DTW = (DT + NW - 1) / NW;  // dimension tiles per wave
 	v4i cacc[DTW][3];
 #pragma unroll
 	for (int i = 0; i < DTW; ++i)
@@ -1963,7 +1967,7 @@ __global__ __launch_bounds__(256) void k_attention_tiled(sslm_launch::AttnArgs a
 			s_p[2][g * 4 + v][pl] = (int8_t)(pr & 127);
 		}
 		// V rows [blk*64, blk*64 + 64) transposed into s_vt: a 4x4 byte block per item
-		for (int it = threadIdx.x; it < (KB / 4) * (D / 4); it += 256) {
+		for (int it = threadIdx.x; it < (KB / 4) * (D / 4); it += 64 * NW) {
 			const int p4 = it / (D / 4), d4 = it % (D / 4);
 			uint32_t r[4];
 #pragma unroll
@@ -1981,13 +1985,16 @@ __global__ __launch_bounds__(256) void k_attention_tiled(sslm_launch::AttnArgs a
 		__syncthreads();
 #pragma unroll
 		for (int i = 0; i < DTW; ++i) {
-			const int dt = wave + 4 * i;
+			const int dt = wave + NW * i;
 			if (dt < DT) {
-				const v4i b = *(const v4i*)&s_vt[dt * 16 + ri][g * 16];
 #pragma unroll
-				for (int k = 0; k < 3; ++k) {
-					const v4i pa = *(const v4i*)&s_p[k][ri][g * 16];
-					cacc[i][k] = __builtin_amdgcn_mfma_i32_16x16x64_i8(pa, b, cacc[i][k], 0, 0, 0);
+				for (int kk = 0; kk < KB / 64; ++kk) {
+					const v4i b = *(const v4i*)&s_vt[dt * 16 + ri][kk * 64 + g * 16];
+#pragma unroll
+					for (int k = 0; k < 3; ++k) {
+						const v4i pa = *(const v4i*)&s_p[k][ri][kk * 64 + g * 16];
+						cacc[i][k] = __builtin_amdgcn_mfma_i32_16x16x64_i8(pa, b, cacc[i][k], 0, 0, 0);
+					}
 				}
 			}
 		}
@@ -1998,7 +2005,7 @@ __global__ __launch_bounds__(256) void k_attention_tiled(sslm_launch::AttnArgs a
 	const int32_t f0 = cf[0], f1 = cf[1], f2 = cf[2];
 #pragma unroll
 	for (int i = 0; i < DTW; ++i) {
-		const int dt = wave + 4 * i;
+		const int dt = wave + NW * i;
 		if (dt < DT) {
 			const int d = dt * 16 + ri;
 #pragma unroll
@@ -2241,11 +2248,14 @@ void attention(const AttnArgs& a, hipStream_t s, bool one_sequence) {
 	}
 	const int groups = ((a.M + 15) / 16) * a.NKV, per_xcd = (groups + 7) / 8;
 	const dim3 grid(per_xcd * 8 * (a.NH / a.NKV));  // see the XCD-aware order in k_attention_tiled
+	// 8 waves (128 positions per step) halve the longest rows' serial chain when the grid is
+	// small; with two or more blocks per CU, 4-wave blocks pack the CUs better
+	const bool wide = (int)grid.x < 2 * 256;  // MI355X: 256 CUs
 	switch (a.D) {
-		case 32: hipLaunchKernelGGL((k_attention_tiled<32>), grid, dim3(256), 0, s, a); break;
-		case 64: hipLaunchKernelGGL((k_attention_tiled<64>), grid, dim3(256), 0, s, a); break;
-		case 128: hipLaunchKernelGGL((k_attention_tiled<128>), grid, dim3(256), 0, s, a); break;
-		case 256: hipLaunchKernelGGL((k_attention_tiled<256>), grid, dim3(256), 0, s, a); break;
+		case 32: if (wide) hipLaunchKernelGGL((k_attention_tiled<32, 8>), grid, dim3(512), 0, s, a); else hipLaunchKernelGGL((k_attention_tiled<32, 4>), grid, dim3(256), 0, s, a); break;
+		case 64: if (wide) hipLaunchKernelGGL((k_attention_tiled<64, 8>), grid, dim3(512), 0, s, a); else hipLaunchKernelGGL((k_attention_tiled<64, 4>), grid, dim3(256), 0, s, a); break;
+		case 128: if (wide) hipLaunchKernelGGL((k_attention_tiled<128, 8>), grid, dim3(512), 0, s, a); else hipLaunchKernelGGL((k_attention_tiled<128, 4>), grid, dim3(256), 0, s, a); break;
+		case 256: if (wide) hipLaunchKernelGGL((k_attention_tiled<256, 8>), grid, dim3(512), 0, s, a); else hipLaunchKernelGGL((k_attention_tiled<256, 4>), grid, dim3(256), 0, s, a); break;
 		default: no_instance("attention", a.D);
 	}
 }
