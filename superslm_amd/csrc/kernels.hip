@@ -2250,7 +2250,9 @@ void attention(const AttnArgs& a, hipStream_t s, bool one_sequence) {
 	const dim3 grid(per_xcd * 8 * (a.NH / a.NKV));  // see the XCD-aware order in k_attention_tiled
 	// 8 waves (128 positions per step) halve the longest rows' serial chain when the grid is
 	// small; with two or more blocks per CU, 4-wave blocks pack the CUs better
-	const bool wide = (int)grid.x < 2 * 256;  // MI355X: 256 CUs
+	// SSLM_HIP_TILED_WAVES=4 or 8 overrides the choice (read per launch; the parity tests run both)
+	const char* fw = getenv("SSLM_HIP_TILED_WAVES");
+	const bool wide = fw && fw[0] ? fw[0] == '8' : (int)grid.x < 2 * 256;  // MI355X: 256 CUs
 	switch (a.D) {
 		case 32: if (wide) hipLaunchKernelGGL((k_attention_tiled<32, 8>), grid, dim3(512), 0, s, a); else hipLaunchKernelGGL((k_attention_tiled<32, 4>), grid, dim3(256), 0, s, a); break;
 		case 64: if (wide) hipLaunchKernelGGL((k_attention_tiled<64, 8>), grid, dim3(512), 0, s, a); else hipLaunchKernelGGL((k_attention_tiled<64, 4>), grid, dim3(256), 0, s, a); break;

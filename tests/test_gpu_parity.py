@@ -238,3 +238,35 @@ def test_option_g_flag_matches_reference(hip_lib, ref_lib):
         assert h[2] == r[2], f"tokens differ: hip {h[2]} ref {r[2]}"
         assert np.array_equal(h[3], r[3]), "KV after decode differs"
         assert h[2] == p[2] and np.array_equal(h[3], p[3])  # the flag changes nothing at the ABI
+
+
+@pytest.mark.parametrize("waves", ["4", "8"])
+def test_tiled_prefill_attention_matches_reference(waves, hip_lib, ref_lib, monkeypatch):
+    """Prefill attention runs over 16-token query tiles in 4- or 8-wave blocks (the grid size picks
+    one; SSLM_HIP_TILED_WAVES forces it): ragged last tiles and chunks that start mid-sequence
+    (D = 128) must leave every KV byte and the following tokens as the reference does."""
+    monkeypatch.setenv("SSLM_HIP_TILED_WAVES", waves)
+    sm, art = synthetic("medium")
+    rng = np.random.default_rng(77)
+    prompt = rng.integers(0, sm.config.vocab, size=90)  # the context cap is 96
+    L = sm.config.layers
+    r = _run(ref_lib, art, prompt, 3, L)
+    for chunk in (90, 37):
+        print(f"case tiled attention waves={waves} chunk={chunk}", flush=True)
+        model = Model(hip_lib, art)
+        pool = model.pool(1)
+        seq = pool.seq()
+        done = 0
+        while done < len(prompt):
+            done += seq.prefill(prompt[done:], chunk_budget=chunk)
+        kv = pool.kv_block(0).copy()
+        toks = []
+        while len(toks) < 3:
+            out = model.decode_step([seq], L)[0]
+            if out >= 0:
+                toks.append(out)
+        assert np.array_equal(kv, r[1]), "KV after prefill differs"
+        assert toks == r[2], f"tokens differ: hip {toks} ref {r[2]}"
+        seq.release()
+        pool.close()
+        model.close()
