@@ -1432,8 +1432,11 @@ __global__ __launch_bounds__(BS) void k_residual_norm(sslm_launch::ResidualArgs 
 // gate/up funnels -> MlpActSite (forward_sites.cpp:796-864) -> act funnel.  The sigmoid of a
 // gate code depends only on the code and the token's gate scale, so the 256 possible values
 // are tabulated per block once the gate plan is known.
+// Rows of up to 9 elements per thread fit in 64 VGPRs: two 1024-thread rows per CU, so a 512-row
+// prefill chunk runs in one round over the CUs.
 template <int BS, int EPT, int RS>
-__global__ __launch_bounds__(BS) void k_mlp_act(sslm_launch::ActArgs a) {
+__global__ __launch_bounds__(BS) __attribute__((amdgpu_waves_per_eu(RS == 0 && EPT <= 9 ? 2048 / BS * BS / 256 : 1)))
+void k_mlp_act(sslm_launch::ActArgs a) {
 	__shared__ uint32_t s_gu[2 * BS / 64], s_a[BS / 64];
 	__shared__ int32_t sig[256];
 	__shared__ int32_t s_silu[1025];  // the SiLU node table, loaded with the row
