@@ -1692,8 +1692,9 @@ __global__ __launch_bounds__(BS) void k_attention(sslm_launch::AttnArgs a, int u
 	// pass 2: i-exp values (SoftmaxRowQ15, intmath.cpp:853-889) and the row sum
 	int64_t sum = 0;
 	uint64_t refused = 0;
+	const double inv_ln2 = c_qln2 >= 1 ? 1.0 / (double)c_qln2 : 0.0;
 	for (int64_t p = threadIdx.x; p < width; p += BS) {
-		int64_t v = iexp_element(ex[p] - mx, c_qln2, c_qb, c_qc, c_M);
+		int64_t v = iexp_fast(ex[p] - mx, c_qln2, inv_ln2, c_qb, c_qc, c_M);  // the row passed check_softmax_width
 		if (v < 0) {
 			refused = 1;
 			v = 0;
@@ -1721,7 +1722,8 @@ __global__ __launch_bounds__(BS) void k_attention(sslm_launch::AttnArgs a, int u
 	}
 	// pass 3: Q15 probabilities p = (e << 15) / max(total, 1)
 	const int64_t denom = sum > 1 ? sum : 1;
-	for (int64_t p = threadIdx.x; p < width; p += BS) ex[p] = div_floor_pos(ex[p] << 15, denom);
+	const double dinv = 1.0 / (double)denom;  // e <= total: quotients at most 2^15
+	for (int64_t p = threadIdx.x; p < width; p += BS) ex[p] = ex[p] == 0 ? 0 : div_rcp(ex[p] << 15, denom, dinv, 32768);
 	__syncthreads();
 	// pass 4: context = sum_p prob * V[p].  A thread owns 16 dimensions (one 16-byte load per
 	// row) of every PG-th position; the loop is unrolled so several rows are in flight.  The sums
