@@ -1,0 +1,38 @@
+// Host check of the exact fast forms in int_math.h (iexp_fast, div_rcp) against the forms they
+// replace (iexp_element, div_floor_pos): random and edge-case inputs; prints the mismatch counts.
+#include "int_math.h"
+#include <cstdlib>
+#include <cstdio>
+#include <random>
+using namespace sslm;
+int main(int argc, char** argv) {
+	const int N = argc > 1 ? atoi(argv[1]) : 4000000;
+	std::mt19937_64 rng(1);
+	long bad = 0, n = 0, nonneg = 0;
+	for (int it = 0; it < N; ++it) {
+		int64_t qln2 = 1 + (int64_t)(rng() % (it % 3 == 0 ? 1000ull : (it % 3 == 1 ? (1ull << 30) : (1ull << 58) / 30)));
+		if (it % 101 == 0) qln2 = kI64Max / 30 + (int64_t)(rng() % 3) - 1;
+		int64_t qb = (int64_t)(rng() % (1ull << 23)) - (1ll << 22);
+		int64_t qc = (int64_t)(rng() % (1ull << 46));
+		if (it % 7 == 0) qb = (int64_t)(rng() % 65536);
+		if ((s128)qb * qb + qc > kSoftmaxMaxSafe) continue;
+		int64_t cm = softmax_ceiling(qb, qc);
+		int64_t sh = -(int64_t)(rng() % (uint64_t)(it % 2 ? 40 * (uint64_t)(qln2 > (1ll << 40) ? (1ll << 40) : qln2) + 1 : 4294967296ull));
+		if (it % 5 == 0) sh = -(int64_t)(rng() % 64);
+		int64_t a = iexp_element(sh, qln2, qb, qc, cm);
+		int64_t b = iexp_fast(sh, qln2, 1.0 / (double)qln2, qb, qc, cm);
+		++n;
+		nonneg += a >= 0;
+		if (a != b) { if (bad < 10) printf("iexp mismatch sh=%lld qln2=%lld qb=%lld qc=%lld: %lld vs %lld\n", (long long)sh, (long long)qln2, (long long)qb, (long long)qc, (long long)a, (long long)b); ++bad; }
+	}
+	printf("iexp: %ld cases (%ld accepted), %ld mismatches\n", n, nonneg, bad);
+	long bd = 0;
+	for (int it = 0; it < N; ++it) {
+		int64_t d = 1 + (int64_t)(rng() % (it % 2 ? (1ull << 60) : 100000ull));
+		int64_t e = (int64_t)(rng() % (uint64_t)(d < (1ll << 47) ? d + 1 : (1ll << 47)));
+		if (it % 3 == 0) e = d < (1ll << 47) ? d : e;
+		int64_t q1 = div_floor_pos(e << 15, d), q2 = div_rcp(e << 15, d, 1.0 / (double)d, 32768);
+		if (q1 != q2) { if (bd < 10) printf("div mismatch %lld/%lld: %lld vs %lld\n", (long long)e, (long long)d, (long long)q1, (long long)q2); ++bd; }
+	}
+	printf("div: %ld mismatches\n", bd);
+}
