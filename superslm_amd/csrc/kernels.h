@@ -34,7 +34,7 @@ struct Segment {
 };
 
 constexpr int kMaxRank = 64;
-constexpr int kPartLd = 512;  // token stride of the per-tile partial maxima (>= tokens per launch)
+constexpr int kPartLd = 8192;  // token stride of the per-tile partial maxima (>= tokens per launch)
 constexpr int kMaxSeg = 3;
 constexpr int kFunnelMaxN = 8192;  // widest row the standalone funnel kernel covers
 
@@ -164,8 +164,16 @@ struct QkvPostArgs {
 	Scale* q_scale;           // [M]
 	unsigned long long* sat;  // [slots]
 	int32_t* status;
+	// Staged landing (prefill spans): when set, the landed K/V codes go to kv_stage
+	// ([M][K heads | V heads][D]) and the clamp counts to sat_stage[M] instead of the pool and
+	// `sat`; kv_commit() then writes them once every token's q funnel has passed.
+	int8_t* kv_stage;
+	uint32_t* sat_stage;
 };
 void qkv_post(const QkvPostArgs& a, hipStream_t s);
+// Writes the staged K/V rows of a prefill span into the pool and adds the clamp counts, unless
+// the slot's status holds a refusal; always clears sat_stage.
+void kv_commit(const QkvPostArgs& a, hipStream_t s);
 
 struct AttnArgs {
 	int M, H, NH, NKV, D;
@@ -289,6 +297,25 @@ struct LoraUArgs {
 	int8_t* u[3];             // [M, kMaxRank]
 };
 void lora_u(const LoraUArgs& a, hipStream_t s);
+
+// Snapshot (or restore) of what one decode launch sequence changes for each of its tokens: the
+// slot's stream row (H codes), scale and clamp counter, and the K/V rows of layers [l0, l1) at
+// the token's position.
+struct SlotCopyArgs {
+	const TokenInfo* tok;  // [n]
+	int8_t* codes;         // [slots, H]
+	Scale* scale;
+	unsigned long long* sat;
+	int8_t* snap_codes;    // [slots, H]
+	Scale* snap_scale;
+	unsigned long long* snap_sat;
+	int8_t* kv_pool;
+	int64_t block_bytes, cap;
+	int32_t H, NKV, D, l0, l1;
+	int8_t* snap_kv;       // [slots, snap_kv_ld]: layer l's K then V rows at l * 2 * NKV * D
+	int64_t snap_kv_ld;
+};
+void slot_state_copy(const SlotCopyArgs& a, int n, bool restore, hipStream_t s);
 
 // per-tile argmax keys -> token ids (lowest index among equal maxima)
 void argmax_finalize(const unsigned long long* keys, int ntiles, int M, int32_t* out_tokens, hipStream_t s);

@@ -1250,6 +1250,20 @@ __global__ __launch_bounds__(BS) void k_qkv_post(sslm_launch::QkvPostArgs a) {
 		}
 	}
 	if (threadIdx.x == 0) a.q_scale[t] = plan.out;
+	if (a.kv_stage) {  // prefill span: staged until every token's q funnel has passed
+		int8_t* row = a.kv_stage + (size_t)t * 2 * KVH;
+#pragma unroll
+		for (int k = 0; k < 2; ++k) {
+			const int p = threadIdx.x + k * BS;
+			if (p < KVH / 2) {
+				*(char2*)(row + 2 * p) = make_char2(kq[k][0], kq[k][1]);
+				*(char2*)(row + KVH + 2 * p) = make_char2(vq[k][0], vq[k][1]);
+			}
+		}
+		sat = wave_sum_i64((int64_t)sat);
+		if ((threadIdx.x & 63) == 0 && sat) atomicAdd(&a.sat_stage[t], (uint32_t)sat);
+		return;
+	}
 	int8_t* blk = a.kv_pool + (int64_t)ti.block * a.block_bytes;
 	const int64_t half = a.cap * (int64_t)KVH;
 	int8_t* kstore = blk + (int64_t)a.layer * half * 2;
@@ -1267,6 +1281,66 @@ __global__ __launch_bounds__(BS) void k_qkv_post(sslm_launch::QkvPostArgs a) {
 	}
 	sat = wave_sum_i64((int64_t)sat);
 	if ((threadIdx.x & 63) == 0 && sat) atomicAdd(&a.sat[ti.slot], (unsigned long long)sat);
+}
+
+__global__ __launch_bounds__(256) void k_slot_state_copy(sslm_launch::SlotCopyArgs a, int restore) {
+	const TokenInfo ti = a.tok[blockIdx.x];
+	const int64_t slot = ti.slot;
+	int8_t* live = a.codes + slot * a.H;
+	int8_t* snap = a.snap_codes + slot * a.H;
+	for (int i = threadIdx.x; i < a.H; i += blockDim.x) {
+		if (restore) live[i] = snap[i];
+		else snap[i] = live[i];
+	}
+	if (threadIdx.x == 0) {
+		if (restore) {
+			a.scale[slot] = a.snap_scale[slot];
+			a.sat[slot] = a.snap_sat[slot];
+		} else {
+			a.snap_scale[slot] = a.scale[slot];
+			a.snap_sat[slot] = a.sat[slot];
+		}
+	}
+	// the K and V rows of layers [l0, l1) at the token's position, 16 bytes per thread
+	const int KVH = a.NKV * a.D, per_layer = 2 * KVH;
+	if (ti.pos < 0 || ti.pos >= a.cap) return;
+	const int64_t half = a.cap * (int64_t)KVH;
+	int8_t* blk = a.kv_pool + (int64_t)ti.block * a.block_bytes;
+	int8_t* srow = a.snap_kv + slot * a.snap_kv_ld;
+	for (int c = threadIdx.x; c < (a.l1 - a.l0) * per_layer / 16; c += blockDim.x) {
+		const int e = c * 16, l = a.l0 + e / per_layer, r = e % per_layer;
+		const int kvsel = r >= KVH, hd = (r - kvsel * KVH) / a.D, d = (r - kvsel * KVH) % a.D;
+		int4* kvp = (int4*)(blk + (int64_t)l * half * 2 + kvsel * half + ((int64_t)hd * a.cap + ti.pos) * a.D + d);
+		int4* sp = (int4*)(srow + (int64_t)l * per_layer + r);
+		if (restore) *kvp = *sp;
+		else *sp = *kvp;
+	}
+}
+
+// One block per token of a prefill span: the staged K/V row into the pool (16 bytes per
+// thread), the token's clamp count into the slot's counter.
+__global__ __launch_bounds__(256) void k_kv_commit(sslm_launch::QkvPostArgs a) {
+	__shared__ int32_t s_st;
+	const int t = blockIdx.x;
+	const TokenInfo ti = a.tok[t];
+	const int D = a.D, KVH = a.NKV * D;
+	if (threadIdx.x == 0) {
+		s_st = a.status[ti.slot];
+		const uint32_t sat = a.sat_stage[t];
+		a.sat_stage[t] = 0;
+		if (s_st == 0 && sat) atomicAdd(&a.sat[ti.slot], (unsigned long long)sat);
+	}
+	__syncthreads();
+	if (s_st != 0) return;
+	const int8_t* row = a.kv_stage + (size_t)t * 2 * KVH;
+	const int64_t half = a.cap * (int64_t)KVH;
+	int8_t* kstore = a.kv_pool + (int64_t)ti.block * a.block_bytes + (int64_t)a.layer * half * 2;
+	for (int c = threadIdx.x; c < 2 * KVH / 16; c += blockDim.x) {
+		const int e = c * 16;              // element of [K heads | V heads]
+		const int kvsel = e >= KVH;        // 0: K, 1: V
+		const int hd = (e - kvsel * KVH) / D, d = (e - kvsel * KVH) % D;
+		*(int4*)(kstore + kvsel * half + ((int64_t)hd * a.cap + ti.pos) * D + d) = *(const int4*)(row + e);
+	}
 }
 
 // funnel over an int32 fold-output row (checked_chain_funnel.cpp:257-364)
@@ -2228,6 +2302,14 @@ void qkv_post(const QkvPostArgs& a, hipStream_t s) {
 	X(1) X(2) X(4) X(8)
 #undef X
 	no_instance("qkv_post", a.H);
+}
+
+void slot_state_copy(const SlotCopyArgs& a, int n, bool restore, hipStream_t s) {
+	hipLaunchKernelGGL(k_slot_state_copy, dim3(n), dim3(256), 0, s, a, restore ? 1 : 0);
+}
+
+void kv_commit(const QkvPostArgs& a, hipStream_t s) {
+	hipLaunchKernelGGL(k_kv_commit, dim3(a.M), dim3(256), 0, s, a);
 }
 
 template <bool FUSED>

@@ -190,12 +190,17 @@ struct Track {
 	uint32_t *mx_q, *mx_ctx, *mx_o, *mx_gu, *mx_down;  // per (16-column tile, token) partial maxima
 	unsigned long long* argmax_key;                    // [token][tile], head tracks only
 	int32_t* raw_part;  // split-K partial planes, consumed by the next row kernel
+	int8_t* kv_stage;    // prefill tracks: landed K/V rows awaiting kv_commit [T][2 * KVH]
+	uint32_t* sat_stage;  // prefill tracks: their clamp counts [T]
 	int8_t* lora_u[3];
 	TokenInfo* lg_tok;    // head tracks: tokens of the joined final norm + head
 	int32_t* lg_slot;
 	const uint8_t** lg_mask;  // head tracks: per token its schema mask page in HBM, or null
 	hipEvent_t done = nullptr;
 	hipEvent_t fork = nullptr;
+	bool prefill = false;    // carries prefill spans (one sequence, consecutive positions)
+	std::vector<void*> own;  // device buffers of this track
+	int gen = 0;             // bumped when the buffers are reallocated (graph keys carry it)
 };
 
 // Damped-greedy anti-LM (src/damped_greedy_antilm.cpp): for each order n in 1..max_order, the
@@ -318,9 +323,15 @@ struct sslm_model_s {
 	unsigned long long* sat;  // [kSlotCapacity]
 	int32_t* status;        // [kSlotCapacity]
 	int32_t* head_status;   // [kSlotCapacity] attention-stage refusals awaiting the ctx funnel
+	int8_t* snap_codes;     // [kSlotCapacity, H] stream rows as a decode call found them
+	Scale* snap_scale;      // [kSlotCapacity]
+	unsigned long long* snap_sat;  // [kSlotCapacity]
+	int8_t* snap_kv;        // [kSlotCapacity, L * 2 * KVH] K/V rows at the call's position
 	std::vector<int> free_slots;
-	std::vector<Track> tracks;  // tracks[0]: prefill and head; all: decode token groups
-	std::map<std::string, hipGraphExec_t> graphs;  // captured decode submissions by shape
+	std::vector<Track> tracks;  // tracks[0]: the LM head; all: decode token groups
+	Track prefill;              // prefill spans: capacity grown on demand up to kMaxPrefillTokens
+	std::map<std::string, hipGraphExec_t> graphs;  // captured submissions by shape
+	std::map<std::string, int> graph_seen;         // prefill shapes seen (captured on a repeat)
 	int8_t* pool_dev = nullptr;  // KV pool of the launch sequence being recorded
 	std::atomic<int> live_refs{0};
 	std::mutex mu;  // serializes GPU submission on this model
@@ -826,10 +837,19 @@ void run_layers(sslm_model m, Track& w, int M, StreamRef st, int l0, int l1, ssl
 			a.status = m->status;
 			a.kv_pool = m->pool_dev;
 			a.raw = raw;
+			// A prefill span lands its K/V only once every token's q funnel has passed, as the
+			// reference runs every q funnel of the span before the first landing
+			// (forward_sites.cpp:2188-2240).
+			a.kv_stage = w.kv_stage;
+			a.sat_stage = w.sat_stage;
 			{
 				ProfScope p(s, kProfRow, 0, 0);
 				sslm_launch::qkv_post(a, s);
 				ck(hipGetLastError());
+				if (a.kv_stage) {
+					sslm_launch::kv_commit(a, s);
+					ck(hipGetLastError());
+				}
 			}
 			sslm_launch::AttnArgs aa = attn_args(m, w, l, M);
 			aa.q_rot = w.q_rot;
@@ -1089,7 +1109,7 @@ void append_le(std::vector<T>* out, const TensorView& t) {
 
 // Upload one model (layer_marshal.h:141-330 naming; src/sslm_abi.cpp:609-676 embed/head/final).
 void alloc_track(sslm_model m, Track& w, int T, bool head) {
-	auto& own = m->owned;
+	auto& own = w.own;
 	const int H = m->H, I = m->I, KVH = m->KVH;
 	w.capacity = T;
 	w.tok = dalloc<TokenInfo>(T, &own);
@@ -1142,13 +1162,27 @@ void alloc_track(sslm_model m, Track& w, int T, bool head) {
 		w.raw_part = elems ? dalloc<int32_t>(elems, &own) : nullptr;
 	}
 	for (int i = 0; i < 3; ++i) w.lora_u[i] = dalloc<int8_t>((size_t)T * kMaxRank, &own);
-	w.attn_scratch = sslm_launch::attention_in_lds(m->cap) ? nullptr : dalloc<int64_t>((size_t)T * m->NH * m->cap, &own);
+	w.kv_stage = w.prefill ? dalloc<int8_t>((size_t)T * 2 * KVH, &own) : nullptr;
+	w.sat_stage = w.prefill ? dalloc<uint32_t>(T, &own) : nullptr;
+	// the per-token attention keeps its rows in global scratch when they exceed LDS; a prefill
+	// track whose spans take the query-tiled kernel (no stored rows) needs none
+	const bool rows_in_scratch = !sslm_launch::attention_in_lds(m->cap) && !(w.prefill && sslm_launch::tiled_attention_enabled());
+	w.attn_scratch = rows_in_scratch ? dalloc<int64_t>((size_t)T * m->NH * m->cap, &own) : nullptr;
 	w.lg_tok = head ? dalloc<TokenInfo>(T, &own) : nullptr;
 	w.lg_slot = head ? dalloc<int32_t>(T, &own) : nullptr;
 	w.lg_mask = head ? (const uint8_t**)dalloc<uintptr_t>(T, &own) : nullptr;
-	ck(hipStreamCreate(&w.stream));
-	ck(hipEventCreateWithFlags(&w.done, hipEventDisableTiming));
-	ck(hipEventCreateWithFlags(&w.fork, hipEventDisableTiming));
+	if (!w.stream) {
+		ck(hipStreamCreate(&w.stream));
+		ck(hipEventCreateWithFlags(&w.done, hipEventDisableTiming));
+		ck(hipEventCreateWithFlags(&w.fork, hipEventDisableTiming));
+	}
+	++w.gen;
+}
+
+void free_track_buffers(Track& w) {
+	for (void* p : w.own) (void)hipFree(p);
+	w.own.clear();
+	w.capacity = 0;
 }
 
 bool build_device_model(sslm_model m, std::string* err) {
@@ -1369,6 +1403,10 @@ bool build_device_model(sslm_model m, std::string* err) {
 	m->sat = dalloc<unsigned long long>(kSlotCapacity, &own);
 	m->status = dalloc<int32_t>(kSlotCapacity, &own);
 	m->head_status = dalloc<int32_t>(kSlotCapacity, &own);
+	m->snap_codes = dalloc<int8_t>((size_t)kSlotCapacity * m->H, &own);
+	m->snap_scale = dalloc<Scale>(kSlotCapacity, &own);
+	m->snap_sat = dalloc<unsigned long long>(kSlotCapacity, &own);
+	m->snap_kv = dalloc<int8_t>((size_t)kSlotCapacity * m->L * 2 * m->KVH, &own);
 	{
 		const std::vector<int32_t> none(kSlotCapacity, kHeadStatusNone);
 		ck(hipMemcpy(m->head_status, none.data(), none.size() * sizeof(int32_t), hipMemcpyHostToDevice));
@@ -1381,64 +1419,159 @@ bool build_device_model(sslm_model m, std::string* err) {
 	return true;
 }
 
+// Every stream of the model: decode tracks and the prefill track.
+template <typename F>
+void for_each_track(sslm_model m, F&& f) {
+	for (Track& w : m->tracks) f(w);
+	f(m->prefill);
+}
+
+void sync_tracks(sslm_model m) {
+	for_each_track(m, [](Track& w) {
+		if (w.stream) ck(hipStreamSynchronize(w.stream));
+	});
+}
+
+// Destroys every captured graph once no launch of one can still be in flight.
+void drop_graphs(sslm_model m) {
+	sync_tracks(m);
+	for (auto& kv : m->graphs) (void)hipGraphExecDestroy(kv.second);
+	m->graphs.clear();
+	m->graph_seen.clear();
+}
+
 void free_model(sslm_model m) {
-	for (Track& w : m->tracks)
+	for_each_track(m, [](Track& w) {
 		if (w.stream) (void)hipStreamSynchronize(w.stream);
+	});
+	for (auto& kv : m->graphs) (void)hipGraphExecDestroy(kv.second);
+	m->graphs.clear();
 	for (void* p : m->owned) (void)hipFree(p);
 	m->owned.clear();
-	for (Track& w : m->tracks) {
+	for_each_track(m, [](Track& w) {
+		free_track_buffers(w);
 		if (w.stream) (void)hipStreamDestroy(w.stream);
 		if (w.done) (void)hipEventDestroy(w.done);
 		if (w.fork) (void)hipEventDestroy(w.fork);
 		w.stream = nullptr;
 		w.done = nullptr;
 		w.fork = nullptr;
+	});
+}
+
+constexpr size_t kGraphCache = 64;
+
+bool graphs_enabled() {
+	static const bool v = [] {
+		const char* e = getenv("SSLM_HIP_GRAPHS");
+		return !(e && atoi(e) == 0);
+	}();
+	return v;
+}
+
+// The captured graph for `key`, recorded from `body` on stream `s` when absent.  A full cache is
+// emptied first -- after every stream has drained, since graphs launched earlier in the same
+// submission may still be running.
+hipGraphExec_t graph_of(sslm_model m, const std::string& key, hipStream_t s, const std::function<void()>& body) {
+	auto it = m->graphs.find(key);
+	if (it != m->graphs.end()) return it->second;
+	if (m->graphs.size() >= kGraphCache) drop_graphs(m);
+	hipGraph_t graph = nullptr;
+	ck(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+	try {
+		body();
+	} catch (...) {
+		(void)hipStreamEndCapture(s, &graph);
+		if (graph) (void)hipGraphDestroy(graph);
+		throw;
 	}
-	for (auto& kv : m->graphs) (void)hipGraphExecDestroy(kv.second);
-	m->graphs.clear();
+	ck(hipStreamEndCapture(s, &graph));
+	hipGraphExec_t exec = nullptr;
+	const hipError_t e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+	(void)hipGraphDestroy(graph);
+	ck(e);
+	return m->graphs.emplace(key, exec).first->second;
 }
 // Upload the TokenInfo of one launch sequence.
 void put_tokens(Track& w, const std::vector<TokenInfo>& ti) {
 	ck(hipMemcpyAsync(w.tok, ti.data(), ti.size() * sizeof(TokenInfo), hipMemcpyHostToDevice, w.stream));
 }
 
-// prefill of `n` admitted tokens (PrefillWholeTokensImpl, src/sslm_abi.cpp:1481-1535)
+// Tokens one prefill launch sequence takes: the whole admitted span up to kPartLd (the token
+// stride of the funnels' partial maxima), unless the per-token attention must keep rows longer
+// than LDS holds in global scratch (query-tiled attention switched off at a long context cap).
+int prefill_limit(sslm_model m) {
+	return (sslm_launch::attention_in_lds(m->cap) || sslm_launch::tiled_attention_enabled()) ? kPartLd : kMaxTokens;
+}
+
+// The prefill track with room for T tokens (grown in steps of kMaxTokens; graphs that captured
+// the old buffers are dropped first).
+Track& prefill_track(sslm_model m, int T) {
+	Track& w = m->prefill;
+	if (w.capacity >= T) return w;
+	drop_graphs(m);
+	free_track_buffers(w);
+	w.prefill = true;
+	alloc_track(m, w, (T + kMaxTokens - 1) / kMaxTokens * kMaxTokens, false);
+	return w;
+}
+
+// Prefill of `n` admitted tokens (PrefillWholeTokensImpl, src/sslm_abi.cpp:1481-1545).  The
+// reference embeds every admitted token, then runs one batched layer loop over all of them, and
+// commits nothing when any step refuses.  Here the span is one launch sequence (embed, then every
+// layer site over all its tokens) when it fits prefill_limit(), else consecutive spans of that
+// many tokens; the sequence's state (stream row, context length) is committed once, after every
+// span has passed.  A repeated span shape replays a captured graph.
 sslm_status prefill_tokens(sslm_model m, sslm_seq s, const int32_t* tokens, int n) {
-	Track& w = m->tracks[0];
 	m->pool_dev = s->pool->dev;
+	const int P = prefill_limit(m);
+	Track& w = prefill_track(m, std::min(n, P));
 	const int H = m->H;
+	std::deque<std::vector<TokenInfo>> staged;  // host copies stay alive until the sync below
 	int done = 0;
+	int last_T = 0;
 	while (done < n) {
-		const int T = std::min(kMaxTokens, n - done);
-		std::vector<TokenInfo> ti(T);
+		const int T = std::min(P, n - done);
+		staged.emplace_back(T);
+		std::vector<TokenInfo>& ti = staged.back();
 		for (int t = 0; t < T; ++t) ti[t] = TokenInfo{s->context_length + done + t, s->slot, (int32_t)s->block};
-		put_tokens(w, ti);
+		ck(hipMemcpyAsync(w.tok, ti.data(), T * sizeof(TokenInfo), hipMemcpyHostToDevice, w.stream));
 		ck(hipMemcpyAsync(w.tok_ids, tokens + done, T * 4, hipMemcpyHostToDevice, w.stream));
-		{
-			ProfScope p(w.stream, kProfRow, 0, 0);
-			sslm_launch::embed(w.tok_ids, T, m->embed, H, m->V, m->embed_site, w.hid_chunk, w.ident,
-			                   w.hid_chunk_scale, w.ident, w.tok, m->status, w.stream);
-			ck(hipGetLastError());
-		}
-		run_layers(m, w, T, StreamRef{w.hid_chunk, w.hid_chunk_scale, w.ident}, 0, m->L, s->adapter, false);
-		int32_t word = 0;
-		ck(hipMemcpyAsync(&word, m->status + s->slot, 4, hipMemcpyDeviceToHost, w.stream));
-		ck(hipStreamSynchronize(w.stream));
-		prof_collect();
-		if (word != 0) {
-			ck(hipMemset(m->status + s->slot, 0, 4));
-			return map_forward_status(word);
-		}
-		// the chunk's last row becomes the sequence's stream state
-		ck(hipMemcpyAsync(m->stream_codes + (size_t)s->slot * H, w.hid_chunk + (size_t)(T - 1) * H, H,
-		                  hipMemcpyDeviceToDevice, w.stream));
-		ck(hipMemcpyAsync(m->stream_scale + s->slot, w.hid_chunk_scale + (T - 1), sizeof(Scale),
-		                  hipMemcpyDeviceToDevice, w.stream));
-		s->context_length += T;
-		s->layer_index = 0;
+		auto body = [&]() {
+			{
+				ProfScope p(w.stream, kProfRow, 0, 0);
+				sslm_launch::embed(w.tok_ids, T, m->embed, H, m->V, m->embed_site, w.hid_chunk, w.ident,
+				                   w.hid_chunk_scale, w.ident, w.tok, m->status, w.stream);
+				ck(hipGetLastError());
+			}
+			run_layers(m, w, T, StreamRef{w.hid_chunk, w.hid_chunk_scale, w.ident}, 0, m->L, s->adapter, false);
+		};
+		const std::string key = "p|" + std::to_string(T) + "|" + std::to_string((uintptr_t)s->adapter) + "|" +
+		                        std::to_string((uintptr_t)m->pool_dev) + "|" + std::to_string(w.gen);
+		// a span shape is captured the second time it is seen: one-off shapes launch directly
+		if (graphs_enabled() && !prof_enabled() && m->graph_seen[key]++ > 0)
+			ck(hipGraphLaunch(graph_of(m, key, w.stream, body), w.stream));
+		else
+			body();
 		done += T;
+		last_T = T;
 	}
+	int32_t word = 0;
+	ck(hipMemcpyAsync(&word, m->status + s->slot, 4, hipMemcpyDeviceToHost, w.stream));
 	ck(hipStreamSynchronize(w.stream));
+	prof_collect();
+	if (word != 0) {
+		ck(hipMemset(m->status + s->slot, 0, 4));
+		return map_forward_status(word);
+	}
+	// the span's last row becomes the sequence's stream state
+	ck(hipMemcpyAsync(m->stream_codes + (size_t)s->slot * H, w.hid_chunk + (size_t)(last_T - 1) * H, H,
+	                  hipMemcpyDeviceToDevice, w.stream));
+	ck(hipMemcpyAsync(m->stream_scale + s->slot, w.hid_chunk_scale + (last_T - 1), sizeof(Scale),
+	                  hipMemcpyDeviceToDevice, w.stream));
+	ck(hipStreamSynchronize(w.stream));
+	s->context_length += n;
+	s->layer_index = 0;
 	return SSLM_OK;
 }
 
@@ -1527,7 +1660,12 @@ sslm_status sslm_kv_pool_create(sslm_model model, void* buf, size_t buf_size, ui
 sslm_status sslm_kv_pool_destroy(sslm_kv_pool pool) {
 	if (!pool) return SSLM_INVALID_ARGUMENT;
 	if (pool->live_refs.load() != 0) return SSLM_POOL_HAS_LIVE_HANDLES;
-	(void)hipStreamSynchronize(pool->model->tracks[0].stream);
+	{
+		std::lock_guard<std::mutex> lk(pool->model->mu);
+		for_each_track(pool->model, [](Track& w) {
+			if (w.stream) (void)hipStreamSynchronize(w.stream);
+		});
+	}
 	(void)hipFree(pool->dev);
 	pool->model->live_refs--;
 	delete pool;
@@ -1713,20 +1851,34 @@ sslm_status sslm_prefill(sslm_model model, sslm_seq seq, const int32_t* tokens, 
 	});
 }
 
+sslm_launch::SlotCopyArgs slot_copy_args(sslm_model m, const TokenInfo* tok, int l0, int l1) {
+	sslm_launch::SlotCopyArgs a{};
+	a.tok = tok;
+	a.codes = m->stream_codes;
+	a.scale = m->stream_scale;
+	a.sat = m->sat;
+	a.snap_codes = m->snap_codes;
+	a.snap_scale = m->snap_scale;
+	a.snap_sat = m->snap_sat;
+	a.kv_pool = m->pool_dev;
+	a.block_bytes = (int64_t)m->block_bytes;
+	a.cap = m->cap;
+	a.H = m->H;
+	a.NKV = m->NKV;
+	a.D = m->D;
+	a.l0 = l0;
+	a.l1 = l1;
+	a.snap_kv = m->snap_kv;
+	a.snap_kv_ld = (int64_t)m->L * 2 * m->KVH;
+	return a;
+}
+
 // Decode tokens are independent, so a batch's layer work can be dealt to up to kTracks streams
 // as token groups of at least track_min() tokens each, so that one group's latency-bound row
 // kernels could overlap another's GEMVs.  Measured on MI355X this is slower than one group (the
 // groups' kernels do not overlap usefully), so one track is the default and SSLM_HIP_TRACKS
 // opts in.  Everything -- embeds, layers, the joined LM head and the status read-back -- is one
 // submission with one host sync.
-bool graphs_enabled() {
-	static const bool v = [] {
-		const char* e = getenv("SSLM_HIP_GRAPHS");
-		return !(e && atoi(e) == 0);
-	}();
-	return v;
-}
-constexpr size_t kGraphCache = 64;
 
 int track_limit() {
 	static const int v = [] {
@@ -1851,6 +2003,9 @@ static sslm_status decode_batch(sslm_model m, sslm_seq* seqs, int32_t n, const s
 		const Unit& un = units[u];
 		Track& w = m->tracks[u % ntr];
 		const int M = (int)un.idx.size();
+		// snapshot of the rows this unit changes, restored if an earlier sequence of the call refuses
+		sslm_launch::slot_state_copy(slot_copy_args(m, w.tok, (int)un.l0, (int)un.l1), M, false, w.stream);
+		ck(hipGetLastError());
 		if (un.l0 == 0) {  // embed the pending token (src/sslm_abi.cpp:2237-2249)
 			ProfScope p(w.stream, kProfRow, 0, 0);
 			sslm_launch::embed(w.tok_ids, M, m->embed, m->H, m->V, m->embed_site, m->stream_codes, w.slot_idx,
@@ -1902,24 +2057,6 @@ static sslm_status decode_batch(sslm_model m, sslm_seq* seqs, int32_t n, const s
 		// Each unit is its own captured graph on its own track's stream (a graph runs its nodes
 		// in order on the stream it is launched on, so one graph per track keeps the tracks
 		// concurrent), forked from and joined back into track 0; the head is one more graph.
-		auto graph_of = [&](const std::string& key, hipStream_t s, const std::function<void()>& body) {
-			auto it = m->graphs.find(key);
-			if (it == m->graphs.end()) {
-				if (m->graphs.size() >= kGraphCache) {
-					for (auto& kv : m->graphs) (void)hipGraphExecDestroy(kv.second);
-					m->graphs.clear();
-				}
-				hipGraph_t graph = nullptr;
-				ck(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
-				body();
-				ck(hipStreamEndCapture(s, &graph));
-				hipGraphExec_t exec = nullptr;
-				ck(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0));
-				(void)hipGraphDestroy(graph);
-				it = m->graphs.emplace(key, exec).first;
-			}
-			return it->second;
-		};
 		const size_t nt = std::min(ntr, units.size());
 		ck(hipEventRecord(t0.fork, t0.stream));
 		for (size_t k = 1; k < nt; ++k) ck(hipStreamWaitEvent(m->tracks[k].stream, t0.fork, 0));
@@ -1930,7 +2067,7 @@ static sslm_status decode_batch(sslm_model m, sslm_seq* seqs, int32_t n, const s
 				const std::string key = "u" + std::to_string(u % ntr) + "|" + std::to_string(un.idx.size()) + "|" +
 				                        std::to_string(un.l0) + "|" + std::to_string(un.l1) + "|" +
 				                        std::to_string((uintptr_t)un.ad) + "|" + std::to_string((uintptr_t)m->pool_dev);
-				ck(hipGraphLaunch(graph_of(key, w.stream, [&] { launch_unit(u); }), w.stream));
+				ck(hipGraphLaunch(graph_of(m, key, w.stream, [&] { launch_unit(u); }), w.stream));
 			} else {
 				launch_unit(u);
 			}
@@ -1942,7 +2079,7 @@ static sslm_status decode_batch(sslm_model m, sslm_seq* seqs, int32_t n, const s
 		if (!lg.empty()) {
 			const int M = (int)lg.size();
 			if (use_graph)
-				ck(hipGraphLaunch(graph_of("lg|" + std::to_string(M) + (rows_needed ? "|r" : "") + (masked ? "|m" : ""), t0.stream,
+				ck(hipGraphLaunch(graph_of(m, "lg|" + std::to_string(M) + (rows_needed ? "|r" : "") + (masked ? "|m" : ""), t0.stream,
 				                           [&] { launch_logits(M); }),
 				                  t0.stream));
 			else launch_logits(M);
@@ -1977,42 +2114,48 @@ static sslm_status decode_batch(sslm_model m, sslm_seq* seqs, int32_t n, const s
 	ck(hipStreamSynchronize(t0.stream));
 	prof_collect();
 
-	// A failure leaves its sequence at the failing layer (its last commit); every other sequence
-	// of the batch advances normally.  Layer failures carry their layer in the status word, head
-	// failures the layer count.
-	sslm_status first_err = SSLM_OK;
-	std::vector<char> failed_layers(n, 0), failed_head(n, 0);
-	for (int i = 0; i < n; ++i) {
-		const int32_t w = words[seqs[i]->slot];
-		if (w == 0) continue;
-		if ((w >> 8) < m->L) failed_layers[i] = 1;
-		else failed_head[i] = 1;
-		ck(hipMemsetAsync(m->status + seqs[i]->slot, 0, 4, t0.stream));
-		if (first_err == SSLM_OK) first_err = map_forward_status(w);
-		out_tokens[i] = -1;
-	}
-	for (auto& g : groups) {
-		const uint32_t l1 = std::min<uint32_t>(m->L, g.first + budget);
+	// Outcomes in call order.  The reference runs the sequences one after another and returns at
+	// the first refusal (src/sslm_abi.cpp:2213-2430): the refusing sequence keeps its last
+	// commit (a layer failure leaves it at the failing layer; a head failure after its layers
+	// at layer L with the context advanced), its output entry and every later sequence are left
+	// as they were.  The batch ran every sequence at once, so a later sequence's device stream
+	// row, scale and clamp counter are restored from the snapshot its unit took; its KV rows at
+	// its uncommitted position keep this call's values.  Layer failures carry their layer in the
+	// status word, head failures the layer count.
+	std::vector<int> in_lg(n, -1);
+	for (size_t k = 0; k < lg.size(); ++k) in_lg[lg[k]] = (int)k;
+	std::vector<uint32_t> unit_l1(n, 0);
+	std::vector<char> in_unit(n, 0);
+	for (auto& g : groups)
 		for (int i : g.second) {
-			if (failed_layers[i]) {
-				seqs[i]->layer_index = (uint32_t)std::min(words[seqs[i]->slot] >> 8, m->L);
-				continue;
-			}
-			seqs[i]->layer_index = l1;
-			if (l1 < (uint32_t)m->L) out_tokens[i] = -1;
-			else seqs[i]->context_length += 1;
+			unit_l1[i] = std::min<uint32_t>(m->L, g.first + budget);
+			in_unit[i] = 1;
 		}
-	}
-	for (size_t k = 0; k < lg.size(); ++k) {
-		const int i = lg[k];
-		if (failed_layers[i]) continue;
+	for (int i = 0; i < n; ++i)
+		if (words[seqs[i]->slot] != 0) ck(hipMemsetAsync(m->status + seqs[i]->slot, 0, 4, t0.stream));
+	sslm_status first_err = SSLM_OK;
+	int stop_at = n;  // sequences from here on are left untouched
+	for (int i = 0; i < n && stop_at == n; ++i) {
 		sslm_seq s = seqs[i];
+		const int32_t w = words[s->slot];
+		if (w != 0 && (w >> 8) < m->L) {  // a layer refused: the last commit is the layer before it
+			s->layer_index = (uint32_t)(w >> 8);
+			first_err = map_forward_status(w);
+			stop_at = i + 1;
+			break;
+		}
+		if (in_unit[i]) {
+			s->layer_index = unit_l1[i];
+			if (unit_l1[i] < (uint32_t)m->L) out_tokens[i] = -1;
+			else s->context_length += 1;
+		}
+		const int k = in_lg[i];
+		if (k < 0) continue;
 		s->ready_for_logits = false;
-		if (failed_head[i]) {
-			s->current_token = toks[k];
-			s->layer_index = 0;
-			out_tokens[i] = -1;
-			continue;
+		if (w != 0) {  // final norm or logits refused
+			first_err = map_forward_status(w);
+			stop_at = i + 1;
+			break;
 		}
 		int32_t tok = toks[k];
 		const SchemaEntry* se = s->schema ? &m->schemas[s->schema->index] : nullptr;
@@ -2025,9 +2168,9 @@ static sslm_status decode_batch(sslm_model m, sslm_seq* seqs, int32_t n, const s
 			if (s->anti_lm.order == 0 || s->anti_lm.order != params.anti_lm_max_order)
 				s->anti_lm.reset(params.anti_lm_max_order);
 			if (!damped_pick(row, m->V, params, s->anti_lm, page, &tok)) {
-				out_tokens[i] = -1;  // refused: no token this call; the sequence keeps its layer index
-				if (first_err == SSLM_OK) first_err = map_forward_status(kSoftmaxKernelRefusedAfterGateAccepted);
-				continue;
+				first_err = map_forward_status(kSoftmaxKernelRefusedAfterGateAccepted);
+				stop_at = i + 1;
+				break;
 			}
 		}  // greedy: tok is the device's argmax, masked for a schema-bound sequence
 		if (se) {  // the walk advances only along an existing transition; none is a dead end (-2)
@@ -2042,6 +2185,17 @@ static sslm_status decode_batch(sslm_model m, sslm_seq* seqs, int32_t n, const s
 		s->current_token = tok;
 		s->layer_index = 0;
 		out_tokens[i] = tok;
+	}
+	for (auto& g : groups) {  // one restore per layer range
+		std::vector<TokenInfo> restore;
+		for (int i : g.second)
+			if (i >= stop_at) restore.push_back(TokenInfo{seqs[i]->context_length, seqs[i]->slot, (int32_t)seqs[i]->block});
+		if (restore.empty()) continue;
+		ck(hipMemcpyAsync(t0.tok, restore.data(), restore.size() * sizeof(TokenInfo), hipMemcpyHostToDevice, t0.stream));
+		sslm_launch::slot_state_copy(slot_copy_args(m, t0.tok, (int)g.first, (int)unit_l1[g.second[0]]), (int)restore.size(),
+		                             true, t0.stream);
+		ck(hipGetLastError());
+		ck(hipStreamSynchronize(t0.stream));
 	}
 	ck(hipStreamSynchronize(t0.stream));
 	return first_err;
@@ -2337,10 +2491,11 @@ sslm_status sslm_adapter_release(sslm_adapter adapter) {
 	{
 		// no decode may still read the adapter's tensors
 		std::lock_guard<std::mutex> lk(adapter->model->mu);
-		for (Track& w : adapter->model->tracks)
-			if (w.stream) (void)hipStreamSynchronize(w.stream);
-		for (auto& kv : adapter->model->graphs) (void)hipGraphExecDestroy(kv.second);
-		adapter->model->graphs.clear();  // captured graphs may hold its device pointers
+		try {
+			drop_graphs(adapter->model);  // captured graphs may hold its device pointers
+		} catch (const HipError&) {
+			return SSLM_INVALID_ARGUMENT;
+		}
 	}
 	for (void* q : adapter->owned) (void)hipFree(q);
 	adapter->model->live_refs--;

@@ -299,6 +299,9 @@ CONFIGS = {
     # wide enough that the decode GEMVs split K (hidden 1024, intermediate 2816)
     "medium": ModelConfig(hidden=1024, layers=2, heads=8, kv_heads=2, head_dim=128, inter=2816, vocab=4096,
                           context_cap=96, tie_embeddings=False, with_bias=True),
+    # a context cap above one 512-token launch, for long prefill spans
+    "long": ModelConfig(hidden=256, layers=2, heads=4, kv_heads=1, head_dim=64, inter=512, vocab=1024,
+                        context_cap=1536, tie_embeddings=False, with_bias=True),
     # Qwen2.5-1.5B shape
     "qwen1.5b": ModelConfig(hidden=1536, layers=28, heads=12, kv_heads=2, head_dim=128, inter=8960,
                             vocab=151936, context_cap=1024, tie_embeddings=True),
@@ -385,7 +388,7 @@ def _codes(rng, shape):
 
 
 def build_synthetic(cfg: ModelConfig, seed: int = 1234, temperature: float = 1.0,
-                    damped_logit_scale: float | None = None, schemas=None) -> SyntheticModel:
+                    damped_logit_scale: float | None = None, schemas=None, edit=None) -> SyntheticModel:
     """Seeded synthetic integer model whose constants follow one real-scale model.
 
     Real value of a code = code * (m * 2^e).  Each projection's WSC1 fold F = acc * mult / 2^(31+s)
@@ -395,7 +398,8 @@ def build_synthetic(cfg: ModelConfig, seed: int = 1234, temperature: float = 1.0
     both incoming scales).  K/V land at a fixed code scale, and softmax_khead folds the k code
     scale with 1/sqrt(head_dim) so the derived i-exp q_ln2 sits near 5e4 score units.
     `damped_logit_scale` (the real value of one logit unit) adds the damped-greedy constants;
-    `schemas` (see scm1) adds a SchemaMasks section."""
+    `schemas` (see scm1) adds a SchemaMasks section.  `edit`, when given, is called with the
+    model before its image is written (constants, folds and biases are still plain arrays)."""
     rng = np.random.Generator(np.random.PCG64(seed))
     c = cfg
     m = SyntheticModel(config=c)
@@ -455,8 +459,23 @@ def build_synthetic(cfg: ModelConfig, seed: int = 1234, temperature: float = 1.0
     m.rope_cos, m.rope_sin = rope_tables(c.context_cap, D, c.rope_theta)
     m.silu = sigmoid_lut()
     m.rng = rng
+    if edit is not None:
+        edit(m)
     m.to_array()
     return m
+
+
+def with_weight_rows(sm: SyntheticModel, name: str, rows: dict) -> bytes:
+    """The image of `sm` with rows of weight tensor `name` replaced ({row index: int8 codes}) and
+    the integrity hash recomputed; `sm` itself is left unchanged."""
+    img = sm.to_array().copy()
+    w = sm.weights[name]
+    off = w.ctypes.data - sm.to_array().ctypes.data
+    width = w.shape[1]
+    for r, codes in rows.items():
+        img[off + r * width:off + (r + 1) * width] = np.asarray(codes, dtype=np.int8).view(np.uint8)
+    flags = int.from_bytes(img[16:20].tobytes(), "little")
+    return with_flags(img.tobytes(), flags)
 
 
 # ADP1 target-module bit order (reference include/superslm/model.h:433 kPeftAdaptableProjections)
