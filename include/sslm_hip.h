@@ -223,6 +223,24 @@ sslm_status sslm_hip_synchronize(void);
 /* Raw int32 GEMM (no epilogue) for verification: out[m, n] = A . W^T, device pointers. */
 sslm_status sslm_hip_gemm_i32(const int8_t* a, const int8_t* w, int32_t m, int32_t n, int32_t k, int32_t* out);
 
+/* sslm_hip_gemm_requant for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  No counterpart in the
+ * reference.  Same arguments, kernels and results as sslm_hip_gemm_requant, plus `stream` (a
+ * hipStream_t; null = the default stream).  It allocates nothing: its scratch (int32 fold
+ * outputs, per-tile partial maxima, per-token routing and scales) is one file-scope device array
+ * of sslm_hip_noalloc_scratch_bytes() bytes (about 21 MB) that each GPU holds until the process
+ * ends.  Asynchronous on `stream`: the outputs are ready once the stream has drained.  Calls on
+ * one GPU share that array, so calls that overlap on one GPU (other streams, other threads) race;
+ * each call writes every scratch element it reads.  Requires 1 <= m <= SSLM_HIP_NOALLOC_MAX_M,
+ * 16 <= n <= SSLM_HIP_NOALLOC_MAX_N, n and k multiples of 16 (else SSLM_INVALID_ARGUMENT, with a
+ * message on stderr, and nothing launched). */
+#define SSLM_HIP_NOALLOC_MAX_M 128
+#define SSLM_HIP_NOALLOC_MAX_N 8192
+size_t sslm_hip_noalloc_scratch_bytes(void);
+sslm_status sslm_hip_gemm_requant_noalloc(const int8_t* a, const int8_t* w, const int32_t* fold, int32_t m, int32_t n,
+                                          int32_t k, int64_t in_m, int64_t in_e, int64_t site_m, int64_t site_e,
+                                          int8_t* out_codes, int64_t* out_me, int32_t* out_status, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -7,4 +7,5 @@ mkdir -p _build
 hipcc $FLAGS -c csrc/kernels.hip -o _build/kernels.o 2>&1 | grep -v "packed-fp32-ops" || true
 hipcc $FLAGS -c csrc/runtime.cpp -o _build/runtime.o 2>&1 | grep -v "packed-fp32-ops" || true
 hipcc $FLAGS -c csrc/artifact.cpp -o _build/artifact.o 2>&1 | grep -v "packed-fp32-ops" || true
-hipcc -shared -fPIC --offload-arch=gfx950 _build/kernels.o _build/runtime.o _build/artifact.o -lcrypto -o libsslm_hip.so
+hipcc $FLAGS -c csrc/noalloc.hip -o _build/noalloc.o 2>&1 | grep -v "packed-fp32-ops" || true
+hipcc -shared -fPIC --offload-arch=gfx950 _build/kernels.o _build/runtime.o _build/artifact.o _build/noalloc.o -lcrypto -o libsslm_hip.so
