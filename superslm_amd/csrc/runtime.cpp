@@ -2732,7 +2732,7 @@ GemmArgs sa_args(const int8_t* a, const int8_t* w, int m, int n, int k) {
 sslm_status sslm_hip_gemm_requant(const int8_t* a, const int8_t* w, const int32_t* fold, int32_t m, int32_t n,
                                   int32_t k, int64_t in_m, int64_t in_e, int64_t site_m, int64_t site_e,
                                   int8_t* out_codes, int64_t* out_me, int32_t* out_status) {
-	if (!a || !w || !fold || !out_codes || !out_me || !out_status || m < 1 || m > kPartLd || n < 1 || k < 16 ||
+	if (!a || !w || !fold || !out_codes || !out_me || !out_status || m < 1 || m > kMaxTokens || n < 1 || k < 16 ||
 	    k % 16 || n % 16 || n > kFunnelMaxN)
 		return SSLM_INVALID_ARGUMENT;
 	return guarded([&]() -> sslm_status {
@@ -2777,7 +2777,7 @@ sslm_status sslm_hip_gemm_requant(const int8_t* a, const int8_t* w, const int32_
 }
 
 sslm_status sslm_hip_gemm_i32(const int8_t* a, const int8_t* w, int32_t m, int32_t n, int32_t k, int32_t* out) {
-	if (!a || !w || !out || m < 1 || m > kPartLd || n < 1 || k < 16 || k % 16) return SSLM_INVALID_ARGUMENT;
+	if (!a || !w || !out || m < 1 || m > kMaxTokens || n < 1 || k < 16 || k % 16) return SSLM_INVALID_ARGUMENT;
 	return guarded([&]() -> sslm_status {
 		std::lock_guard<std::mutex> lk(g_sa.mu);
 		sa_reserve(m, n);
