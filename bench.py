@@ -1,18 +1,20 @@
 """Benchmark of the HIP backend on BASELINE configuration 1: Qwen2.5-1.5B-shaped integer decode.
 
-One step = one sslm_decode_step over a batch of sequences through all 28 layers and the LM head
-(greedy token out), with every weight, KV block and stream state resident in HBM.  Prints one
-JSON line.  Alongside it, the same run measures:
-  * the decode GEMV roofline: algorithmic bytes of every projection GEMV and the LM head of a
-    step over their launch durations (HIP events around each launch on the library's stream, in
-    a profiled pass of the same steps), per launch shape and in aggregate; HBM traffic per
-    launch from rocprofv3 PMC runs when profiles/decode_gemv_traffic.json holds them,
-  * single-sequence decode,
-  * the int8 prefill GEMM rate of a 512-token chunk (BASELINE configuration 2's prefill),
-  * the reference's own CPU path (oracle/_ref, compiled from the reference sources) on a bounded
-    sample of the same workload, whose tokens must equal the GPU's.
+One step = one sslm_decode_step over a batch of 16 sequences through all 28 layers and the LM
+head (greedy token out), with every weight, KV block and stream state resident in HBM.  Prints
+one JSON line whose value is the decode rate.  Alongside it, the same run measures:
+  * roofline: the decode GEMVs of a step (every layer's projections with its own weights, then
+    the LM head) back to back between two HIP events -- algorithmic bytes over time against
+    8 TB/s; HBM traffic per launch from rocprofv3 PMC runs when profiles/decode_gemv_traffic.json
+    holds them; and the whole step against its HBM floor,
+  * prefill_roofline: the 112 projection GEMMs of a 512-token chunk the same way, against the
+    5.0 POPS dense int8 MFMA peak, and the 512-token prefill rate (configuration 2's chunk),
+  * single-sequence decode, configuration 0 (GEMM + requant), configuration 3 (LoRA r16 on q, v)
+    and configuration 4 (7B shape, 32 x 2048-token prefill, then decode),
+  * cpu_baseline: the reference compiled from its own sources (oracle/_ref) on this host's cores
+    -- one sequence on one core and P sequences on P cores -- whose tokens must equal the GPU's.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--batch B] [--phase all|decode|prefill]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--batch B] [--phase all|decode|prefill|config4]
        python bench.py --traffic-from FETCH.csv WRITE.csv   (summarise two rocprofv3 --pmc runs)
 """
 import argparse
@@ -209,49 +211,100 @@ def extras(hip, model, pool, cfg, sm, rng, args, line):
     return out
 
 
-def config4(args):
-    """BASELINE configuration 4 on one GPU: the 7B shape (H 3584, I 18944, 28 layers, 28 / 4
-    heads, context cap 4608), 32 sequences each prefilled with 2048 tokens in 512-token chunks,
-    then greedy decode steps over all 32 at context ~2048 (one GPU's share; no CPU leg -- the
-    reference needs minutes per token at this shape)."""
+def config4(hip, args):
+    """BASELINE configuration 4 at one GPU's share: the 7B shape (H 3584, I 18944, 28 layers,
+    28 / 4 heads, context cap 4608), 32 sequences each prefilled with a 2048-token prompt in one
+    2048-token chunk, then greedy decode steps over all 32 at context ~2048.  No CPU leg (the
+    reference needs minutes per token at this shape); its parity is pinned by
+    tests/test_gpu_workloads.py."""
     cfg = CONFIGS["qwen7b"]
     t0 = time.time()
     sm = build_synthetic(cfg, seed=7007)
     image = sm.to_array()
     print(f"[bench] synthetic 7B artifact {image.nbytes / 1e9:.2f} GB in {time.time() - t0:.1f}s",
           file=sys.stderr, flush=True)
-    hip = SslmLib(os.path.join(ROOT, "superslm_amd", "libsslm_hip.so"))
     model = Model(hip, image)
     B, ctx = 32, 2048
-    pool = model.pool(B)
+    pool = model.pool(B + 1)
     rng = np.random.default_rng(4)
     seqs = [pool.seq() for _ in range(B)]
+    prompts = [rng.integers(0, cfg.vocab, size=ctx) for _ in range(B)]
+    warm = pool.seq()
+    warm.prefill(prompts[0], chunk_budget=ctx)  # the 2048-token span shape, seen once
+    warm.release()
+    hip.lib.sslm_hip_synchronize()
     t0 = time.perf_counter()
-    for s in seqs:
-        p = rng.integers(0, cfg.vocab, size=ctx)
-        done = 0
-        while done < ctx:
-            done += s.prefill(p[done:], chunk_budget=512)
+    for s, p in zip(seqs, prompts):
+        assert s.prefill(p, chunk_budget=ctx) == ctx
     hip.lib.sslm_hip_synchronize()
     pre_s = time.perf_counter() - t0
     print(f"[bench] config4 prefill {B} x {ctx}: {pre_s:.2f} s, {B * ctx / pre_s:.0f} tok/s", file=sys.stderr, flush=True)
-    for _ in range(max(2, args.warmup)):
+    for _ in range(3):
         model.decode_step(seqs, cfg.layers)
     hip.lib.sslm_hip_synchronize()
-    steps = max(4, min(args.steps, 32))
+    steps = 16
     t0 = time.perf_counter()
     for _ in range(steps):
         model.decode_step(seqs, cfg.layers)
     hip.lib.sslm_hip_synchronize()
     dt = time.perf_counter() - t0
-    line = {"metric": "config4 7B decode tok/s (32 sequences at context ~2048)", "value": round(B * steps / dt, 2),
-            "unit": "tok/s", "n_gpus": 1, "steps": steps, "warmup": max(2, args.warmup),
-            "ms_per_step": round(dt * 1e3 / steps, 3), "higher_is_better": True, "scaling": "weak",
-            "vs_baseline": None, "dtype": "int8", "data": "synthetic",
-            "config": {"workload": "config4: Qwen2.5-7B shape, 32 sequences x 2048-token chunked prefill, then "
-                                   "greedy decode", "batch": B, "context": ctx},
-            "prefill_tok_s": round(B * ctx / pre_s, 1)}
-    print(json.dumps(line))
+    out = {"config4_7b": {"workload": "Qwen2.5-7B shape, 32 sequences x 2048-token prompt (one chunk each), then "
+                                      "greedy decode at context ~2048",
+                          "prefill_tok_s": round(B * ctx / pre_s, 1), "decode_tok_s": round(B * steps / dt, 1),
+                          "decode_ms_per_step": round(dt * 1e3 / steps, 3), "decode_steps": steps}}
+    print(f"[bench] config4 decode: {out['config4_7b']['decode_tok_s']} tok/s", file=sys.stderr, flush=True)
+    for s in seqs:
+        s.release()
+    pool.close()
+    model.close()
+    return out
+
+
+TIERS = {0: "SSE2", 1: "AVX2", 2: "AVX-512"}
+
+
+def cpu_baseline(image, cfg, prompts, gpu_calls, calls):
+    """The reference compiled from its own sources (oracle/_ref) on this host's cores, same
+    artifact and prompts: (i) one sequence on one core, (ii) P sequences on P cores (one thread
+    per sequence; the reference's forward is single-threaded per sequence), each prefilled with
+    its prompt and then decoded for `calls` calls.  Tokens must equal the GPU's first calls."""
+    from concurrent.futures import ThreadPoolExecutor
+    ref_so = os.path.join(ROOT, "oracle", "_ref", "libsuperslm_ref.so")
+    ref = SslmLib(ref_so)
+    ref.lib.ref_dot_row_tier.restype = ctypes.c_int
+    tier = TIERS.get(ref.lib.ref_dot_row_tier(), "?")
+    ncpu = os.cpu_count() or 1
+    P = max(1, min(16, ncpu, len(prompts)))
+    rmodel = Model(ref, image)
+    L = cfg.layers
+
+    def run(k):
+        pool = rmodel.pool(k)
+        seqs = [pool.seq() for _ in range(k)]
+        with ThreadPoolExecutor(k) as ex:
+            list(ex.map(lambda sp: sp[0].prefill(sp[1]), zip(seqs, prompts[:k])))
+            t0 = time.perf_counter()
+            toks = list(ex.map(lambda s: [rmodel.decode_step([s], L)[0] for _ in range(calls)], seqs))
+            dt = time.perf_counter() - t0
+        for s in seqs:
+            s.release()
+        pool.close()
+        return toks, dt
+
+    t_all = time.time()
+    one_toks, one_dt = run(1)
+    p_toks, p_dt = run(P)
+    exact = all(p_toks[i] == [c[i] for c in gpu_calls[:calls]] for i in range(P)) and one_toks[0] == p_toks[0]
+    rmodel.close()
+    out = {"value": round(P * calls / p_dt, 3), "unit": "tok/s", "cores": P, "kind": "reference",
+           "sample": f"{P} sequences on {P} threads x {calls} decode calls (28 layers + LM head) after "
+                     f"{len(prompts[0])}-token prompts, same artifact; host {cpu_model()}, nproc {ncpu}, "
+                     f"reference matmul tier {tier}",
+           "one_core_tok_s": round(calls / one_dt, 3), "matmul_tier": tier, "nproc": ncpu,
+           "cpu_model": cpu_model()}
+    print(f"[bench] CPU reference ({tier}): 1 core {out['one_core_tok_s']} tok/s, {P} cores {out['value']} tok/s, "
+          f"tokens equal: {exact} ({time.time() - t_all:.1f}s)", file=sys.stderr, flush=True)
+    return out, exact
 
 
 def main():
@@ -261,12 +314,13 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--batch", type=int, default=16)
     ap.add_argument("--prompt", type=int, default=32)
-    ap.add_argument("--cpu-seqs", type=int, default=2)
+    ap.add_argument("--cpu-calls", type=int, default=32, help="decode calls per sequence in the CPU baseline")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-config4", action="store_true")
     ap.add_argument("--phase", choices=["all", "decode", "prefill", "config4"], default="all")
     ap.add_argument("--calibrate", action="store_true", help="add the PMC calibration copy")
     ap.add_argument("--pmc-steps", action="store_true",
-                    help="decode steps only (no profiled pass, GEMV timing or M = 1 decode): for --pmc runs")
+                    help="decode steps only (no profiled pass or M = 1 decode): for --pmc runs")
     ap.add_argument("--traffic-from", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"))
     args = ap.parse_args()
     if args.traffic_from:
@@ -277,8 +331,9 @@ def main():
               "(sequences shard across GPUs with no exchange; see DESIGN.md)", file=sys.stderr)
         sys.exit(2)
 
+    hip = SslmLib(os.path.join(ROOT, "superslm_amd", "libsslm_hip.so"))
     if args.phase == "config4":
-        config4(args)
+        print(json.dumps(config4(hip, args)))
         return
     cfg = CONFIGS["qwen1.5b"]
     t0 = time.time()
@@ -286,8 +341,6 @@ def main():
     image = sm.to_array()
     print(f"[bench] synthetic 1.5B artifact {image.nbytes / 1e9:.2f} GB in {time.time() - t0:.1f}s",
           file=sys.stderr, flush=True)
-
-    hip = SslmLib(os.path.join(ROOT, "superslm_amd", "libsslm_hip.so"))
     if args.calibrate:
         copy_calibration(hip)
     model = Model(hip, image)
@@ -296,21 +349,20 @@ def main():
     rng = np.random.default_rng(99)
     prompts = [rng.integers(0, cfg.vocab, size=args.prompt) for _ in range(B)]
     line = None
-    first_tokens = second_tokens = None
+    gpu_calls = []
+    seqs = []
     if args.phase in ("all", "decode"):
         seqs = [pool.seq() for _ in range(B)]
         for s, p in zip(seqs, prompts):
             s.prefill(p)
         print("[bench] prefilled", B, "sequences", file=sys.stderr, flush=True)
-        # decode: warmup (the first step only computes logits for the prefilled rows)
-        first_tokens = model.decode_step(seqs, cfg.layers)
-        second_tokens = model.decode_step(seqs, cfg.layers)
-        for _ in range(max(0, args.warmup - 2)):
-            model.decode_step(seqs, cfg.layers)
+        # warmup: the first call only computes the logits of the prefilled rows
+        for _ in range(max(2, args.warmup)):
+            gpu_calls.append(model.decode_step(seqs, cfg.layers))
         hip.lib.sslm_hip_synchronize()
         t0 = time.perf_counter()
         for _ in range(args.steps):
-            model.decode_step(seqs, cfg.layers)
+            gpu_calls.append(model.decode_step(seqs, cfg.layers))
         hip.lib.sslm_hip_synchronize()
         dt = time.perf_counter() - t0
         tok_s = B * args.steps / dt
@@ -318,39 +370,35 @@ def main():
         print(f"[bench] decode B={B}: {ms_step:.3f} ms/step, {tok_s:.1f} tok/s", file=sys.stderr, flush=True)
         if args.pmc_steps:
             return
+        # tokens of the calls the CPU baseline compares against
+        while len(gpu_calls) < args.cpu_calls:
+            gpu_calls.append(model.decode_step(seqs, cfg.layers))
 
-        # profiled pass of the same steps: events around every launch, per class and per shape
+        # profiled pass of the same steps: events around every launch, per class (where the
+        # step's time goes; per-launch events add their own overhead to each figure)
+        n_prof = max(4, args.steps // 2)
         profile(hip, True)
-        for _ in range(args.steps):
+        for _ in range(n_prof):
             model.decode_step(seqs, cfg.layers)
         ms, la, by, op = profile_read(hip)
-        shapes = profile_shapes(hip)
         profile(hip, False)
-        # the dominant kernel: the decode GEMVs, each shape timed back to back with HIP events
-        L = hip.lib
-        L.sslm_hip_bench_decode_gemv.restype = ctypes.c_int32
-        L.sslm_hip_bench_decode_gemv.argtypes = [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32] + [ctypes.c_void_p] * 3 + [ctypes.c_int32]
-        us = (ctypes.c_double * 8)()
-        gb = (ctypes.c_int64 * 8)()
-        gk = (ctypes.c_int64 * 8)()
-        ng = L.sslm_hip_bench_decode_gemv(model.handle, B, 50, us, gb, gk, 8)
-        if ng != 5:
+        step_prof = {"gemv_ms": ms[0] / n_prof, "head_ms": ms[1] / n_prof,
+                     "attention_ms": ms[2] / n_prof, "row_ms": ms[3] / n_prof,
+                     "launches_per_step": sum(la) / n_prof}
+        # the dominant kernel: every GEMV launch of a step (28 layers' q|k|v, o, gate|up, down with
+        # their own weights, then the LM head) back to back between two HIP events
+        L_ = hip.lib
+        L_.sslm_hip_bench_decode_gemv.restype = ctypes.c_int32
+        L_.sslm_hip_bench_decode_gemv.argtypes = [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32] + \
+            [ctypes.c_void_p] * 3 + [ctypes.c_int32]
+        g_us, g_bytes, g_n = (ctypes.c_double * 1)(), (ctypes.c_int64 * 1)(), (ctypes.c_int64 * 1)()
+        if L_.sslm_hip_bench_decode_gemv(model.handle, B, 10, g_us, g_bytes, g_n, 1) != 1:
             raise RuntimeError("sslm_hip_bench_decode_gemv failed")
-        names = ["q|k|v", "o", "gate|up", "down", "lm_head"]
-        per_step = [cfg.layers] * 4 + [1]
-        per_shape = [{"gemv": names[i], "M": B, "N": gk[i] >> 20, "K": gk[i] & 0xFFFFF, "launches_per_step": per_step[i],
-                      "us_per_launch": round(us[i], 3), "bytes_per_launch": gb[i],
-                      "gbs": round(gb[i] / (us[i] * 1e-6) / 1e9, 1)} for i in range(5)]
-        g_bytes = sum(per_step[i] * gb[i] for i in range(5))
-        g_us = sum(per_step[i] * us[i] for i in range(5))
-        g_launch = sum(per_step)
-        all_gbs = g_bytes / (g_us * 1e-6) / 1e9
-        step_prof = {"gemv_ms": ms[0] / args.steps, "head_ms": ms[1] / args.steps,
-                     "attention_ms": ms[2] / args.steps, "row_ms": ms[3] / args.steps,
-                     "launches_per_step": sum(la) / args.steps}
+        achieved = g_bytes[0] / (g_us[0] * 1e-6) / 1e9
         traffic = None
         if os.path.exists(TRAFFIC_FILE):
             traffic = json.load(open(TRAFFIC_FILE)).get("mean_traffic_bytes_per_launch")
+        floor_bytes = g_bytes[0]
 
         # single-sequence decode (M = 1)
         one = seqs[:1]
@@ -378,37 +426,39 @@ def main():
                                    f"LM head per step, seeded random int8 weights", "batch": B,
                        "prompt_tokens": args.prompt, "hidden": cfg.hidden, "layers": cfg.layers,
                        "intermediate": cfg.inter, "vocab": cfg.vocab},
-            "roofline": {"bound": "hbm", "achieved": round(all_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                         "frac": round(all_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
-                         "kernel": "decode GEMV k_gemv over one step's launches (28 x q|k|v, o, gate|up, down + "
-                                   "LM head), each timed back to back with HIP events: sum of algorithmic bytes / "
-                                   "sum of launch durations; traffic = mean HBM bytes per launch (rocprofv3 "
-                                   "FETCH_SIZE + WRITE_SIZE, copy-calibrated)",
-                         "bytes_per_launch": g_bytes // g_launch,
-                         "us_per_launch": round(g_us / g_launch, 3)},
+            "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                         "kernel": "decode GEMV (k_gemv): the 113 GEMV launches of one step at M = 16 (28 layers' "
+                                   "q|k|v, o, gate|up, down with their own weights, then the LM head) back to back "
+                                   "between two HIP events on the library's stream, so every weight byte streams "
+                                   "from HBM as in a step: algorithmic bytes per pass / pass time (launch gaps "
+                                   "included); traffic = mean HBM bytes per launch (rocprofv3 FETCH_SIZE + "
+                                   "WRITE_SIZE, copy-calibrated)",
+                         "bytes_per_launch": g_bytes[0] // max(1, g_n[0]),
+                         "us_per_launch": round(g_us[0] / max(1, g_n[0]), 3),
+                         "launches_per_pass": g_n[0]},
+            "decode_step_hbm_floor_ms": round(floor_bytes / (HBM_PEAK_GBS * 1e9) * 1e3, 4),
+            "decode_step_hbm_frac": round(floor_bytes / (HBM_PEAK_GBS * 1e9) / (ms_step * 1e-3), 4),
             "cpu_baseline": None,
             "bit_exact_vs_cpu": None,
             "decode_m1_tok_s": round(m1_tok_s, 2),
-            "decode_gemv_shapes": per_shape,
             "step_profile_ms": {k: round(v, 4) for k, v in step_prof.items()},
         }
 
     if args.phase in ("all", "prefill"):
-        # prefill: one 512-token chunk (BASELINE configuration 2's chunk), GEMM rate from the profile
+        # prefill: one 512-token chunk (BASELINE configuration 2's chunk)
         chunk = rng.integers(0, cfg.vocab, size=512)
+        for n in (8, 512, 512):  # warm: small shapes, then the 512-token span twice (its graph)
+            pseq = pool.seq()
+            pseq.prefill(chunk[:n])
+            pseq.release()
         pseq = pool.seq()
-        pseq.prefill(chunk[:8])  # warm
-        pseq.release()
-        pseq = pool.seq()
-        pseq.prefill(chunk)  # warm the 512-token shapes
-        pseq.release()
-        pseq = pool.seq()
-        profile(hip, True)  # one profiled chunk for the GEMM rate
+        profile(hip, True)  # one profiled chunk: per-launch events, graphs off
         pseq.prefill(chunk)
         pms, pla, pby, pop = profile_read(hip)
         profile(hip, False)
         pseq.release()
-        times = []  # then the median of 5 unprofiled chunks, each into a fresh sequence
+        times = []  # then the median of 5 unprofiled chunks (graph replay), each into a fresh sequence
         for _ in range(5):
             pseq = pool.seq()
             t0 = time.perf_counter()
@@ -416,10 +466,24 @@ def main():
             times.append(time.perf_counter() - t0)
             pseq.release()
         pre_s = float(np.median(times))
-        prefill_tops = pop[0] / (pms[0] * 1e-3) / 1e12 if pms[0] else 0.0
-        print(f"[bench] prefill 512: {pre_s * 1e3:.1f} ms, GEMM {prefill_tops:.1f} TOPS", file=sys.stderr, flush=True)
-        pre = {"prefill_512_tok_s": round(512 / pre_s, 1), "prefill_gemm_tops": round(prefill_tops, 2),
-               "prefill_gemm_mfma_frac": round(prefill_tops / INT8_PEAK_TOPS, 4)}
+        L_ = hip.lib
+        L_.sslm_hip_bench_prefill_gemm.restype = ctypes.c_int32
+        L_.sslm_hip_bench_prefill_gemm.argtypes = [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32] + [ctypes.c_void_p] * 3
+        p_us, p_ops, p_n = (ctypes.c_double * 1)(), (ctypes.c_int64 * 1)(), (ctypes.c_int64 * 1)()
+        if L_.sslm_hip_bench_prefill_gemm(model.handle, 512, 5, p_us, p_ops, p_n) != 1:
+            raise RuntimeError("sslm_hip_bench_prefill_gemm failed")
+        prefill_tops = p_ops[0] / (p_us[0] * 1e-6) / 1e12
+        print(f"[bench] prefill 512: {pre_s * 1e3:.2f} ms, GEMM {prefill_tops:.1f} TOPS", file=sys.stderr, flush=True)
+        pre = {"prefill_512_tok_s": round(512 / pre_s, 1), "prefill_512_ms": round(pre_s * 1e3, 3),
+               "prefill_roofline": {"bound": "mfma", "achieved": round(prefill_tops, 1), "peak": INT8_PEAK_TOPS,
+                                    "unit": "TOPS", "frac": round(prefill_tops / INT8_PEAK_TOPS, 4),
+                                    "kernel": "prefill GEMM (k_gemm_mfma): the 112 projection GEMMs of one "
+                                              "512-token chunk (28 layers' q|k|v, o, gate|up, down, the layer loop's "
+                                              "launch shapes) back to back between two HIP events: sum of 2*M*N*K "
+                                              "/ pass time; peak = MI355X dense int8 MFMA",
+                                    "us_per_pass": round(p_us[0], 2), "launches_per_pass": p_n[0]},
+               "prefill_profile_ms": {"gemm_ms": round(pms[0], 3), "attention_ms": round(pms[2], 3),
+                                      "row_ms": round(pms[3], 3), "launches": int(sum(pla))}}
         if line is None:
             line = {"metric": METRIC, "value": round(prefill_tops, 2), "unit": "TOPS", "n_gpus": 1, "steps": 5,
                     "warmup": 2, "ms_per_step": round(pre_s * 1e3, 3), "higher_is_better": True,
@@ -430,28 +494,16 @@ def main():
     if args.phase == "all":
         line.update(extras(hip, model, pool, cfg, sm, rng, args, line))
 
-    # CPU baseline: the reference compiled from its sources, same artifact, bounded sample
-    ref_so = os.path.join(ROOT, "oracle", "_ref", "libsuperslm_ref.so")
-    if args.phase in ("all", "decode") and not args.no_cpu and os.path.exists(ref_so):
-        ref = SslmLib(ref_so)
-        t0 = time.time()
-        rmodel = Model(ref, image)
-        rpool = rmodel.pool(args.cpu_seqs)
-        rseqs = [rpool.seq() for _ in range(args.cpu_seqs)]
-        for s, p in zip(rseqs, prompts):
-            s.prefill(p)
-        r_first = rmodel.decode_step(rseqs, cfg.layers)  # logits of the prefilled rows
-        t1 = time.perf_counter()
-        r_second = rmodel.decode_step(rseqs, cfg.layers)  # one full decode step per sequence
-        cpu_dt = time.perf_counter() - t1
-        bit_exact = (r_first == first_tokens[:args.cpu_seqs]) and (r_second == second_tokens[:args.cpu_seqs])
-        line["cpu_baseline"] = {
-            "value": round(args.cpu_seqs / cpu_dt, 3), "unit": "tok/s", "cores": 1, "kind": "reference",
-            "sample": f"{args.cpu_seqs} sequences x 1 decode step (28 layers + LM head) after a "
-                      f"{args.prompt}-token prefill, same artifact; host {cpu_model()}, nproc {os.cpu_count()}"}
-        line["bit_exact_vs_cpu"] = bit_exact
-        print(f"[bench] CPU reference: {line['cpu_baseline']['value']} tok/s, tokens equal: {bit_exact} "
-              f"({time.time() - t0:.1f}s)", file=sys.stderr, flush=True)
+    if args.phase in ("all", "decode") and not args.no_cpu and os.path.exists(
+            os.path.join(ROOT, "oracle", "_ref", "libsuperslm_ref.so")):
+        line["cpu_baseline"], line["bit_exact_vs_cpu"] = cpu_baseline(image, cfg, prompts, gpu_calls, args.cpu_calls)
+    for s in seqs:
+        s.release()
+    pool.close()
+    model.close()
+    del sm, image
+    if args.phase == "all" and not args.no_config4:
+        line.update(config4(hip, args))
     print(json.dumps(line))
 
 

@@ -188,13 +188,21 @@ sslm_status sslm_detokenize_stream(sslm_model model, sslm_detok_state* state, co
 void sslm_hip_profile_enable(int on);
 void sslm_hip_profile_read(double* ms, int64_t* launches, int64_t* bytes, int64_t* ops, int classes);
 void sslm_hip_profile_reset(void);
-/* The decode GEMVs of one step (layer 0's q|k|v, o, gate|up and down projections and the LM
- * head, as the layer loop launches them for M tokens) timed back to back, `iters` launches each,
- * with HIP events on the model's stream.  Writes per GEMV the mean microseconds per launch, the
- * algorithmic bytes per launch (weights + activations + outputs + fold tables) and N << 20 | K;
- * returns the number written (5), or -1.  Sequence state is not touched. */
+/* The decode GEMVs of one step for M tokens -- every layer's q|k|v, o, gate|up and down
+ * projections with that layer's own weights, in the layer loop's order, then the LM head --
+ * launched back to back `iters` times between two HIP events on the model's stream (so every
+ * weight byte streams from HBM, as in a step).  Writes us[0] = mean microseconds per pass,
+ * bytes[0] = algorithmic bytes per pass (weights + activations + outputs + fold tables) and
+ * shapes[0] = launches per pass; returns 1, or -1.  Sequence state is not touched. */
 int32_t sslm_hip_bench_decode_gemv(sslm_model model, int32_t M, int32_t iters, double* us, int64_t* bytes,
                                    int64_t* shapes, int32_t cap);
+/* The projection GEMMs of one M-token prefill chunk (65 <= M <= 512) -- every layer's q|k|v, o,
+ * gate|up and down, each layer's own weights, the layer loop's launch shapes -- back to back
+ * `iters` times between two HIP events on the model's stream.  Writes us[0] = mean
+ * microseconds per pass, ops[0] = 2*M*N*K summed over the pass, launches[0] = launches per
+ * pass; returns 1, or -1.  Sequence state is not touched. */
+int32_t sslm_hip_bench_prefill_gemm(sslm_model model, int32_t M, int32_t iters, double* us, int64_t* ops,
+                                    int64_t* launches);
 /* Per GEMM launch shape: key = class << 56 | M << 40 | N << 20 | K; returns the number of
  * shapes recorded (entries beyond `cap` are not written). */
 int sslm_hip_profile_shapes(int64_t* keys, double* ms, int64_t* launches, int64_t* bytes, int64_t* ops, int cap);

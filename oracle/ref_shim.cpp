@@ -3,6 +3,8 @@
 // (read in place under /root/reference, never copied) into oracle/_ref/libsuperslm_ref.so, so
 // the CPU tests can compare the C restatement in sslm_oracle.c against the reference primitive
 // by primitive on random inputs.  The reference's own sslm_* C ABI is exported by the same .so.
+#include <cpuid.h>
+
 #include <cstdint>
 #include <span>
 
@@ -109,6 +111,25 @@ void ref_rope_pair(int32_t x, int32_t y, int32_t c, int32_t s, int64_t* out2) {
 
 void ref_gemm_i8(const int8_t* a, const int8_t* w, size_t m, size_t k, size_t n, int64_t* out) {
 	superslm::GemmInt8Accumulate(a, w, m, k, n, out);
+}
+
+// The matmul tier the reference's dispatch selects on this host: this host's CPUID / XGETBV
+// fields through the reference's own resolver (0 SSE2, 1 AVX2, 2 AVX-512).
+int ref_dot_row_tier(void) {
+	unsigned a = 0, b = 0, c = 0, d = 0;
+	__get_cpuid_count(0, 0, &a, &b, &c, &d);
+	const int max_leaf = (int)a;
+	unsigned c1 = 0;
+	__get_cpuid_count(1, 0, &a, &b, &c1, &d);
+	unsigned b7 = 0;
+	if (max_leaf >= 7) __get_cpuid_count(7, 0, &a, &b7, &c, &d);
+	unsigned long long xcr0 = 0;
+	if (c1 & (1u << 27)) {
+		unsigned lo = 0, hi = 0;
+		__asm__ volatile("xgetbv" : "=a"(lo), "=d"(hi) : "c"(0));
+		xcr0 = ((unsigned long long)hi << 32) | lo;
+	}
+	return superslm::ResolveDotRowTier(max_leaf, (int)c1, (int)b7, xcr0);
 }
 
 }  // extern "C"

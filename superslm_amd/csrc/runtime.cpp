@@ -2815,49 +2815,106 @@ sslm_status sslm_hip_synchronize(void) { return hipDeviceSynchronize() == hipSuc
 
 int32_t sslm_hip_bench_decode_gemv(sslm_model model, int32_t M, int32_t iters, double* us, int64_t* bytes,
                                    int64_t* shapes, int32_t cap) {
-	if (!model || M < 1 || M > 64 || iters < 1 || cap < 5) return -1;
+	if (!model || M < 1 || M > 64 || iters < 1 || cap < 1) return -1;
 	sslm_model m = model;
 	std::lock_guard<std::mutex> lk(m->mu);
-	int32_t n = 0;
 	const sslm_status st = guarded([&]() -> sslm_status {
 		Track& w = m->tracks[0];
 		std::vector<TokenInfo> ti(M);
 		for (int t = 0; t < M; ++t) ti[t] = TokenInfo{0, t, 0};
 		ck(hipMemcpyAsync(w.tok, ti.data(), M * sizeof(TokenInfo), hipMemcpyHostToDevice, w.stream));
 		ck(hipMemcpyAsync(w.lg_tok, ti.data(), M * sizeof(TokenInfo), hipMemcpyHostToDevice, w.stream));
-		std::vector<GemmArgs> gs = {qkv_args(m, w, 0, M, nullptr, fused_attention_enabled()).g, o_args(m, w, 0, M, nullptr).g,
-		                            gu_args(m, w, 0, M, nullptr).g, down_args(m, w, 0, M, nullptr).g,
-		                            head_args(m, w, M, w.lg_tok)};
+		// every layer's four projections in the layer loop's order, then the LM head: the weights
+		// stream from HBM as in a step (one layer's 46.8 MB at the 1.5B shape, 1.3 GB per pass)
+		std::vector<GemmArgs> gs;
+		for (int l = 0; l < m->L; ++l) {
+			gs.push_back(qkv_args(m, w, l, M, nullptr, fused_attention_enabled()).g);
+			gs.push_back(o_args(m, w, l, M, nullptr).g);
+			gs.push_back(gu_args(m, w, l, M, nullptr).g);
+			gs.push_back(down_args(m, w, l, M, nullptr).g);
+		}
+		gs.push_back(head_args(m, w, M, w.lg_tok));
 		// The timed launches run on whatever the workspaces hold: their epilogue refusals must not
 		// reach the sequences' status words, so they write a private array.
 		int32_t* scratch_status = nullptr;
 		ck(hipMalloc(&scratch_status, (size_t)kSlotCapacity * sizeof(int32_t)));
 		ck(hipMemsetAsync(scratch_status, 0, (size_t)kSlotCapacity * sizeof(int32_t), w.stream));
-		for (GemmArgs& g : gs) g.epi.status = scratch_status;
+		int64_t seq_bytes = 0;
+		for (GemmArgs& g : gs) {
+			g.epi.status = scratch_status;
+			seq_bytes += (int64_t)g.N * g.K + (int64_t)g.M * g.K + 12LL * g.N + (g.epi.argmax_key ? 0 : (int64_t)g.M * g.N * 4);
+		}
 		hipEvent_t a, b;
 		ck(hipEventCreate(&a));
 		ck(hipEventCreate(&b));
-		for (const GemmArgs& g : gs) {
-			for (int i = 0; i < 3; ++i) sslm_launch::gemm(g, w.stream);
-			ck(hipEventRecord(a, w.stream));
-			for (int i = 0; i < iters; ++i) sslm_launch::gemm(g, w.stream);
-			ck(hipEventRecord(b, w.stream));
-			ck(hipEventSynchronize(b));
-			float ms = 0;
-			ck(hipEventElapsedTime(&ms, a, b));
-			const int64_t out_bytes = g.epi.argmax_key ? 0 : (int64_t)g.M * g.N * 4;
-			us[n] = ms * 1e3 / iters;
-			bytes[n] = (int64_t)g.N * g.K + (int64_t)g.M * g.K + 12LL * g.N + out_bytes;
-			shapes[n] = ((int64_t)g.N << 20) | g.K;
-			++n;
-		}
+		for (const GemmArgs& g : gs) sslm_launch::gemm(g, w.stream);  // warm (instruction caches, TLB)
+		ck(hipEventRecord(a, w.stream));
+		for (int i = 0; i < iters; ++i)
+			for (const GemmArgs& g : gs) sslm_launch::gemm(g, w.stream);
+		ck(hipEventRecord(b, w.stream));
+		ck(hipEventSynchronize(b));
+		float ms = 0;
+		ck(hipEventElapsedTime(&ms, a, b));
+		us[0] = ms * 1e3 / iters;
+		bytes[0] = seq_bytes;
+		shapes[0] = (int64_t)gs.size();
 		(void)hipEventDestroy(a);
 		(void)hipEventDestroy(b);
 		ck(hipStreamSynchronize(w.stream));
 		ck(hipFree(scratch_status));
 		return SSLM_OK;
 	});
-	return st == SSLM_OK ? n : -1;
+	return st == SSLM_OK ? 1 : -1;
+}
+
+int32_t sslm_hip_bench_prefill_gemm(sslm_model model, int32_t M, int32_t iters, double* us, int64_t* ops,
+                                    int64_t* launches) {
+	if (!model || M < 65 || M > kMaxTokens || iters < 1 || !us || !ops || !launches) return -1;
+	sslm_model m = model;
+	std::lock_guard<std::mutex> lk(m->mu);
+	const sslm_status st = guarded([&]() -> sslm_status {
+		Track& w = m->tracks[0];
+		std::vector<TokenInfo> ti(M);
+		for (int t = 0; t < M; ++t) ti[t] = TokenInfo{0, 0, 0};
+		ck(hipMemcpyAsync(w.tok, ti.data(), M * sizeof(TokenInfo), hipMemcpyHostToDevice, w.stream));
+		// the chunk's projection GEMMs in the layer loop's order, each layer's own weights, with
+		// the launch shapes (split-K planes included) the layer loop uses
+		std::vector<GemmArgs> gs;
+		for (int l = 0; l < m->L; ++l) {
+			gs.push_back(qkv_args(m, w, l, M, nullptr, false).g);
+			gs.push_back(o_args(m, w, l, M, nullptr).g);
+			gs.push_back(gu_args(m, w, l, M, nullptr).g);
+			gs.push_back(down_args(m, w, l, M, nullptr).g);
+		}
+		int32_t* scratch_status = nullptr;
+		ck(hipMalloc(&scratch_status, (size_t)kSlotCapacity * sizeof(int32_t)));
+		ck(hipMemsetAsync(scratch_status, 0, (size_t)kSlotCapacity * sizeof(int32_t), w.stream));
+		int64_t pass_ops = 0;
+		for (GemmArgs& g : gs) {
+			g.epi.status = scratch_status;
+			pass_ops += 2LL * g.M * g.N * g.K;
+		}
+		hipEvent_t a, b;
+		ck(hipEventCreate(&a));
+		ck(hipEventCreate(&b));
+		for (const GemmArgs& g : gs) sslm_launch::gemm(g, w.stream);
+		ck(hipEventRecord(a, w.stream));
+		for (int i = 0; i < iters; ++i)
+			for (const GemmArgs& g : gs) sslm_launch::gemm(g, w.stream);
+		ck(hipEventRecord(b, w.stream));
+		ck(hipEventSynchronize(b));
+		float ms = 0;
+		ck(hipEventElapsedTime(&ms, a, b));
+		us[0] = ms * 1e3 / iters;
+		ops[0] = pass_ops;
+		launches[0] = (int64_t)gs.size();
+		(void)hipEventDestroy(a);
+		(void)hipEventDestroy(b);
+		ck(hipStreamSynchronize(w.stream));
+		ck(hipFree(scratch_status));
+		return SSLM_OK;
+	});
+	return st == SSLM_OK ? 1 : -1;
 }
 
 // ---- profiling ----
