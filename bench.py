@@ -320,7 +320,8 @@ def main():
     ap.add_argument("--phase", choices=["all", "decode", "prefill", "config4"], default="all")
     ap.add_argument("--calibrate", action="store_true", help="add the PMC calibration copy")
     ap.add_argument("--pmc-steps", action="store_true",
-                    help="decode steps only (no profiled pass or M = 1 decode): for --pmc runs")
+                    help="for --pmc runs: decode steps only (--phase decode), or one chunk and one pass of its "
+                         "GEMMs (--phase prefill)")
     ap.add_argument("--traffic-from", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"))
     args = ap.parse_args()
     if args.traffic_from:
@@ -445,6 +446,17 @@ def main():
             "step_profile_ms": {k: round(v, 4) for k, v in step_prof.items()},
         }
 
+    if args.phase == "prefill" and args.pmc_steps:
+        # counter runs: one 512-token chunk, then one pass of the chunk's 112 projection GEMMs
+        pseq = pool.seq()
+        pseq.prefill(rng.integers(0, cfg.vocab, size=512))
+        pseq.release()
+        L_ = hip.lib
+        L_.sslm_hip_bench_prefill_gemm.restype = ctypes.c_int32
+        L_.sslm_hip_bench_prefill_gemm.argtypes = [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32] + [ctypes.c_void_p] * 3
+        p_us, p_ops, p_n = (ctypes.c_double * 1)(), (ctypes.c_int64 * 1)(), (ctypes.c_int64 * 1)()
+        L_.sslm_hip_bench_prefill_gemm(model.handle, 512, 1, p_us, p_ops, p_n)
+        return
     if args.phase in ("all", "prefill"):
         # prefill: one 512-token chunk (BASELINE configuration 2's chunk)
         chunk = rng.integers(0, cfg.vocab, size=512)

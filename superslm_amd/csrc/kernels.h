@@ -74,6 +74,7 @@ struct GemvPlan {
 	int splits;  // K splits over gridDim.y
 	int cps;     // 128-byte K chunks per split
 	int cpw;     // chunks per wave per load batch
+	bool wave_tile;  // the wave-per-tile kernel (raw / split planes / argmax at M <= 16)
 };
 constexpr int kGemvTargetBlocks = 512;
 
@@ -116,8 +117,9 @@ using namespace sslm;
 
 void gemm(const GemmArgs& g, hipStream_t s);
 // launch shape of the decode GEMV (M <= 64, K % 128 == 0); `split_ok`: the caller consumes raw
-// split-K partials
-GemvPlan gemv_plan(int M, int N, int K, bool split_ok);
+// split-K partials; `raw_or_argmax`: no projection epilogue in the kernel (raw accumulators or
+// argmax keys)
+GemvPlan gemv_plan(int M, int N, int K, bool split_ok, bool raw_or_argmax = false);
 bool gemv_eligible(int M, int K);
 // launch shape of the prefill GEMM; `split_ok` as for gemv_plan
 PrefillPlan prefill_plan(int M, int N, int K, bool split_ok);

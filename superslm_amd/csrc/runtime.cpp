@@ -575,7 +575,7 @@ RawIn split_raw(sslm_model m, Track& w, GemmArgs& g, bool allow_multi, bool allo
 	// stream.  A prefill GEMM keeps its own epilogue unless it splits K.  The flags say which
 	// raw consumers fit their register budget (several planes / one plane).
 	if (sslm_launch::gemv_eligible(g.M, g.K)) {
-		splits = allow_multi ? sslm_launch::gemv_plan(g.M, g.N, g.K, true).splits : 1;
+		splits = allow_multi ? sslm_launch::gemv_plan(g.M, g.N, g.K, true, true).splits : 1;
 		if (splits == 1 && !allow_single) return r;
 	} else {
 		if (!allow_multi || lora || !sslm_launch::prefill_mfma_k(g.K)) return r;
@@ -1154,7 +1154,7 @@ void alloc_track(sslm_model m, Track& w, int T, bool head) {
 			for (int rows = 1; rows <= T; ++rows) {
 				int sp = 1;
 				const bool gemv = sslm_launch::gemv_eligible(rows, sh[1]);
-				if (gemv) sp = sslm_launch::gemv_plan(rows, sh[0], sh[1], true).splits;
+				if (gemv) sp = sslm_launch::gemv_plan(rows, sh[0], sh[1], true, true).splits;
 				else if (sslm_launch::prefill_mfma_k(sh[1])) sp = sslm_launch::prefill_plan(rows, sh[0], sh[1], true).splits;
 				if (sp > 1 || gemv) elems = std::max(elems, (size_t)sp * rows * sh[0]);  // a GEMV is always raw
 			}

@@ -22,7 +22,9 @@ def _lib(hip_lib):
                                    (64, 1536, 8960), (1, 1536, 8960), (16, 2048, 1536), (16, 1536, 65536),
                                    (48, 96, 4096), (65, 384, 256), (200, 640, 1536), (512, 256, 128),
                                    # ragged row and column tiles at several K steps
-                                   (300, 16512, 256), (257, 4224, 384)])
+                                   (300, 16512, 256), (257, 4224, 384),
+                                   # wave-per-tile GEMV (N >= 16384 at M <= 16), ragged N and batches
+                                   (16, 17920, 1536), (1, 151936, 1536), (13, 16400, 640), (7, 16448, 1280)])
 def test_gemm_i32_exact(m, n, k, hip_lib):
     L = _lib(hip_lib)
     dev = Device(hip_lib)
