@@ -284,8 +284,22 @@ struct ActArgs {
 	Scale* act_scale;        // [M]
 	int32_t layer;
 	int32_t* status;
+	// sliced form (decode rows, funnel-epilogue input): the SiLU products, per-slice maxima and
+	// the gate / up scales between its two kernels
+	int64_t* prod;           // [M, I]
+	uint32_t* act_maxpart;   // [kMaxActSlices * kPartLd]
+	Scale* gu_scale;         // [M, 2] gate, up
 };
+constexpr int kMaxActSlices = 16;
+constexpr int kMaxSlicedActRows = 64;  // rows the sliced form's buffers hold
 void mlp_act(const ActArgs& a, hipStream_t s);
+// The same step on every row cut into column slices, one block per (row, slice), in two
+// launches: gate and up funnels, SiLU products and per-slice maxima; then the act funnel over the
+// slices' maxima and the codes.  For short batches (decode), whose one block per row would leave
+// most CUs idle; requires the funnel-epilogue input (tile maxima, no raw planes) and
+// M <= kMaxSlicedActRows.
+bool mlp_act_sliced_ok(const ActArgs& a);
+void mlp_act_sliced(const ActArgs& a, hipStream_t s);
 
 // whether the row kernels' register tiling covers this geometry
 bool row_geometry_ok(int H, int I, int NKV, int D);

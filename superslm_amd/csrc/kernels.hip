@@ -1688,6 +1688,109 @@ void k_mlp_act(sslm_launch::ActArgs a) {
 	if (threadIdx.x == 0) a.act_scale[t] = ap.out;
 }
 
+// mlp_act over column slices (forward_sites.cpp:796-869): block (t, s) takes columns
+// [s * per, (s + 1) * per) of row t.  Part 1: the gate and up funnels from the projection's
+// tile maxima (every block derives the same plans), the SiLU-LUT sigmoid table, the products
+// and the slice's maximum; the block of slice 0 keeps the gate and up scales for part 2.
+template <int BS, int EPT>
+__global__ __launch_bounds__(BS) void k_mlp_act_s1(sslm_launch::ActArgs a, int per) {
+	__shared__ uint32_t s_gu[2 * BS / 64], s_a[BS / 64];
+	__shared__ int32_t sig[256];
+	__shared__ int32_t s_silu[1025];
+	__shared__ int32_t s_st;
+	const int t = blockIdx.x, sl = blockIdx.y, I = a.I;
+	const int slot = a.tok[t].slot;
+	const int j0 = sl * per, j1 = min(I, j0 + per);
+	const int32_t* gfr = a.gu_f + (size_t)t * 2 * I;
+	const int32_t* ufr = gfr + I;
+	int32_t gf[EPT], uf[EPT];
+#pragma unroll
+	for (int k = 0; k < EPT; ++k) {
+		const int i = j0 + threadIdx.x + k * BS;
+		gf[k] = i < j1 ? gfr[i] : 0;
+		uf[k] = i < j1 ? ufr[i] : 0;
+	}
+	uint32_t gm = part_max32<BS>(a.gu_maxpart, 0, I / 16, t);
+	uint32_t um = part_max32<BS>(a.gu_maxpart, I / 16, I / 16, t);
+	const Scale inc = a.in_scale[t];
+	for (int i = threadIdx.x; i < 1025; i += BS) s_silu[i] = a.silu[i];
+	if (threadIdx.x == 0) s_st = a.status[slot];
+	blk_max32x2<BS>(gm, um, s_gu);
+	if (s_st != 0) return;
+	FunnelPlan gp, up;
+	int32_t st = funnel_plan(gm, &inc, 1, a.gate_site, &gp);
+	if (st == kOk) st = funnel_plan(um, &inc, 1, a.up_site, &up);
+	if (st == kOk) st = check_silu_scale(gp.out.m, gp.out.e);
+	if (st != kOk) {
+		if (threadIdx.x == 0) set_status(a.status, slot, a.layer, st);
+		return;
+	}
+	const Scale gs = gp.out;
+	if (threadIdx.x < 256) sig[threadIdx.x] = silu_sigmoid_q15(s_silu, (int8_t)(threadIdx.x - 128), gs.m, (int)gs.e);
+	int32_t gc[EPT], uc[EPT];
+#pragma unroll
+	for (int k = 0; k < EPT; ++k) {
+		gc[k] = requant_code_small(gf[k], (uint64_t)gp.r, gp.s);
+		uc[k] = requant_code_small(uf[k], (uint64_t)up.r, up.s);
+	}
+	__syncthreads();
+	uint32_t mx = 0;
+	int64_t* prow = a.prod + (size_t)t * I;
+#pragma unroll
+	for (int k = 0; k < EPT; ++k) {
+		const int i = j0 + threadIdx.x + k * BS;
+		const int64_t w = (int64_t)gc[k] * sig[gc[k] + 128] * (int64_t)uc[k];  // sigmoid values are artifact data: no bound assumed
+		if (i < j1) {
+			prow[i] = w;
+			mx = max(mx, sat_abs_u32(w));
+		}
+	}
+	mx = blk_max32<BS>(mx, s_a);
+	if (threadIdx.x == 0) {
+		a.act_maxpart[(size_t)sl * kPartLd + t] = mx;
+		if (sl == 0) {
+			a.gu_scale[2 * t] = gp.out;
+			a.gu_scale[2 * t + 1] = up.out;
+		}
+	}
+}
+
+// Part 2: the act funnel over the slices' maxima (every block derives the same plan) and the
+// slice's codes; slice 0 writes the row's act scale.
+template <int BS, int EPT>
+__global__ __launch_bounds__(BS) void k_mlp_act_s2(sslm_launch::ActArgs a, int per) {
+	__shared__ int32_t s_st;
+	const int t = blockIdx.x, sl = blockIdx.y, I = a.I, S = gridDim.y;
+	const int slot = a.tok[t].slot;
+	const int j0 = sl * per, j1 = min(I, j0 + per);
+	const int64_t* prow = a.prod + (size_t)t * I;
+	int64_t w[EPT];
+#pragma unroll
+	for (int k = 0; k < EPT; ++k) {
+		const int i = j0 + threadIdx.x + k * BS;
+		w[k] = i < j1 ? prow[i] : 0;
+	}
+	uint32_t mx = 0;
+	for (int i = 0; i < S; ++i) mx = max(mx, a.act_maxpart[(size_t)i * kPartLd + t]);
+	const Scale inc2[2] = {a.gu_scale[2 * t], a.gu_scale[2 * t + 1]};
+	if (threadIdx.x == 0) s_st = a.status[slot];
+	__syncthreads();
+	if (s_st != 0) return;
+	FunnelPlan ap;
+	const int32_t st = funnel_plan(mx, inc2, 2, a.act_site, &ap);
+	if (st != kOk) {
+		if (threadIdx.x == 0) set_status(a.status, slot, a.layer, st);
+		return;
+	}
+	int8_t* act = a.act + (size_t)t * I;
+#pragma unroll
+	for (int k = 0; k < EPT; ++k) {
+		const int i = j0 + threadIdx.x + k * BS;
+		if (i < j1) act[i] = requant_code_small(w[k], (uint64_t)ap.r, ap.s);
+	}
+	if (threadIdx.x == 0 && sl == 0) a.act_scale[t] = ap.out;
+}
+
 // Attention for one (query head, token): the head's query against positions [0, pos]
 // (forward_sites.cpp:1791-1905).  Scores, i-exp values and Q15 probabilities of the row live in
 // LDS when the context fits (else in the per-launch global scratch); each thread owns the
@@ -2509,6 +2612,30 @@ void mlp_act(const ActArgs& a, hipStream_t s) {
 	SSLM_ACT_EPT_CASES(X)
 #undef X
 	no_instance("mlp_act", a.I);
+}
+
+constexpr int kActSliceBS = 256;
+constexpr int kActSliceMax = 1280;  // columns per slice: EPT <= 5
+
+bool mlp_act_sliced_ok(const ActArgs& a) {
+	return !a.raw.part && a.M <= kMaxSlicedActRows && a.prod && a.act_maxpart && a.gu_scale &&
+	       a.I <= kMaxActSlices * kActSliceMax;
+}
+
+void mlp_act_sliced(const ActArgs& a, hipStream_t s) {
+	const int S = std::max(1, std::min(kMaxActSlices, (a.I + kActSliceMax - 1) / kActSliceMax));
+	const int per = ((a.I + S - 1) / S + 15) / 16 * 16;
+	const int ept = (per + kActSliceBS - 1) / kActSliceBS;
+	const dim3 grid(a.M, (a.I + per - 1) / per);
+#define X(E)                                                                                                  \
+	if (ept <= E) {                                                                                           \
+		hipLaunchKernelGGL((k_mlp_act_s1<kActSliceBS, E>), grid, dim3(kActSliceBS), 0, s, a, per);             \
+		hipLaunchKernelGGL((k_mlp_act_s2<kActSliceBS, E>), grid, dim3(kActSliceBS), 0, s, a, per);             \
+		return;                                                                                               \
+	}
+	X(1) X(2) X(3) X(4) X(5)
+#undef X
+	no_instance("mlp_act_sliced", a.I);
 }
 
 bool row_geometry_ok(int H, int I, int NKV, int D) {

@@ -190,6 +190,9 @@ struct Track {
 	uint32_t *mx_q, *mx_ctx, *mx_o, *mx_gu, *mx_down;  // per (16-column tile, token) partial maxima
 	unsigned long long* argmax_key;                    // [token][tile], head tracks only
 	int32_t* raw_part;  // split-K partial planes, consumed by the next row kernel
+	int64_t* act_prod;       // decode tracks: SiLU products of the sliced mlp_act [64, I]
+	uint32_t* act_maxpart;   // its per-slice maxima
+	Scale* gu_scale;         // its gate / up scales [64, 2]
 	int8_t* kv_stage;    // prefill tracks: landed K/V rows awaiting kv_commit [T][2 * KVH]
 	uint32_t* sat_stage;  // prefill tracks: their clamp counts [T]
 	int8_t* lora_u[3];
@@ -937,8 +940,14 @@ void run_layers(sslm_model m, Track& w, int M, StreamRef st, int l0, int l1, ssl
 			a.layer = l;
 			a.status = m->status;
 			a.raw = raw;
+			a.prod = w.act_prod;
+			a.act_maxpart = w.act_maxpart;
+			a.gu_scale = w.gu_scale;
 			ProfScope p(s, kProfRow, 0, 0);
-			sslm_launch::mlp_act(a, s);
+			// decode rows: one block per (row, column slice) in two launches, instead of one
+			// block per row that leaves most CUs idle
+			if (decode && sslm_launch::mlp_act_sliced_ok(a)) sslm_launch::mlp_act_sliced(a, s);
+			else sslm_launch::mlp_act(a, s);
 			ck(hipGetLastError());
 		}
 		{  // down_proj (forward_sites.cpp:1969-1977)
@@ -1162,6 +1171,9 @@ void alloc_track(sslm_model m, Track& w, int T, bool head) {
 		w.raw_part = elems ? dalloc<int32_t>(elems, &own) : nullptr;
 	}
 	for (int i = 0; i < 3; ++i) w.lora_u[i] = dalloc<int8_t>((size_t)T * kMaxRank, &own);
+	w.act_prod = w.prefill ? nullptr : dalloc<int64_t>((size_t)sslm_launch::kMaxSlicedActRows * I, &own);
+	w.act_maxpart = w.prefill ? nullptr : dalloc<uint32_t>((size_t)sslm_launch::kMaxActSlices * kPartLd, &own);
+	w.gu_scale = w.prefill ? nullptr : dalloc<Scale>((size_t)sslm_launch::kMaxSlicedActRows * 2, &own);
 	w.kv_stage = w.prefill ? dalloc<int8_t>((size_t)T * 2 * KVH, &own) : nullptr;
 	w.sat_stage = w.prefill ? dalloc<uint32_t>(T, &own) : nullptr;
 	// the per-token attention keeps its rows in global scratch when they exceed LDS; a prefill
