@@ -2391,7 +2391,9 @@ GemvPlan gemv_plan(int M, int N, int K, bool split_ok, bool raw_or_argmax) {
 			p.tpw = 4;
 			p.cps = cps;
 			p.splits = (C + cps - 1) / cps;
-			p.cpw = cps <= 9 && p.splits > 1 ? 9 : 3;
+			// one load batch covers a split's whole range where an instance fits it (no clamped
+			// duplicate loads), else batches of 3
+			p.cpw = cps <= 2 ? 2 : (cps <= 3 ? 3 : (cps <= 6 ? 6 : (cps <= 9 ? 9 : 3)));
 			return p;
 		}
 	}
@@ -2419,8 +2421,12 @@ void gemm(const GemmArgs& g, hipStream_t s) {
 		if (p.wave_tile) {
 			const dim3 grid((g.N + 63) / 64, p.splits), block(256);
 			const size_t lds = (size_t)16 * p.cps * 128;
-			if (p.cpw == 9) hipLaunchKernelGGL((k_gemv_w<9>), grid, block, lds, s, g, p.cps);
-			else hipLaunchKernelGGL((k_gemv_w<3>), grid, block, lds, s, g, p.cps);
+			switch (p.cpw) {
+				case 2: hipLaunchKernelGGL((k_gemv_w<2>), grid, block, lds, s, g, p.cps); break;
+				case 6: hipLaunchKernelGGL((k_gemv_w<6>), grid, block, lds, s, g, p.cps); break;
+				case 9: hipLaunchKernelGGL((k_gemv_w<9>), grid, block, lds, s, g, p.cps); break;
+				default: hipLaunchKernelGGL((k_gemv_w<3>), grid, block, lds, s, g, p.cps); break;
+			}
 			return;
 		}
 		const int mblocks = (g.M + 15) / 16;
