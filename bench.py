@@ -430,7 +430,7 @@ def main():
                        "intermediate": cfg.inter, "vocab": cfg.vocab},
             "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-                         "kernel": "decode GEMV (k_gemv): the 113 GEMV launches of one step at M = 16 (28 layers' "
+                         "kernel": "decode GEMV (k_gemv with projection epilogues, k_gemv_w for o, down and the LM head): the 113 GEMV launches of one step at M = 16 (28 layers' "
                                    "q|k|v, o, gate|up, down with their own weights, then the LM head) back to back "
                                    "between two HIP events on the library's stream, so every weight byte streams "
                                    "from HBM as in a step: algorithmic bytes per pass / pass time (launch gaps "
