@@ -84,6 +84,7 @@ struct PrefillPlan {
 	int splits;  // K splits over gridDim.z (raw partial planes)
 	int kspan;   // K per split (multiple of 128)
 	int blocks;  // gridDim.x: one tile per block
+	bool narrow;  // raw output of the 64 x 64-tile kernel, one plane over the whole K
 };
 constexpr int kPrefillTargetBlocks = 256;
 constexpr int kMaxRawSplits = 8;  // split planes a raw consumer adds

@@ -945,6 +945,101 @@ __global__ __launch_bounds__(BM / 32 * 64, 1) void k_gemm_mfma(GemmArgs g, Prefi
 }
 
 // ------------------------------------------------------------------------------------------
+// Narrow prefill GEMM (M > 64, few 256 x 128 tiles): 64 x 64 block tiles over the whole K, raw
+// int32 output (one plane; the consuming row kernel applies the epilogue, RawIn).  The
+// projections whose N is a few thousand columns (q|k|v, o, down) have too few 256 x 128 tiles
+// to fill 256 CUs; the K-split alternative writes one int32 plane per split, several times the
+// output, which then is read back.  Small tiles fill the chip with the whole K per block and
+// write the output once.
+// Block: 4 waves, wave w owns the 32 x 32 sub-tile (w / 2, w % 2) as two v_mfma_i32_32x32x32_i8
+// accumulators (even and odd 32-deep steps, two independent chains).  Operands go global ->
+// LDS directly through NN = 4 stages of 128-deep K steps (16 KB each, XOR-swizzled rows as in
+// lds_chunk); two blocks per CU overlap one's loads and epilogue with the other's MFMAs.
+// Loads are unconditional (rows past M or N read a clamped valid row; their products land only in
+// discarded outputs) and K is a multiple of 128.
+// ------------------------------------------------------------------------------------------
+constexpr int kNarrowTile = 64, kNarrowStages = 4, kNarrowMaxK = 4096;
+
+// lgkmcnt(0) that the two fragments pass through
+__device__ __forceinline__ void lgkm_wait2(v4i& a, v4i& b) { asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a), "+v"(b)); }
+
+__global__ __launch_bounds__(256, 2) void k_gemm_narrow(GemmArgs g) {
+	constexpr int NN = kNarrowStages, T = kNarrowTile;
+	constexpr int STAGE = 2 * T * kPStride;  // A rows then W rows, 128 bytes each
+	constexpr int CPT = STAGE / 1024 / 4;    // 1 KB direct loads per wave per stage
+	__shared__ __attribute__((aligned(1024))) int8_t smem[NN * STAGE];
+	const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+	const int tiles_m = (g.M + T - 1) / T;
+	const int B = gridDim.x;
+	// XCD-aware order (workgroups go round-robin over the 8 XCDs): tiles that share W rows
+	// (same column block) land in one XCD's L2
+	const int vb = B % 8 == 0 ? (int)(blockIdx.x % 8) * (B / 8) + (int)(blockIdx.x / 8) : (int)blockIdx.x;
+	const int m0 = (vb % tiles_m) * T, n0 = (vb / tiles_m) * T;
+	const int S = g.K / kPBK;
+	const int8_t* src[CPT];
+#pragma unroll
+	for (int j = 0; j < CPT; ++j) {
+		const int slot = (wave * CPT + j) * 64 + lane;
+		const int row = slot >> 3, pc = slot & 7;
+		const int q = pc ^ ((row >> 1) & 7);
+		if (row < T) src[j] = g.a + (size_t)min(m0 + row, g.M - 1) * g.lda + q * 16;
+		else src[j] = g.w + (size_t)min(n0 + row - T, g.N - 1) * g.K + q * 16;
+	}
+	auto issue = [&](int st, int t) {  // past the last step the last is fetched again (never read)
+		const size_t kb = (size_t)min(t, S - 1) * kPBK;
+#pragma unroll
+		for (int j = 0; j < CPT; ++j)
+			__builtin_amdgcn_global_load_lds((const void*)(src[j] + kb),
+			                                 (__attribute__((address_space(3))) void*)(smem + st * STAGE + (wave * CPT + j) * 1024),
+			                                 16, 0, 0);
+	};
+	const int wm = (wave >> 1) * 32, wn = (wave & 1) * 32;
+	const uint32_t lds0 = (uint32_t)(size_t)(__attribute__((address_space(3))) int8_t*)smem;
+	uint32_t aoff[4], boff[4];  // the lane's 16-byte chunk of each 32-deep step
+#pragma unroll
+	for (int ks = 0; ks < 4; ++ks) {
+		aoff[ks] = lds0 + lds_chunk(wm + (lane & 31), 2 * ks + (lane >> 5));
+		boff[ks] = lds0 + lds_chunk(T + wn + (lane & 31), 2 * ks + (lane >> 5));
+	}
+	v16i acc0, acc1;
+#pragma unroll
+	for (int v = 0; v < 16; ++v) acc0[v] = acc1[v] = 0;
+#pragma unroll
+	for (int s0 = 0; s0 < NN - 1; ++s0) issue(s0, s0);
+	for (int t = 0; t < S; ++t) {
+		wait_vmcnt<(NN - 2) * CPT>();  // own loads of step t have landed
+		// bare barrier: every wave's loads of step t have landed and every wave is done with step
+		// t - 1, whose stage takes step t + NN - 1 (a __syncthreads() fence would drain the loads)
+		__builtin_amdgcn_s_barrier();
+		issue((t + NN - 1) % NN, t + NN - 1);
+		const uint32_t so = (uint32_t)((t % NN) * STAGE);
+		v4i a0 = lds_read16<0>(aoff[0] + so), b0 = lds_read16<0>(boff[0] + so);
+		v4i a1 = lds_read16<0>(aoff[1] + so), b1 = lds_read16<0>(boff[1] + so);
+		v4i a2 = lds_read16<0>(aoff[2] + so), b2 = lds_read16<0>(boff[2] + so);
+		v4i a3 = lds_read16<0>(aoff[3] + so), b3 = lds_read16<0>(boff[3] + so);
+		lgkm_wait2(a0, b0);
+		lgkm_wait2(a1, b1);
+		lgkm_wait2(a2, b2);
+		lgkm_wait2(a3, b3);
+		acc0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, b0, acc0, 0, 0, 0);
+		acc1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, b1, acc1, 0, 0, 0);
+		acc0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a2, b2, acc0, 0, 0, 0);
+		acc1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a3, b3, acc1, 0, 0, 0);
+	}
+	wait_vmcnt<0>();  // the trailing (clamped) loads land before the block ends
+	// 32x32 layout: lane holds column lane % 32, rows 8 (v / 4) + 4 (lane / 32) + v % 4
+	int32_t* out = g.epi.raw_out;
+	const int col = n0 + wn + (lane & 31);
+	if (col < g.N) {
+#pragma unroll
+		for (int v = 0; v < 16; ++v) {
+			const int row = m0 + wm + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+			if (row < g.M) out[(size_t)row * g.N + col] = acc0[v] + acc1[v];
+		}
+	}
+}
+
+// ------------------------------------------------------------------------------------------
 // row kernels (one block per token)
 // ------------------------------------------------------------------------------------------
 
@@ -2446,6 +2541,12 @@ void gemm(const GemmArgs& g, hipStream_t s) {
 	for (int i = 0; i < g.epi.nseg; ++i) lora = lora || g.epi.seg[i].lora_b;
 	if (!lora && !g.epi.argmax_key && prefill_mfma_k(g.K) && (g.epi.raw_out || g.N % 16 == 0)) {
 		// g.splits > 1 only as prefill_plan(M, N, K, true).splits, sized by the caller
+		// a raw single-plane launch of a narrow shape takes the 64 x 64-tile kernel
+		if (g.epi.raw_out && g.splits <= 1 && prefill_plan(g.M, g.N, g.K, true).narrow) {
+			const int tiles = ((g.M + kNarrowTile - 1) / kNarrowTile) * ((g.N + kNarrowTile - 1) / kNarrowTile);
+			hipLaunchKernelGGL(k_gemm_narrow, dim3(tiles), dim3(256), 0, s, g);
+			return;
+		}
 		const PrefillPlan p = prefill_plan(g.M, g.N, g.K, g.splits > 1);
 		const dim3 grid(p.blocks, 1, p.splits);
 		if (p.bm == 256) hipLaunchKernelGGL((k_gemm_mfma<256, kPrefillStages>), grid, dim3(512), 0, s, g, p);
@@ -2464,6 +2565,15 @@ PrefillPlan prefill_plan(int M, int N, int K, bool split_ok) {
 	const int tiles = ((M + p.bm - 1) / p.bm) * ((N + kPBN - 1) / kPBN);
 	const int steps = (K + kPBK - 1) / kPBK;
 	p.splits = 1;
+	// narrow: raw output of 64 x 64 tiles, one plane, for consumers that add raw planes.  Every
+	// small tile streams its whole K of both operands, so long K (the down projection) keeps
+	// the large tiles with K split into planes.
+	p.narrow = split_ok && tiles < kPrefillTargetBlocks && K <= kNarrowMaxK;
+	if (p.narrow) {
+		p.kspan = K;
+		p.blocks = tiles;
+		return p;
+	}
 	if (split_ok && tiles < kPrefillTargetBlocks)
 		p.splits = std::max(1, std::min({(kPrefillTargetBlocks + tiles - 1) / tiles, steps / 2, kMaxRawSplits}));
 	const int steps_per = (steps + p.splits - 1) / p.splits;

@@ -582,8 +582,10 @@ RawIn split_raw(sslm_model m, Track& w, GemmArgs& g, bool allow_multi, bool allo
 		if (splits == 1 && !allow_single) return r;
 	} else {
 		if (!allow_multi || lora || !sslm_launch::prefill_mfma_k(g.K)) return r;
-		splits = sslm_launch::prefill_plan(g.M, g.N, g.K, true).splits;
-		if (splits <= 1) return r;
+		const PrefillPlan pp = sslm_launch::prefill_plan(g.M, g.N, g.K, true);
+		splits = pp.splits;
+		if (pp.narrow && !allow_single) return r;  // the 64 x 64-tile kernel writes raw only
+		if (splits <= 1 && !pp.narrow) return r;
 	}
 	r.part = w.raw_part;
 	r.splits = splits;
@@ -1164,8 +1166,14 @@ void alloc_track(sslm_model m, Track& w, int T, bool head) {
 				int sp = 1;
 				const bool gemv = sslm_launch::gemv_eligible(rows, sh[1]);
 				if (gemv) sp = sslm_launch::gemv_plan(rows, sh[0], sh[1], true, true).splits;
-				else if (sslm_launch::prefill_mfma_k(sh[1])) sp = sslm_launch::prefill_plan(rows, sh[0], sh[1], true).splits;
-				if (sp > 1 || gemv) elems = std::max(elems, (size_t)sp * rows * sh[0]);  // a GEMV is always raw
+				bool narrow = false;
+				if (!gemv && sslm_launch::prefill_mfma_k(sh[1])) {
+					const PrefillPlan pp = sslm_launch::prefill_plan(rows, sh[0], sh[1], true);
+					sp = pp.splits;
+					narrow = pp.narrow;
+				}
+				// a GEMV and the narrow prefill kernel are always raw
+				if (sp > 1 || gemv || narrow) elems = std::max(elems, (size_t)sp * rows * sh[0]);
 			}
 		}
 		w.raw_part = elems ? dalloc<int32_t>(elems, &own) : nullptr;

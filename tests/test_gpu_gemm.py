@@ -24,14 +24,18 @@ def _lib(hip_lib):
                                    # ragged row and column tiles at several K steps
                                    (300, 16512, 256), (257, 4224, 384),
                                    # wave-per-tile GEMV (N >= 16384 at M <= 16), ragged N and batches
-                                   (16, 17920, 1536), (1, 151936, 1536), (13, 16400, 640), (7, 16448, 1280)])
+                                   (16, 17920, 1536), (1, 151936, 1536), (13, 16400, 640), (7, 16448, 1280),
+                                   # the gate|up shape of a 512-token chunk, 128-row tiles over 296
+                                   # column tiles, ragged rows at two K steps
+                                   (512, 17920, 1536), (100, 37888, 512), (448, 33024, 256)])
 def test_gemm_i32_exact(m, n, k, hip_lib):
     L = _lib(hip_lib)
     dev = Device(hip_lib)
     rng = np.random.default_rng(m * 1000 + n + k)
     a = rng.integers(-127, 128, size=(m, k), dtype=np.int8)
     w = rng.integers(-128, 128, size=(n, k), dtype=np.int8)
-    exp = a.astype(np.int64) @ w.astype(np.int64).T
+    # |sums| < 2^53: float64 products are exact and take the BLAS path
+    exp = (a.astype(np.float64) @ w.astype(np.float64).T).astype(np.int64)
     da, dw = dev.upload(a), dev.upload(w)
     out = dev.zeros((m, n), np.int32)
     print(f"case gemm m={m} n={n} k={k}", flush=True)
