@@ -337,4 +337,12 @@ void slot_state_copy(const SlotCopyArgs& a, int n, bool restore, hipStream_t s);
 // per-tile argmax keys -> token ids (lowest index among equal maxima)
 void argmax_finalize(const unsigned long long* keys, int ntiles, int M, int32_t* out_tokens, hipStream_t s);
 
+// Damped greedy's candidate set on the device: per row of raw logits [M][V] (masked logits, per
+// the row's mask page, count as INT32_MIN), the k entries first in the order (logit descending,
+// legal before masked, index ascending), written unordered as (index, logit) pairs to
+// out[row * k ..].  k <= kTopKMax.
+constexpr int kTopKMax = 1024;
+void topk_candidates(const int32_t* logits, int V, int M, const uint8_t* const* mask_page, int k, int2* out,
+                     hipStream_t s);
+
 }  // namespace sslm_launch

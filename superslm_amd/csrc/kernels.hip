@@ -2432,6 +2432,64 @@ __global__ __launch_bounds__(kBlock) void k_lora_u(sslm_launch::LoraUArgs a) {
 // lowest-index argmax (forward_sites.cpp:2427-2437) from per-tile keys: the key orders by
 // logit, then by the complement of the index, so the maximum key is the lowest maximal index.
 // One block per token over its contiguous key row; loads go out in batches of 8 per thread.
+// Damped greedy's top-k set (src/damped_greedy_topk.cpp's FsdTopK order) by radix selection:
+// each element's 64-bit key -- biased logit (INT32_MIN when masked) in the high word, then the
+// legal bit, then 2^31 - 1 - index -- is unique and orders like the reference's comparator, so
+// the k largest keys are the candidate set.  Eight passes fix the k-th largest key a byte at a
+// time from the top (a 256-bin histogram of the elements still matching the fixed prefix); a
+// last pass writes every element whose key is at least that one.
+constexpr int kTopKBlock = 1024;
+__device__ __forceinline__ uint64_t topk_key(const int32_t* row, const uint8_t* page, int i) {
+	const bool legal = !page || ((page[i >> 3] >> (i & 7)) & 1u);
+	const int32_t v = legal ? row[i] : INT32_MIN;
+	return ((uint64_t)((uint32_t)v ^ 0x80000000u) << 32) | ((uint64_t)legal << 31) | (uint32_t)(0x7fffffff - i);
+}
+
+__global__ __launch_bounds__(kTopKBlock) void k_topk(const int32_t* logits, int V, const uint8_t* const* mask_page,
+                                                    int k, int2* out) {
+	__shared__ uint32_t hist[256];
+	__shared__ uint64_t s_prefix;
+	__shared__ int s_need, s_count;
+	const int r = blockIdx.x;
+	const int32_t* row = logits + (size_t)r * V;
+	const uint8_t* page = mask_page ? mask_page[r] : nullptr;
+	uint64_t prefix = 0, fixed = 0;  // the k-th largest key's bits fixed so far, and their mask
+	int need = k;                    // its rank among the elements matching the prefix
+	for (int shift = 56; shift >= 0; shift -= 8) {
+		for (int b = threadIdx.x; b < 256; b += kTopKBlock) hist[b] = 0;
+		__syncthreads();
+		for (int i = threadIdx.x; i < V; i += kTopKBlock) {
+			const uint64_t key = topk_key(row, page, i);
+			if ((key & fixed) == prefix) atomicAdd(&hist[(key >> shift) & 0xff], 1u);
+		}
+		__syncthreads();
+		if (threadIdx.x == 0) {
+			int acc = 0, b = 255;
+			for (; b > 0; --b) {
+				if (acc + (int)hist[b] >= need) break;
+				acc += (int)hist[b];
+			}
+			s_need = need - acc;
+			s_prefix = prefix | ((uint64_t)b << shift);
+		}
+		__syncthreads();
+		need = s_need;
+		prefix = s_prefix;
+		fixed |= (uint64_t)0xff << shift;
+		__syncthreads();
+	}
+	if (threadIdx.x == 0) s_count = 0;
+	__syncthreads();
+	int2* o = out + (size_t)r * k;
+	for (int i = threadIdx.x; i < V; i += kTopKBlock) {
+		const uint64_t key = topk_key(row, page, i);
+		if (key >= prefix) {
+			const int at = atomicAdd(&s_count, 1);
+			if (at < k) o[at] = make_int2(i, (int32_t)((uint32_t)(key >> 32) ^ 0x80000000u));
+		}
+	}
+}
+
 __global__ __launch_bounds__(kRowBlock) void k_argmax_finalize(const unsigned long long* keys, int ntiles,
                                                                int32_t* out) {
 	__shared__ uint64_t red[kRowBlock / 64];
@@ -2760,6 +2818,12 @@ bool row_geometry_ok(int H, int I, int NKV, int D) {
 }
 
 void lora_u(const LoraUArgs& a, hipStream_t s) { hipLaunchKernelGGL(k_lora_u, dim3(a.M, a.nproj), dim3(kBlock), 0, s, a); }
+
+void topk_candidates(const int32_t* logits, int V, int M, const uint8_t* const* mask_page, int k, int2* out,
+                     hipStream_t s) {
+	if (M <= 0) return;
+	hipLaunchKernelGGL(k_topk, dim3(M), dim3(kTopKBlock), 0, s, logits, V, mask_page, k, out);
+}
 
 void argmax_finalize(const unsigned long long* keys, int ntiles, int M, int32_t* out_tokens, hipStream_t s) {
 	hipLaunchKernelGGL(k_argmax_finalize, dim3(M), dim3(kRowBlock), 0, s, keys, ntiles, out_tokens);

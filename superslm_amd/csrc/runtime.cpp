@@ -315,6 +315,7 @@ struct sslm_model_s {
 	bool dg_available = false;
 	int64_t dg_q_ln2 = 0, dg_q_b = 0, dg_q_c = 0;
 	int32_t* logits = nullptr;  // [kMaxTokens, V] raw head rows, allocated on first use
+	int2* topk = nullptr;       // [kMaxTokens, kTopKMax] damped greedy's device candidates
 	std::vector<SchemaEntry> schemas;
 	std::vector<sslm_schema_s> schema_handles;
 	uint32_t page_bytes = 0;  // (V + 7) / 8
@@ -1017,29 +1018,21 @@ void run_logits(sslm_model m, Track& w, int M, StreamRef st, const TokenInfo* to
 // Q15 (TopKRenormalizeQ15: each against the row-max peak, refused when any is out of domain);
 // p_omega from the anti-LM; winner = max of q_theta - (alpha * p_omega >> 15), lowest index on
 // ties.  Returns false when refused.
-bool damped_pick(const int32_t* row, int V, const sslm_decode_params& p, const AntiLm& lm, const uint8_t* page,
-                 int32_t* token) {
+// The selection after top-k: `idx` and `val` are the k candidates in FsdTopK order.
+bool damped_select(const int32_t* idx, const int32_t* val, const sslm_decode_params& p, const AntiLm& lm,
+                   const uint8_t* page, int32_t* token) {
 	const int k = p.top_k;
 	auto legal = [&](int32_t t) { return !page || ((page[t >> 3] >> (t & 7)) & 1u); };
-	std::vector<int32_t> idx(V);
-	for (int i = 0; i < V; ++i) idx[i] = i;
-	// FsdTopK order: logit desc, then legal before masked, then index asc
-	auto before = [&](int32_t a, int32_t b) {
-		if (row[a] != row[b]) return row[a] > row[b];
-		if (legal(a) != legal(b)) return legal(a);
-		return a < b;
-	};
-	std::partial_sort(idx.begin(), idx.begin() + k, idx.end(), before);
 	if (check_softmax_width(p.q_b, p.q_c, k) != kOk) return false;
-	int64_t row_max = row[idx[0]];
-	for (int i = 1; i < k; ++i) row_max = std::max<int64_t>(row_max, row[idx[i]]);
+	int64_t row_max = val[0];
+	for (int i = 1; i < k; ++i) row_max = std::max<int64_t>(row_max, val[i]);
 	const int64_t peak = iexp_element(0, p.q_ln2, p.q_b, p.q_c, kI64Max);
 	const bool peak_ok = peak >= 1 && peak <= kSoftmaxMaxSafe;
 	std::vector<int64_t> q(k, 0);
 	bool well_formed = peak_ok;
 	int64_t total = 0;
 	for (int i = 0; i < k; ++i) {
-		const int64_t v = iexp_element((int64_t)row[idx[i]] - row_max, p.q_ln2, p.q_b, p.q_c, kI64Max);
+		const int64_t v = iexp_element((int64_t)val[i] - row_max, p.q_ln2, p.q_b, p.q_c, kI64Max);
 		if (v < 0 || !peak_ok || v > peak) {  // refused construction, or outside [0, peak]
 			well_formed = false;
 			continue;
@@ -1051,7 +1044,7 @@ bool damped_pick(const int32_t* row, int V, const sslm_decode_params& p, const A
 	const int64_t denom = total > 1 ? total : 1;
 	for (int i = 0; i < k; ++i) q[i] = (q[i] << 15) / denom;
 	std::vector<int64_t> omega(k, 0);
-	lm.penalize(idx.data(), k, omega.data());
+	lm.penalize(idx, k, omega.data());
 	int64_t best = 0;
 	int32_t best_tok = -1;
 	for (int i = 0; i < k; ++i) {
@@ -1063,6 +1056,46 @@ bool damped_pick(const int32_t* row, int V, const sslm_decode_params& p, const A
 	}
 	*token = best_tok;
 	return true;
+}
+
+// FsdTopK order: logit desc, then legal before masked, then index asc
+struct TopKOrder {
+	const uint8_t* page;
+	bool legal(int32_t t) const { return !page || ((page[t >> 3] >> (t & 7)) & 1u); }
+	bool operator()(int32_t a, int32_t va, int32_t b, int32_t vb) const {
+		if (va != vb) return va > vb;
+		if (legal(a) != legal(b)) return legal(a);
+		return a < b;
+	}
+};
+
+// Over a whole logit row (masked logits already INT32_MIN).
+bool damped_pick(const int32_t* row, int V, const sslm_decode_params& p, const AntiLm& lm, const uint8_t* page,
+                 int32_t* token) {
+	const int k = p.top_k;
+	const TopKOrder ord{page};
+	std::vector<int32_t> idx(V);
+	for (int i = 0; i < V; ++i) idx[i] = i;
+	std::partial_sort(idx.begin(), idx.begin() + k, idx.end(),
+	                  [&](int32_t a, int32_t b) { return ord(a, row[a], b, row[b]); });
+	std::vector<int32_t> val(k);
+	for (int i = 0; i < k; ++i) val[i] = row[idx[i]];
+	return damped_select(idx.data(), val.data(), p, lm, page, token);
+}
+
+// Over the device's candidate set: the k (index, logit) pairs first in FsdTopK order, unordered.
+bool damped_pick_candidates(const int2* cand, const sslm_decode_params& p, const AntiLm& lm, const uint8_t* page,
+                            int32_t* token) {
+	const int k = p.top_k;
+	const TopKOrder ord{page};
+	std::vector<int2> c(cand, cand + k);
+	std::sort(c.begin(), c.end(), [&](const int2& a, const int2& b) { return ord(a.x, a.y, b.x, b.y); });
+	std::vector<int32_t> idx(k), val(k);
+	for (int i = 0; i < k; ++i) {
+		idx[i] = c[i].x;
+		val[i] = c[i].y;
+	}
+	return damped_select(idx.data(), val.data(), p, lm, page, token);
 }
 
 sslm_status map_forward_status(int32_t word) {
@@ -1983,10 +2016,14 @@ static sslm_status decode_batch(sslm_model m, sslm_seq* seqs, int32_t n, const s
 	lg.insert(lg.end(), finished.begin(), finished.end());
 	// whole logit rows come back to the host for damped greedy; a schema-bound sequence's greedy
 	// argmax is masked on the device (its mask page per token)
-	const bool rows_needed = damped;
+	// Damped greedy takes the head's raw int32 rows; up to kTopKMax candidates per row are chosen
+	// on the device and only they come back, else the whole rows do.
+	const bool cands = damped && params.top_k <= sslm_launch::kTopKMax;
+	const bool rows_needed = damped && !cands;
 	bool masked = false;
 	for (int i : lg) masked = masked || seqs[i]->schema;
-	if (rows_needed && !m->logits) m->logits = dalloc<int32_t>((size_t)kMaxTokens * m->V, &m->owned);
+	if (damped && !m->logits) m->logits = dalloc<int32_t>((size_t)kMaxTokens * m->V, &m->owned);
+	if (cands && !m->topk) m->topk = dalloc<int2>((size_t)kMaxTokens * sslm_launch::kTopKMax, &m->owned);
 
 	// Host staging, uploaded before the kernels (kept alive until the sync below).  The common
 	// shape -- at most one unit per track and one head chunk -- stages every unit's tokens in its
@@ -2060,14 +2097,20 @@ static sslm_status decode_batch(sslm_model m, sslm_seq* seqs, int32_t n, const s
 	auto launch_logits = [&](int M) {
 		run_logits(m, t0, M, StreamRef{m->stream_codes, m->stream_scale, t0.lg_slot}, t0.lg_tok,
 		           masked ? t0.lg_mask : nullptr);
-		if (rows_needed) {  // the whole logit rows as well: the head's raw int32 accumulators
+		if (damped) {  // the whole logit rows as well: the head's raw int32 accumulators
 			GemmArgs g = head_args(m, t0, M, t0.lg_tok);
 			g.epi.argmax_key = nullptr;
 			g.epi.raw_out = m->logits;
 			run_gemm(m, t0, g, kProfHead);
+			if (cands) {
+				sslm_launch::topk_candidates(m->logits, m->V, M, masked ? t0.lg_mask : nullptr, params.top_k, m->topk,
+				                             t0.stream);
+				ck(hipGetLastError());
+			}
 		}
 	};
 	std::vector<int32_t> rows(rows_needed ? lg.size() * (size_t)m->V : 0);
+	std::vector<int2> cand(cands ? lg.size() * (size_t)params.top_k : 0);
 	// every sequence of one call shares the pool of the first (checked by the caller)
 	m->pool_dev = seqs[0]->pool->dev;
 	std::vector<int32_t> toks(lg.size());
@@ -2099,7 +2142,9 @@ static sslm_status decode_batch(sslm_model m, sslm_seq* seqs, int32_t n, const s
 		if (!lg.empty()) {
 			const int M = (int)lg.size();
 			if (use_graph)
-				ck(hipGraphLaunch(graph_of(m, "lg|" + std::to_string(M) + (rows_needed ? "|r" : "") + (masked ? "|m" : ""), t0.stream,
+				ck(hipGraphLaunch(graph_of(m, "lg|" + std::to_string(M) + (rows_needed ? "|r" : "") +
+				                                  (cands ? "|c" + std::to_string(params.top_k) : "") + (masked ? "|m" : ""),
+				                           t0.stream,
 				                           [&] { launch_logits(M); }),
 				                  t0.stream));
 			else launch_logits(M);
@@ -2107,6 +2152,8 @@ static sslm_status decode_batch(sslm_model m, sslm_seq* seqs, int32_t n, const s
 		if (!lg.empty()) ck(hipMemcpyAsync(toks.data(), t0.out_tokens, lg.size() * 4, hipMemcpyDeviceToHost, t0.stream));
 		if (rows_needed && !lg.empty())
 			ck(hipMemcpyAsync(rows.data(), m->logits, rows.size() * 4, hipMemcpyDeviceToHost, t0.stream));
+		if (cands && !lg.empty())
+			ck(hipMemcpyAsync(cand.data(), m->topk, cand.size() * sizeof(int2), hipMemcpyDeviceToHost, t0.stream));
 	} else {
 		std::vector<bool> used(ntr, false);
 		for (size_t u = 0; u < units.size(); ++u) {
@@ -2127,6 +2174,9 @@ static sslm_status decode_batch(sslm_model m, sslm_seq* seqs, int32_t n, const s
 			if (rows_needed)
 				ck(hipMemcpyAsync(rows.data() + b * (size_t)m->V, m->logits, (size_t)M * m->V * 4, hipMemcpyDeviceToHost,
 				                  t0.stream));
+			if (cands)
+				ck(hipMemcpyAsync(cand.data() + b * (size_t)params.top_k, m->topk, (size_t)M * params.top_k * sizeof(int2),
+				                  hipMemcpyDeviceToHost, t0.stream));
 		}
 	}
 	std::vector<int32_t> words(kSlotCapacity);
@@ -2187,7 +2237,9 @@ static sslm_status decode_batch(sslm_model m, sslm_seq* seqs, int32_t n, const s
 		if (damped) {  // src/sslm_abi.cpp:2301-2384
 			if (s->anti_lm.order == 0 || s->anti_lm.order != params.anti_lm_max_order)
 				s->anti_lm.reset(params.anti_lm_max_order);
-			if (!damped_pick(row, m->V, params, s->anti_lm, page, &tok)) {
+			const bool ok = cands ? damped_pick_candidates(cand.data() + k * (size_t)params.top_k, params, s->anti_lm, page, &tok)
+			                      : damped_pick(row, m->V, params, s->anti_lm, page, &tok);
+			if (!ok) {
 				first_err = map_forward_status(kSoftmaxKernelRefusedAfterGateAccepted);
 				stop_at = i + 1;
 				break;

@@ -8,7 +8,7 @@ import numpy as np
 import pytest
 
 from superslm_amd.sslm import Model
-from superslm_amd.sslm_artifact import CONFIGS, build_synthetic, with_flags
+from superslm_amd.sslm_artifact import CONFIGS, build_synthetic, with_flags, with_weight_rows
 
 pytestmark = pytest.mark.gpu
 
@@ -82,6 +82,48 @@ def test_damped_decode_matches_reference(name, hip_lib, ref_lib):
         if name == "small":  # its greedy continuations repeat, so the anti-LM penalty bites
             g = _run(ref_lib, art, prompts, steps, budget, lambda m, b: m.decode_params(b, 0))
             assert g[0] != r[0], "damping changed no token: the test would not see it"
+
+
+def _run_raw(lib, art, prompts, steps, budget, top_k):
+    """Decode with damped greedy at `top_k`: per step (status, tokens), then every KV block."""
+    model = Model(lib, art)
+    pool = model.pool(len(prompts))
+    seqs = [pool.seq() for _ in prompts]
+    for sq, p in zip(seqs, prompts):
+        sq.prefill(p)
+    out = []
+    for _ in range(steps):
+        params = model.decode_params(budget, 1)
+        params.top_k = top_k
+        out.append(model.decode_step(seqs, budget, raw=True, params=params))
+    kv = [pool.kv_block(i).copy() for i in range(len(prompts))]
+    for sq in seqs:
+        sq.release()
+    pool.close()
+    model.close()
+    return out, kv
+
+
+@pytest.mark.parametrize("tied", [False, True])
+@pytest.mark.parametrize("top_k", [1, 37, 1024, 1500])
+def test_damped_candidate_sets_match_reference(top_k, tied, hip_lib, ref_lib):
+    """The device's top-k candidate set (k <= 1024; above that whole rows come back) against the
+    reference's partial sort, on a 4096-token vocabulary; `tied`: the LM head's rows repeat every
+    64, so every logit value occurs 64 times and the cut at k falls inside runs of equal logits
+    (ordered by index)."""
+    sm, art = damped_artifact("medium")
+    if tied:
+        head = sm.weights["lm_head"]
+        art = with_weight_rows(sm, "lm_head", {r: head[r % 64] for r in range(64, sm.config.vocab)})
+    rng = np.random.default_rng(top_k)
+    prompts = [rng.integers(0, sm.config.vocab, size=n) for n in (5, 3)]
+    L = sm.config.layers
+    print(f"case damped top_k={top_k} tied={tied}", flush=True)
+    r = _run_raw(ref_lib, art, prompts, 6, L, top_k)
+    h = _run_raw(hip_lib, art, prompts, 6, L, top_k)
+    assert h[0] == r[0], f"statuses / tokens differ: hip {h[0]} ref {r[0]}"
+    for i in range(len(prompts)):
+        assert np.array_equal(h[1][i], r[1][i]), f"KV of sequence {i} differs"
 
 
 def test_damped_restore_continues_like_reference(hip_lib, ref_lib):
