@@ -207,6 +207,16 @@ int32_t sslm_hip_bench_prefill_gemm(sslm_model model, int32_t M, int32_t iters, 
  * shapes recorded (entries beyond `cap` are not written). */
 int sslm_hip_profile_shapes(int64_t* keys, double* ms, int64_t* launches, int64_t* bytes, int64_t* ops, int cap);
 
+/* Per-site trace for bisecting a parity failure (no counterpart in the reference's C ABI; the
+ * reference declares the same per-site record, codes and carried scale, in
+ * include/superslm/trace_hook.h:36-112 but never installs it from sslm_abi.cpp): after a
+ * sslm_decode_step whose sequences ran as one decode unit, the codes and carried scale of row
+ * `row` (the row-th sequence of the call) at `site` for the last layer the unit ran --
+ * 0 attention RMSNorm, 1 attention context funnel, 2 attention residual, 3 MLP RMSNorm,
+ * 4 MLP activation.  With layer_budget 1 every call exposes one layer.  `codes` holds the row
+ * (hidden or intermediate size), `scale_me` its (m, e).  Returns the row's length, or -1. */
+int32_t sslm_hip_debug_site(sslm_model model, int32_t site, int32_t row, int8_t* codes, int64_t* scale_me);
+
 /* The single GEMM + requant of BASELINE configuration 0, on device buffers: int8 A [m, k] x int8
  * W [n, k]^T, int32 accumulate, per-output-row WSC1 fold `fold` [n, 3] (identity, mult, shift),
  * then the per-token dynamic requant funnel with incoming scale `in_m/in_e` and site constant

@@ -730,6 +730,16 @@ static int check_geometry(const or_model* m) {
 
 /* forward_sites.cpp:1429-2014 -- sliced decode: up to `layer_budget` layers, one commit per
  * layer, context_length advanced after the last layer. */
+static or_trace_fn g_trace_fn;
+static void* g_trace_user;
+void or_set_trace(or_trace_fn fn, void* user) {
+	g_trace_fn = fn;
+	g_trace_user = fn ? user : NULL;
+}
+static void trace_site(uint32_t layer, int site, const int8_t* codes, size_t n, or_scale sc) {
+	if (g_trace_fn) g_trace_fn(g_trace_user, layer, site, codes, n, sc.m, sc.e);
+}
+
 int or_run_layer_loop(const or_model* m, or_seq* seq, uint32_t layer_budget, int8_t* kv) {
 	if (layer_budget == 0) return OR_INVALID_LAYER_BUDGET;
 	int st = check_geometry(m);
@@ -760,30 +770,41 @@ int or_run_layer_loop(const or_model* m, or_seq* seq, uint32_t layer_budget, int
 		or_scale ns, qs, cs, os, as, mns, gs, us, acts, ds, ss;
 		uint32_t r = lw->lora_rank;
 		if ((st = or_rmsnorm_site(seq->hidden, lw->attn_gain, H, lw->attn_norm_sc, normed, &ns))) break;
+		trace_site(l, OR_SITE_ATTN_NORM, normed, H, ns);
 		if ((st = or_project_row(normed, ns, H, H, lw->w[OR_Q], lw->fold[OR_Q], lw->bias[0], lw->lora[OR_Q],
 		                         r, lw->q_sc, q, &qs)))
 			break;
+		trace_site(l, OR_SITE_Q, q, H, qs);
 		or_gemm_i8(normed, lw->w[OR_K], 1, H, KVH, kacc);
 		or_gemm_i8(normed, lw->w[OR_V], 1, H, KVH, vacc);
 		if ((st = land_kv(m, lw, l, kacc, vacc, normed, ns, pos, kv, &seq->kv_saturation_count))) break;
 		if ((st = rope_q_and_k(m, l, q, pos, kv, q_rot))) break;
 		if ((st = attention(m, lw, l, q_rot, qs, pos, kv, ctx, &cs))) break;
+		trace_site(l, OR_SITE_CTX, ctx, H, cs);
 		if ((st = or_project_row(ctx, cs, H, H, lw->w[OR_O], lw->fold[OR_O], NULL, lw->lora[OR_O], r, lw->o_sc, o,
 		                         &os)))
 			break;
+		trace_site(l, OR_SITE_O, o, H, os);
 		if ((st = or_residual_site(o, os, seq->hidden, seq->scale, H, lw->attn_res_sc, attn_stream, &as))) break;
+		trace_site(l, OR_SITE_ATTN_RESIDUAL, attn_stream, H, as);
 		if ((st = or_rmsnorm_site(attn_stream, lw->mlp_gain, H, lw->mlp_norm_sc, normed, &mns))) break;
+		trace_site(l, OR_SITE_MLP_NORM, normed, H, mns);
 		if ((st = or_project_row(normed, mns, H, I, lw->w[OR_GATE], lw->fold[OR_GATE], NULL, lw->lora[OR_GATE], r,
 		                         lw->gate_sc, gate, &gs)))
 			break;
 		if ((st = or_project_row(normed, mns, H, I, lw->w[OR_UP], lw->fold[OR_UP], NULL, lw->lora[OR_UP], r,
 		                         lw->up_sc, up, &us)))
 			break;
+		trace_site(l, OR_SITE_GATE, gate, I, gs);
+		trace_site(l, OR_SITE_UP, up, I, us);
 		if ((st = or_mlp_act_site(gate, gs, up, us, I, m->silu_table, lw->act_sc, act, &acts))) break;
+		trace_site(l, OR_SITE_ACT, act, I, acts);
 		if ((st = or_project_row(act, acts, I, H, lw->w[OR_DOWN], lw->fold[OR_DOWN], NULL, lw->lora[OR_DOWN], r,
 		                         lw->down_sc, down, &ds)))
 			break;
+		trace_site(l, OR_SITE_DOWN, down, H, ds);
 		if ((st = or_residual_site(down, ds, attn_stream, as, H, lw->mlp_res_sc, next, &ss))) break;
+		trace_site(l, OR_SITE_MLP_RESIDUAL, next, H, ss);
 		memcpy(seq->hidden, next, H);
 		seq->scale = ss;
 		seq->layer_index = l + 1;

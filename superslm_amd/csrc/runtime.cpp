@@ -2989,6 +2989,35 @@ int32_t sslm_hip_bench_prefill_gemm(sslm_model model, int32_t M, int32_t iters, 
 	return st == SSLM_OK ? 1 : -1;
 }
 
+int32_t sslm_hip_debug_site(sslm_model model, int32_t site, int32_t row, int8_t* codes, int64_t* scale_me) {
+	if (!model || !codes || !scale_me || row < 0) return -1;
+	sslm_model m = model;
+	std::lock_guard<std::mutex> lk(m->mu);
+	if (m->tracks.empty() || row >= m->tracks[0].capacity) return -1;
+	const Track& w = m->tracks[0];
+	const int8_t* src = nullptr;
+	const Scale* sc = nullptr;
+	int n = m->H;
+	switch (site) {
+		case 0: src = w.normed; sc = w.normed_scale; break;
+		case 1: src = w.ctx; sc = w.ctx_scale; break;
+		case 2: src = w.attn_stream; sc = w.attn_stream_scale; break;
+		case 3: src = w.mlp_normed; sc = w.mlp_scale; break;
+		case 4: src = w.act; sc = w.act_scale; n = m->I; break;
+		default: return -1;
+	}
+	const sslm_status st = guarded([&]() -> sslm_status {
+		ck(hipStreamSynchronize(w.stream));
+		ck(hipMemcpy(codes, src + (size_t)row * n, n, hipMemcpyDeviceToHost));
+		Scale h{};
+		ck(hipMemcpy(&h, sc + row, sizeof(Scale), hipMemcpyDeviceToHost));
+		scale_me[0] = h.m;
+		scale_me[1] = h.e;
+		return SSLM_OK;
+	});
+	return st == SSLM_OK ? n : -1;
+}
+
 // ---- profiling ----
 void sslm_hip_profile_enable(int on) { g_prof.on = on != 0; }
 void sslm_hip_profile_reset(void) {
