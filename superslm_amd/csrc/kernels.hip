@@ -945,6 +945,217 @@ __global__ __launch_bounds__(BM / 32 * 64, 1) void k_gemm_mfma(GemmArgs g, Prefi
 }
 
 // ------------------------------------------------------------------------------------------
+// Wide prefill GEMM (the gate|up projection: N in the tens of thousands): 256 x 160 block tiles,
+// so a 512-token chunk's 17,920 columns make 224 tiles -- one round over 256 CUs, where 256 x 128
+// tiles make 280 and leave a second round mostly idle with its own prologue and epilogue.
+// Block: 4 waves, wave w owns rows [64 w, 64 w + 64) x all 160 columns as 4 x 10
+// v_mfma_i32_16x16x64_i8 accumulators.  Operands go global -> LDS directly through 3 stages of
+// 128-deep K steps (416 rows of 128 bytes, XOR-swizzled as in lds_chunk; 13 one-kilobyte wave
+// loads per wave per stage); a stage's two 64-deep halves are read from LDS together, the second
+// while the first's MFMAs run.  Epilogue: raw int32, or funnel segments (WSC1 fold, int32 store,
+// per-(16-column tile, token) maxima) without bias or LoRA -- a 16 x 16 accumulator is one
+// column tile, reduced over its 16 lanes with DPP.  The fold parameters are loaded before the
+// main loop.  Loads are unconditional (rows past M or N read a clamped valid row) and K is a
+// multiple of 128.
+// ------------------------------------------------------------------------------------------
+constexpr int kWideBM = 256, kWideBN = 160, kWideStages = 3;
+
+__device__ __forceinline__ void lgkm_wait_n14(v4i (&a)[4], v4i (&b)[10]) {
+	asm volatile("s_waitcnt lgkmcnt(14)"
+	             : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]), "+v"(b[0]), "+v"(b[1]), "+v"(b[2]), "+v"(b[3]),
+	               "+v"(b[4]), "+v"(b[5]), "+v"(b[6]), "+v"(b[7]), "+v"(b[8]), "+v"(b[9]));
+}
+__device__ __forceinline__ void lgkm_wait_n0(v4i (&a)[4], v4i (&b)[10]) {
+	asm volatile("s_waitcnt lgkmcnt(0)"
+	             : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]), "+v"(b[0]), "+v"(b[1]), "+v"(b[2]), "+v"(b[3]),
+	               "+v"(b[4]), "+v"(b[5]), "+v"(b[6]), "+v"(b[7]), "+v"(b[8]), "+v"(b[9]));
+}
+
+__global__ __launch_bounds__(256, 1) void k_gemm_wide(GemmArgs g) {
+	constexpr int BM = kWideBM, BN = kWideBN, NS = kWideStages, NB = BN / 16;
+	constexpr int ROWS = BM + BN, STAGE = ROWS * kPStride;
+	constexpr int CPT = STAGE / 1024 / 4;  // 13
+	static_assert(CPT * 4 * 1024 == STAGE, "stage must split evenly over the waves");
+	static_assert((NS - 1) * CPT < 64, "stages in flight must fit vmcnt");
+	__shared__ __attribute__((aligned(1024))) int8_t smem[NS * STAGE];
+	const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+	const int tiles_m = (g.M + BM - 1) / BM;
+	const int B = gridDim.x;
+	const int vb = B % 8 == 0 ? (int)(blockIdx.x % 8) * (B / 8) + (int)(blockIdx.x / 8) : (int)blockIdx.x;
+	const int m0 = (vb % tiles_m) * BM, n0 = (vb / tiles_m) * BN;
+	const int S = g.K / kPBK;
+	const Epilogue& e = g.epi;
+	const bool raw = e.raw_out != nullptr;
+	const int cl = lane & 15;
+	// The epilogue's fold parameters of the tile's 160 columns (480 int32, 120 chunks of 16
+	// bytes, 12 per 16-column tile), loaded before the main loop, one chunk per thread, and
+	// parked in LDS after it.
+	constexpr int kParamChunks = BN * 3 / 4;
+	v4i fchunk = v4i{0, 0, 0, 0};
+	if (!raw && (int)threadIdx.x < kParamChunks) {
+		const int c = threadIdx.x, c0 = n0 + 16 * (c / 12);
+		if (c0 < g.N) {
+			const int si = (e.nseg > 1 && c0 >= e.seg[0].n_end) ? ((e.nseg > 2 && c0 >= e.seg[1].n_end) ? 2 : 1) : 0;
+			const int32_t* fold = si == 0 ? e.seg[0].fold : (si == 1 ? e.seg[1].fold : e.seg[2].fold);
+			const int nb = si == 0 ? e.seg[0].n_begin : (si == 1 ? e.seg[1].n_begin : e.seg[2].n_begin);
+			fchunk = load16((const int8_t*)(fold + 3 * (c0 - nb) + 4 * (c % 12)));
+		}
+	}
+	const int8_t* src[CPT];
+#pragma unroll
+	for (int j = 0; j < CPT; ++j) {
+		const int slot = (wave * CPT + j) * 64 + lane;
+		const int row = slot >> 3, pc = slot & 7;
+		const int q = pc ^ ((row >> 1) & 7);
+		if (row < BM) src[j] = g.a + (size_t)min(m0 + row, g.M - 1) * g.lda + q * 16;
+		else src[j] = g.w + (size_t)min(n0 + row - BM, g.N - 1) * g.K + q * 16;
+	}
+	auto issue = [&](int st, int t) {  // past the last step the last is fetched again (never read)
+		const size_t kb = (size_t)min(t, S - 1) * kPBK;
+#pragma unroll
+		for (int j = 0; j < CPT; ++j)
+			__builtin_amdgcn_global_load_lds((const void*)(src[j] + kb),
+			                                 (__attribute__((address_space(3))) void*)(smem + st * STAGE + (wave * CPT + j) * 1024),
+			                                 16, 0, 0);
+	};
+	const uint32_t lds0 = (uint32_t)(size_t)(__attribute__((address_space(3))) int8_t*)smem;
+	// the lane's fragment rows: A rows 64 w + 16 i + lane % 16, B rows BM + 16 j + lane % 16; in a
+	// 64-deep half h the lane reads 16-byte chunk 4 h + lane / 16
+	uint32_t aoff[2], boff[2];
+#pragma unroll
+	for (int h = 0; h < 2; ++h) {
+		aoff[h] = lds0 + lds_chunk(64 * wave + cl, 4 * h + (lane >> 4));
+		boff[h] = lds0 + lds_chunk(BM + cl, 4 * h + (lane >> 4));
+	}
+	constexpr int R16 = 16 * kPStride;  // 16 rows further: the swizzle depends on row bits 1..3 only
+	v4i acc[4][NB];
+#pragma unroll
+	for (int i = 0; i < 4; ++i)
+#pragma unroll
+		for (int j = 0; j < NB; ++j) acc[i][j] = v4i{0, 0, 0, 0};
+#pragma unroll
+	for (int s0 = 0; s0 < NS - 1; ++s0) issue(s0, s0);
+	for (int t = 0; t < S; ++t) {
+		wait_vmcnt<(NS - 2) * CPT>();  // own loads of step t have landed
+		__builtin_amdgcn_s_barrier();  // everyone's have; everyone is done with step t - 1
+		issue((t + NS - 1) % NS, t + NS - 1);
+		const uint32_t so = (uint32_t)((t % NS) * STAGE);
+		v4i a0[4], b0[NB], a1[4], b1[NB];
+		a0[0] = lds_read16<0>(aoff[0] + so);
+		a0[1] = lds_read16<R16>(aoff[0] + so);
+		a0[2] = lds_read16<2 * R16>(aoff[0] + so);
+		a0[3] = lds_read16<3 * R16>(aoff[0] + so);
+		b0[0] = lds_read16<0>(boff[0] + so);
+		b0[1] = lds_read16<R16>(boff[0] + so);
+		b0[2] = lds_read16<2 * R16>(boff[0] + so);
+		b0[3] = lds_read16<3 * R16>(boff[0] + so);
+		b0[4] = lds_read16<4 * R16>(boff[0] + so);
+		b0[5] = lds_read16<5 * R16>(boff[0] + so);
+		b0[6] = lds_read16<6 * R16>(boff[0] + so);
+		b0[7] = lds_read16<7 * R16>(boff[0] + so);
+		b0[8] = lds_read16<8 * R16>(boff[0] + so);
+		b0[9] = lds_read16<9 * R16>(boff[0] + so);
+		a1[0] = lds_read16<0>(aoff[1] + so);
+		a1[1] = lds_read16<R16>(aoff[1] + so);
+		a1[2] = lds_read16<2 * R16>(aoff[1] + so);
+		a1[3] = lds_read16<3 * R16>(aoff[1] + so);
+		b1[0] = lds_read16<0>(boff[1] + so);
+		b1[1] = lds_read16<R16>(boff[1] + so);
+		b1[2] = lds_read16<2 * R16>(boff[1] + so);
+		b1[3] = lds_read16<3 * R16>(boff[1] + so);
+		b1[4] = lds_read16<4 * R16>(boff[1] + so);
+		b1[5] = lds_read16<5 * R16>(boff[1] + so);
+		b1[6] = lds_read16<6 * R16>(boff[1] + so);
+		b1[7] = lds_read16<7 * R16>(boff[1] + so);
+		b1[8] = lds_read16<8 * R16>(boff[1] + so);
+		b1[9] = lds_read16<9 * R16>(boff[1] + so);
+		lgkm_wait_n14(a0, b0);  // the first half's 14 reads done (the second's 14 may be pending)
+#pragma unroll
+		for (int i = 0; i < 4; ++i)
+#pragma unroll
+			for (int j = 0; j < NB; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0[i], b0[j], acc[i][j], 0, 0, 0);
+		lgkm_wait_n0(a1, b1);
+#pragma unroll
+		for (int i = 0; i < 4; ++i)
+#pragma unroll
+			for (int j = 0; j < NB; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1[i], b1[j], acc[i][j], 0, 0, 0);
+	}
+	wait_vmcnt<0>();  // the trailing (clamped) loads land before the stages are reused
+	__syncthreads();
+	// 16x16 layout: lane holds column lane % 16, rows 4 (lane / 16) + v
+	if (raw) {
+		const int rbase = m0 + 64 * wave + 4 * (lane >> 4);
+#pragma unroll
+		for (int j = 0; j < NB; ++j) {
+			const int col = n0 + 16 * j + cl;
+#pragma unroll
+			for (int i = 0; i < 4; ++i)
+#pragma unroll
+				for (int v = 0; v < 4; ++v) {
+					const int row = rbase + 16 * i + v;
+					if (col < g.N && row < g.M) e.raw_out[(size_t)row * g.N + col] = acc[i][j][v];
+				}
+		}
+		return;
+	}
+	// Funnel segments: each wave parks half of its 64 x 160 accumulators (64 x 80, rows padded to
+	// 84 words: the four 4-row groups of a store fall in distinct banks) in its own LDS slab, then
+	// reads them back four consecutive columns per lane -- one 16-byte store per lane, the
+	// 16-column tile's maximum over 4 values and a lane quad.
+	constexpr int HALF = NB / 2, LDW = 84, SLAB = 64 * LDW;
+	static_assert(NB % 2 == 0 && 4 * SLAB * 4 + BN * 12 <= NS * STAGE, "epilogue LDS");
+	int32_t* slab = (int32_t*)smem + wave * SLAB;
+	int32_t* prm = (int32_t*)smem + 4 * SLAB;  // [BN][3]
+	if ((int)threadIdx.x < kParamChunks) *(v4i*)&prm[4 * threadIdx.x] = fchunk;
+	__syncthreads();
+#pragma unroll
+	for (int hf = 0; hf < 2; ++hf) {
+#pragma unroll
+		for (int jj = 0; jj < HALF; ++jj)
+#pragma unroll
+			for (int i = 0; i < 4; ++i)
+#pragma unroll
+				for (int v = 0; v < 4; ++v)
+					slab[(16 * i + 4 * (lane >> 4) + v) * LDW + 16 * jj + cl] = acc[i][hf * HALF + jj][v];
+		// the wave reads back only what it wrote: LDS operations of a wave complete in order
+#pragma unroll 4
+		for (int k = 0; k < 20; ++k) {
+			const int idx = k * 64 + lane, r = idx / 20, grp = idx % 20;
+			const int lc = hf * 80 + 4 * grp;  // tile column of the lane's first value
+			const int row = m0 + 64 * wave + r, col = n0 + lc;
+			const v4i a = *(const v4i*)&slab[r * LDW + 4 * grp];
+			const int32_t* pf = prm + 3 * lc;
+			const v4i p0 = *(const v4i*)pf, p1 = *(const v4i*)(pf + 4), p2 = *(const v4i*)(pf + 8);
+			// parameters of columns lc .. lc + 3: (p0.x p0.y p0.z) (p0.w p1.x p1.y) (p1.z p1.w p2.x) (p2.y p2.z p2.w)
+			v4i o;
+			o[0] = fold32(a[0], p0[0], p0[1], p0[2]);
+			o[1] = fold32(a[1], p0[3], p1[0], p1[1]);
+			o[2] = fold32(a[2], p1[2], p1[3], p2[0]);
+			o[3] = fold32(a[3], p2[1], p2[2], p2[3]);
+			const int c0 = col & ~15;
+			const int si = (e.nseg > 1 && c0 >= e.seg[0].n_end) ? ((e.nseg > 2 && c0 >= e.seg[1].n_end) ? 2 : 1) : 0;
+#define SSLM_SEG_FIELD(f) (si == 0 ? e.seg[0].f : (si == 1 ? e.seg[1].f : e.seg[2].f))
+			const int nbeg = SSLM_SEG_FIELD(n_begin), ld = SSLM_SEG_FIELD(ld_out);
+			int32_t* sout = (int32_t*)SSLM_SEG_FIELD(out);
+			uint32_t* smax = SSLM_SEG_FIELD(maxpart);
+#undef SSLM_SEG_FIELD
+			const bool ok = row < g.M && col < g.N;
+			if (ok) *(v4i*)(sout + (size_t)row * ld + (col - nbeg)) = o;
+			uint32_t mx = 0;
+#pragma unroll
+			for (int q = 0; q < 4; ++q) mx = max(mx, o[q] < 0 ? 0u - (uint32_t)o[q] : (uint32_t)o[q]);
+			if (!ok) mx = 0;
+			// quad max (quad_perm [1,0,3,2] then [2,3,0,1]): the 4 lanes of one 16-column tile
+			uint32_t w2 = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)mx, 0xb1, 0xf, 0xf, false);
+			mx = max(mx, w2);
+			w2 = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)mx, 0x4e, 0xf, 0xf, false);
+			mx = max(mx, w2);
+			if ((lane & 3) == 0 && ok && smax) smax[(size_t)(c0 >> 4) * kPartLd + row] = mx;
+		}
+	}
+}
+
+// ------------------------------------------------------------------------------------------
 // Narrow prefill GEMM (M > 64, few 256 x 128 tiles): 64 x 64 block tiles over the whole K, raw
 // int32 output (one plane; the consuming row kernel applies the epilogue, RawIn).  The
 // projections whose N is a few thousand columns (q|k|v, o, down) have too few 256 x 128 tiles
@@ -2138,7 +2349,9 @@ __global__ __launch_bounds__(BS) void k_attention(sslm_launch::AttnArgs a, int u
 // below 2^22 in magnitude).  V is staged transposed in LDS ([dim][position], 4x4 byte blocks
 // transposed in registers) so a lane's 16 B operand holds 16 positions of one dimension.
 // The launch must hold one sequence's consecutive positions (a prefill chunk).
-template <int D, int NW>
+// MAXB > 0: the rows span at most MAXB steps of KB positions, and the scores of pass 1 stay in
+// registers for passes 2 and 3 (K read once); MAXB = 0: every pass recomputes them.
+template <int D, int NW, int MAXB>
 __global__ __launch_bounds__(64 * NW) void k_attention_tiled(sslm_launch::AttnArgs a) {
 	constexpr int TQ = 16, KB = 16 * NW, NC = (D + 63) / 64, DT = D / 16, PS = KB + 16, VS = KB + 16;
 	__shared__ __attribute__((aligned(16))) int8_t s_p[3][TQ][PS];  // probability parts [part][token][pos]
@@ -2238,15 +2451,37 @@ __global__ __launch_bounds__(64 * NW) void k_attention_tiled(sslm_launch::AttnAr
 		*p_out = p;
 		return acc;
 	};
+	// the passes over the steps: `body(blk, scores, position)` with the scores kept (when the
+	// rows fit MAXB steps; the launch's choice of MAXB is only a hint) or recomputed
+	v4i sv[MAXB > 0 ? MAXB : 1];
+	const bool kept = MAXB > 0 && nblk <= MAXB;
+	auto each_step = [&](auto&& body) {
+		if (kept) {
+#pragma unroll
+			for (int b = 0; b < (MAXB > 0 ? MAXB : 1); ++b)
+				if (b < nblk) body(b, sv[b], b * KB + wave * 16 + ri);
+		} else {
+			for (int b = 0; b < nblk; ++b) {
+				int p;
+				const v4i sc = scores(b, &p);
+				body(b, sc, p);
+			}
+		}
+	};
+	if (kept) {  // every step's K rows in flight together
+#pragma unroll
+		for (int b = 0; b < (MAXB > 0 ? MAXB : 1); ++b) {
+			int p;
+			if (b < nblk) sv[b] = scores(b, &p);
+		}
+	}
 	// pass 1: row maxima
 	int32_t mx[4] = {INT32_MIN, INT32_MIN, INT32_MIN, INT32_MIN};
-	for (int blk = 0; blk < nblk; ++blk) {
-		int p;
-		const v4i s = scores(blk, &p);
+	each_step([&](int, const v4i& s, int p) {
 #pragma unroll
 		for (int v = 0; v < 4; ++v)
 			if (tok_ok[v] && p <= tpos[v]) mx[v] = max(mx[v], s[v]);
-	}
+	});
 #pragma unroll
 	for (int v = 0; v < 4; ++v) {
 		for (int o = 8; o > 0; o >>= 1) mx[v] = max(mx[v], __shfl_xor(mx[v], o, 16));
@@ -2273,9 +2508,7 @@ __global__ __launch_bounds__(64 * NW) void k_attention_tiled(sslm_launch::AttnAr
 	// pass 2: i-exp values (SoftmaxRowQ15, intmath.cpp:853-889) and the row sums
 	int64_t sum[4] = {0, 0, 0, 0};
 	uint32_t refused = 0;
-	for (int blk = 0; blk < nblk; ++blk) {
-		int p;
-		const v4i s = scores(blk, &p);
+	each_step([&](int, const v4i& s, int p) {
 #pragma unroll
 		for (int v = 0; v < 4; ++v) {
 			if (tok_ok[v] && p <= tpos[v]) {
@@ -2284,7 +2517,7 @@ __global__ __launch_bounds__(64 * NW) void k_attention_tiled(sslm_launch::AttnAr
 				else sum[v] += e;
 			}
 		}
-	}
+	});
 #pragma unroll
 	for (int v = 0; v < 4; ++v) {
 		for (int o = 8; o > 0; o >>= 1) sum[v] += __shfl_xor(sum[v], o, 16);
@@ -2316,9 +2549,7 @@ __global__ __launch_bounds__(64 * NW) void k_attention_tiled(sslm_launch::AttnAr
 	for (int i = 0; i < DTW; ++i)
 #pragma unroll
 		for (int k = 0; k < 3; ++k) cacc[i][k] = v4i{0, 0, 0, 0};
-	for (int blk = 0; blk < nblk; ++blk) {
-		int p;
-		const v4i s = scores(blk, &p);
+	each_step([&](int blk, const v4i& s, int p) {
 		const int pl = wave * 16 + ri;
 #pragma unroll
 		for (int v = 0; v < 4; ++v) {
@@ -2365,7 +2596,7 @@ __global__ __launch_bounds__(64 * NW) void k_attention_tiled(sslm_launch::AttnAr
 			}
 		}
 		__syncthreads();
-	}
+	});
 	// epilogue: recombine the parts, fold, store; the per-token maximum over the head's dims
 	const int32_t* cf = a.ctx_fold + 3 * h;
 	const int32_t f0 = cf[0], f1 = cf[1], f2 = cf[2];
@@ -2597,6 +2828,11 @@ void gemm(const GemmArgs& g, hipStream_t s) {
 	}
 	bool lora = false;
 	for (int i = 0; i < g.epi.nseg; ++i) lora = lora || g.epi.seg[i].lora_b;
+	if (wide_gemm_ok(g)) {
+		const int tiles = ((g.M + kWideBM - 1) / kWideBM) * ((g.N + kWideBN - 1) / kWideBN);
+		hipLaunchKernelGGL(k_gemm_wide, dim3(tiles), dim3(256), 0, s, g);
+		return;
+	}
 	if (!lora && !g.epi.argmax_key && prefill_mfma_k(g.K) && (g.epi.raw_out || g.N % 16 == 0)) {
 		// g.splits > 1 only as prefill_plan(M, N, K, true).splits, sized by the caller
 		// a raw single-plane launch of a narrow shape takes the 64 x 64-tile kernel
@@ -2616,6 +2852,23 @@ void gemm(const GemmArgs& g, hipStream_t s) {
 }
 
 bool prefill_mfma_k(int K) { return K > 0 && K % kPBK == 0; }
+
+// The 256 x 160-tile kernel where it takes fewer tile rounds' worth of columns than 256 x 128
+// tiles (a round: 256 tiles, one per CU), for raw output or funnel segments without bias / LoRA.
+bool wide_gemm_ok(const GemmArgs& g) {
+	if (g.M <= 64 || g.splits > 1 || g.epi.argmax_key || !prefill_mfma_k(g.K)) return false;
+	if (!g.epi.raw_out) {
+		if (g.N % 16 != 0 || g.epi.nseg < 1) return false;
+		for (int i = 0; i < g.epi.nseg; ++i) {
+			const Segment& sg = g.epi.seg[i];
+			if (sg.mode != kSegFunnel || sg.bias || sg.lora_b || sg.n_begin % 16 || sg.n_end % 16) return false;
+		}
+	}
+	const int64_t rows = (g.M + 255) / 256;
+	const int64_t t128 = rows * ((g.N + kPBN - 1) / kPBN), t160 = rows * ((g.N + kWideBN - 1) / kWideBN);
+	if (t128 < kPrefillTargetBlocks) return false;
+	return ((t160 + 255) / 256) * kWideBN < ((t128 + 255) / 256) * kPBN;
+}
 
 PrefillPlan prefill_plan(int M, int N, int K, bool split_ok) {
 	PrefillPlan p{};
@@ -2718,25 +2971,52 @@ static void launch_attention(const AttnArgs& a, hipStream_t s) {
 	}
 }
 
+static int tiled_grid(const AttnArgs& a) {
+	const int groups = ((a.M + 15) / 16) * a.NKV, per_xcd = (groups + 7) / 8;
+	return per_xcd * 8 * (a.NH / a.NKV);
+}
+
+// 8 waves (128 positions per step) halve the longest rows' serial chain when the grid is small;
+// with two or more blocks per CU, 4-wave blocks pack the CUs better.  SSLM_HIP_TILED_WAVES=4 or 8
+// overrides the choice (read per launch; the parity tests run both).
+bool tiled_wide(const AttnArgs& a) {
+	const char* fw = getenv("SSLM_HIP_TILED_WAVES");
+	return fw && fw[0] ? fw[0] == '8' : tiled_grid(a) < 2 * 256;  // MI355X: 256 CUs
+}
+
+int tiled_keep(const AttnArgs& a) {
+	if (a.pos_end <= 0) return 0;
+	const int kb = tiled_wide(a) ? 128 : 64;
+	const int64_t steps = (a.pos_end + kb - 1) / kb;
+	// 16 steps of 4-wave blocks would not fit their registers
+	return steps <= 4 ? 4 : (steps <= 16 && kb == 128 ? 16 : 0);
+}
+
 void attention(const AttnArgs& a, hipStream_t s, bool one_sequence) {
 	if (!one_sequence || !tiled_attention_enabled()) {
 		launch_attention<false>(a, s);
 		return;
 	}
-	const int groups = ((a.M + 15) / 16) * a.NKV, per_xcd = (groups + 7) / 8;
-	const dim3 grid(per_xcd * 8 * (a.NH / a.NKV));  // see the XCD-aware order in k_attention_tiled
-	// 8 waves (128 positions per step) halve the longest rows' serial chain when the grid is
-	// small; with two or more blocks per CU, 4-wave blocks pack the CUs better
-	// SSLM_HIP_TILED_WAVES=4 or 8 overrides the choice (read per launch; the parity tests run both)
-	const char* fw = getenv("SSLM_HIP_TILED_WAVES");
-	const bool wide = fw && fw[0] ? fw[0] == '8' : (int)grid.x < 2 * 256;  // MI355X: 256 CUs
+	const dim3 grid(tiled_grid(a));  // see the XCD-aware order in k_attention_tiled
+	const bool wide = tiled_wide(a);
+	const int keep = tiled_keep(a);
+#define SSLM_TILED(D_, NW_, MB_) hipLaunchKernelGGL((k_attention_tiled<D_, NW_, MB_>), grid, dim3(64 * NW_), 0, s, a)
+#define SSLM_TILED_D(D_)                                \
+	if (wide && keep == 16) SSLM_TILED(D_, 8, 16);      \
+	else if (wide && keep == 4) SSLM_TILED(D_, 8, 4);   \
+	else if (wide) SSLM_TILED(D_, 8, 0);                \
+	else if (keep == 4) SSLM_TILED(D_, 4, 4);           \
+	else SSLM_TILED(D_, 4, 0);                          \
+	break;
 	switch (a.D) {
-		case 32: if (wide) hipLaunchKernelGGL((k_attention_tiled<32, 8>), grid, dim3(512), 0, s, a); else hipLaunchKernelGGL((k_attention_tiled<32, 4>), grid, dim3(256), 0, s, a); break;
-		case 64: if (wide) hipLaunchKernelGGL((k_attention_tiled<64, 8>), grid, dim3(512), 0, s, a); else hipLaunchKernelGGL((k_attention_tiled<64, 4>), grid, dim3(256), 0, s, a); break;
-		case 128: if (wide) hipLaunchKernelGGL((k_attention_tiled<128, 8>), grid, dim3(512), 0, s, a); else hipLaunchKernelGGL((k_attention_tiled<128, 4>), grid, dim3(256), 0, s, a); break;
-		case 256: if (wide) hipLaunchKernelGGL((k_attention_tiled<256, 8>), grid, dim3(512), 0, s, a); else hipLaunchKernelGGL((k_attention_tiled<256, 4>), grid, dim3(256), 0, s, a); break;
+		case 32: SSLM_TILED_D(32)
+		case 64: SSLM_TILED_D(64)
+		case 128: SSLM_TILED_D(128)
+		case 256: SSLM_TILED_D(256)
 		default: no_instance("attention", a.D);
 	}
+#undef SSLM_TILED_D
+#undef SSLM_TILED
 }
 
 bool tiled_attention_enabled() {
