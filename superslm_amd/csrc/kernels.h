@@ -211,16 +211,11 @@ struct AttnArgs {
 	const int64_t* rope_cos;    // [cap, D/2]
 	const int64_t* rope_sin;
 	unsigned long long* sat;    // [slots]
-	// prefill spans: the launch's positions end before pos_end (0: unknown); a hint for how many
-	// key steps the query-tiled kernel keeps in registers
-	int64_t pos_end;
 };
 // `one_sequence`: the launch holds one sequence's consecutive positions (a prefill chunk), so
 // the query-tiled kernel may run (unless SSLM_HIP_TILED_ATTN=0).
 void attention(const AttnArgs& a, hipStream_t s, bool one_sequence = false);
 bool tiled_attention_enabled();
-bool tiled_wide(const AttnArgs& a);  // the query-tiled launch's 8-wave form
-int tiled_keep(const AttnArgs& a);   // its key steps kept in registers (0: recomputed per pass)
 // Decode attention with the q|k|v post-processing fused in (one block per (query head, token)):
 // valid when every token of the launch belongs to a different sequence, so no token attends to
 // a position another block of the launch writes.

@@ -2349,9 +2349,7 @@ __global__ __launch_bounds__(BS) void k_attention(sslm_launch::AttnArgs a, int u
 // below 2^22 in magnitude).  V is staged transposed in LDS ([dim][position], 4x4 byte blocks
 // transposed in registers) so a lane's 16 B operand holds 16 positions of one dimension.
 // The launch must hold one sequence's consecutive positions (a prefill chunk).
-// MAXB > 0: the rows span at most MAXB steps of KB positions, and the scores of pass 1 stay in
-// registers for passes 2 and 3 (K read once); MAXB = 0: every pass recomputes them.
-template <int D, int NW, int MAXB>
+template <int D, int NW>
 __global__ __launch_bounds__(64 * NW) void k_attention_tiled(sslm_launch::AttnArgs a) {
 	constexpr int TQ = 16, KB = 16 * NW, NC = (D + 63) / 64, DT = D / 16, PS = KB + 16, VS = KB + 16;
 	__shared__ __attribute__((aligned(16))) int8_t s_p[3][TQ][PS];  // probability parts [part][token][pos]
@@ -2451,37 +2449,15 @@ __global__ __launch_bounds__(64 * NW) void k_attention_tiled(sslm_launch::AttnAr
 		*p_out = p;
 		return acc;
 	};
-	// the passes over the steps: `body(blk, scores, position)` with the scores kept (when the
-	// rows fit MAXB steps; the launch's choice of MAXB is only a hint) or recomputed
-	v4i sv[MAXB > 0 ? MAXB : 1];
-	const bool kept = MAXB > 0 && nblk <= MAXB;
-	auto each_step = [&](auto&& body) {
-		if (kept) {
-#pragma unroll
-			for (int b = 0; b < (MAXB > 0 ? MAXB : 1); ++b)
-				if (b < nblk) body(b, sv[b], b * KB + wave * 16 + ri);
-		} else {
-			for (int b = 0; b < nblk; ++b) {
-				int p;
-				const v4i sc = scores(b, &p);
-				body(b, sc, p);
-			}
-		}
-	};
-	if (kept) {  // every step's K rows in flight together
-#pragma unroll
-		for (int b = 0; b < (MAXB > 0 ? MAXB : 1); ++b) {
-			int p;
-			if (b < nblk) sv[b] = scores(b, &p);
-		}
-	}
 	// pass 1: row maxima
 	int32_t mx[4] = {INT32_MIN, INT32_MIN, INT32_MIN, INT32_MIN};
-	each_step([&](int, const v4i& s, int p) {
+	for (int blk = 0; blk < nblk; ++blk) {
+		int p;
+		const v4i s = scores(blk, &p);
 #pragma unroll
 		for (int v = 0; v < 4; ++v)
 			if (tok_ok[v] && p <= tpos[v]) mx[v] = max(mx[v], s[v]);
-	});
+	}
 #pragma unroll
 	for (int v = 0; v < 4; ++v) {
 		for (int o = 8; o > 0; o >>= 1) mx[v] = max(mx[v], __shfl_xor(mx[v], o, 16));
@@ -2508,7 +2484,9 @@ __global__ __launch_bounds__(64 * NW) void k_attention_tiled(sslm_launch::AttnAr
 	// pass 2: i-exp values (SoftmaxRowQ15, intmath.cpp:853-889) and the row sums
 	int64_t sum[4] = {0, 0, 0, 0};
 	uint32_t refused = 0;
-	each_step([&](int, const v4i& s, int p) {
+	for (int blk = 0; blk < nblk; ++blk) {
+		int p;
+		const v4i s = scores(blk, &p);
 #pragma unroll
 		for (int v = 0; v < 4; ++v) {
 			if (tok_ok[v] && p <= tpos[v]) {
@@ -2517,7 +2495,7 @@ __global__ __launch_bounds__(64 * NW) void k_attention_tiled(sslm_launch::AttnAr
 				else sum[v] += e;
 			}
 		}
-	});
+	}
 #pragma unroll
 	for (int v = 0; v < 4; ++v) {
 		for (int o = 8; o > 0; o >>= 1) sum[v] += __shfl_xor(sum[v], o, 16);
@@ -2549,7 +2527,9 @@ __global__ __launch_bounds__(64 * NW) void k_attention_tiled(sslm_launch::AttnAr
 	for (int i = 0; i < DTW; ++i)
 #pragma unroll
 		for (int k = 0; k < 3; ++k) cacc[i][k] = v4i{0, 0, 0, 0};
-	each_step([&](int blk, const v4i& s, int p) {
+	for (int blk = 0; blk < nblk; ++blk) {
+		int p;
+		const v4i s = scores(blk, &p);
 		const int pl = wave * 16 + ri;
 #pragma unroll
 		for (int v = 0; v < 4; ++v) {
@@ -2596,7 +2576,7 @@ __global__ __launch_bounds__(64 * NW) void k_attention_tiled(sslm_launch::AttnAr
 			}
 		}
 		__syncthreads();
-	});
+	}
 	// epilogue: recombine the parts, fold, store; the per-token maximum over the head's dims
 	const int32_t* cf = a.ctx_fold + 3 * h;
 	const int32_t f0 = cf[0], f1 = cf[1], f2 = cf[2];
@@ -2971,52 +2951,25 @@ static void launch_attention(const AttnArgs& a, hipStream_t s) {
 	}
 }
 
-static int tiled_grid(const AttnArgs& a) {
-	const int groups = ((a.M + 15) / 16) * a.NKV, per_xcd = (groups + 7) / 8;
-	return per_xcd * 8 * (a.NH / a.NKV);
-}
-
-// 8 waves (128 positions per step) halve the longest rows' serial chain when the grid is small;
-// with two or more blocks per CU, 4-wave blocks pack the CUs better.  SSLM_HIP_TILED_WAVES=4 or 8
-// overrides the choice (read per launch; the parity tests run both).
-bool tiled_wide(const AttnArgs& a) {
-	const char* fw = getenv("SSLM_HIP_TILED_WAVES");
-	return fw && fw[0] ? fw[0] == '8' : tiled_grid(a) < 2 * 256;  // MI355X: 256 CUs
-}
-
-int tiled_keep(const AttnArgs& a) {
-	if (a.pos_end <= 0) return 0;
-	const int kb = tiled_wide(a) ? 128 : 64;
-	const int64_t steps = (a.pos_end + kb - 1) / kb;
-	// 16 steps of 4-wave blocks would not fit their registers
-	return steps <= 4 ? 4 : (steps <= 16 && kb == 128 ? 16 : 0);
-}
-
 void attention(const AttnArgs& a, hipStream_t s, bool one_sequence) {
 	if (!one_sequence || !tiled_attention_enabled()) {
 		launch_attention<false>(a, s);
 		return;
 	}
-	const dim3 grid(tiled_grid(a));  // see the XCD-aware order in k_attention_tiled
-	const bool wide = tiled_wide(a);
-	const int keep = tiled_keep(a);
-#define SSLM_TILED(D_, NW_, MB_) hipLaunchKernelGGL((k_attention_tiled<D_, NW_, MB_>), grid, dim3(64 * NW_), 0, s, a)
-#define SSLM_TILED_D(D_)                                \
-	if (wide && keep == 16) SSLM_TILED(D_, 8, 16);      \
-	else if (wide && keep == 4) SSLM_TILED(D_, 8, 4);   \
-	else if (wide) SSLM_TILED(D_, 8, 0);                \
-	else if (keep == 4) SSLM_TILED(D_, 4, 4);           \
-	else SSLM_TILED(D_, 4, 0);                          \
-	break;
+	const int groups = ((a.M + 15) / 16) * a.NKV, per_xcd = (groups + 7) / 8;
+	const dim3 grid(per_xcd * 8 * (a.NH / a.NKV));  // see the XCD-aware order in k_attention_tiled
+	// 8 waves (128 positions per step) halve the longest rows' serial chain when the grid is
+	// small; with two or more blocks per CU, 4-wave blocks pack the CUs better
+	// SSLM_HIP_TILED_WAVES=4 or 8 overrides the choice (read per launch; the parity tests run both)
+	const char* fw = getenv("SSLM_HIP_TILED_WAVES");
+	const bool wide = fw && fw[0] ? fw[0] == '8' : (int)grid.x < 2 * 256;  // MI355X: 256 CUs
 	switch (a.D) {
-		case 32: SSLM_TILED_D(32)
-		case 64: SSLM_TILED_D(64)
-		case 128: SSLM_TILED_D(128)
-		case 256: SSLM_TILED_D(256)
+		case 32: if (wide) hipLaunchKernelGGL((k_attention_tiled<32, 8>), grid, dim3(512), 0, s, a); else hipLaunchKernelGGL((k_attention_tiled<32, 4>), grid, dim3(256), 0, s, a); break;
+		case 64: if (wide) hipLaunchKernelGGL((k_attention_tiled<64, 8>), grid, dim3(512), 0, s, a); else hipLaunchKernelGGL((k_attention_tiled<64, 4>), grid, dim3(256), 0, s, a); break;
+		case 128: if (wide) hipLaunchKernelGGL((k_attention_tiled<128, 8>), grid, dim3(512), 0, s, a); else hipLaunchKernelGGL((k_attention_tiled<128, 4>), grid, dim3(256), 0, s, a); break;
+		case 256: if (wide) hipLaunchKernelGGL((k_attention_tiled<256, 8>), grid, dim3(512), 0, s, a); else hipLaunchKernelGGL((k_attention_tiled<256, 4>), grid, dim3(256), 0, s, a); break;
 		default: no_instance("attention", a.D);
 	}
-#undef SSLM_TILED_D
-#undef SSLM_TILED
 }
 
 bool tiled_attention_enabled() {

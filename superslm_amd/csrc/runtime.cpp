@@ -193,7 +193,6 @@ struct Track {
 	int64_t* act_prod;       // decode tracks: SiLU products of the sliced mlp_act [64, I]
 	uint32_t* act_maxpart;   // its per-slice maxima
 	Scale* gu_scale;         // its gate / up scales [64, 2]
-	int64_t span_end = 0;  // prefill tracks: the current span's last position + 1
 	int8_t* kv_stage;    // prefill tracks: landed K/V rows awaiting kv_commit [T][2 * KVH]
 	uint32_t* sat_stage;  // prefill tracks: their clamp counts [T]
 	int8_t* lora_u[3];
@@ -861,7 +860,6 @@ void run_layers(sslm_model m, Track& w, int M, StreamRef st, int l0, int l1, ssl
 			sslm_launch::AttnArgs aa = attn_args(m, w, l, M);
 			aa.q_rot = w.q_rot;
 			aa.q_scale = w.q_scale;
-			aa.pos_end = w.prefill ? w.span_end : 0;
 			ProfScope p(s, kProfAttn, 0, 0);
 			sslm_launch::attention(aa, s, !decode);  // prefill chunks: one sequence, consecutive positions
 			ck(hipGetLastError());
@@ -1592,7 +1590,6 @@ sslm_status prefill_tokens(sslm_model m, sslm_seq s, const int32_t* tokens, int 
 		for (int t = 0; t < T; ++t) ti[t] = TokenInfo{s->context_length + done + t, s->slot, (int32_t)s->block};
 		ck(hipMemcpyAsync(w.tok, ti.data(), T * sizeof(TokenInfo), hipMemcpyHostToDevice, w.stream));
 		ck(hipMemcpyAsync(w.tok_ids, tokens + done, T * 4, hipMemcpyHostToDevice, w.stream));
-		w.span_end = s->context_length + done + T;
 		auto body = [&]() {
 			{
 				ProfScope p(w.stream, kProfRow, 0, 0);
@@ -1602,14 +1599,8 @@ sslm_status prefill_tokens(sslm_model m, sslm_seq s, const int32_t* tokens, int 
 			}
 			run_layers(m, w, T, StreamRef{w.hid_chunk, w.hid_chunk_scale, w.ident}, 0, m->L, s->adapter, false);
 		};
-		sslm_launch::AttnArgs probe{};  // the attention launch form varies with the span's end
-		probe.M = T;
-		probe.NH = m->NH;
-		probe.NKV = m->NKV;
-		probe.pos_end = w.span_end;
 		const std::string key = "p|" + std::to_string(T) + "|" + std::to_string((uintptr_t)s->adapter) + "|" +
-		                        std::to_string((uintptr_t)m->pool_dev) + "|" + std::to_string(w.gen) + "|" +
-		                        std::to_string(sslm_launch::tiled_keep(probe));
+		                        std::to_string((uintptr_t)m->pool_dev) + "|" + std::to_string(w.gen);
 		// a span shape is captured the second time it is seen: one-off shapes launch directly
 		if (graphs_enabled() && !prof_enabled() && m->graph_seen[key]++ > 0)
 			ck(hipGraphLaunch(graph_of(m, key, w.stream, body), w.stream));
