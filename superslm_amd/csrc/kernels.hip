@@ -2762,7 +2762,9 @@ GemvPlan gemv_plan(int M, int N, int K, bool split_ok, bool raw_or_argmax) {
 		}
 	}
 	const int mblocks = (M + 15) / 16;
-	p.tpw = (mblocks == 1 && tiles >= 1024) ? 2 : 1;
+	// two tiles per block halve the activation rows each block reads per weight byte; at two row
+	// groups the activations are twice the weights per tile, so wide launches take it there too
+	p.tpw = (mblocks <= 2 && tiles >= 1024) ? 2 : 1;
 	const int blocks = (tiles + p.tpw - 1) / p.tpw;
 	p.splits = 1;
 	if (split_ok && blocks < kGemvTargetBlocks)
@@ -2796,6 +2798,8 @@ void gemm(const GemmArgs& g, hipStream_t s) {
 		const int mblocks = (g.M + 15) / 16;
 		if (p.tpw == 2 && mblocks == 1) {
 			launch_gemv<1, 2>(g, p, s);
+		} else if (p.tpw == 2 && mblocks == 2) {
+			launch_gemv<2, 2>(g, p, s);
 		} else {
 			switch (mblocks) {
 				case 1: launch_gemv<1, 1>(g, p, s); break;
