@@ -393,10 +393,16 @@ def main():
         L_.sslm_hip_bench_decode_gemv.restype = ctypes.c_int32
         L_.sslm_hip_bench_decode_gemv.argtypes = [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32] + \
             [ctypes.c_void_p] * 3 + [ctypes.c_int32]
-        g_us, g_bytes, g_n = (ctypes.c_double * 1)(), (ctypes.c_int64 * 1)(), (ctypes.c_int64 * 1)()
-        if L_.sslm_hip_bench_decode_gemv(model.handle, B, 10, g_us, g_bytes, g_n, 1) != 1:
+        g_us, g_bytes, g_n = (ctypes.c_double * 6)(), (ctypes.c_int64 * 6)(), (ctypes.c_int64 * 6)()
+        if L_.sslm_hip_bench_decode_gemv(model.handle, B, 10, g_us, g_bytes, g_n, 6) != 1:
             raise RuntimeError("sslm_hip_bench_decode_gemv failed")
         achieved = g_bytes[0] / (g_us[0] * 1e-6) / 1e9
+        # the same passes per projection class (all layers' launches of one class back to back)
+        by_class = {}
+        for c, name in enumerate(("q|k|v", "o", "gate|up", "down", "lm_head"), start=1):
+            gbs = g_bytes[c] / (g_us[c] * 1e-6) / 1e9
+            by_class[name] = {"us_per_launch": round(g_us[c] / g_n[c], 2), "bytes_per_launch": g_bytes[c] // g_n[c],
+                              "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
         traffic = None
         if os.path.exists(TRAFFIC_FILE):
             traffic = json.load(open(TRAFFIC_FILE)).get("mean_traffic_bytes_per_launch")
@@ -438,7 +444,8 @@ def main():
                                    "WRITE_SIZE, copy-calibrated)",
                          "bytes_per_launch": g_bytes[0] // max(1, g_n[0]),
                          "us_per_launch": round(g_us[0] / max(1, g_n[0]), 3),
-                         "launches_per_pass": g_n[0]},
+                         "launches_per_pass": g_n[0],
+                         "by_class": by_class},
             "decode_step_hbm_floor_ms": round(floor_bytes / (HBM_PEAK_GBS * 1e9) * 1e3, 4),
             "decode_step_hbm_frac": round(floor_bytes / (HBM_PEAK_GBS * 1e9) / (ms_step * 1e-3), 4),
             "cpu_baseline": None,

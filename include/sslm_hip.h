@@ -193,7 +193,9 @@ void sslm_hip_profile_reset(void);
  * launched back to back `iters` times between two HIP events on the model's stream (so every
  * weight byte streams from HBM, as in a step).  Writes us[0] = mean microseconds per pass,
  * bytes[0] = algorithmic bytes per pass (weights + activations + outputs + fold tables) and
- * shapes[0] = launches per pass; returns 1, or -1.  Sequence state is not touched. */
+ * shapes[0] = launches per pass; with cap >= 6 also, per projection class c = 1..5 (q|k|v, o,
+ * gate|up, down, LM head), the same for a pass of that class's launches alone (all layers').
+ * Returns 1, or -1.  Sequence state is not touched. */
 int32_t sslm_hip_bench_decode_gemv(sslm_model model, int32_t M, int32_t iters, double* us, int64_t* bytes,
                                    int64_t* shapes, int32_t cap);
 /* The projection GEMMs of one M-token prefill chunk (65 <= M <= 512) -- every layer's q|k|v, o,
