@@ -288,7 +288,7 @@ struct ActArgs {
 	int32_t* status;
 	// sliced form (decode rows, funnel-epilogue input): the SiLU products, per-slice maxima and
 	// the gate / up scales between its two kernels
-	int64_t* prod;           // [M, I]
+	int32_t* prod;           // [M, I]
 	uint32_t* act_maxpart;   // [kMaxActSlices * kPartLd]
 	Scale* gu_scale;         // [M, 2] gate, up
 };

@@ -1970,12 +1970,14 @@ void k_mlp_act(sslm_launch::ActArgs a) {
 		uc[k] = requant_code_small(uf[k], (uint64_t)up.r, up.s);
 	}
 	__syncthreads();
-	int64_t w[EPT];  // the sigmoid table is artifact data: no bound is assumed on it
+	// The loader admits only the canonical SiLU table (values in [0, 32768]) and the sigmoid
+	// interpolates between its entries, so |code * sig * code| <= 127 * 32768 * 127 < 2^31.
+	int32_t w[EPT];
 	uint32_t mx = 0;
 #pragma unroll
 	for (int k = 0; k < EPT; ++k) {
-		w[k] = (int64_t)gc[k] * sig[gc[k] + 128] * (int64_t)uc[k];
-		mx = max(mx, sat_abs_u32(w[k]));
+		w[k] = gc[k] * sig[gc[k] + 128] * uc[k];
+		mx = max(mx, (uint32_t)abs(w[k]));
 	}
 	mx = blk_max32<BS>(mx, s_a);
 	const Scale inc2[2] = {gp.out, up.out};
@@ -2041,14 +2043,14 @@ __global__ __launch_bounds__(BS) void k_mlp_act_s1(sslm_launch::ActArgs a, int p
 	}
 	__syncthreads();
 	uint32_t mx = 0;
-	int64_t* prow = a.prod + (size_t)t * I;
+	int32_t* prow = a.prod + (size_t)t * I;
 #pragma unroll
 	for (int k = 0; k < EPT; ++k) {
 		const int i = j0 + threadIdx.x + k * BS;
-		const int64_t w = (int64_t)gc[k] * sig[gc[k] + 128] * (int64_t)uc[k];  // sigmoid values are artifact data: no bound assumed
+		const int32_t w = gc[k] * sig[gc[k] + 128] * uc[k];  // < 2^31: canonical SiLU table, as in k_mlp_act
 		if (i < j1) {
 			prow[i] = w;
-			mx = max(mx, sat_abs_u32(w));
+			mx = max(mx, (uint32_t)abs(w));
 		}
 	}
 	mx = blk_max32<BS>(mx, s_a);
@@ -2069,8 +2071,8 @@ __global__ __launch_bounds__(BS) void k_mlp_act_s2(sslm_launch::ActArgs a, int p
 	const int t = blockIdx.x, sl = blockIdx.y, I = a.I, S = gridDim.y;
 	const int slot = a.tok[t].slot;
 	const int j0 = sl * per, j1 = min(I, j0 + per);
-	const int64_t* prow = a.prod + (size_t)t * I;
-	int64_t w[EPT];
+	const int32_t* prow = a.prod + (size_t)t * I;
+	int32_t w[EPT];
 #pragma unroll
 	for (int k = 0; k < EPT; ++k) {
 		const int i = j0 + threadIdx.x + k * BS;

@@ -190,7 +190,7 @@ struct Track {
 	uint32_t *mx_q, *mx_ctx, *mx_o, *mx_gu, *mx_down;  // per (16-column tile, token) partial maxima
 	unsigned long long* argmax_key;                    // [token][tile], head tracks only
 	int32_t* raw_part;  // split-K partial planes, consumed by the next row kernel
-	int64_t* act_prod;       // decode tracks: SiLU products of the sliced mlp_act [64, I]
+	int32_t* act_prod;       // decode tracks: SiLU products of the sliced mlp_act [64, I]
 	uint32_t* act_maxpart;   // its per-slice maxima
 	Scale* gu_scale;         // its gate / up scales [64, 2]
 	int8_t* kv_stage;    // prefill tracks: landed K/V rows awaiting kv_commit [T][2 * KVH]
@@ -1212,7 +1212,7 @@ void alloc_track(sslm_model m, Track& w, int T, bool head) {
 		w.raw_part = elems ? dalloc<int32_t>(elems, &own) : nullptr;
 	}
 	for (int i = 0; i < 3; ++i) w.lora_u[i] = dalloc<int8_t>((size_t)T * kMaxRank, &own);
-	w.act_prod = w.prefill ? nullptr : dalloc<int64_t>((size_t)sslm_launch::kMaxSlicedActRows * I, &own);
+	w.act_prod = w.prefill ? nullptr : dalloc<int32_t>((size_t)sslm_launch::kMaxSlicedActRows * I, &own);
 	w.act_maxpart = w.prefill ? nullptr : dalloc<uint32_t>((size_t)sslm_launch::kMaxActSlices * kPartLd, &own);
 	w.gu_scale = w.prefill ? nullptr : dalloc<Scale>((size_t)sslm_launch::kMaxSlicedActRows * 2, &own);
 	w.kv_stage = w.prefill ? dalloc<int8_t>((size_t)T * 2 * KVH, &own) : nullptr;
