@@ -61,6 +61,28 @@ SSLM_HD int64_t apply_fold(int64_t acc, int32_t identity, int32_t mult, int32_t 
 	return (int64_t)rdbpot32(srdhm((int32_t)acc, mult), shift);
 }
 
+// apply_fold for |acc| <= 2^29 (an int8 GEMM accumulator over K <= 32768), with the shift's
+// rounding constants prepared per column by fold_consts: there srdhm cannot saturate
+// (|acc * mult| < 2^60), and x / 2^s with ties away from zero is (x + 2^(s-1) - [x < 0]) >> s
+// for s > 0 (|x| <= 2^29, so the sum stays in int32).
+struct FoldConsts {
+	int32_t mult, shift, half, nmask, identity;
+};
+SSLM_HD FoldConsts fold_consts(int32_t identity, int32_t mult, int32_t shift) {
+	FoldConsts c;
+	c.mult = mult;
+	c.shift = shift;
+	c.half = shift > 0 ? (int32_t)(1u << (shift - 1)) : 0;
+	c.nmask = shift > 0 ? -1 : 0;
+	c.identity = identity;
+	return c;
+}
+SSLM_HD int32_t fold_bounded(int32_t acc, const FoldConsts& c) {
+	const int32_t hi = (int32_t)(((int64_t)acc * c.mult + ((int64_t)1 << 30)) >> 31);
+	const int32_t folded = (hi + c.half + ((hi >> 31) & c.nmask)) >> c.shift;
+	return c.identity != 0 ? acc : folded;
+}
+
 // src/intmath.cpp:270-277
 SSLM_HD int32_t sat_shl32(int32_t x, int shift) {
 	if (shift <= 0) return x;

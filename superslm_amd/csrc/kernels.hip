@@ -958,7 +958,7 @@ __global__ __launch_bounds__(BM / 32 * 64, 1) void k_gemm_mfma(GemmArgs g, Prefi
 // main loop.  Loads are unconditional (rows past M or N read a clamped valid row) and K is a
 // multiple of 128.
 // ------------------------------------------------------------------------------------------
-constexpr int kWideBM = 256, kWideBN = 160, kWideStages = 3;
+constexpr int kWideBM = 256, kWideBN = 160, kWideStages = 3, kWideFoldMaxK = 32768;
 
 __device__ __forceinline__ void lgkm_wait_n14(v4i (&a)[4], v4i (&b)[10]) {
 	asm volatile("s_waitcnt lgkmcnt(14)"
@@ -969,6 +969,15 @@ __device__ __forceinline__ void lgkm_wait_n0(v4i (&a)[4], v4i (&b)[10]) {
 	asm volatile("s_waitcnt lgkmcnt(0)"
 	             : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]), "+v"(b[0]), "+v"(b[1]), "+v"(b[2]), "+v"(b[3]),
 	               "+v"(b[4]), "+v"(b[5]), "+v"(b[6]), "+v"(b[7]), "+v"(b[8]), "+v"(b[9]));
+}
+
+// v_mfma_i32_16x16x64_i8 with the accumulator tied to one AGPR quad (dst = srcC).  Through the
+// builtin the register allocator rotated a third of the 40 accumulators of k_gemm_wide through
+// VGPR copies every K step, each copy waiting for its MFMA to retire.  The asm carries no
+// hazard information: between two MFMAs on one accumulator there are 39 others, and the
+// kernel pads with s_nop before VALU reads the accumulators after the loop.
+__device__ __forceinline__ void mfma16_tied(v4i& acc, const v4i& a, const v4i& b) {
+	asm("v_mfma_i32_16x16x64_i8 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
 }
 
 __global__ __launch_bounds__(256, 1) void k_gemm_wide(GemmArgs g) {
@@ -1035,7 +1044,8 @@ __global__ __launch_bounds__(256, 1) void k_gemm_wide(GemmArgs g) {
 		for (int j = 0; j < NB; ++j) acc[i][j] = v4i{0, 0, 0, 0};
 #pragma unroll
 	for (int s0 = 0; s0 < NS - 1; ++s0) issue(s0, s0);
-	for (int t = 0; t < S; ++t) {
+	int t = 0;
+	do {  // S >= 1 (K is a positive multiple of 128): no zero-trip path, no accumulator copy at its exit
 		wait_vmcnt<(NS - 2) * CPT>();  // own loads of step t have landed
 		__builtin_amdgcn_s_barrier();  // everyone's have; everyone is done with step t - 1
 		issue((t + NS - 1) % NS, t + NS - 1);
@@ -1073,13 +1083,21 @@ __global__ __launch_bounds__(256, 1) void k_gemm_wide(GemmArgs g) {
 #pragma unroll
 		for (int i = 0; i < 4; ++i)
 #pragma unroll
-			for (int j = 0; j < NB; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0[i], b0[j], acc[i][j], 0, 0, 0);
+			for (int j = 0; j < NB; ++j) mfma16_tied(acc[i][j], a0[i], b0[j]);
 		lgkm_wait_n0(a1, b1);
 #pragma unroll
 		for (int i = 0; i < 4; ++i)
 #pragma unroll
-			for (int j = 0; j < NB; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1[i], b1[j], acc[i][j], 0, 0, 0);
-	}
+			for (int j = 0; j < NB; ++j) mfma16_tied(acc[i][j], a1[i], b1[j]);
+	} while (++t < S);
+	// The last MFMAs' results settle before anything reads the accumulators: the padding, then an
+	// empty asm per accumulator that claims to rewrite it, so no read is scheduled above the
+	// padding (the accumulators are registers: a memory clobber alone does not hold them back).
+	asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+#pragma unroll
+	for (int i = 0; i < 4; ++i)
+#pragma unroll
+		for (int j = 0; j < NB; ++j) asm volatile("" : "+a"(acc[i][j]));
 	wait_vmcnt<0>();  // the trailing (clamped) loads land before the stages are reused
 	__syncthreads();
 	// 16x16 layout: lane holds column lane % 16, rows 4 (lane / 16) + v
@@ -1100,14 +1118,21 @@ __global__ __launch_bounds__(256, 1) void k_gemm_wide(GemmArgs g) {
 	}
 	// Funnel segments: each wave parks half of its 64 x 160 accumulators (64 x 80, rows padded to
 	// 84 words: the four 4-row groups of a store fall in distinct banks) in its own LDS slab, then
-	// reads them back four consecutive columns per lane -- one 16-byte store per lane, the
-	// 16-column tile's maximum over 4 values and a lane quad.
-	constexpr int HALF = NB / 2, LDW = 84, SLAB = 64 * LDW;
+	// reads them back four consecutive columns per lane: lane l < 60 keeps column group l % 20 of
+	// the half and walks rows l / 20, + 3, + 6, ... (lanes 60..63 idle), so its fold constants,
+	// output segment and addresses are set once per half.  A lane quad is one 16-column tile of
+	// one row (20 groups are 5 whole quads), so the tile maximum is a quad DPP maximum.
+	constexpr int HALF = NB / 2, LDW = 84, SLAB = 64 * LDW, GRPS = HALF * 4, RST = 64 / GRPS;
+	constexpr int RITER = (64 + RST - 1) / RST;
 	static_assert(NB % 2 == 0 && 4 * SLAB * 4 + BN * 12 <= NS * STAGE, "epilogue LDS");
+	static_assert(GRPS % 4 == 0 && RST * GRPS <= 64 && RST == 3, "readback lane map");
+	static_assert(3 * SLAB + (RITER * RST + RST - 1) * LDW + 4 * GRPS <= 4 * SLAB + BN * 3, "readback rows stay in LDS");
 	int32_t* slab = (int32_t*)smem + wave * SLAB;
 	int32_t* prm = (int32_t*)smem + 4 * SLAB;  // [BN][3]
 	if ((int)threadIdx.x < kParamChunks) *(v4i*)&prm[4 * threadIdx.x] = fchunk;
 	__syncthreads();
+	const int grp = lane % GRPS, rp = lane / GRPS;  // rp == RST: idle lane
+	const int rowb = m0 + 64 * wave + rp;
 #pragma unroll
 	for (int hf = 0; hf < 2; ++hf) {
 #pragma unroll
@@ -1118,29 +1143,39 @@ __global__ __launch_bounds__(256, 1) void k_gemm_wide(GemmArgs g) {
 				for (int v = 0; v < 4; ++v)
 					slab[(16 * i + 4 * (lane >> 4) + v) * LDW + 16 * jj + cl] = acc[i][hf * HALF + jj][v];
 		// the wave reads back only what it wrote: LDS operations of a wave complete in order
-#pragma unroll 4
-		for (int k = 0; k < 20; ++k) {
-			const int idx = k * 64 + lane, r = idx / 20, grp = idx % 20;
-			const int lc = hf * 80 + 4 * grp;  // tile column of the lane's first value
-			const int row = m0 + 64 * wave + r, col = n0 + lc;
-			const v4i a = *(const v4i*)&slab[r * LDW + 4 * grp];
-			const int32_t* pf = prm + 3 * lc;
-			const v4i p0 = *(const v4i*)pf, p1 = *(const v4i*)(pf + 4), p2 = *(const v4i*)(pf + 8);
-			// parameters of columns lc .. lc + 3: (p0.x p0.y p0.z) (p0.w p1.x p1.y) (p1.z p1.w p2.x) (p2.y p2.z p2.w)
-			v4i o;
-			o[0] = fold32(a[0], p0[0], p0[1], p0[2]);
-			o[1] = fold32(a[1], p0[3], p1[0], p1[1]);
-			o[2] = fold32(a[2], p1[2], p1[3], p2[0]);
-			o[3] = fold32(a[3], p2[1], p2[2], p2[3]);
-			const int c0 = col & ~15;
-			const int si = (e.nseg > 1 && c0 >= e.seg[0].n_end) ? ((e.nseg > 2 && c0 >= e.seg[1].n_end) ? 2 : 1) : 0;
+		const int lc = hf * 80 + 4 * grp;  // tile column of the lane's first value
+		const int col = n0 + lc, c0 = col & ~15;
+		const int32_t* pf = prm + 3 * lc;
+		const v4i p0 = *(const v4i*)pf, p1 = *(const v4i*)(pf + 4), p2 = *(const v4i*)(pf + 8);
+		// parameters of columns lc .. lc + 3: (p0.x p0.y p0.z) (p0.w p1.x p1.y) (p1.z p1.w p2.x) (p2.y p2.z p2.w)
+		const FoldConsts fc0 = fold_consts(p0[0], p0[1], p0[2]), fc1 = fold_consts(p0[3], p1[0], p1[1]);
+		const FoldConsts fc2 = fold_consts(p1[2], p1[3], p2[0]), fc3 = fold_consts(p2[1], p2[2], p2[3]);
+		const int si = (e.nseg > 1 && c0 >= e.seg[0].n_end) ? ((e.nseg > 2 && c0 >= e.seg[1].n_end) ? 2 : 1) : 0;
 #define SSLM_SEG_FIELD(f) (si == 0 ? e.seg[0].f : (si == 1 ? e.seg[1].f : e.seg[2].f))
-			const int nbeg = SSLM_SEG_FIELD(n_begin), ld = SSLM_SEG_FIELD(ld_out);
-			int32_t* sout = (int32_t*)SSLM_SEG_FIELD(out);
-			uint32_t* smax = SSLM_SEG_FIELD(maxpart);
+		const int nbeg = SSLM_SEG_FIELD(n_begin), ld = SSLM_SEG_FIELD(ld_out);
+		int32_t* sout = (int32_t*)SSLM_SEG_FIELD(out);
+		uint32_t* smax = SSLM_SEG_FIELD(maxpart);
 #undef SSLM_SEG_FIELD
-			const bool ok = row < g.M && col < g.N;
-			if (ok) *(v4i*)(sout + (size_t)row * ld + (col - nbeg)) = o;
+		const bool col_ok = rp < RST && col < g.N;
+		int32_t* op = sout + (size_t)rowb * ld + (col - nbeg);
+		uint32_t* mp = smax ? smax + (size_t)(c0 >> 4) * kPartLd + rowb : nullptr;
+		// all the half's reads first (rows up to 66 of the last wave's slab stay inside the
+		// parameter block after it; rows past 63 are read, never used)
+		const int32_t* sp = slab + rp * LDW + 4 * grp;
+		v4i av[RITER];
+#pragma unroll
+		for (int k = 0; k < RITER; ++k) av[k] = *(const v4i*)(sp + k * RST * LDW);
+#pragma unroll
+		for (int k = 0; k < RITER; ++k) {
+			if (k * RST + RST > 64 && rp >= 64 - k * RST) break;  // past the slab (quad-uniform)
+			const v4i a = av[k];
+			v4i o;
+			o[0] = fold_bounded(a[0], fc0);
+			o[1] = fold_bounded(a[1], fc1);
+			o[2] = fold_bounded(a[2], fc2);
+			o[3] = fold_bounded(a[3], fc3);
+			const bool ok = col_ok && rowb + k * RST < g.M;
+			if (ok) *(v4i*)(op + (size_t)k * RST * ld) = o;
 			uint32_t mx = 0;
 #pragma unroll
 			for (int q = 0; q < 4; ++q) mx = max(mx, o[q] < 0 ? 0u - (uint32_t)o[q] : (uint32_t)o[q]);
@@ -1150,7 +1185,7 @@ __global__ __launch_bounds__(256, 1) void k_gemm_wide(GemmArgs g) {
 			mx = max(mx, w2);
 			w2 = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)mx, 0x4e, 0xf, 0xf, false);
 			mx = max(mx, w2);
-			if ((lane & 3) == 0 && ok && smax) smax[(size_t)(c0 >> 4) * kPartLd + row] = mx;
+			if ((lane & 3) == 0 && ok && mp) mp[k * RST] = mx;
 		}
 	}
 }
@@ -2844,7 +2879,8 @@ bool prefill_mfma_k(int K) { return K > 0 && K % kPBK == 0; }
 bool wide_gemm_ok(const GemmArgs& g) {
 	if (g.M <= 64 || g.splits > 1 || g.epi.argmax_key || !prefill_mfma_k(g.K)) return false;
 	if (!g.epi.raw_out) {
-		if (g.N % 16 != 0 || g.epi.nseg < 1) return false;
+		// the epilogue's fold_bounded needs |acc| <= 2^29: K <= 32768 int8 products
+		if (g.N % 16 != 0 || g.epi.nseg < 1 || g.K > kWideFoldMaxK) return false;
 		for (int i = 0; i < g.epi.nseg; ++i) {
 			const Segment& sg = g.epi.seg[i];
 			if (sg.mode != kSegFunnel || sg.bias || sg.lora_b || sg.n_begin % 16 || sg.n_end % 16) return false;

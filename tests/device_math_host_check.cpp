@@ -179,6 +179,11 @@ int main(int argc, char** argv) {
 		const int32_t sh = (int32_t)uni(0, 31), ex = (int32_t)uni(-31, 31);
 		EXPECT(apply_fold(a64, id, mult, sh) == or_apply_fold(a64, id, mult, sh), "fold");
 		EXPECT(apply_amp_fold(a64, id, mult, ex) == or_apply_amp_fold(a64, id, mult, ex), "amp fold");
+		// the bounded GEMM-epilogue fold: |acc| <= 2^29, any int32 multiplier, shifts 0..31
+		const int32_t ab = (i % 7 == 0) ? (int32_t)((i & 8) ? (1 << 29) : -(1 << 29)) : (int32_t)uni(-(1LL << 29), 1LL << 29);
+		const int32_t mb = (i % 5 == 0) ? (int32_t)((i & 16) ? INT32_MAX : INT32_MIN) : (int32_t)uni(INT32_MIN, INT32_MAX);
+		const int32_t sb = (int32_t)(i % 32);
+		EXPECT(fold_bounded(ab, fold_consts(id, mb, sb)) == or_apply_fold(ab, id, mb, sb), "bounded fold %d %d %d", ab, mb, sb);
 		const int32_t x = (int32_t)uni(-127, 127), y = (int32_t)uni(-127, 127);
 		const int32_t c = (int32_t)uni(-(1LL << 30), 1LL << 30), s = (int32_t)uni(-(1LL << 30), 1LL << 30);
 		int64_t x1, y1, x2, y2;
