@@ -206,6 +206,28 @@ SSLM_HD int8_t requant_code_small(int64_t x, uint64_t r, int s) {
 	return (int8_t)(x < 0 ? -q : q);
 }
 
+// requant_code_small in double arithmetic, for |x| <= 2^31 and a funnel plan's (r, s), r in
+// (2^31, 2^32] and s in [-1, 30].  The code is floor(q + 1/2), clamped to 127, for the exact
+// quotient q = |x| 127 r / 2^(62-s).  f = 127 r 2^-(62-s) is exact in a double (127 r < 2^39),
+// so |x| f is q rounded once and fma returns that rounding error exactly.  Rounding is
+// monotone, so m0 = floor(rounded q + 1/2) is the code or one more; it is one more exactly when
+// (rounded q - (m0 - 1/2)) + err < 0, a sign that is exact wherever it can be near zero
+// (Sterbenz: there the rounded q is within 2^-40 of m0 - 1/2 >= 1/2).  Every operation is full
+// rate on CDNA's FP64 pipes, where the 128-bit integer form takes eight quarter-rate multiplies.
+SSLM_HD double requant_factor(int64_t r, int s) { return ldexp((double)(r * 127), -(62 - s)); }
+SSLM_HD int8_t requant_code_f(int64_t x, double f) {
+#pragma clang fp contract(off)
+	const uint32_t ax = x < 0 ? 0u - (uint32_t)x : (uint32_t)x;
+	const double a = (double)ax;
+	const double qh = a * f;
+	const double er = fma(a, f, -qh);
+	const double q = fmin(qh, 255.0);  // past 255 the code saturates whatever the error
+	const double m0 = floor(q + 0.5);
+	const double m = (q - (m0 - 0.5)) + er < 0.0 ? m0 - 1.0 : m0;
+	const int32_t c = (int32_t)fmin(m, 127.0);
+	return (int8_t)(x < 0 ? -c : c);
+}
+
 // src/intmath.cpp:502-524
 SSLM_HD int64_t isqrt(int64_t n) {
 	int64_t rem = n, root = 0, bit = (int64_t)1 << 62;

@@ -1318,7 +1318,7 @@ __global__ __launch_bounds__(kRowBlock) void k_embed(const int32_t* tokens, cons
 		return;
 	}
 	int8_t* out = out_codes + (size_t)out_idx[t] * H;
-	for (int i = threadIdx.x; i < H; i += kRowBlock) out[i] = requant_code_small(row[i], (uint64_t)plan.r, plan.s);
+	for (int i = threadIdx.x; i < H; i += kRowBlock) out[i] = requant_code_f(row[i], requant_factor(plan.r, plan.s));
 	if (threadIdx.x == 0) out_scale[scale_idx[t]] = plan.out;
 }
 
@@ -1527,7 +1527,7 @@ __device__ __forceinline__ int32_t rmsnorm_regs(const int32_t (&h)[EPT], const i
 #pragma unroll
 	for (int k = 0; k < EPT; ++k) {
 		const int i = threadIdx.x + k * BS;
-		if (i < H) out[i] = requant_code_small(w[k], (uint64_t)plan.r, plan.s);
+		if (i < H) out[i] = requant_code_f(w[k], requant_factor(plan.r, plan.s));
 	}
 	if (threadIdx.x == 0) {
 		*out_scale = plan.out;
@@ -1672,8 +1672,8 @@ __global__ __launch_bounds__(BS) void k_qkv_post(sslm_launch::QkvPostArgs a) {
 		const int p = threadIdx.x + k * BS;
 		if (p < H / 2) {
 			const int i = p % pairs;
-			const int32_t x = requant_code_small(qv[k].x, (uint64_t)plan.r, plan.s);
-			const int32_t y = requant_code_small(qv[k].y, (uint64_t)plan.r, plan.s);
+			const int32_t x = requant_code_f(qv[k].x, requant_factor(plan.r, plan.s));
+			const int32_t y = requant_code_f(qv[k].y, requant_factor(plan.r, plan.s));
 			int64_t xr, yr;
 			rope_pair(x, y, (int32_t)cs[i], (int32_t)sn[i], &xr, &yr);
 			qo[p] = make_char2((char)clamp_code(xr), (char)clamp_code(yr));
@@ -1812,7 +1812,7 @@ __global__ __launch_bounds__(BS) void k_funnel(sslm_launch::FunnelArgs a) {
 #pragma unroll
 	for (int k = 0; k < EPT; ++k) {
 		const int i = threadIdx.x + k * BS;
-		if (i < N) out[i] = requant_code_small(f[k], (uint64_t)plan.r, plan.s);
+		if (i < N) out[i] = requant_code_f(f[k], requant_factor(plan.r, plan.s));
 	}
 	if (threadIdx.x == 0) a.out_scale[t] = plan.out;
 }
@@ -1878,7 +1878,7 @@ __global__ __launch_bounds__(BS) void k_residual_norm(sslm_launch::ResidualArgs 
 	// INT64_MIN marks a code whose landing exceeds int64.
 	int32_t code[EPT];
 #pragma unroll
-	for (int k = 0; k < EPT; ++k) code[k] = requant_code_small(bf[k], (uint64_t)bplan.r, bplan.s);
+	for (int k = 0; k < EPT; ++k) code[k] = requant_code_f(bf[k], requant_factor(bplan.r, bplan.s));
 	if (threadIdx.x < 255) {
 		const int64_t r_h = reciprocal_fast(ss.m);
 		const int64_t kx = composed_exponent(bplan.out.e, ss.e);
@@ -1919,7 +1919,7 @@ __global__ __launch_bounds__(BS) void k_residual_norm(sslm_launch::ResidualArgs 
 		const int i = threadIdx.x + k * BS;
 		c[k] = 0;
 		if (i < H) {
-			c[k] = requant_code_small(w[k], (uint64_t)rplan.r, rplan.s);
+			c[k] = requant_code_f(w[k], requant_factor(rplan.r, rplan.s));
 			out[i] = (int8_t)c[k];
 		}
 	}
@@ -2001,8 +2001,8 @@ void k_mlp_act(sslm_launch::ActArgs a) {
 	int32_t gc[EPT], uc[EPT];
 #pragma unroll
 	for (int k = 0; k < EPT; ++k) {
-		gc[k] = requant_code_small(gf[k], (uint64_t)gp.r, gp.s);
-		uc[k] = requant_code_small(uf[k], (uint64_t)up.r, up.s);
+		gc[k] = requant_code_f(gf[k], requant_factor(gp.r, gp.s));
+		uc[k] = requant_code_f(uf[k], requant_factor(up.r, up.s));
 	}
 	__syncthreads();
 	// The loader admits only the canonical SiLU table (values in [0, 32768]) and the sigmoid
@@ -2026,7 +2026,7 @@ void k_mlp_act(sslm_launch::ActArgs a) {
 #pragma unroll
 	for (int k = 0; k < EPT; ++k) {
 		const int i = threadIdx.x + k * BS;
-		if (i < I) act[i] = requant_code_small(w[k], (uint64_t)ap.r, ap.s);
+		if (i < I) act[i] = requant_code_f(w[k], requant_factor(ap.r, ap.s));
 	}
 	if (threadIdx.x == 0) a.act_scale[t] = ap.out;
 }
@@ -2073,8 +2073,8 @@ __global__ __launch_bounds__(BS) void k_mlp_act_s1(sslm_launch::ActArgs a, int p
 	int32_t gc[EPT], uc[EPT];
 #pragma unroll
 	for (int k = 0; k < EPT; ++k) {
-		gc[k] = requant_code_small(gf[k], (uint64_t)gp.r, gp.s);
-		uc[k] = requant_code_small(uf[k], (uint64_t)up.r, up.s);
+		gc[k] = requant_code_f(gf[k], requant_factor(gp.r, gp.s));
+		uc[k] = requant_code_f(uf[k], requant_factor(up.r, up.s));
 	}
 	__syncthreads();
 	uint32_t mx = 0;
@@ -2129,7 +2129,7 @@ __global__ __launch_bounds__(BS) void k_mlp_act_s2(sslm_launch::ActArgs a, int p
 #pragma unroll
 	for (int k = 0; k < EPT; ++k) {
 		const int i = j0 + threadIdx.x + k * BS;
-		if (i < j1) act[i] = requant_code_small(w[k], (uint64_t)ap.r, ap.s);
+		if (i < j1) act[i] = requant_code_f(w[k], requant_factor(ap.r, ap.s));
 	}
 	if (threadIdx.x == 0 && sl == 0) a.act_scale[t] = ap.out;
 }
@@ -2234,8 +2234,8 @@ __global__ __launch_bounds__(BS) void k_attention(sslm_launch::AttnArgs a, int u
 				*(char2*)(kstore + off) = kc;
 				*(char2*)(kstore + half + off) = vc;
 			}
-			const int32_t x = requant_code_small(qv.x, (uint64_t)plan.r, plan.s);
-			const int32_t y = requant_code_small(qv.y, (uint64_t)plan.r, plan.s);
+			const int32_t x = requant_code_f(qv.x, requant_factor(plan.r, plan.s));
+			const int32_t y = requant_code_f(qv.y, requant_factor(plan.r, plan.s));
 			rope_pair(x, y, c, sn, &xr, &yr);
 			((char2*)s_qc)[i] = make_char2((char)clamp_code(xr), (char)clamp_code(yr));
 		}

@@ -3,6 +3,7 @@
 // reciprocal and division, 64-bit-half requant and landing, double-estimate isqrt, the
 // per-element softmax -- must equal the reference restatements bit for bit.  Built and run
 // by tests/test_device_math_host.py; prints "ok" and exits 0 when every case agrees.
+#include <math.h>
 #include <stdio.h>
 
 #include <random>
@@ -25,6 +26,22 @@ static long g_fail = 0;
 			++g_fail;                              \
 		}                                          \
 	} while (0)
+
+// floor(a f + 1/2) clamped to 127, exactly: f = M 2^E with a 53-bit integer M, the product in
+// 128 bits (the reference for requant_code_f's rounding logic on any non-negative double f)
+static int exact_half_up(uint32_t a, double f) {
+	if (a == 0 || f == 0.0) return 0;
+	int E;
+	const double fm = frexp(f, &E);
+	const uint64_t M = (uint64_t)ldexp(fm, 53);
+	E -= 53;
+	const unsigned __int128 p = (unsigned __int128)a * M;
+	if (E >= 0) return 127;  // a f >= 2^52
+	const int sh = -E;
+	if (sh > 120) return 0;  // a f < 2^-30
+	const unsigned __int128 mag = (2 * p + ((unsigned __int128)1 << sh)) >> (sh + 1);
+	return mag > 127 ? 127 : (int)mag;
+}
 
 int main(int argc, char** argv) {
 	const long N = argc > 1 ? atol(argv[1]) : 200000;
@@ -64,7 +81,50 @@ int main(int argc, char** argv) {
 		const int s = (int)uni(-1, 30);
 		EXPECT(requant_code_small(x, (uint64_t)r, s) == or_requant_code_wide(x, r, s), "%lld %lld %d", (long long)x,
 		       (long long)r, s);
+		EXPECT(requant_code_f(x, requant_factor(r, s)) == or_requant_code_wide(x, r, s), "f %lld %lld %d", (long long)x,
+		       (long long)r, s);
 	}
+	// the double form at the rounding boundaries: x around (n - 1/2) 2^(62-s) / (127 r) for every
+	// code n (a third of the cases with r near 2^32)
+	for (long i = 0; i < N / 4; ++i) {
+		const int64_t dn = i % 3 ? uni(1LL << 30, (1LL << 31) - 1) : (1LL << 30) + uni(0, 64);
+		const int64_t r = or_reciprocal(dn);
+		const int s = (int)uni(-1, 30);
+		const int n = (int)uni(0, 128);
+		const long double xb = ((long double)n - 0.5L) * ldexpl(1.0L, 62 - s) / (127.0L * (long double)r);
+		const int64_t x0 = (int64_t)floorl(xb);
+		for (int64_t d = -2; d <= 2; ++d) {
+			const int64_t xa = x0 + d;
+			if (xa < 0 || xa > (1LL << 31)) continue;
+			for (int sg = 0; sg < 2; ++sg) {
+				const int64_t x = sg ? -xa : xa;
+				EXPECT(requant_code_f(x, requant_factor(r, s)) == or_requant_code_wide(x, r, s), "edge %lld %lld %d",
+				       (long long)x, (long long)r, s);
+			}
+		}
+	}
+	// requant_code_f's rounding logic for any double factor, within a few ulps of every
+	// half-integer m - 1/2 (where the product's rounding error decides the code)
+	for (long i = 0; i < N / 2; ++i) {
+		const uint32_t a = (uint32_t)(i % 4 ? uni(1, 1LL << 31) : uni(1, 4096));
+		const int m = (int)uni(1, 128);
+		double f = ((double)m - 0.5) / (double)a;
+		for (int st = 0; st < 3; ++st) f = nextafter(f, 0.0);
+		for (int st = 0; st < 7; ++st, f = nextafter(f, 1e300))
+			for (int sg = 0; sg < 2; ++sg) {
+				const int64_t x = sg ? -(int64_t)a : (int64_t)a;
+				const int want = exact_half_up(a, f);
+				EXPECT(requant_code_f(x, f) == (int8_t)(sg ? -want : want), "near tie a=%u m=%d f=%.17g", a, m, f);
+			}
+	}
+	// exact ties: q = 127 x r / 2^(62-s) is a half-integer below 128 only at q = 63.5 (127 must
+	// divide 2m - 1), i.e. x r = 2^(61-s): r = 2^32, x = 2^(29-s).  Every such input, both signs.
+	for (int s = -1; s <= 29; ++s)
+		for (int sg = 0; sg < 2; ++sg) {
+			const int64_t r = 1LL << 32, x = (sg ? -1 : 1) * (1LL << (29 - s));
+			EXPECT(requant_code_f(x, requant_factor(r, s)) == or_requant_code_wide(x, r, s), "tie %lld %d", (long long)x, s);
+			EXPECT(or_requant_code_wide(x, r, s) == (sg ? -64 : 64), "tie rounds away from zero");
+		}
 	// landing on residual operands, every exponent band
 	for (long i = 0; i < N; ++i) {
 		const int64_t branch = uni(-127, 127);
@@ -113,6 +173,8 @@ int main(int argc, char** argv) {
 		if (st == 0 && ost == 0) {
 			EXPECT(plan.out.m == out.m && plan.out.e == out.e, "scale");
 			for (int j = 0; j < n; ++j) EXPECT(requant_code_small(row[j], (uint64_t)plan.r, plan.s) == codes[j], "code");
+			const double f = requant_factor(plan.r, plan.s);
+			for (int j = 0; j < n; ++j) EXPECT(requant_code_f(row[j], f) == codes[j], "code f");
 		}
 	}
 	// softmax row as the attention kernel computes it (constants, gate, per-element i-exp, Q15)
