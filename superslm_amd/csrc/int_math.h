@@ -614,6 +614,47 @@ SSLM_HD int64_t iexp_fast(int64_t shifted, int64_t q_ln2, double inv_ln2, int64_
 }
 
 // The softmax's per-element ceiling M = q_b^2 + q_c when usable (intmath.cpp:831-851), else 0.
+// iexp_fast on 32-bit operands, for a row whose constants pass iexp_small_ok (and the width
+// gate: q_c >= 0, q_b^2 + q_c <= kSoftmaxMaxSafe): then x, z, r and base = q_b - r fit int32
+// and base^2 + q_c is one 32 x 32 + 64-bit multiply-add; same value, or -1 when refused.
+SSLM_HD bool iexp_small_ok(int64_t q_ln2, int64_t q_b, int64_t m_ceiling) {
+	const int64_t ab = q_b < 0 ? -q_b : q_b;
+	return q_ln2 >= 1 && q_ln2 <= kI32Max / 30 && ab <= kI32Max - q_ln2 && m_ceiling > 0;
+}
+SSLM_HD int64_t iexp_small(int64_t shifted, int32_t q_ln2, double inv_ln2, int32_t q_b, int64_t q_c,
+                           int64_t m_ceiling) {
+	const int32_t lim = 30 * q_ln2;
+	const int32_t x = shifted < -(int64_t)lim ? lim : (int32_t)(-shifted);
+	int32_t z = (int32_t)((double)x * inv_ln2);
+	z = z < 0 ? 0 : (z > 30 ? 30 : z);
+	int32_t r = x - z * q_ln2;
+	while (r < 0) {
+		--z;
+		r += q_ln2;
+	}
+	while (r >= q_ln2) {
+		++z;
+		r -= q_ln2;
+	}
+	const int32_t base = q_b - r;
+	const uint32_t ab = base < 0 ? 0u - (uint32_t)base : (uint32_t)base;
+	const uint64_t v = ((uint64_t)ab * ab + (uint64_t)q_c) >> z;
+	return v > (uint64_t)m_ceiling ? -1 : (int64_t)v;
+}
+
+// The Q15 probability floor((e << 15) / d) for 0 <= e <= d < 2^38 in doubles: e 2^15 and d are
+// exact, the estimate n / d is off by less than 2^-37, and fma gives the remainder n - q d
+// exactly, so one step corrects it (div_floor_pos's value).
+SSLM_HD bool div_q15_small_ok(int64_t d) { return d >= 1 && d < ((int64_t)1 << 38); }
+SSLM_HD int32_t div_q15_small(int64_t e, double d, double inv) {
+#pragma clang fp contract(off)
+	const double n = (double)e * 32768.0;
+	double q = fmin(trunc(n * inv), 32768.0);
+	const double r = fma(-q, d, n);
+	q = r < 0.0 ? q - 1.0 : (r >= d ? q + 1.0 : q);
+	return (int32_t)q;
+}
+
 SSLM_HD int64_t softmax_ceiling(int64_t q_b, int64_t q_c) {
 	s128 m128 = (s128)q_b * q_b + (s128)q_c;
 	bool usable = m128 <= (s128)kI64Max && m128 >= 1 && m128 <= (s128)kSoftmaxMaxSafe;

@@ -2302,14 +2302,23 @@ __global__ __launch_bounds__(BS) void k_attention(sslm_launch::AttnArgs a, int u
 	int64_t sum = 0;
 	uint64_t refused = 0;
 	const double inv_ln2 = c_qln2 >= 1 ? 1.0 / (double)c_qln2 : 0.0;
-	for (int64_t p = threadIdx.x; p < width; p += BS) {
-		int64_t v = iexp_fast(ex[p] - mx, c_qln2, inv_ln2, c_qb, c_qc, c_M);  // the row passed check_softmax_width
-		if (v < 0) {
-			refused = 1;
-			v = 0;
+	// the row passed check_softmax_width; the 32-bit form where its constants allow
+	if (iexp_small_ok(c_qln2, c_qb, c_M)) {
+		for (int64_t p = threadIdx.x; p < width; p += BS) {
+			int64_t v = iexp_small(ex[p] - mx, (int32_t)c_qln2, inv_ln2, (int32_t)c_qb, c_qc, c_M);
+			refused |= v < 0 ? 1u : 0u;
+			v = v < 0 ? 0 : v;
+			ex[p] = v;
+			sum += v;
 		}
-		ex[p] = v;
-		sum += v;
+	} else {
+		for (int64_t p = threadIdx.x; p < width; p += BS) {
+			int64_t v = iexp_fast(ex[p] - mx, c_qln2, inv_ln2, c_qb, c_qc, c_M);
+			refused |= v < 0 ? 1u : 0u;
+			v = v < 0 ? 0 : v;
+			ex[p] = v;
+			sum += v;
+		}
 	}
 	sum = wave_sum_i64(sum);
 	refused = wave_max_u64(refused);
@@ -2332,7 +2341,12 @@ __global__ __launch_bounds__(BS) void k_attention(sslm_launch::AttnArgs a, int u
 	// pass 3: Q15 probabilities p = (e << 15) / max(total, 1)
 	const int64_t denom = sum > 1 ? sum : 1;
 	const double dinv = 1.0 / (double)denom;  // e <= total: quotients at most 2^15
-	for (int64_t p = threadIdx.x; p < width; p += BS) ex[p] = ex[p] == 0 ? 0 : div_rcp(ex[p] << 15, denom, dinv, 32768);
+	if (div_q15_small_ok(denom)) {
+		const double dd = (double)denom;
+		for (int64_t p = threadIdx.x; p < width; p += BS) ex[p] = ex[p] == 0 ? 0 : div_q15_small(ex[p], dd, dinv);
+	} else {
+		for (int64_t p = threadIdx.x; p < width; p += BS) ex[p] = ex[p] == 0 ? 0 : div_rcp(ex[p] << 15, denom, dinv, 32768);
+	}
 	__syncthreads();
 	// pass 4: context = sum_p prob * V[p].  A thread owns 16 dimensions (one 16-byte load per
 	// row) of every PG-th position; the loop is unrolled so several rows are in flight.  The sums
@@ -2387,7 +2401,7 @@ __global__ __launch_bounds__(BS) void k_attention(sslm_launch::AttnArgs a, int u
 // transposed in registers) so a lane's 16 B operand holds 16 positions of one dimension.
 // The launch must hold one sequence's consecutive positions (a prefill chunk).
 template <int D, int NW>
-__global__ __launch_bounds__(64 * NW) void k_attention_tiled(sslm_launch::AttnArgs a) {
+__global__ __launch_bounds__(64 * NW, NW == 4 ? 3 : 1) void k_attention_tiled(sslm_launch::AttnArgs a) {
 	constexpr int TQ = 16, KB = 16 * NW, NC = (D + 63) / 64, DT = D / 16, PS = KB + 16, VS = KB + 16;
 	__shared__ __attribute__((aligned(16))) int8_t s_p[3][TQ][PS];  // probability parts [part][token][pos]
 	__shared__ __attribute__((aligned(16))) int8_t s_vt[D][VS];     // V^T of the current step's positions
@@ -2511,12 +2525,18 @@ __global__ __launch_bounds__(64 * NW) void k_attention_tiled(sslm_launch::AttnAr
 	}
 	int64_t cq[4][4];
 	double inv[4];
+	bool esmall[4];  // the token's constants admit iexp_small
 #pragma unroll
 	for (int v = 0; v < 4; ++v) {
 #pragma unroll
 		for (int i = 0; i < 4; ++i) cq[v][i] = s_c[g * 4 + v][i];
 		inv[v] = s_inv[g * 4 + v];
+		esmall[v] = iexp_small_ok(cq[v][0], cq[v][1], cq[v][3]);
 	}
+	auto iexp_tok = [&](int v, int64_t shifted) {
+		return esmall[v] ? iexp_small(shifted, (int32_t)cq[v][0], inv[v], (int32_t)cq[v][1], cq[v][2], cq[v][3])
+		                 : iexp_fast(shifted, cq[v][0], inv[v], cq[v][1], cq[v][2], cq[v][3]);
+	};
 	__syncthreads();
 	// pass 2: i-exp values (SoftmaxRowQ15, intmath.cpp:853-889) and the row sums
 	int64_t sum[4] = {0, 0, 0, 0};
@@ -2527,7 +2547,7 @@ __global__ __launch_bounds__(64 * NW) void k_attention_tiled(sslm_launch::AttnAr
 #pragma unroll
 		for (int v = 0; v < 4; ++v) {
 			if (tok_ok[v] && p <= tpos[v]) {
-				const int64_t e = iexp_fast((int64_t)s[v] - rmx[v], cq[v][0], inv[v], cq[v][1], cq[v][2], cq[v][3]);
+				const int64_t e = iexp_tok(v, (int64_t)s[v] - rmx[v]);
 				if (e < 0) refused |= 1u << v;
 				else sum[v] += e;
 			}
@@ -2544,7 +2564,8 @@ __global__ __launch_bounds__(64 * NW) void k_attention_tiled(sslm_launch::AttnAr
 			if (refused >> v & 1) s_rf[g * 4 + v] = 1;
 	__syncthreads();
 	int64_t denom[4];
-	double dinv[4];
+	double dinv[4], ddn[4];
+	bool dsmall[4];  // the token's total admits div_q15_small
 #pragma unroll
 	for (int v = 0; v < 4; ++v) {
 		const int tq = g * 4 + v;
@@ -2553,6 +2574,8 @@ __global__ __launch_bounds__(64 * NW) void k_attention_tiled(sslm_launch::AttnAr
 		for (int w = 0; w < NW; ++w) tot += s_red[w][tq];
 		denom[v] = tot > 1 ? tot : 1;
 		dinv[v] = 1.0 / (double)denom[v];
+		dsmall[v] = div_q15_small_ok(denom[v]);
+		ddn[v] = (double)denom[v];
 		tok_ok[v] = tok_ok[v] && s_rf[tq] == 0;
 	}
 	if (threadIdx.x < nt && s_ok[threadIdx.x] == kOk && s_rf[threadIdx.x] != 0)
@@ -2573,8 +2596,9 @@ __global__ __launch_bounds__(64 * NW) void k_attention_tiled(sslm_launch::AttnAr
 			int32_t pr = 0;
 			if (tok_ok[v] && p <= tpos[v]) {
 				// e <= total, so the quotient is at most 2^15
-				const int64_t e = iexp_fast((int64_t)s[v] - rmx[v], cq[v][0], inv[v], cq[v][1], cq[v][2], cq[v][3]);
-				pr = e == 0 ? 0 : (int32_t)div_rcp(e << 15, denom[v], dinv[v], 32768);
+				const int64_t e = iexp_tok(v, (int64_t)s[v] - rmx[v]);
+				pr = e == 0 ? 0
+				            : (dsmall[v] ? div_q15_small(e, ddn[v], dinv[v]) : (int32_t)div_rcp(e << 15, denom[v], dinv[v], 32768));
 			}
 			s_p[0][g * 4 + v][pl] = (int8_t)(pr >> 14);
 			s_p[1][g * 4 + v][pl] = (int8_t)((pr >> 7) & 127);

@@ -22,5 +22,8 @@ def test_fast_forms_match(tmp_path):
     print(out)
     assert "iexp: " in out and ", 0 mismatches" in out.splitlines()[0]
     assert "div: 0 mismatches" in out
+    assert "div_q15_small: 0 mismatches" in out
+    small = [l for l in out.splitlines() if l.startswith("iexp_small:")][0]
+    assert small.endswith(", 0 mismatches") and int(small.split("(")[1].split(" accepted")[0]) > 10000
     accepted = int(out.split("(")[1].split(" accepted")[0])
     assert accepted > 10000  # the accepted (non-refused) path is exercised, not only refusals
