@@ -20,6 +20,7 @@
 namespace sslm {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v2i __attribute__((ext_vector_type(2)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 
 constexpr int kBlock = 256;
@@ -2397,14 +2398,14 @@ __global__ __launch_bounds__(BS) void k_attention(sslm_launch::AttnArgs a, int u
 // sum, pass 3 recomputes them once more for the Q15 probabilities and multiplies by V.  P.V runs
 // on the same MFMA: a probability (0 .. 2^15) is split into three 7-bit parts p = a*2^14 + b*2^7
 // + c, each an int8 operand, and the three int32 products recombine exactly (the true sum is
-// below 2^22 in magnitude).  V is staged transposed in LDS ([dim][position], 4x4 byte blocks
-// transposed in registers) so a lane's 16 B operand holds 16 positions of one dimension.
+// below 2^22 in magnitude).  V rows are staged in LDS as stored ([position][dim]) and read with
+// gfx950's byte-transposing LDS load, so a lane's 16 B operand holds 16 positions of one dimension.
 // The launch must hold one sequence's consecutive positions (a prefill chunk).
 template <int D, int NW>
 __global__ __launch_bounds__(64 * NW, NW == 4 ? 3 : 1) void k_attention_tiled(sslm_launch::AttnArgs a) {
-	constexpr int TQ = 16, KB = 16 * NW, NC = (D + 63) / 64, DT = D / 16, PS = KB + 16, VS = KB + 16;
+	constexpr int TQ = 16, KB = 16 * NW, NC = (D + 63) / 64, DT = D / 16, PS = KB + 16, VS = D + 16;
 	__shared__ __attribute__((aligned(16))) int8_t s_p[3][TQ][PS];  // probability parts [part][token][pos]
-	__shared__ __attribute__((aligned(16))) int8_t s_vt[D][VS];     // V^T of the current step's positions
+	__shared__ __attribute__((aligned(16))) int8_t s_v[KB][VS];     // the current step's V rows, padded
 	__shared__ int64_t s_c[TQ][4];                                   // per token: q_ln2, q_b, q_c, ceiling
 	__shared__ double s_inv[TQ];                                     // per token: 1 / q_ln2
 	__shared__ int64_t s_red[NW][TQ];
@@ -2604,21 +2605,11 @@ __global__ __launch_bounds__(64 * NW, NW == 4 ? 3 : 1) void k_attention_tiled(ss
 			s_p[1][g * 4 + v][pl] = (int8_t)((pr >> 7) & 127);
 			s_p[2][g * 4 + v][pl] = (int8_t)(pr & 127);
 		}
-		// V rows [blk*64, blk*64 + 64) transposed into s_vt: a 4x4 byte block per item
-		for (int it = threadIdx.x; it < (KB / 4) * (D / 4); it += 64 * NW) {
-			const int p4 = it / (D / 4), d4 = it % (D / 4);
-			uint32_t r[4];
-#pragma unroll
-			for (int i = 0; i < 4; ++i) {
-				const int pr = min(blk * KB + p4 * 4 + i, (int)a.cap - 1);
-				r[i] = *(const uint32_t*)(vbase + (int64_t)pr * D + d4 * 4);
-			}
-#pragma unroll
-			for (int j = 0; j < 4; ++j) {
-				const uint32_t c = ((r[0] >> (8 * j)) & 0xffu) | (((r[1] >> (8 * j)) & 0xffu) << 8) |
-				                   (((r[2] >> (8 * j)) & 0xffu) << 16) | (((r[3] >> (8 * j)) & 0xffu) << 24);
-				*(uint32_t*)&s_vt[d4 * 4 + j][p4 * 4] = c;
-			}
+		// the step's V rows, as stored (16-byte copies; rows past the cap repeat the last one)
+		for (int c = threadIdx.x; c < KB * (D / 16); c += 64 * NW) {
+			const int pr = c / (D / 16), ch = c % (D / 16);
+			const int64_t pos = min(blk * KB + pr, (int)a.cap - 1);
+			*(v4i*)&s_v[pr][ch * 16] = load16(vbase + pos * D + ch * 16);
 		}
 		__syncthreads();
 #pragma unroll
@@ -2627,7 +2618,15 @@ __global__ __launch_bounds__(64 * NW, NW == 4 ? 3 : 1) void k_attention_tiled(ss
 			if (dt < DT) {
 #pragma unroll
 				for (int kk = 0; kk < KB / 64; ++kk) {
-					const v4i b = *(const v4i*)&s_vt[dt * 16 + ri][kk * 64 + g * 16];
+					// B operand (dimension dt*16 + ri, positions kk*64 + 16g + 0..15) by two LDS
+					// transpose reads: in each 16-lane group, lane m names the 8 bytes at row
+					// (position) m/2, dimensions dt*16 + 8(m%2) + 0..7, and lane ri receives byte
+					// ri%8 of rows 2j + ri/8, j = 0..7 -- dimension dt*16 + ri at 8 positions
+					const int8_t* vp = &s_v[kk * 64 + g * 16 + (ri >> 1)][dt * 16 + 8 * (ri & 1)];
+					const v2i lo = __builtin_amdgcn_ds_read_tr8_b64_v2i32((__attribute__((address_space(3))) v2i*)vp);
+					const v2i hi =
+					    __builtin_amdgcn_ds_read_tr8_b64_v2i32((__attribute__((address_space(3))) v2i*)(vp + 8 * VS));
+					const v4i b = v4i{lo.x, lo.y, hi.x, hi.y};
 #pragma unroll
 					for (int k = 0; k < 3; ++k) {
 						const v4i pa = *(const v4i*)&s_p[k][ri][kk * 64 + g * 16];
