@@ -497,7 +497,7 @@ def main():
         pre = {"prefill_512_tok_s": round(512 / pre_s, 1), "prefill_512_ms": round(pre_s * 1e3, 3),
                "prefill_roofline": {"bound": "mfma", "achieved": round(prefill_tops, 1), "peak": INT8_PEAK_TOPS,
                                     "unit": "TOPS", "frac": round(prefill_tops / INT8_PEAK_TOPS, 4),
-                                    "kernel": "prefill GEMM (k_gemm_mfma; k_gemm_narrow for q|k|v and o): the 112 projection GEMMs of one "
+                                    "kernel": "prefill GEMM (k_gemm_wide for gate|up, k_gemm_mfma split-K for down, k_gemm_narrow for q|k|v and o): the 112 projection GEMMs of one "
                                               "512-token chunk (28 layers' q|k|v, o, gate|up, down, the layer loop's "
                                               "launch shapes) back to back between two HIP events: sum of 2*M*N*K "
                                               "/ pass time; peak = MI355X dense int8 MFMA",

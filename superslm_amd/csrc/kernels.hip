@@ -2837,8 +2837,24 @@ GemvPlan gemv_plan(int M, int N, int K, bool split_ok, bool raw_or_argmax) {
 	return p;
 }
 
+// Every GEMM launch writes where its caller provided: raw int32 output, split-K planes, argmax
+// keys, or epilogue segments with output and fold buffers that cover the columns.  Anything else
+// is a caller bug that the kernels would turn into stores through null pointers: refuse it.
+static void check_gemm_outputs(const GemmArgs& g) {
+	bool ok = g.epi.raw_out || g.epi.argmax_key || (g.splits > 1 && g.split_part);
+	if (!ok && g.epi.nseg >= 1 && g.epi.nseg <= kMaxSeg) {
+		ok = g.epi.seg[0].n_begin == 0 && g.epi.seg[g.epi.nseg - 1].n_end >= g.N;
+		for (int i = 0; i < g.epi.nseg; ++i) ok = ok && g.epi.seg[i].out && g.epi.seg[i].fold;
+	}
+	if (!ok) {
+		fprintf(stderr, "sslm_hip: GEMM launch (%d x %d x %d) without a complete output\n", g.M, g.N, g.K);
+		abort();
+	}
+}
+
 void gemm(const GemmArgs& g, hipStream_t s) {
 	if (g.M <= 0 || g.N <= 0) return;
+	check_gemm_outputs(g);
 	if (gemv_eligible(g.M, g.K)) {
 		// g.splits > 1 only as gemv_plan(M, N, K, true, raw).splits, for which the caller sized
 		// split_part
