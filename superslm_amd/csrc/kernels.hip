@@ -427,23 +427,25 @@ __device__ __forceinline__ int tile_segment(const Epilogue& e, int c0) {
 	return (e.nseg > 1 && c0 >= e.seg[0].n_end) ? ((e.nseg > 2 && c0 >= e.seg[1].n_end) ? 2 : 1) : 0;
 }
 
-template <int CPW>
+template <int MB, int CPW>  // MB row groups of 16 tokens
 __global__ __launch_bounds__(256) void k_gemv_p(GemmArgs g) {
-	__shared__ v4i red[2][kGemvWaves][64];
+	__shared__ v4i red[2][kGemvWaves][MB][64];
 	const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, ri = lane & 15, grp = lane >> 4;
 	const int C = g.K >> 7, T = (g.N + 15) / 16;
 	const v4i z = v4i{0, 0, 0, 0};
 	const Epilogue& e = g.epi;
-	v4i x[CPW][2];
-	{
-		const bool rok = ri < g.M;
-		const int8_t* arow = g.a + (size_t)(rok ? ri : g.M - 1) * g.lda + grp * 32;
+	v4i x[MB][CPW][2];
+#pragma unroll
+	for (int mb = 0; mb < MB; ++mb) {
+		const int r = mb * 16 + ri;
+		const bool rok = r < g.M;
+		const int8_t* arow = g.a + (size_t)(rok ? r : g.M - 1) * g.lda + grp * 32;
 #pragma unroll
 		for (int i = 0; i < CPW; ++i) {
 			const int c = wave + kGemvWaves * i;
 			const bool ok = rok && c < C;
-			x[i][0] = ok ? load16(arow + (size_t)c * 128) : z;
-			x[i][1] = ok ? load16(arow + (size_t)c * 128 + 16) : z;
+			x[mb][i][0] = ok ? load16(arow + (size_t)c * 128) : z;
+			x[mb][i][1] = ok ? load16(arow + (size_t)c * 128 + 16) : z;
 		}
 	}
 	// weight chunks and fold parameters of tile t (past the last tile: the last one again)
@@ -470,43 +472,51 @@ __global__ __launch_bounds__(256) void k_gemv_p(GemmArgs g) {
 	};
 	auto step = [&](int tile, int it, Tile& cur, Tile& nxt) {
 		load_tile(tile + (int)gridDim.x, nxt);
-		v4i acc = z;
+		v4i acc[MB];
 #pragma unroll
-		for (int i = 0; i < CPW; ++i)
-			if (wave + kGemvWaves * i < C) {
-				acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(x[i][0], cur.b[i][0], acc, 0, 0, 0);
-				acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(x[i][1], cur.b[i][1], acc, 0, 0, 0);
-			}
-		red[it & 1][wave][lane] = acc;
+		for (int mb = 0; mb < MB; ++mb) {
+			acc[mb] = z;
+#pragma unroll
+			for (int i = 0; i < CPW; ++i)
+				if (wave + kGemvWaves * i < C) {
+					acc[mb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(x[mb][i][0], cur.b[i][0], acc[mb], 0, 0, 0);
+					acc[mb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(x[mb][i][1], cur.b[i][1], acc[mb], 0, 0, 0);
+				}
+			red[it & 1][wave][mb][lane] = acc[mb];
+		}
 		__syncthreads();
 		if (wave != (it & 3)) return;
-		v4i tot = red[it & 1][0][lane];
-#pragma unroll
-		for (int w = 1; w < kGemvWaves; ++w) {
-			const v4i y = red[it & 1][w][lane];
-			tot[0] += y[0];
-			tot[1] += y[1];
-			tot[2] += y[2];
-			tot[3] += y[3];
-		}
 		const SegView sg = seg_view(e, tile_segment(e, tile * 16));
-		const int j = tile * 16 + ri, t0 = grp * 4, jj = j - sg.n_begin;
-		int64_t val[4];
-		uint32_t mabs[4];
+		const int j = tile * 16 + ri, jj = j - sg.n_begin;
 #pragma unroll
-		for (int v = 0; v < 4; ++v) {
-			const bool live = t0 + v < g.M && j < g.N;
-			val[v] = apply_fold((int64_t)tot[v], cur.f0, cur.f1, cur.f2);
-			mabs[v] = dpp_max16(live && sg.mode == kSegFunnel ? sat_abs_u32(val[v]) : 0u);  // tile max
-		}
+		for (int mb = 0; mb < MB; ++mb) {
+			v4i tot = red[it & 1][0][mb][lane];
 #pragma unroll
-		for (int v = 0; v < 4; ++v) {
-			if (t0 + v < g.M && j < g.N) {
-				if (sg.mode == kSegWide) ((int64_t*)sg.out)[(size_t)(t0 + v) * sg.ld_out + jj] = val[v];
-				else ((int32_t*)sg.out)[(size_t)(t0 + v) * sg.ld_out + jj] = sat_i32(val[v]);
+			for (int w = 1; w < kGemvWaves; ++w) {
+				const v4i y = red[it & 1][w][mb][lane];
+				tot[0] += y[0];
+				tot[1] += y[1];
+				tot[2] += y[2];
+				tot[3] += y[3];
 			}
-			if (sg.mode == kSegFunnel && sg.maxpart && ri == 0 && t0 + v < g.M)
-				sg.maxpart[(size_t)tile * kPartLd + t0 + v] = mabs[v];
+			const int t0 = mb * 16 + grp * 4;
+			int64_t val[4];
+			uint32_t mabs[4];
+#pragma unroll
+			for (int v = 0; v < 4; ++v) {
+				const bool live = t0 + v < g.M && j < g.N;
+				val[v] = apply_fold((int64_t)tot[v], cur.f0, cur.f1, cur.f2);
+				mabs[v] = dpp_max16(live && sg.mode == kSegFunnel ? sat_abs_u32(val[v]) : 0u);  // tile max
+			}
+#pragma unroll
+			for (int v = 0; v < 4; ++v) {
+				if (t0 + v < g.M && j < g.N) {
+					if (sg.mode == kSegWide) ((int64_t*)sg.out)[(size_t)(t0 + v) * sg.ld_out + jj] = val[v];
+					else ((int32_t*)sg.out)[(size_t)(t0 + v) * sg.ld_out + jj] = sat_i32(val[v]);
+				}
+				if (sg.mode == kSegFunnel && sg.maxpart && ri == 0 && t0 + v < g.M)
+					sg.maxpart[(size_t)tile * kPartLd + t0 + v] = mabs[v];
+			}
 		}
 	};
 	Tile t0buf, t1buf;
@@ -2950,10 +2960,10 @@ GemvPlan gemv_plan(int M, int N, int K, bool split_ok, bool raw_or_argmax) {
 	return p;
 }
 
-// The persistent decode GEMV takes projection launches at M <= 16 and K <= 4096 whose segments
+// The persistent decode GEMV takes projection launches at M <= 32 and K <= 4096 whose segments
 // are funnel or wide outputs without bias or LoRA, K split nowhere (k_gemv_p).
 static bool gemv_persistent_ok(const GemmArgs& g) {
-	if (g.M > 16 || g.K > 4096 || g.K % 128 || g.splits > 1 || g.epi.raw_out || g.epi.argmax_key) return false;
+	if (g.M > 32 || g.K > 4096 || g.K % 128 || g.splits > 1 || g.epi.raw_out || g.epi.argmax_key) return false;
 	if (g.epi.nseg < 1 || g.epi.nseg > kMaxSeg) return false;
 	for (int i = 0; i < g.epi.nseg; ++i) {
 		const Segment& sg = g.epi.seg[i];
@@ -2961,6 +2971,24 @@ static bool gemv_persistent_ok(const GemmArgs& g) {
 		if (sg.n_begin % 16 || (sg.n_end % 16 && i + 1 < g.epi.nseg)) return false;
 	}
 	return true;
+}
+
+static int device_cus();
+
+template <int MB>
+void launch_gemv_p(const GemmArgs& g, hipStream_t s) {
+	const int C = g.K >> 7, T = (g.N + 15) / 16;
+	const dim3 grid(std::min(T, device_cus())), block(256);
+	switch ((C + kGemvWaves - 1) / kGemvWaves) {
+		case 1: hipLaunchKernelGGL((k_gemv_p<MB, 1>), grid, block, 0, s, g); break;
+		case 2: hipLaunchKernelGGL((k_gemv_p<MB, 2>), grid, block, 0, s, g); break;
+		case 3: hipLaunchKernelGGL((k_gemv_p<MB, 3>), grid, block, 0, s, g); break;
+		case 4: hipLaunchKernelGGL((k_gemv_p<MB, 4>), grid, block, 0, s, g); break;
+		case 5: hipLaunchKernelGGL((k_gemv_p<MB, 5>), grid, block, 0, s, g); break;
+		case 6: hipLaunchKernelGGL((k_gemv_p<MB, 6>), grid, block, 0, s, g); break;
+		case 7: hipLaunchKernelGGL((k_gemv_p<MB, 7>), grid, block, 0, s, g); break;
+		default: hipLaunchKernelGGL((k_gemv_p<MB, 8>), grid, block, 0, s, g); break;
+	}
 }
 
 // compute units of the current device (one persistent block each)
@@ -3010,18 +3038,8 @@ void gemm(const GemmArgs& g, hipStream_t s) {
 		}
 		const int mblocks = (g.M + 15) / 16;
 		if (gemv_persistent_ok(g)) {
-			const int C = g.K >> 7, T = (g.N + 15) / 16;
-			const dim3 grid(std::min(T, device_cus())), block(256);
-			switch ((C + kGemvWaves - 1) / kGemvWaves) {
-				case 1: hipLaunchKernelGGL((k_gemv_p<1>), grid, block, 0, s, g); break;
-				case 2: hipLaunchKernelGGL((k_gemv_p<2>), grid, block, 0, s, g); break;
-				case 3: hipLaunchKernelGGL((k_gemv_p<3>), grid, block, 0, s, g); break;
-				case 4: hipLaunchKernelGGL((k_gemv_p<4>), grid, block, 0, s, g); break;
-				case 5: hipLaunchKernelGGL((k_gemv_p<5>), grid, block, 0, s, g); break;
-				case 6: hipLaunchKernelGGL((k_gemv_p<6>), grid, block, 0, s, g); break;
-				case 7: hipLaunchKernelGGL((k_gemv_p<7>), grid, block, 0, s, g); break;
-				default: hipLaunchKernelGGL((k_gemv_p<8>), grid, block, 0, s, g); break;
-			}
+			if (mblocks == 1) launch_gemv_p<1>(g, s);
+			else launch_gemv_p<2>(g, s);
 			return;
 		}
 		if (p.tpw == 2 && mblocks == 1) {

@@ -62,7 +62,7 @@ IN_SCALE = (1 << 30, -37)
 SITE = (1518500250, -45)
 
 
-@pytest.mark.parametrize("m", [32, 1, 5, 16, 128, 300])
+@pytest.mark.parametrize("m", [32, 1, 5, 16, 20, 128, 300])
 def test_config0_requant_matches_oracle(m, hip_lib, oracle_lib):
     from oracle_bind import project_rows
     L = _lib(hip_lib)
