@@ -2524,6 +2524,8 @@ __global__ __launch_bounds__(BS) void k_attention(sslm_launch::AttnArgs a, int u
 // below 2^22 in magnitude).  V rows are staged in LDS as stored ([position][dim]) and read with
 // gfx950's byte-transposing LDS load, so a lane's 16 B operand holds 16 positions of one dimension.
 // The launch must hold one sequence's consecutive positions (a prefill chunk).
+constexpr int kTiledECache = 512;  // positions whose i-exp values an 8-wave tiled-attention block keeps
+
 template <int D, int NW>
 __global__ __launch_bounds__(64 * NW, NW == 4 ? 3 : 1) void k_attention_tiled(sslm_launch::AttnArgs a) {
 	constexpr int TQ = 16, KB = 16 * NW, NC = (D + 63) / 64, DT = D / 16, PS = KB + 16, VS = D + 16;
@@ -2535,6 +2537,10 @@ __global__ __launch_bounds__(64 * NW, NW == 4 ? 3 : 1) void k_attention_tiled(ss
 	__shared__ int32_t s_pos[TQ], s_ok[TQ];
 	__shared__ uint32_t s_mab[TQ], s_rf[TQ];  // per token: |context| maximum, softmax refused
 	__shared__ int32_t s_st;
+	// 8-wave blocks keep pass 2's i-exp values for rows up to kTiledECache positions, so pass 3
+	// neither recomputes the scores nor the i-exp values; each lane reads back only what it wrote
+	constexpr int ECP = NW == 8 ? kTiledECache : 1;
+	__shared__ int64_t s_e[NW == 8 ? TQ : 1][ECP];
 	const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, ri = lane & 15, g = lane >> 4;
 	const int group = a.NH / a.NKV, ntiles = (a.M + TQ - 1) / TQ;
 	int h, tile;
@@ -2611,6 +2617,7 @@ __global__ __launch_bounds__(64 * NW, NW == 4 ? 3 : 1) void k_attention_tiled(ss
 		tok_ok[v] = s_ok[g * 4 + v] == kOk;
 	}
 	const int nblk = (wmax + KB - 1) / KB;
+	const bool ecache = NW == 8 && nblk * KB <= ECP;
 	auto scores = [&](int blk, int* p_out) {
 		const int p = blk * KB + wave * 16 + ri;
 		const int8_t* kr = kbase + (int64_t)min(p, (int)a.cap - 1) * D;
@@ -2672,6 +2679,7 @@ __global__ __launch_bounds__(64 * NW, NW == 4 ? 3 : 1) void k_attention_tiled(ss
 		for (int v = 0; v < 4; ++v) {
 			if (tok_ok[v] && p <= tpos[v]) {
 				const int64_t e = iexp_tok(v, (int64_t)s[v] - rmx[v]);
+				if (ecache) s_e[NW == 8 ? g * 4 + v : 0][NW == 8 ? p : 0] = e;
 				if (e < 0) refused |= 1u << v;
 				else sum[v] += e;
 			}
@@ -2713,14 +2721,16 @@ __global__ __launch_bounds__(64 * NW, NW == 4 ? 3 : 1) void k_attention_tiled(ss
 		for (int k = 0; k < 3; ++k) cacc[i][k] = v4i{0, 0, 0, 0};
 	for (int blk = 0; blk < nblk; ++blk) {
 		int p;
-		const v4i s = scores(blk, &p);
+		v4i s = v4i{0, 0, 0, 0};
+		if (ecache) p = blk * KB + wave * 16 + ri;
+		else s = scores(blk, &p);
 		const int pl = wave * 16 + ri;
 #pragma unroll
 		for (int v = 0; v < 4; ++v) {
 			int32_t pr = 0;
 			if (tok_ok[v] && p <= tpos[v]) {
 				// e <= total, so the quotient is at most 2^15
-				const int64_t e = iexp_tok(v, (int64_t)s[v] - rmx[v]);
+				const int64_t e = ecache ? s_e[NW == 8 ? g * 4 + v : 0][NW == 8 ? p : 0] : iexp_tok(v, (int64_t)s[v] - rmx[v]);
 				pr = e == 0 ? 0
 				            : (dsmall[v] ? div_q15_small(e, ddn[v], dinv[v]) : (int32_t)div_rcp(e << 15, denom[v], dinv[v], 32768));
 			}
