@@ -193,11 +193,13 @@ def extras(hip, model, pool, cfg, sm, rng, args, line):
     ad = model.adapter(blob)
     B = args.batch
     seqs = [pool.seq() for _ in range(B)]
-    for s, p in zip(seqs, [rng.integers(0, cfg.vocab, size=args.prompt) for _ in range(B)]):
+    c3_prompts = [rng.integers(0, cfg.vocab, size=args.prompt) for _ in range(B)]
+    for s, p in zip(seqs, c3_prompts):
         s.set_adapter(ad)
         s.prefill(p)
+    c3_tokens = []  # sequence 0's first calls, checked against the CPU reference with the same adapter
     for _ in range(3):
-        model.decode_step(seqs, cfg.layers)
+        c3_tokens.append(model.decode_step(seqs, cfg.layers)[0])
     hip.lib.sslm_hip_synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
@@ -205,6 +207,7 @@ def extras(hip, model, pool, cfg, sm, rng, args, line):
     hip.lib.sslm_hip_synchronize()
     dt = time.perf_counter() - t0
     out["config3_lora_decode_tok_s"] = round(B * args.steps / dt, 2)
+    out["_config3_check"] = (blob, c3_prompts[0], c3_tokens)
     print(f"[bench] config3 (LoRA r16 q,v): {out['config3_lora_decode_tok_s']} tok/s", file=sys.stderr, flush=True)
     for s in seqs:
         s.release()
@@ -264,7 +267,7 @@ def config4(hip, args):
 TIERS = {0: "SSE2", 1: "AVX2", 2: "AVX-512"}
 
 
-def cpu_baseline(image, cfg, prompts, gpu_calls, calls):
+def cpu_baseline(image, cfg, prompts, gpu_calls, calls, lora_check=None):
     """The reference compiled from its own sources (oracle/_ref) on this host's cores, same
     artifact and prompts: (i) one sequence on one core, (ii) P sequences on P cores (one thread
     per sequence; the reference's forward is single-threaded per sequence), each prefilled with
@@ -296,6 +299,18 @@ def cpu_baseline(image, cfg, prompts, gpu_calls, calls):
     one_toks, one_dt = run(1)
     p_toks, p_dt = run(P)
     exact = all(p_toks[i] == [c[i] for c in gpu_calls[:calls]] for i in range(P)) and one_toks[0] == p_toks[0]
+    lora_exact = None
+    if lora_check is not None:  # configuration 3: the same adapter blob, prompt and calls on the reference
+        blob, prompt, gpu_toks = lora_check
+        rad = rmodel.adapter(blob)
+        pool = rmodel.pool(1)
+        rs = pool.seq()
+        rs.set_adapter(rad)
+        rs.prefill(prompt)
+        lora_exact = [rmodel.decode_step([rs], L)[0] for _ in range(len(gpu_toks))] == list(gpu_toks)
+        rs.release()
+        pool.close()
+        rad.release()
     rmodel.close()
     out = {"value": round(P * calls / p_dt, 3), "unit": "tok/s", "cores": P, "kind": "reference",
            "sample": f"{P} sequences on {P} threads x {calls} decode calls (28 layers + LM head) after "
@@ -305,6 +320,8 @@ def cpu_baseline(image, cfg, prompts, gpu_calls, calls):
            "cpu_model": cpu_model()}
     print(f"[bench] CPU reference ({tier}): 1 core {out['one_core_tok_s']} tok/s, {P} cores {out['value']} tok/s, "
           f"tokens equal: {exact} ({time.time() - t_all:.1f}s)", file=sys.stderr, flush=True)
+    if lora_exact is not None:
+        out["config3_lora_tokens_equal"] = lora_exact
     return out, exact
 
 
@@ -516,7 +533,11 @@ def main():
 
     if args.phase in ("all", "decode") and not args.no_cpu and os.path.exists(
             os.path.join(ROOT, "oracle", "_ref", "libsuperslm_ref.so")):
-        line["cpu_baseline"], line["bit_exact_vs_cpu"] = cpu_baseline(image, cfg, prompts, gpu_calls, args.cpu_calls)
+        line["cpu_baseline"], line["bit_exact_vs_cpu"] = cpu_baseline(image, cfg, prompts, gpu_calls, args.cpu_calls,
+                                                                      line.get("_config3_check"))
+        if "config3_lora_tokens_equal" in line["cpu_baseline"]:
+            line["config3_bit_exact_vs_cpu"] = line["cpu_baseline"].pop("config3_lora_tokens_equal")
+    line.pop("_config3_check", None)
     for s in seqs:
         s.release()
     pool.close()
