@@ -416,10 +416,12 @@ __global__ __launch_bounds__(64 * kGemvWaves) void k_gemv(GemmArgs g, int cps) {
 // tiles blockIdx.x, + gridDim.x, ...; wave w keeps its K chunks (w + 4 i) of the 16 activation
 // rows in registers for the whole launch and loads the next tile's weight chunks (and fold
 // parameters) while it multiplies the current tile's, two register sets alternating; the four
-// partial sums meet in a double-buffered LDS slot and one wave, rotating per tile, applies the
-// epilogue of k_gemv (WSC1 fold, 16-lane tile maximum, stores).  Against one block per tile
-// pair, whose load -> reduce -> epilogue runs once per block with nothing behind it: gate|up at
-// 16 tokens with HBM-cold weights 11.5 -> 9 us.
+// partial sums meet in a double-buffered LDS slot and every wave applies the epilogue of k_gemv
+// (WSC1 fold, 16-lane tile maximum, stores) to a quarter of the tile, one token row of each
+// group of four per wave (one wave per tile, rotating, held the other three at the next
+// barrier: in-step gate|up 9.9 -> 9.1 us).  Against one block per tile pair, whose load ->
+// reduce -> epilogue runs once per block with nothing behind it: gate|up at 16 tokens with
+// HBM-cold weights 11.5 -> 9 us.
 // ------------------------------------------------------------------------------------------
 // segment of the 16-column tile starting at column c0 (bounds are multiples of 16), with
 // constant indices so the fields stay scalar kernel-argument loads
@@ -485,38 +487,24 @@ __global__ __launch_bounds__(256) void k_gemv_p(GemmArgs g) {
 			red[it & 1][wave][mb][lane] = acc[mb];
 		}
 		__syncthreads();
-		if (wave != (it & 3)) return;
+		// every wave takes a quarter of the epilogue: row v = wave of each 4-token group, one value
+		// per lane, so no wave carries a whole tile's epilogue into the next tile's barrier
 		const SegView sg = seg_view(e, tile_segment(e, tile * 16));
-		const int j = tile * 16 + ri, jj = j - sg.n_begin;
+		const int j = tile * 16 + ri, jj = j - sg.n_begin, v = wave;
 #pragma unroll
 		for (int mb = 0; mb < MB; ++mb) {
-			v4i tot = red[it & 1][0][mb][lane];
+			int32_t tot = 0;
 #pragma unroll
-			for (int w = 1; w < kGemvWaves; ++w) {
-				const v4i y = red[it & 1][w][mb][lane];
-				tot[0] += y[0];
-				tot[1] += y[1];
-				tot[2] += y[2];
-				tot[3] += y[3];
+			for (int w = 0; w < kGemvWaves; ++w) tot += ((const int32_t*)&red[it & 1][w][mb][lane])[v];
+			const int tk = mb * 16 + grp * 4 + v;
+			const bool live = tk < g.M && j < g.N;
+			const int64_t val = apply_fold((int64_t)tot, cur.f0, cur.f1, cur.f2);
+			const uint32_t mabs = dpp_max16(live && sg.mode == kSegFunnel ? sat_abs_u32(val) : 0u);  // tile max
+			if (live) {
+				if (sg.mode == kSegWide) ((int64_t*)sg.out)[(size_t)tk * sg.ld_out + jj] = val;
+				else ((int32_t*)sg.out)[(size_t)tk * sg.ld_out + jj] = sat_i32(val);
 			}
-			const int t0 = mb * 16 + grp * 4;
-			int64_t val[4];
-			uint32_t mabs[4];
-#pragma unroll
-			for (int v = 0; v < 4; ++v) {
-				const bool live = t0 + v < g.M && j < g.N;
-				val[v] = apply_fold((int64_t)tot[v], cur.f0, cur.f1, cur.f2);
-				mabs[v] = dpp_max16(live && sg.mode == kSegFunnel ? sat_abs_u32(val[v]) : 0u);  // tile max
-			}
-#pragma unroll
-			for (int v = 0; v < 4; ++v) {
-				if (t0 + v < g.M && j < g.N) {
-					if (sg.mode == kSegWide) ((int64_t*)sg.out)[(size_t)(t0 + v) * sg.ld_out + jj] = val[v];
-					else ((int32_t*)sg.out)[(size_t)(t0 + v) * sg.ld_out + jj] = sat_i32(val[v]);
-				}
-				if (sg.mode == kSegFunnel && sg.maxpart && ri == 0 && t0 + v < g.M)
-					sg.maxpart[(size_t)tile * kPartLd + t0 + v] = mabs[v];
-			}
+			if (sg.mode == kSegFunnel && sg.maxpart && ri == 0 && tk < g.M) sg.maxpart[(size_t)tile * kPartLd + tk] = mabs;
 		}
 	};
 	Tile t0buf, t1buf;
