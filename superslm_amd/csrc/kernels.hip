@@ -114,9 +114,22 @@ __device__ __forceinline__ int64_t lora_delta_v(const int8_t* lora_b, const int8
 // Called out of line: adapters are optional, and inlined into an epilogue the delta costs the
 // common path registers (the decode GEMV must stay within 128 VGPRs for 4 waves per SIMD) and,
 // unrolled per element, code size in the row kernels.
+// A leaf function (its byte loop inline, no further call): a non-leaf callee saves its return
+// address in scratch memory, and any private segment on a kernel costs every dispatch of it
+// about 0.5 us of launch time on MI355X, taken or not.
 __device__ __attribute__((noinline)) int64_t lora_delta_cold(const int8_t* lora_b, const int8_t* lora_u,
                                                              const int32_t* dfold, int rank, int t, int jj) {
-	return lora_delta_v(lora_b, lora_u, dfold, rank, t, jj);
+	const int8_t* br = lora_b + (size_t)jj * rank;
+	const int8_t* ur = lora_u + (size_t)t * kMaxRank;
+	int32_t d = 0;
+	if ((rank & 3) == 0) {
+		for (int r = 0; r < rank; r += 4)
+			d = __builtin_amdgcn_sdot4(*(const int32_t*)(br + r), *(const int32_t*)(ur + r), d, false);
+	} else {
+		for (int r = 0; r < rank; ++r) d += (int32_t)br[r] * (int32_t)ur[r];
+	}
+	const int32_t* df = dfold + 3 * jj;
+	return apply_amp_fold((int64_t)d, df[0], df[1], df[2]);
 }
 
 __device__ __forceinline__ int64_t lora_delta(const Segment& sg, int rank, int t, int jj) {
@@ -3113,6 +3126,23 @@ PrefillPlan prefill_plan(int M, int N, int K, bool split_ok) {
 		p.kspan = K;
 		p.blocks = tiles;
 		return p;
+	}
+	// A long-K shape of few 256-row tiles (the down projection at 512 tokens: 24 tiles) takes
+	// 128-row tiles when they still fill the chip in one round with at least two K splits: 48
+	// tiles x 5 splits = 240 blocks of 14 steps against 24 x 8 = 192 blocks of 9 steps, and 5
+	// raw planes for the consumer to add instead of 8 (1.5B prefill GEMM pass 1748 -> 1708 us).
+	if (split_ok && tiles < kPrefillTargetBlocks && M >= 256) {
+		const int t128 = ((M + 127) / 128) * ((N + kPBN - 1) / kPBN);
+		const int s128 = std::min({kPrefillTargetBlocks / t128, steps / 2, kMaxRawSplits});
+		if (s128 >= 2) {
+			p.bm = 128;
+			p.splits = s128;
+			const int sp = (steps + p.splits - 1) / p.splits;
+			p.kspan = sp * kPBK;
+			p.splits = (K + p.kspan - 1) / p.kspan;
+			p.blocks = t128;
+			return p;
+		}
 	}
 	if (split_ok && tiles < kPrefillTargetBlocks)
 		p.splits = std::max(1, std::min({(kPrefillTargetBlocks + tiles - 1) / tiles, steps / 2, kMaxRawSplits}));
