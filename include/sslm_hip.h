@@ -253,7 +253,9 @@ sslm_status sslm_hip_gemm_i32(const int8_t* a, const int8_t* w, int32_t m, int32
  * one GPU share that array, so calls that overlap on one GPU (other streams, other threads) race;
  * each call writes every scratch element it reads.  Requires 1 <= m <= SSLM_HIP_NOALLOC_MAX_M,
  * 16 <= n <= SSLM_HIP_NOALLOC_MAX_N, n and k multiples of 16 (else SSLM_INVALID_ARGUMENT, with a
- * message on stderr, and nothing launched). */
+ * message on stderr, and nothing launched).  A launch that fails after the first one was enqueued
+ * returns SSLM_HIP_LAUNCH_FAILED (the outputs are then undefined). */
+#define SSLM_HIP_LAUNCH_FAILED ((sslm_status)SSLM_STATUS_NEXT_FREE)
 #define SSLM_HIP_NOALLOC_MAX_M 128
 #define SSLM_HIP_NOALLOC_MAX_N 8192
 size_t sslm_hip_noalloc_scratch_bytes(void);

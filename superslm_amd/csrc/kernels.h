@@ -116,6 +116,13 @@ __device__ __forceinline__ void report_head(int32_t* head_status, int32_t slot, 
 namespace sslm_launch {
 using namespace sslm;
 
+// Thrown by a launch wrapper, before anything is enqueued, when a launch does not fit any kernel
+// it has (a GEMM without a complete output, a row no instance covers).  Such a launch is a bug of
+// the caller; the runtime's entry points catch it and return a status instead of launching.
+struct LaunchRefused {
+	const char* what;
+};
+
 void gemm(const GemmArgs& g, hipStream_t s);
 // launch shape of the decode GEMV (M <= 64, K % 128 == 0); `split_ok`: the caller consumes raw
 // split-K partials; `raw_or_argmax`: no projection epilogue in the kernel (raw accumulators or

@@ -3024,7 +3024,7 @@ static void check_gemm_outputs(const GemmArgs& g) {
 	}
 	if (!ok) {
 		fprintf(stderr, "sslm_hip: GEMM launch (%d x %d x %d) without a complete output\n", g.M, g.N, g.K);
-		abort();
+		throw LaunchRefused{"gemm: incomplete output"};
 	}
 }
 
@@ -3177,7 +3177,7 @@ static int row_ept(int n, int bs) { return (n + bs - 1) / bs; }
 // test entry points); a row no instance covers is a bug, not a case to skip silently.
 [[noreturn]] static void no_instance(const char* kernel, int n) {
 	fprintf(stderr, "sslm_hip: no %s instance for a row of %d elements\n", kernel, n);
-	abort();
+	throw LaunchRefused{kernel};
 }
 
 void rmsnorm(const RowNormArgs& a, int M, int H, const TokenInfo* tok, int32_t* status, int32_t layer,

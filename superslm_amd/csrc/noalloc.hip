@@ -82,12 +82,14 @@ sslm_status sslm_hip_gemm_requant_noalloc(const int8_t* a, const int8_t* w, cons
 	}
 	unsigned char* base = scratch_ptr();
 	if (!base) return SSLM_INVALID_ARGUMENT;
+	(void)hipGetLastError();  // an error left by an unrelated earlier call is not this call's
 	int32_t* f = (int32_t*)(base + kOffF);
 	uint32_t* mx = (uint32_t*)(base + kOffMx);
 	TokenInfo* tok = (TokenInfo*)(base + kOffTok);
 	Scale* in = (Scale*)(base + kOffIn);
 
 	hipLaunchKernelGGL(k_noalloc_setup, dim3((m + 255) / 256), dim3(256), 0, stream, tok, in, out_status, m, in_m, in_e);
+	if (hipGetLastError() != hipSuccess) return SSLM_HIP_LAUNCH_FAILED;
 	GemmArgs g{};
 	g.a = a;
 	g.w = w;
@@ -106,7 +108,12 @@ sslm_status sslm_hip_gemm_requant_noalloc(const int8_t* a, const int8_t* w, cons
 	sg.ld_out = n;
 	sg.maxpart = mx;
 	sg.fold = fold;
-	sslm_launch::gemm(g, stream);
+	try {
+		sslm_launch::gemm(g, stream);
+	} catch (const sslm_launch::LaunchRefused&) {
+		return SSLM_HIP_LAUNCH_FAILED;
+	}
+	if (hipGetLastError() != hipSuccess) return SSLM_HIP_LAUNCH_FAILED;
 	sslm_launch::FunnelArgs fa{};
 	fa.M = m;
 	fa.N = n;
@@ -121,8 +128,12 @@ sslm_status sslm_hip_gemm_requant_noalloc(const int8_t* a, const int8_t* w, cons
 	fa.out_scale = (Scale*)out_me;
 	fa.layer = 0;
 	fa.status = out_status;
-	sslm_launch::funnel(fa, stream);
-	if (hipGetLastError() != hipSuccess) return SSLM_INVALID_ARGUMENT;
+	try {
+		sslm_launch::funnel(fa, stream);
+	} catch (const sslm_launch::LaunchRefused&) {
+		return SSLM_HIP_LAUNCH_FAILED;
+	}
+	if (hipGetLastError() != hipSuccess) return SSLM_HIP_LAUNCH_FAILED;
 	return SSLM_OK;
 }
 

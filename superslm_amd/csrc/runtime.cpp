@@ -1105,8 +1105,11 @@ sslm_status map_forward_status(int32_t word) {
 	return SSLM_ARTIFACT_REJECTED;  // src/sslm_abi.cpp:1352-1360
 }
 
+// Runs an entry point's body, turning HIP errors and refused launches into statuses.  `refused`:
+// the status of a launch refused by a launch wrapper (SSLM_INVALID_ARGUMENT at the boundary;
+// the forward verbs pass SSLM_NUMERIC_STEP_REFUSED and leave every sequence's state as it was).
 template <typename F>
-sslm_status guarded(F&& f) {
+sslm_status guarded(F&& f, sslm_status refused = SSLM_INVALID_ARGUMENT) {
 	try {
 		return f();
 	} catch (const HipError& e) {
@@ -1114,6 +1117,12 @@ sslm_status guarded(F&& f) {
 		return e.e == hipErrorOutOfMemory ? SSLM_ALLOCATION_FAILED : SSLM_INVALID_ARGUMENT;
 	} catch (const std::bad_alloc&) {
 		return SSLM_ALLOCATION_FAILED;
+	} catch (const sslm_launch::LaunchRefused& e) {
+		// nothing of the refused launch was enqueued; let what was enqueued before it finish so
+		// no kernel still runs on buffers the caller may free after this status
+		fprintf(stderr, "sslm_hip: launch refused (%s)\n", e.what);
+		(void)hipDeviceSynchronize();
+		return refused;
 	}
 }
 
@@ -1602,10 +1611,17 @@ sslm_status prefill_tokens(sslm_model m, sslm_seq s, const int32_t* tokens, int 
 		const std::string key = "p|" + std::to_string(T) + "|" + std::to_string((uintptr_t)s->adapter) + "|" +
 		                        std::to_string((uintptr_t)m->pool_dev) + "|" + std::to_string(w.gen);
 		// a span shape is captured the second time it is seen: one-off shapes launch directly
-		if (graphs_enabled() && !prof_enabled() && m->graph_seen[key]++ > 0)
-			ck(hipGraphLaunch(graph_of(m, key, w.stream, body), w.stream));
-		else
-			body();
+		try {
+			if (graphs_enabled() && !prof_enabled() && m->graph_seen[key]++ > 0)
+				ck(hipGraphLaunch(graph_of(m, key, w.stream, body), w.stream));
+			else
+				body();
+		} catch (const sslm_launch::LaunchRefused&) {
+			// nothing is committed; clear what the enqueued kernels reported for the slot
+			ck(hipStreamSynchronize(w.stream));
+			ck(hipMemset(m->status + s->slot, 0, 4));
+			throw;
+		}
 		done += T;
 		last_T = T;
 	}
@@ -1901,7 +1917,7 @@ sslm_status sslm_prefill(sslm_model model, sslm_seq seq, const int32_t* tokens, 
 			seq->ready_for_logits = true;  // src/sslm_abi.cpp:1969-1972
 		}
 		return stop;
-	});
+	}, SSLM_NUMERIC_STEP_REFUSED);
 }
 
 sslm_launch::SlotCopyArgs slot_copy_args(sslm_model m, const TokenInfo* tok, int l0, int l1) {
@@ -2056,6 +2072,10 @@ static sslm_status decode_batch(sslm_model m, sslm_seq* seqs, int32_t n, const s
 		ck(hipMemcpyAsync(w.slot_idx, slots.data(), M * 4, hipMemcpyHostToDevice, s));
 		if (un.l0 == 0) ck(hipMemcpyAsync(w.tok_ids, ids.data(), M * 4, hipMemcpyHostToDevice, s));
 	};
+	// units whose snapshot was enqueued for execution (not merely recorded into a graph that a
+	// refused launch then discarded): what a refused launch must restore
+	std::vector<char> snapped(units.size(), 0);
+	bool capturing = false;
 	auto launch_unit = [&](size_t u) {
 		const Unit& un = units[u];
 		Track& w = m->tracks[u % ntr];
@@ -2063,6 +2083,7 @@ static sslm_status decode_batch(sslm_model m, sslm_seq* seqs, int32_t n, const s
 		// snapshot of the rows this unit changes, restored if an earlier sequence of the call refuses
 		sslm_launch::slot_state_copy(slot_copy_args(m, w.tok, (int)un.l0, (int)un.l1), M, false, w.stream);
 		ck(hipGetLastError());
+		if (!capturing) snapped[u] = 1;
 		if (un.l0 == 0) {  // embed the pending token (src/sslm_abi.cpp:2237-2249)
 			ProfScope p(w.stream, kProfRow, 0, 0);
 			sslm_launch::embed(w.tok_ids, M, m->embed, m->H, m->V, m->embed_site, m->stream_codes, w.slot_idx,
@@ -2114,70 +2135,94 @@ static sslm_status decode_batch(sslm_model m, sslm_seq* seqs, int32_t n, const s
 	// every sequence of one call shares the pool of the first (checked by the caller)
 	m->pool_dev = seqs[0]->pool->dev;
 	std::vector<int32_t> toks(lg.size());
-	if (one_per_track) {
-		for (size_t u = 0; u < units.size(); ++u) stage_unit(u, t0.stream);
-		if (!lg.empty()) stage_logits(0, (int)lg.size(), t0.stream);
-		// Each unit is its own captured graph on its own track's stream (a graph runs its nodes
-		// in order on the stream it is launched on, so one graph per track keeps the tracks
-		// concurrent), forked from and joined back into track 0; the head is one more graph.
-		const size_t nt = std::min(ntr, units.size());
-		ck(hipEventRecord(t0.fork, t0.stream));
-		for (size_t k = 1; k < nt; ++k) ck(hipStreamWaitEvent(m->tracks[k].stream, t0.fork, 0));
-		for (size_t u = 0; u < units.size(); ++u) {
-			Track& w = m->tracks[u % ntr];
-			if (use_graph) {
-				const Unit& un = units[u];
-				const std::string key = "u" + std::to_string(u % ntr) + "|" + std::to_string(un.idx.size()) + "|" +
-				                        std::to_string(un.l0) + "|" + std::to_string(un.l1) + "|" +
-				                        std::to_string((uintptr_t)un.ad) + "|" + std::to_string((uintptr_t)m->pool_dev);
-				ck(hipGraphLaunch(graph_of(m, key, w.stream, [&] { launch_unit(u); }), w.stream));
-			} else {
+	try {
+		if (one_per_track) {
+			for (size_t u = 0; u < units.size(); ++u) stage_unit(u, t0.stream);
+			if (!lg.empty()) stage_logits(0, (int)lg.size(), t0.stream);
+			// Each unit is its own captured graph on its own track's stream (a graph runs its nodes
+			// in order on the stream it is launched on, so one graph per track keeps the tracks
+			// concurrent), forked from and joined back into track 0; the head is one more graph.
+			const size_t nt = std::min(ntr, units.size());
+			ck(hipEventRecord(t0.fork, t0.stream));
+			for (size_t k = 1; k < nt; ++k) ck(hipStreamWaitEvent(m->tracks[k].stream, t0.fork, 0));
+			for (size_t u = 0; u < units.size(); ++u) {
+				Track& w = m->tracks[u % ntr];
+				if (use_graph) {
+					const Unit& un = units[u];
+					const std::string key = "u" + std::to_string(u % ntr) + "|" + std::to_string(un.idx.size()) + "|" +
+					                        std::to_string(un.l0) + "|" + std::to_string(un.l1) + "|" +
+					                        std::to_string((uintptr_t)un.ad) + "|" + std::to_string((uintptr_t)m->pool_dev);
+					capturing = true;
+					const hipGraphExec_t ge = graph_of(m, key, w.stream, [&] { launch_unit(u); });
+					capturing = false;
+					ck(hipGraphLaunch(ge, w.stream));
+					snapped[u] = 1;
+				} else {
+					launch_unit(u);
+				}
+			}
+			for (size_t k = 1; k < nt; ++k) {
+				ck(hipEventRecord(m->tracks[k].done, m->tracks[k].stream));
+				ck(hipStreamWaitEvent(t0.stream, m->tracks[k].done, 0));
+			}
+			if (!lg.empty()) {
+				const int M = (int)lg.size();
+				if (use_graph)
+					ck(hipGraphLaunch(graph_of(m, "lg|" + std::to_string(M) + (rows_needed ? "|r" : "") +
+					                                  (cands ? "|c" + std::to_string(params.top_k) : "") + (masked ? "|m" : ""),
+					                           t0.stream,
+					                           [&] { launch_logits(M); }),
+					                  t0.stream));
+				else launch_logits(M);
+			}
+			if (!lg.empty()) ck(hipMemcpyAsync(toks.data(), t0.out_tokens, lg.size() * 4, hipMemcpyDeviceToHost, t0.stream));
+			if (rows_needed && !lg.empty())
+				ck(hipMemcpyAsync(rows.data(), m->logits, rows.size() * 4, hipMemcpyDeviceToHost, t0.stream));
+			if (cands && !lg.empty())
+				ck(hipMemcpyAsync(cand.data(), m->topk, cand.size() * sizeof(int2), hipMemcpyDeviceToHost, t0.stream));
+		} else {
+			std::vector<bool> used(ntr, false);
+			for (size_t u = 0; u < units.size(); ++u) {
+				stage_unit(u, m->tracks[u % ntr].stream);
+				used[u % ntr] = true;
 				launch_unit(u);
 			}
+			for (size_t k = 1; k < ntr; ++k) {
+				if (!used[k]) continue;
+				ck(hipEventRecord(m->tracks[k].done, m->tracks[k].stream));
+				ck(hipStreamWaitEvent(t0.stream, m->tracks[k].done, 0));
+			}
+			for (size_t b = 0; b < lg.size(); b += kMaxTokens) {
+				const int M = (int)std::min(lg.size() - b, (size_t)kMaxTokens);
+				stage_logits(b, M, t0.stream);
+				launch_logits(M);
+				ck(hipMemcpyAsync(toks.data() + b, t0.out_tokens, M * 4, hipMemcpyDeviceToHost, t0.stream));
+				if (rows_needed)
+					ck(hipMemcpyAsync(rows.data() + b * (size_t)m->V, m->logits, (size_t)M * m->V * 4, hipMemcpyDeviceToHost,
+					                  t0.stream));
+				if (cands)
+					ck(hipMemcpyAsync(cand.data() + b * (size_t)params.top_k, m->topk, (size_t)M * params.top_k * sizeof(int2),
+					                  hipMemcpyDeviceToHost, t0.stream));
+			}
 		}
-		for (size_t k = 1; k < nt; ++k) {
-			ck(hipEventRecord(m->tracks[k].done, m->tracks[k].stream));
-			ck(hipStreamWaitEvent(t0.stream, m->tracks[k].done, 0));
-		}
-		if (!lg.empty()) {
-			const int M = (int)lg.size();
-			if (use_graph)
-				ck(hipGraphLaunch(graph_of(m, "lg|" + std::to_string(M) + (rows_needed ? "|r" : "") +
-				                                  (cands ? "|c" + std::to_string(params.top_k) : "") + (masked ? "|m" : ""),
-				                           t0.stream,
-				                           [&] { launch_logits(M); }),
-				                  t0.stream));
-			else launch_logits(M);
-		}
-		if (!lg.empty()) ck(hipMemcpyAsync(toks.data(), t0.out_tokens, lg.size() * 4, hipMemcpyDeviceToHost, t0.stream));
-		if (rows_needed && !lg.empty())
-			ck(hipMemcpyAsync(rows.data(), m->logits, rows.size() * 4, hipMemcpyDeviceToHost, t0.stream));
-		if (cands && !lg.empty())
-			ck(hipMemcpyAsync(cand.data(), m->topk, cand.size() * sizeof(int2), hipMemcpyDeviceToHost, t0.stream));
-	} else {
-		std::vector<bool> used(ntr, false);
+	} catch (const sslm_launch::LaunchRefused&) {
+		// A launch wrapper refused a launch before enqueuing it.  Let what was enqueued finish,
+		// put back the rows of every unit that ran (or began to run) from its snapshot and clear
+		// the call's status words: the host state of every sequence was not advanced, so the call
+		// leaves the sequences as it found them.
+		ck(hipDeviceSynchronize());
 		for (size_t u = 0; u < units.size(); ++u) {
-			stage_unit(u, m->tracks[u % ntr].stream);
-			used[u % ntr] = true;
-			launch_unit(u);
+			if (!snapped[u]) continue;
+			std::vector<TokenInfo> back;
+			for (int i : units[u].idx) back.push_back(TokenInfo{seqs[i]->context_length, seqs[i]->slot, (int32_t)seqs[i]->block});
+			ck(hipMemcpy(t0.tok, back.data(), back.size() * sizeof(TokenInfo), hipMemcpyHostToDevice));
+			sslm_launch::slot_state_copy(slot_copy_args(m, t0.tok, (int)units[u].l0, (int)units[u].l1), (int)back.size(),
+			                             true, t0.stream);
+			ck(hipGetLastError());
+			ck(hipStreamSynchronize(t0.stream));
 		}
-		for (size_t k = 1; k < ntr; ++k) {
-			if (!used[k]) continue;
-			ck(hipEventRecord(m->tracks[k].done, m->tracks[k].stream));
-			ck(hipStreamWaitEvent(t0.stream, m->tracks[k].done, 0));
-		}
-		for (size_t b = 0; b < lg.size(); b += kMaxTokens) {
-			const int M = (int)std::min(lg.size() - b, (size_t)kMaxTokens);
-			stage_logits(b, M, t0.stream);
-			launch_logits(M);
-			ck(hipMemcpyAsync(toks.data() + b, t0.out_tokens, M * 4, hipMemcpyDeviceToHost, t0.stream));
-			if (rows_needed)
-				ck(hipMemcpyAsync(rows.data() + b * (size_t)m->V, m->logits, (size_t)M * m->V * 4, hipMemcpyDeviceToHost,
-				                  t0.stream));
-			if (cands)
-				ck(hipMemcpyAsync(cand.data() + b * (size_t)params.top_k, m->topk, (size_t)M * params.top_k * sizeof(int2),
-				                  hipMemcpyDeviceToHost, t0.stream));
-		}
+		for (int i = 0; i < n; ++i) ck(hipMemset(m->status + seqs[i]->slot, 0, 4));
+		throw;
 	}
 	std::vector<int32_t> words(kSlotCapacity);
 	ck(hipMemcpyAsync(words.data(), m->status, kSlotCapacity * 4, hipMemcpyDeviceToHost, t0.stream));
@@ -2189,8 +2234,8 @@ static sslm_status decode_batch(sslm_model m, sslm_seq* seqs, int32_t n, const s
 	// commit (a layer failure leaves it at the failing layer; a head failure after its layers
 	// at layer L with the context advanced), its output entry and every later sequence are left
 	// as they were.  The batch ran every sequence at once, so a later sequence's device stream
-	// row, scale and clamp counter are restored from the snapshot its unit took; its KV rows at
-	// its uncommitted position keep this call's values.  Layer failures carry their layer in the
+	// row, scale and clamp counter, and the K/V rows its unit's layers landed at its position, are
+	// restored from the snapshot its unit took.  Layer failures carry their layer in the
 	// status word, head failures the layer count.
 	std::vector<int> in_lg(n, -1);
 	for (size_t k = 0; k < lg.size(); ++k) in_lg[lg[k]] = (int)k;
@@ -2337,7 +2382,7 @@ static sslm_status decode_impl(sslm_model model, sslm_seq* seqs, int32_t n, cons
 			i = j;
 		}
 		return SSLM_OK;
-	});
+	}, SSLM_NUMERIC_STEP_REFUSED);
 }
 
 // src/sslm_abi.cpp:2436-2449: the v1.1 verb reads only the layer budget (its struct was one
