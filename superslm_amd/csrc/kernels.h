@@ -60,6 +60,9 @@ struct Epilogue {
 struct GemmArgs {
 	const int8_t* a;   // [M, K] activation codes, row stride lda
 	const int8_t* w;   // [N, K] weights
+	// the same weights in the packed decode layout (k_gemv_pk in kernels.hip), or null; decode
+	// GEMVs at M <= 32 read them instead of w
+	const int8_t* wp;
 	int32_t M, N, K, lda;
 	Epilogue epi;
 	// Decode GEMV split-K: with splits > 1 every split stores its raw int32 partial sums to plane
@@ -129,6 +132,13 @@ void gemm(const GemmArgs& g, hipStream_t s);
 // argmax keys)
 GemvPlan gemv_plan(int M, int N, int K, bool split_ok, bool raw_or_argmax = false);
 bool gemv_eligible(int M, int K);
+// Split-K planes a raw decode GEMV writes for a consumer that adds them: the packed kernels' plan
+// when g.wp is set and they take the launch, else gemv_plan's.  1 = a single plane.
+int gemv_raw_splits(const GemmArgs& g);
+// bytes of the packed decode copy of an [N, K] matrix (whole 16-row tiles)
+size_t packed_bytes(int N, int K);
+// writes the packed decode copy of w [N, K] (K % 128 == 0) into wp
+void pack_gemv(const int8_t* w, int N, int K, int8_t* wp, hipStream_t s);
 bool wide_gemm_ok(const GemmArgs& g);  // the prefill launch takes the 256 x 160-tile kernel
 // launch shape of the prefill GEMM; `split_ok` as for gemv_plan
 PrefillPlan prefill_plan(int M, int N, int K, bool split_ok);

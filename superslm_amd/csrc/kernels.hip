@@ -546,7 +546,14 @@ __global__ __launch_bounds__(256) void k_gemv_p(GemmArgs g) {
 // column l % 16).  Measured against k_gemv on the 1.5B decode shapes with every layer's weights
 // streaming from HBM: LM head 59 -> 49 us, down projection (8 planes) 8.4 -> 6.4 us.
 // ------------------------------------------------------------------------------------------
-template <int NCH>
+// lane `lane`'s 16 bytes of chunk 0, half 0 of `tile` in a packed decode copy (k_gemv_pk)
+__device__ __forceinline__ const int8_t* pk_lane(const int8_t* wp, int tile, int C, int lane) {
+	return wp + (size_t)tile * C * 2048 + lane * 16;
+}
+
+// PK: the weights are read from the packed decode copy g.wp (see k_gemv_pk), the activations
+// with its lane -> k map.
+template <int NCH, bool PK>
 __global__ __launch_bounds__(256) void k_gemv_w(GemmArgs g, int cps) {
 	extern __shared__ __attribute__((aligned(16))) int8_t xs[];  // [16][span] activation rows
 	const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
@@ -556,7 +563,10 @@ __global__ __launch_bounds__(256) void k_gemv_w(GemmArgs g, int cps) {
 	const int c_begin = split * cps, c_end = min(C, c_begin + cps);
 	const int span = max(0, c_end - c_begin) * 128;
 	const v4i z = v4i{0, 0, 0, 0};
-	const int8_t* wrow = g.w + (size_t)min(tile * 16 + ri, g.N - 1) * g.K + grp * 32;
+	// chunk c of this lane's weight row: bytes [c * wstep, + 16) and [c * wstep + hoff, + 16)
+	const int8_t* wrow = PK ? pk_lane(g.wp, min(tile, (g.N + 15) / 16 - 1), C, lane)
+	                        : g.w + (size_t)min(tile * 16 + ri, g.N - 1) * g.K + grp * 32;
+	constexpr int wstep = PK ? 2048 : 128, hoff = PK ? 1024 : 16;
 	// the first batch of weights goes out before the activations are staged
 	v4i b[NCH][2];
 	int c0 = c_begin;
@@ -564,8 +574,8 @@ __global__ __launch_bounds__(256) void k_gemv_w(GemmArgs g, int cps) {
 #pragma unroll
 	for (int i = 0; i < NCH; ++i) {
 		const int c = min(c0 + i, c_last);
-		b[i][0] = load16(wrow + (size_t)c * 128);
-		b[i][1] = load16(wrow + (size_t)c * 128 + 16);
+		b[i][0] = load16(wrow + (size_t)c * wstep);
+		b[i][1] = load16(wrow + (size_t)c * wstep + hoff);
 	}
 	{
 		const int vecs = span >> 4;  // 16-byte vectors per row
@@ -577,13 +587,16 @@ __global__ __launch_bounds__(256) void k_gemv_w(GemmArgs g, int cps) {
 	}
 	__syncthreads();
 	v4i acc = z;
-	const int8_t* xrow = xs + ri * span + grp * 32 - c_begin * 128;
+	// activations in the weights' lane -> k map: bytes 128 c + {0, 64} + 16 grp (packed) or
+	// 128 c + 32 grp + {0, 16}
+	constexpr int xoff = PK ? 64 : 16;
+	const int8_t* xrow = xs + ri * span + grp * (PK ? 16 : 32) - c_begin * 128;
 	while (c0 < c_end) {
 #pragma unroll
 		for (int i = 0; i < NCH; ++i) {
 			const int c = c0 + i;
 			if (c < c_end) {
-				const v4i x0 = *(const v4i*)(xrow + c * 128), x1 = *(const v4i*)(xrow + c * 128 + 16);
+				const v4i x0 = *(const v4i*)(xrow + c * 128), x1 = *(const v4i*)(xrow + c * 128 + xoff);
 				acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(x0, b[i][0], acc, 0, 0, 0);
 				acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(x1, b[i][1], acc, 0, 0, 0);
 			}
@@ -593,8 +606,8 @@ __global__ __launch_bounds__(256) void k_gemv_w(GemmArgs g, int cps) {
 #pragma unroll
 		for (int i = 0; i < NCH; ++i) {
 			const int c = min(c0 + i, c_last);
-			b[i][0] = load16(wrow + (size_t)c * 128);
-			b[i][1] = load16(wrow + (size_t)c * 128 + 16);
+			b[i][0] = load16(wrow + (size_t)c * wstep);
+			b[i][1] = load16(wrow + (size_t)c * wstep + hoff);
 		}
 	}
 	if (tile * 16 >= g.N) return;
@@ -620,6 +633,253 @@ __global__ __launch_bounds__(256) void k_gemv_w(GemmArgs g, int cps) {
 			}
 			if (ri == 0 && t0 + v < g.M) e.argmax_key[(size_t)(t0 + v) * e.key_ld + tile] = key;
 		}
+	}
+}
+
+// ------------------------------------------------------------------------------------------
+// Decode GEMVs on the packed weight layout (M <= 32).  Each projection keeps, beside its
+// row-major matrix (read by the prefill GEMMs), a decode copy stored tile-major: for 16-column
+// tile t, 128-byte K chunk c and half h, the 1 KB block at ((t * C + c) * 2 + h) * 1024 holds,
+// for lane l = 16 grp + ri, the 16 bytes W[16 t + ri][128 c + 64 h + 16 grp .. +16) (rows past N
+// zero).  A 16-byte load per lane then reads 1 KB of contiguous memory that is already the weight
+// operand of v_mfma_i32_16x16x64_i8; the activations are read with the same lane -> k map (row ri,
+// bytes 128 c + 64 h + 16 grp), so the integer sums are exact.  Against the row-major layout,
+// where one load instruction touches 16 rows at a 32-byte stride, this cut the weight stream of
+// the 1.5B decode shapes by 10-25 % in a study with 28 rotating weight copies.
+// ------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_pack_gemv(const int8_t* w, int N, int K, int8_t* wp, int64_t units) {
+	const int64_t u = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);  // (tile, c, h) 1 KB block
+	if (u >= units) return;
+	const int lane = threadIdx.x & 63, C = K >> 7;
+	const int h = (int)(u & 1), c = (int)((u >> 1) % C);
+	const int64_t tile = (u >> 1) / C;
+	const int64_t row = tile * 16 + (lane & 15);
+	const v4i z = v4i{0, 0, 0, 0};
+	const v4i v = row < N ? load16(w + row * K + c * 128 + h * 64 + (lane >> 4) * 16) : z;
+	*(v4i*)(wp + u * 1024 + lane * 16) = v;
+}
+
+
+// Projection GEMV: NT tiles per block (tile blockIdx.x + i * gridDim.x), the loop fully unrolled
+// so that the wait counts before each tile's MFMAs are exact: the weights of tile i + 2 are issued
+// as tile i's are consumed, two register sets alternating.  A runtime tile loop put a full drain
+// of the vector-memory counter at its back edge (a store-address register reused by a loop-carried
+// copy), and one 4-wave block per CU with an even share of tiles is what the memory system rewards:
+// in a study of the 1.5B gate|up shape, 224 blocks x 5 tiles took 6.9 us and 280 x 4 (24 CUs
+// holding two blocks) 9.0 us.  Wave w owns K chunks [w CPW, w CPW + CPW) of every tile and keeps
+// their activation rows in registers for the whole launch; the four partial sums meet in a
+// double-buffered LDS slot, and wave w finishes row w of each 4-token group: raw int32 output, or
+// the projection epilogue of k_gemv (WSC1 fold, LoRA delta, bias reconcile, funnel tile maximum).
+// EPI: kPkRaw (raw int32 output), kPkFunnel (funnel segments without bias or LoRA: fold, tile
+// maximum, stores, in straight-line code) or kPkGeneral (any projection epilogue).
+enum PkEpi { kPkRaw = 0, kPkFunnel = 1, kPkGeneral = 2 };
+
+template <int MB, int NT, int CPW, int EPI>
+__global__ __launch_bounds__(256) void k_gemv_pk(GemmArgs g) {
+	__shared__ v4i red[2][kGemvWaves][MB][64];
+	const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, ri = lane & 15, grp = lane >> 4;
+	const int C = g.K >> 7, T = (g.N + 15) / 16;
+	const v4i z = v4i{0, 0, 0, 0};
+	// the weights of the first two tiles go out first: they need only wp, K and N
+	// a tile's weights, and its column's fold parameters, bias and segment fields, all fetched two
+	// tiles ahead so that no epilogue waits on a load
+	struct Slot {
+		v4i b[CPW][2];
+		int32_t f0, f1, f2;
+		int64_t bias;
+		SegView sg;
+	};
+	Slot S[2];
+	const int8_t* const wp = g.wp;
+	auto load_w = [&](int i, Slot& d) {
+		const int tile = min((int)blockIdx.x + i * (int)gridDim.x, T - 1);
+		const int8_t* tp = pk_lane(wp, tile, C, lane);
+#pragma unroll
+		for (int c2 = 0; c2 < CPW; ++c2) {
+			const int c = min(wave * CPW + c2, C - 1);
+			d.b[c2][0] = load16(tp + (size_t)c * 2048);
+			d.b[c2][1] = load16(tp + (size_t)c * 2048 + 1024);
+		}
+	};
+	load_w(0, S[0]);
+	if (NT > 1) load_w(1, S[1]);
+	v4i x[MB][CPW][2];
+#pragma unroll
+	for (int mb = 0; mb < MB; ++mb) {
+		const int r = mb * 16 + ri;
+		const bool rok = r < g.M;
+		const int8_t* arow = g.a + (size_t)(rok ? r : g.M - 1) * g.lda + grp * 16;
+#pragma unroll
+		for (int i = 0; i < CPW; ++i) {
+			const int c = wave * CPW + i;
+			const bool ok = rok && c < C;
+			const int cc = c < C ? c : C - 1;
+			const v4i a0 = load16(arow + cc * 128), a1 = load16(arow + cc * 128 + 64);
+			x[mb][i][0] = ok ? a0 : z;  // chunks past K multiply clamped weights by zero
+			x[mb][i][1] = ok ? a1 : z;
+		}
+	}
+	const Epilogue& e = g.epi;
+	int32_t* const raw_out = e.raw_out;
+	constexpr bool proj = EPI != kPkRaw;
+	// fold parameters and bias of tile i's column for this lane, issued behind the weights.  The
+	// loads are unconditional, from always-valid addresses (the weights stand in for values a launch
+	// does not use): a load under a branch leaves the wait counts after the join unknown, and the
+	// compiler then drains every outstanding load, the prefetched weights included.
+	auto load_p = [&](int i, Slot& d) {
+		const int tile = min((int)blockIdx.x + i * (int)gridDim.x, T - 1);
+		const SegView sg = seg_view(e, proj ? tile_segment(e, tile * 16) : 0);
+		d.sg = sg;
+		const int jj = min(tile * 16 + ri, g.N - 1) - sg.n_begin;
+		const int32_t* fp = proj ? sg.fold + 3 * jj : (const int32_t*)wp;
+		d.f0 = fp[0];
+		d.f1 = fp[1];
+		d.f2 = fp[2];
+		if (EPI == kPkGeneral) d.bias = *(sg.bias ? sg.bias + jj : (const int64_t*)wp);
+	};
+	load_p(0, S[0]);
+	if (NT > 1) load_p(1, S[1]);
+	// bias reconcile inputs of this lane's epilogue tokens (mb * 16 + 4 grp + wave)
+	int64_t p_rcp[MB], p_ein[MB];
+	const int64_t* const in_recip = e.in_recip;
+	const Scale* const in_scale = e.in_scale;
+#pragma unroll
+	for (int mb = 0; mb < MB; ++mb) {
+		const int tk = min(mb * 16 + grp * 4 + wave, g.M - 1);
+		p_rcp[mb] = EPI == kPkGeneral ? *(in_recip ? in_recip + tk : (const int64_t*)wp) : 0;
+		p_ein[mb] = EPI == kPkGeneral ? (in_scale ? in_scale + tk : (const Scale*)wp)->e : 0;
+	}
+	const int rank = e.rank, layer = e.layer;
+	int32_t* const status = e.status;
+	const TokenInfo* const tok = e.tok;
+#pragma unroll
+	for (int i = 0; i < NT; ++i) {
+		Slot& cur = S[i & 1];
+		v4i acc[MB];
+#pragma unroll
+		for (int mb = 0; mb < MB; ++mb) {
+			acc[mb] = z;
+#pragma unroll
+			for (int c2 = 0; c2 < CPW; ++c2) {
+				acc[mb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(x[mb][c2][0], cur.b[c2][0], acc[mb], 0, 0, 0);
+				acc[mb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(x[mb][c2][1], cur.b[c2][1], acc[mb], 0, 0, 0);
+			}
+		}
+		const int32_t f0 = cur.f0, f1 = cur.f1, f2 = cur.f2;
+		const int64_t bias = cur.bias;
+		const SegView sg = cur.sg;
+		if (i + 2 < NT) {
+			load_w(i + 2, cur);
+			load_p(i + 2, cur);
+		}
+#pragma unroll
+		for (int mb = 0; mb < MB; ++mb) red[i & 1][wave][mb][lane] = acc[mb];
+		__builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes have landed
+		__builtin_amdgcn_s_barrier();
+		const int tile = blockIdx.x + i * gridDim.x;
+		const int j = tile * 16 + ri;
+		const bool col_ok = tile < T && j < g.N;
+		const int jj = j - sg.n_begin;
+#pragma unroll
+		for (int mb = 0; mb < MB; ++mb) {
+			int32_t tot = 0;
+#pragma unroll
+			for (int w = 0; w < kGemvWaves; ++w) tot += ((const int32_t*)&red[i & 1][w][mb][lane])[wave];
+			const int tk = mb * 16 + grp * 4 + wave;
+			const bool live = col_ok && tk < g.M;
+			if (EPI == kPkRaw) {
+				if (live) raw_out[(size_t)tk * g.N + j] = tot;
+				continue;
+			}
+			if (EPI == kPkFunnel) {
+				// |tot| <= 127^2 K < 2^29 for K <= 4096: the bounded fold applies
+				const int32_t val = fold_bounded(tot, fold_consts(f0, f1, f2));
+				const uint32_t mabs = dpp_max16(live ? (uint32_t)(val < 0 ? -val : val) : 0u);
+				if (live) ((int32_t*)sg.out)[(size_t)tk * sg.ld_out + jj] = val;
+				if (ri == 0 && tk < g.M && tile < T) sg.maxpart[(size_t)tile * kPartLd + tk] = mabs;
+				continue;
+			}
+			int64_t val = apply_fold((int64_t)tot, f0, f1, f2);
+			if (sg.lora_b && live) val += lora_delta_cold(sg.lora_b, sg.lora_u, sg.lora_dfold, rank, tk, jj);
+			if (sg.bias) {
+				int64_t term;
+				if (bias_term(bias, p_rcp[mb], p_ein[mb], val, &term)) val += term;
+				else if (live) set_status(status, tok[tk].slot, layer, kBiasReconcileProductOutOfDomain);
+			}
+			const uint32_t mabs = dpp_max16(live && sg.mode == kSegFunnel ? sat_abs_u32(val) : 0u);  // tile max
+			if (live) {
+				if (sg.mode == kSegWide) ((int64_t*)sg.out)[(size_t)tk * sg.ld_out + jj] = val;
+				else ((int32_t*)sg.out)[(size_t)tk * sg.ld_out + jj] = sat_i32(val);
+			}
+			if (sg.mode == kSegFunnel && sg.maxpart && ri == 0 && tk < g.M && tile < T)
+				sg.maxpart[(size_t)tile * kPartLd + tk] = mabs;
+		}
+	}
+}
+
+// Split-K GEMV with raw partial planes (long K: the down projection).  Block (tile group x,
+// split y) covers NTB consecutive tiles and K chunks [y cps, y cps + cps), cps = WPB * CPW; wave w
+// holds chunks y cps + w CPW .. + CPW of the activation rows in registers and multiplies them
+// into all NTB tiles, so each activation byte is read once per tile group rather than once per
+// tile.  The waves' sums meet by integer adds into LDS (exact in any order) and the block stores
+// plane y of [splits][M][N].  1.5B down (K 8960) in a study: 4.7 us against 6.3 us for the
+// wave-per-tile form on row-major weights.
+template <int MB, int NTB, int CPW, int WPB>
+__global__ __launch_bounds__(64 * WPB) void k_gemv_sk(GemmArgs g, int cps) {
+	__shared__ int32_t sum[NTB][MB * 16][16];
+	const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, ri = lane & 15, grp = lane >> 4;
+	const int C = g.K >> 7, T = (g.N + 15) / 16, split = blockIdx.y;
+	const int c0 = split * cps, c1 = min(C, c0 + cps);
+	const int tile0 = blockIdx.x * NTB;
+	for (int i = threadIdx.x; i < NTB * MB * 256; i += 64 * WPB) (&sum[0][0][0])[i] = 0;
+	__syncthreads();
+	const v4i z = v4i{0, 0, 0, 0};
+	v4i b[NTB][CPW][2];
+#pragma unroll
+	for (int t = 0; t < NTB; ++t) {
+		const int8_t* tp = pk_lane(g.wp, min(tile0 + t, T - 1), C, lane);
+#pragma unroll
+		for (int i = 0; i < CPW; ++i) {
+			const int c = min(c0 + wave * CPW + i, c1 - 1);
+			b[t][i][0] = load16(tp + (size_t)c * 2048);
+			b[t][i][1] = load16(tp + (size_t)c * 2048 + 1024);
+		}
+	}
+	v4i x[MB][CPW][2];
+#pragma unroll
+	for (int mb = 0; mb < MB; ++mb) {
+		const int r = mb * 16 + ri;
+		const bool rok = r < g.M;
+		const int8_t* arow = g.a + (size_t)(rok ? r : g.M - 1) * g.lda + grp * 16;
+#pragma unroll
+		for (int i = 0; i < CPW; ++i) {
+			const int c = c0 + wave * CPW + i;
+			const bool ok = rok && c < c1;
+			const int cc = min(c, c1 - 1);
+			const v4i a0 = load16(arow + (size_t)cc * 128), a1 = load16(arow + (size_t)cc * 128 + 64);
+			x[mb][i][0] = ok ? a0 : z;
+			x[mb][i][1] = ok ? a1 : z;
+		}
+	}
+#pragma unroll
+	for (int t = 0; t < NTB; ++t)
+#pragma unroll
+		for (int mb = 0; mb < MB; ++mb) {
+			v4i acc = z;
+#pragma unroll
+			for (int i = 0; i < CPW; ++i) {
+				acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(x[mb][i][0], b[t][i][0], acc, 0, 0, 0);
+				acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(x[mb][i][1], b[t][i][1], acc, 0, 0, 0);
+			}
+#pragma unroll
+			for (int v = 0; v < 4; ++v) atomicAdd(&sum[t][mb * 16 + grp * 4 + v][ri], acc[v]);
+		}
+	__syncthreads();
+	int32_t* plane = g.split_part + (size_t)split * g.M * g.N;
+	for (int i = threadIdx.x; i < NTB * MB * 256; i += 64 * WPB) {
+		const int t = i / (MB * 256), rem = i - t * MB * 256, tk = rem >> 4, col = rem & 15;
+		const int j = (tile0 + t) * 16 + col;
+		if (tk < g.M && j < g.N) plane[(size_t)tk * g.N + j] = sum[t][tk][col];
 	}
 }
 
@@ -3028,9 +3288,150 @@ static void check_gemm_outputs(const GemmArgs& g) {
 	}
 }
 
+// ---- packed decode GEMVs ----
+size_t packed_bytes(int N, int K) { return (size_t)((N + 15) / 16) * 16 * (size_t)K; }
+
+void pack_gemv(const int8_t* w, int N, int K, int8_t* wp, hipStream_t s) {
+	const int64_t units = (int64_t)((N + 15) / 16) * (K / 128) * 2;
+	hipLaunchKernelGGL(k_pack_gemv, dim3((unsigned)((units + 3) / 4)), dim3(256), 0, s, w, N, K, wp, units);
+}
+
+constexpr int kPkMaxM = 32;  // two 16-token row groups
+constexpr int kSkWaves = 8;
+
+// tiles per block of k_gemv_pk: the smallest instance >= an even share over the CUs
+static int pk_nt(int T) {
+	const int need = (T + device_cus() - 1) / device_cus();
+	for (int nt : {1, 2, 3, 5, 10})
+		if (nt >= need) return nt;
+	return 0;
+}
+
+// k_gemv_pk takes a launch without split planes or argmax keys at M <= 32, K <= 4096
+static bool pk_ok(const GemmArgs& g) {
+	return g.wp && g.M >= 1 && g.M <= kPkMaxM && g.K % 128 == 0 && g.K <= 4096 && !g.epi.argmax_key &&
+	       g.splits <= 1 && pk_nt((g.N + 15) / 16) > 0;
+}
+
+struct SkPlan {
+	int ntb, cpw, cps, splits, bx;
+};
+
+// k_gemv_sk: 8 waves of cpw chunks per split (at most kMaxRawSplits planes), ntb tiles per block
+// so that about one block per CU covers the matrix
+static SkPlan sk_plan(int N, int K) {
+	SkPlan p{};
+	const int C = K / 128, T = (N + 15) / 16;
+	p.cpw = (C + kSkWaves * kMaxRawSplits - 1) / (kSkWaves * kMaxRawSplits);
+	if (p.cpw > 4) return SkPlan{};
+	p.cps = kSkWaves * p.cpw;
+	p.splits = (C + p.cps - 1) / p.cps;
+	p.ntb = std::min(8, std::max(1, (T * p.splits + device_cus() - 1) / device_cus()));
+	if (p.ntb == 5) p.ntb = 6;  // instances: 1, 2, 3, 4, 6, 7, 8
+	p.bx = (T + p.ntb - 1) / p.ntb;
+	return p;
+}
+
+static bool sk_ok(int M, int K, const GemmArgs* g) {
+	return M >= 1 && M <= kPkMaxM && K % 128 == 0 && K > 4096 && (!g || g->wp) && sk_plan(1, K).cpw > 0;
+}
+
+int gemv_raw_splits(const GemmArgs& g) {
+	if (g.wp && g.M <= kPkMaxM && !g.epi.argmax_key && gemv_eligible(g.M, g.K)) {
+		if (g.K <= 4096 && pk_nt((g.N + 15) / 16) > 0) return 1;
+		if (sk_ok(g.M, g.K, &g)) return sk_plan(g.N, g.K).splits;
+	}
+	return gemv_plan(g.M, g.N, g.K, true, true).splits;
+}
+
+// chunks per wave of the k_gemv_pk instances: the smallest >= ceil(C / 4) (a larger one loads the
+// last chunk again, an L2 hit, and multiplies it by zero activations)
+static int pk_cpw(int C) {
+	const int need = (C + kGemvWaves - 1) / kGemvWaves;
+	for (int w : {1, 2, 3, 4, 7, 8})
+		if (w >= need) return w;
+	return 0;
+}
+
+// the epilogue form of a k_gemv_pk launch
+static int pk_epi(const GemmArgs& g) {
+	if (g.epi.raw_out) return kPkRaw;
+	for (int i = 0; i < g.epi.nseg; ++i) {
+		const Segment& sg = g.epi.seg[i];
+		if (sg.mode != kSegFunnel || sg.bias || sg.lora_b || !sg.maxpart) return kPkGeneral;
+	}
+	return kPkFunnel;
+}
+
+template <int MB, int NT, int EPI>
+static bool launch_pk_nt(const GemmArgs& g, int grid, int cpw, hipStream_t s) {
+	switch (cpw) {
+#define X(W) \
+	case W: hipLaunchKernelGGL((k_gemv_pk<MB, NT, W, EPI>), dim3(grid), dim3(256), 0, s, g); return true;
+		X(1) X(2) X(3) X(4) X(7) X(8)
+#undef X
+	}
+	return false;
+}
+
+template <int MB, int NT>
+static bool launch_pk_epi(const GemmArgs& g, int grid, int cpw, hipStream_t s) {
+	switch (pk_epi(g)) {
+		case kPkRaw: return launch_pk_nt<MB, NT, kPkRaw>(g, grid, cpw, s);
+		case kPkFunnel: return launch_pk_nt<MB, NT, kPkFunnel>(g, grid, cpw, s);
+		default: return launch_pk_nt<MB, NT, kPkGeneral>(g, grid, cpw, s);
+	}
+}
+
+static bool launch_gemv_pk(const GemmArgs& g, hipStream_t s) {
+	const int T = (g.N + 15) / 16, C = g.K / 128;
+	const int nt = pk_nt(T), grid = (T + nt - 1) / nt, cpw = pk_cpw(C);
+	const bool two = g.M > 16;
+	switch (nt) {
+#define X(N) \
+	case N: return two ? launch_pk_epi<2, N>(g, grid, cpw, s) : launch_pk_epi<1, N>(g, grid, cpw, s);
+		X(1) X(2) X(3) X(5) X(10)
+#undef X
+	}
+	return false;
+}
+
+template <int MB, int NTB>
+static bool launch_sk_ntb(const GemmArgs& g, const SkPlan& p, hipStream_t s) {
+	const dim3 grid(p.bx, p.splits), block(64 * kSkWaves);
+	switch (p.cpw) {
+#define X(W) \
+	case W: hipLaunchKernelGGL((k_gemv_sk<MB, NTB, W, kSkWaves>), grid, block, 0, s, g, p.cps); return true;
+		X(1) X(2) X(3) X(4)
+#undef X
+	}
+	return false;
+}
+
+static bool launch_gemv_sk(const GemmArgs& g, hipStream_t s) {
+	const SkPlan p = sk_plan(g.N, g.K);
+	// the caller sized its planes by gemv_raw_splits(): a launch with another count is refused
+	if (p.cpw == 0 || g.splits != p.splits || !g.split_part) throw LaunchRefused{"gemv_sk: split count"};
+	const bool two = g.M > 16;
+	switch (p.ntb) {
+#define X(N) \
+	case N: return two ? launch_sk_ntb<2, N>(g, p, s) : launch_sk_ntb<1, N>(g, p, s);
+		X(1) X(2) X(3) X(4) X(6) X(7) X(8)
+#undef X
+	}
+	return false;
+}
+
 void gemm(const GemmArgs& g, hipStream_t s) {
 	if (g.M <= 0 || g.N <= 0) return;
 	check_gemm_outputs(g);
+	if (gemv_eligible(g.M, g.K) && g.wp && g.M <= kPkMaxM && !g.epi.argmax_key) {
+		if (g.splits > 1 && sk_ok(g.M, g.K, &g)) {
+			if (launch_gemv_sk(g, s)) return;
+		} else if (pk_ok(g)) {
+			if (launch_gemv_pk(g, s)) return;
+		}
+	}
 	if (gemv_eligible(g.M, g.K)) {
 		// g.splits > 1 only as gemv_plan(M, N, K, true, raw).splits, for which the caller sized
 		// split_part
@@ -3039,11 +3440,20 @@ void gemm(const GemmArgs& g, hipStream_t s) {
 		if (p.wave_tile) {
 			const dim3 grid((g.N + 63) / 64, p.splits), block(256);
 			const size_t lds = (size_t)16 * p.cps * 128;
+			if (g.wp) {
+				switch (p.cpw) {
+					case 2: hipLaunchKernelGGL((k_gemv_w<2, true>), grid, block, lds, s, g, p.cps); break;
+					case 6: hipLaunchKernelGGL((k_gemv_w<6, true>), grid, block, lds, s, g, p.cps); break;
+					case 9: hipLaunchKernelGGL((k_gemv_w<9, true>), grid, block, lds, s, g, p.cps); break;
+					default: hipLaunchKernelGGL((k_gemv_w<3, true>), grid, block, lds, s, g, p.cps); break;
+				}
+				return;
+			}
 			switch (p.cpw) {
-				case 2: hipLaunchKernelGGL((k_gemv_w<2>), grid, block, lds, s, g, p.cps); break;
-				case 6: hipLaunchKernelGGL((k_gemv_w<6>), grid, block, lds, s, g, p.cps); break;
-				case 9: hipLaunchKernelGGL((k_gemv_w<9>), grid, block, lds, s, g, p.cps); break;
-				default: hipLaunchKernelGGL((k_gemv_w<3>), grid, block, lds, s, g, p.cps); break;
+				case 2: hipLaunchKernelGGL((k_gemv_w<2, false>), grid, block, lds, s, g, p.cps); break;
+				case 6: hipLaunchKernelGGL((k_gemv_w<6, false>), grid, block, lds, s, g, p.cps); break;
+				case 9: hipLaunchKernelGGL((k_gemv_w<9, false>), grid, block, lds, s, g, p.cps); break;
+				default: hipLaunchKernelGGL((k_gemv_w<3, false>), grid, block, lds, s, g, p.cps); break;
 			}
 			return;
 		}

@@ -152,6 +152,7 @@ enum ProfClass { kProfGemm = 0, kProfHead = 1, kProfAttn = 2, kProfRow = 3, kPro
 // ------------------------------------------------------------------------------------------
 struct DevLayer {
 	int8_t *w_qkv, *w_o, *w_gu, *w_down;
+	int8_t *p_qkv, *p_o, *p_gu, *p_down;  // packed decode copies (sslm_launch::pack_gemv), or null
 	int32_t *f_qkv, *f_o, *f_gu, *f_down, *ctx_fold;
 	int64_t *b_q, *b_k, *b_v;
 	int32_t *attn_gain, *mlp_gain;
@@ -307,6 +308,7 @@ struct sslm_model_s {
 	std::vector<void*> owned;
 	std::vector<DevLayer> layers;
 	int8_t *embed, *head;
+	int8_t* head_pk = nullptr;  // packed decode copy of the LM head, or null
 	int32_t *final_gain, *silu;
 	int64_t *rope_cos, *rope_sin;
 	Scale embed_site, final_site;
@@ -530,10 +532,12 @@ bool schema_accepting(const SchemaEntry& e, uint32_t state) {  // src/sslm_abi.c
 // ------------------------------------------------------------------------------------------
 // launch helpers
 // ------------------------------------------------------------------------------------------
-GemmArgs gemm_args(sslm_model m, Track& w, const int8_t* a, int M, int lda, const int8_t* wt, int N, int K) {
+GemmArgs gemm_args(sslm_model m, Track& w, const int8_t* a, int M, int lda, const int8_t* wt, int N, int K,
+                   const int8_t* wpk = nullptr) {
 	GemmArgs g{};
 	g.a = a;
 	g.w = wt;
+	g.wp = wpk;
 	g.M = M;
 	g.N = N;
 	g.K = K;
@@ -579,7 +583,7 @@ RawIn split_raw(sslm_model m, Track& w, GemmArgs& g, bool allow_multi, bool allo
 	// stream.  A prefill GEMM keeps its own epilogue unless it splits K.  The flags say which
 	// raw consumers fit their register budget (several planes / one plane).
 	if (sslm_launch::gemv_eligible(g.M, g.K)) {
-		splits = allow_multi ? sslm_launch::gemv_plan(g.M, g.N, g.K, true, true).splits : 1;
+		splits = allow_multi ? sslm_launch::gemv_raw_splits(g) : 1;
 		if (splits == 1 && !allow_single) return r;
 	} else {
 		if (!allow_multi || lora || !sslm_launch::prefill_mfma_k(g.K)) return r;
@@ -644,7 +648,7 @@ struct ProjArgs {
 ProjArgs qkv_args(sslm_model m, Track& w, int l, int M, sslm_adapter ad, bool fused) {
 	const DevLayer& lw = m->layers[l];
 	const int H = m->H, KVH = m->KVH;
-	GemmArgs g = gemm_args(m, w, w.normed, M, H, lw.w_qkv, H + 2 * KVH, H);
+	GemmArgs g = gemm_args(m, w, w.normed, M, H, lw.w_qkv, H + 2 * KVH, H, lw.p_qkv);
 	g.epi.layer = l;
 	g.epi.in_recip = w.normed_recip;
 	g.epi.in_scale = w.normed_scale;
@@ -679,7 +683,7 @@ ProjArgs qkv_args(sslm_model m, Track& w, int l, int M, sslm_adapter ad, bool fu
 ProjArgs o_args(sslm_model m, Track& w, int l, int M, sslm_adapter ad) {
 	const DevLayer& lw = m->layers[l];
 	const int H = m->H;
-	GemmArgs g = gemm_args(m, w, w.ctx, M, H, lw.w_o, H, H);
+	GemmArgs g = gemm_args(m, w, w.ctx, M, H, lw.w_o, H, H, lw.p_o);
 	g.epi.layer = l;
 	g.epi.rank = ad ? (int)ad->rank : 0;
 	g.epi.nseg = 1;
@@ -693,7 +697,7 @@ ProjArgs o_args(sslm_model m, Track& w, int l, int M, sslm_adapter ad) {
 ProjArgs gu_args(sslm_model m, Track& w, int l, int M, sslm_adapter ad) {
 	const DevLayer& lw = m->layers[l];
 	const int H = m->H, I = m->I;
-	GemmArgs g = gemm_args(m, w, w.mlp_normed, M, H, lw.w_gu, 2 * I, H);
+	GemmArgs g = gemm_args(m, w, w.mlp_normed, M, H, lw.w_gu, 2 * I, H, lw.p_gu);
 	g.epi.layer = l;
 	g.epi.rank = ad ? (int)ad->rank : 0;
 	g.epi.nseg = 2;
@@ -709,7 +713,7 @@ ProjArgs gu_args(sslm_model m, Track& w, int l, int M, sslm_adapter ad) {
 ProjArgs down_args(sslm_model m, Track& w, int l, int M, sslm_adapter ad) {
 	const DevLayer& lw = m->layers[l];
 	const int H = m->H, I = m->I;
-	GemmArgs g = gemm_args(m, w, w.act, M, I, lw.w_down, H, I);
+	GemmArgs g = gemm_args(m, w, w.act, M, I, lw.w_down, H, I, lw.p_down);
 	g.epi.layer = l;
 	g.epi.rank = ad ? (int)ad->rank : 0;
 	g.epi.nseg = 1;
@@ -721,7 +725,7 @@ ProjArgs down_args(sslm_model m, Track& w, int l, int M, sslm_adapter ad) {
 }
 
 GemmArgs head_args(sslm_model m, Track& w, int M, const TokenInfo* tok) {
-	GemmArgs g = gemm_args(m, w, w.final_codes, M, m->H, m->head, m->V, m->H);
+	GemmArgs g = gemm_args(m, w, w.final_codes, M, m->H, m->head, m->V, m->H, m->head_pk);
 	g.epi.tok = tok;
 	g.epi.argmax_key = w.argmax_key;
 	g.epi.key_ld = (m->V + 15) / 16;
@@ -1247,6 +1251,8 @@ void free_track_buffers(Track& w) {
 	w.capacity = 0;
 }
 
+bool packed_enabled();
+
 bool build_device_model(sslm_model m, std::string* err) {
 	const Artifact& A = m->art;
 	const ModelConfig& c = A.config;
@@ -1459,6 +1465,26 @@ bool build_device_model(sslm_model m, std::string* err) {
 			memcpy(pages.data() + m->page_off[i], m->schemas[i].pages, (size_t)m->schemas[i].states * m->page_bytes);
 		m->d_pages = dupload(pages, &own);
 	}
+	// Packed decode copies of every projection and the LM head (read by the decode GEMVs at
+	// M <= 32; the row-major matrices stay for the prefill GEMMs).  SSLM_HIP_PACKED=0 keeps the
+	// decode GEMVs on the row-major matrices.
+	if (packed_enabled()) {
+		auto packed = [&](const int8_t* wt, int N, int K) -> int8_t* {
+			if (K % 128) return nullptr;
+			int8_t* p = dalloc<int8_t>(sslm_launch::packed_bytes(N, K), &own);
+			sslm_launch::pack_gemv(wt, N, K, p, nullptr);
+			ck(hipGetLastError());
+			return p;
+		};
+		for (DevLayer& d : m->layers) {
+			d.p_qkv = packed(d.w_qkv, H + 2 * m->KVH, H);
+			d.p_o = packed(d.w_o, H, H);
+			d.p_gu = packed(d.w_gu, 2 * I, H);
+			d.p_down = packed(d.w_down, H, I);
+		}
+		m->head_pk = packed(m->head, m->V, H);
+		ck(hipDeviceSynchronize());
+	}
 	// slots
 	m->stream_codes = dalloc<int8_t>((size_t)kSlotCapacity * H, &own);
 	m->stream_scale = dalloc<Scale>(kSlotCapacity, &own);
@@ -1522,6 +1548,14 @@ void free_model(sslm_model m) {
 }
 
 constexpr size_t kGraphCache = 64;
+
+bool packed_enabled() {
+	static const bool v = [] {
+		const char* e = getenv("SSLM_HIP_PACKED");
+		return !(e && e[0] == '0');
+	}();
+	return v;
+}
 
 bool graphs_enabled() {
 	static const bool v = [] {
