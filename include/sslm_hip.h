@@ -219,6 +219,21 @@ int sslm_hip_profile_shapes(int64_t* keys, double* ms, int64_t* launches, int64_
  * (hidden or intermediate size), `scale_me` its (m, e).  Returns the row's length, or -1. */
 int32_t sslm_hip_debug_site(sslm_model model, int32_t site, int32_t row, int8_t* codes, int64_t* scale_me);
 
+/* Debug capture of every site of every layer (the records of include/superslm/trace_hook.h:36-112
+ * for prefill spans and decode batches alike, which the reference's C ABI never installs).  With
+ * max_tokens > 0, every later launch sequence of at most max_tokens tokens (a prefill span, or a
+ * decode unit) also writes, per layer it runs, each site's codes and carried scale into a
+ * device-side capture area; captured graphs are not used meanwhile.  max_tokens = 0 frees the area
+ * and ends the capture.  Sites, in the order of sslm_hip_debug_site's numbering extended:
+ * 0 attention RMSNorm, 1 attention context funnel, 2 attention residual, 3 MLP RMSNorm, 4 MLP
+ * activation, 5 MLP residual (the committed row), 6 q after RoPE, 7 o_proj funnel, 8 gate funnel,
+ * 9 up funnel, 10 down funnel.  sslm_hip_debug_capture_read returns the row of `token` (launch
+ * order) at (layer, site) of the last launch sequence that ran that layer: its length (hidden or
+ * intermediate size), or -1. */
+sslm_status sslm_hip_debug_capture(sslm_model model, int32_t max_tokens);
+int32_t sslm_hip_debug_capture_read(sslm_model model, int32_t layer, int32_t site, int32_t token, int8_t* codes,
+                                    int64_t* scale_me);
+
 /* The single GEMM + requant of BASELINE configuration 0, on device buffers: int8 A [m, k] x int8
  * W [n, k]^T, int32 accumulate, per-output-row WSC1 fold `fold` [n, 3] (identity, mult, shift),
  * then the per-token dynamic requant funnel with incoming scale `in_m/in_e` and site constant

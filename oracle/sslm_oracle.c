@@ -779,6 +779,7 @@ int or_run_layer_loop(const or_model* m, or_seq* seq, uint32_t layer_budget, int
 		or_gemm_i8(normed, lw->w[OR_V], 1, H, KVH, vacc);
 		if ((st = land_kv(m, lw, l, kacc, vacc, normed, ns, pos, kv, &seq->kv_saturation_count))) break;
 		if ((st = rope_q_and_k(m, l, q, pos, kv, q_rot))) break;
+		trace_site(l, OR_SITE_Q_ROT, q_rot, H, qs);
 		if ((st = attention(m, lw, l, q_rot, qs, pos, kv, ctx, &cs))) break;
 		trace_site(l, OR_SITE_CTX, ctx, H, cs);
 		if ((st = or_project_row(ctx, cs, H, H, lw->w[OR_O], lw->fold[OR_O], NULL, lw->lora[OR_O], r, lw->o_sc, o,
@@ -855,42 +856,65 @@ int or_run_chunk(const or_model* m, int8_t* hid, or_scale* scales, size_t T, int
 			                          BIAS, lw->lora[P], lw->lora_rank, SITE, (OUT) + t * (NOUT), &(OSC)[t]); \
 	} while (0)
 
+/* every token's row of one site, in position order */
+#define TRACE_ROWS(SITE, CODES, N, SC)                                                \
+	do {                                                                              \
+		for (size_t t = 0; t < T && !st; ++t) trace_site(l, SITE, (CODES) + t * (N), N, (SC)[t]); \
+	} while (0)
+
 	for (uint32_t l = 0; l < m->layers && !st; ++l) {
 		const or_layer* lw = &m->layer[l];
 		for (size_t t = 0; t < T && !st; ++t)
 			st = or_rmsnorm_site(hid + t * H, lw->attn_gain, H, lw->attn_norm_sc, normed + t * H, &ns[t]);
 		if (st) break;
+		TRACE_ROWS(OR_SITE_ATTN_NORM, normed, H, ns);
 		BATCHED(normed, ns, H, H, OR_Q, lw->bias[0], lw->q_sc, q, qs);
 		if (st) break;
+		TRACE_ROWS(OR_SITE_Q, q, H, qs);
 		or_gemm_i8(normed, lw->w[OR_K], T, H, KVH, kacc);
 		or_gemm_i8(normed, lw->w[OR_V], T, H, KVH, vacc);
 		for (size_t t = 0; t < T && !st; ++t) {
 			int64_t pos = ctx_start + (int64_t)t;
 			st = land_kv(m, lw, l, kacc + t * KVH, vacc + t * KVH, normed + t * H, ns[t], pos, kv, sat);
 			if (!st) st = rope_q_and_k(m, l, q + t * H, pos, kv, q_rot);
+			if (!st) trace_site(l, OR_SITE_Q_ROT, q_rot, H, qs[t]);
 			if (!st) st = attention(m, lw, l, q_rot, qs[t], pos, kv, ctx + t * H, &cs[t]);
 		}
 		if (st) break;
+		TRACE_ROWS(OR_SITE_CTX, ctx, H, cs);
 		BATCHED(ctx, cs, H, H, OR_O, NULL, lw->o_sc, o, os);
+		if (st) break;
+		TRACE_ROWS(OR_SITE_O, o, H, os);
 		for (size_t t = 0; t < T && !st; ++t)
 			st = or_residual_site(o + t * H, os[t], hid + t * H, scales[t], H, lw->attn_res_sc, as_c + t * H, &ass[t]);
+		if (st) break;
+		TRACE_ROWS(OR_SITE_ATTN_RESIDUAL, as_c, H, ass);
 		for (size_t t = 0; t < T && !st; ++t)
 			st = or_rmsnorm_site(as_c + t * H, lw->mlp_gain, H, lw->mlp_norm_sc, mn + t * H, &mns[t]);
 		if (st) break;
+		TRACE_ROWS(OR_SITE_MLP_NORM, mn, H, mns);
 		BATCHED(mn, mns, H, I, OR_GATE, NULL, lw->gate_sc, gate, gs);
 		if (st) break;
 		BATCHED(mn, mns, H, I, OR_UP, NULL, lw->up_sc, up, us);
+		if (st) break;
+		TRACE_ROWS(OR_SITE_GATE, gate, I, gs);
+		TRACE_ROWS(OR_SITE_UP, up, I, us);
 		for (size_t t = 0; t < T && !st; ++t)
 			st = or_mlp_act_site(gate + t * I, gs[t], up + t * I, us[t], I, m->silu_table, lw->act_sc, act + t * I,
 			                     &acts[t]);
 		if (st) break;
+		TRACE_ROWS(OR_SITE_ACT, act, I, acts);
 		BATCHED(act, acts, I, H, OR_DOWN, NULL, lw->down_sc, down, ds);
+		if (st) break;
+		TRACE_ROWS(OR_SITE_DOWN, down, H, ds);
 		for (size_t t = 0; t < T && !st; ++t)
 			st = or_residual_site(down + t * H, ds[t], as_c + t * H, ass[t], H, lw->mlp_res_sc, next + t * H, &ss[t]);
 		if (st) break;
+		TRACE_ROWS(OR_SITE_MLP_RESIDUAL, next, H, ss);
 		memcpy(hid, next, T * H);
 		memcpy(scales, ss, T * sizeof(or_scale));
 	}
+#undef TRACE_ROWS
 #undef BATCHED
 	free(normed); free(q); free(ctx); free(o); free(as_c); free(mn); free(gate); free(up); free(act);
 	free(down); free(next); free(q_rot); free(acc); free(kacc); free(vacc); free(ns);

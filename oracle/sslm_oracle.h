@@ -165,10 +165,12 @@ int or_run_chunk(const or_model* m, int8_t* hidden_chunk, or_scale* scales, size
 int or_final_logits(const or_model* m, const int8_t* hidden, int32_t* out_logits);
 int32_t or_argmax(const int32_t* logits, size_t n);
 
-/* Per-site trace of the decode layer loop (the instrument the reference declares in
+/* Per-site trace of the layer loops (the instrument the reference declares in
  * include/superslm/trace_hook.h:36-112 -- per site and token the codes and the carried scale):
- * when set, or_run_layer_loop calls `fn` after each listed site of every layer it runs.  One
- * process-wide hook: test infrastructure, single-threaded use only. */
+ * when set, or_run_layer_loop calls `fn` after each listed site of every layer it runs, and
+ * or_run_chunk after each site of every layer, once per token in position order (its sites run
+ * over the whole chunk, as forward_sites.cpp:2098-2410 does).  One process-wide hook: test
+ * infrastructure, single-threaded use only. */
 enum {
 	OR_SITE_ATTN_NORM = 0,
 	OR_SITE_CTX = 1,
@@ -180,7 +182,8 @@ enum {
 	OR_SITE_O = 7,
 	OR_SITE_GATE = 8,
 	OR_SITE_UP = 9,
-	OR_SITE_DOWN = 10
+	OR_SITE_DOWN = 10,
+	OR_SITE_Q_ROT = 11 /* q after RoPE (no reference site; checks the backends' fused q landing) */
 };
 typedef void (*or_trace_fn)(void* user, uint32_t layer, int site, const int8_t* codes, size_t n, int64_t scale_m,
                             int64_t scale_e);

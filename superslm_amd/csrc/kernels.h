@@ -57,6 +57,14 @@ struct Epilogue {
 	int32_t* raw_out;
 };
 
+// Debug tap (sslm_hip_debug_capture): when `codes` is non-null, a kernel also stores the codes
+// [M, n] and carried scales [M] it computed at a site that otherwise stays in registers.
+struct SiteTap {
+	int8_t* codes;
+	Scale* scale;
+	int32_t ld;  // row stride of codes
+};
+
 struct GemmArgs {
 	const int8_t* a;   // [M, K] activation codes, row stride lda
 	const int8_t* w;   // [N, K] weights
@@ -228,6 +236,7 @@ struct AttnArgs {
 	const int64_t* rope_cos;    // [cap, D/2]
 	const int64_t* rope_sin;
 	unsigned long long* sat;    // [slots]
+	SiteTap q_tap;              // attention_decode: the rotated q codes of each head, and the q scale
 };
 // `one_sequence`: the launch holds one sequence's consecutive positions (a prefill chunk), so
 // the query-tiled kernel may run (unless SSLM_HIP_TILED_ATTN=0).
@@ -283,6 +292,7 @@ struct ResidualArgs {
 	int64_t* norm_recip;       // [M]
 	int32_t layer;
 	int32_t* status;
+	SiteTap branch_tap;        // the projection funnel's codes (o / down) and scale
 };
 void residual_norm(const ResidualArgs& a, hipStream_t s);
 
@@ -308,6 +318,7 @@ struct ActArgs {
 	int32_t* prod;           // [M, I]
 	uint32_t* act_maxpart;   // [kMaxActSlices * kPartLd]
 	Scale* gu_scale;         // [M, 2] gate, up
+	SiteTap gate_tap, up_tap;  // the gate / up funnels' codes and scales
 };
 constexpr int kMaxActSlices = 16;
 constexpr int kMaxSlicedActRows = 64;  // rows the sliced form's buffers hold
@@ -353,6 +364,10 @@ struct SlotCopyArgs {
 void slot_state_copy(const SlotCopyArgs& a, int n, bool restore, hipStream_t s);
 
 // per-tile argmax keys -> token ids (lowest index among equal maxima)
+// Debug capture: rows t < M of src (row idx[t], or t when idx is null) of n codes and their scales
+// into dst[t * ld] / sdst[t].
+void debug_gather(const int8_t* src, const Scale* ssrc, const int32_t* idx, int n, int M, int8_t* dst, Scale* sdst,
+                  int ld, hipStream_t s);
 void argmax_finalize(const unsigned long long* keys, int ntiles, int M, int32_t* out_tokens, hipStream_t s);
 
 // Damped greedy's candidate set on the device: per row of raw logits [M][V] (masked logits, per

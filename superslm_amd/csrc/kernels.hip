@@ -2264,6 +2264,14 @@ __global__ __launch_bounds__(BS) void k_residual_norm(sslm_launch::ResidualArgs 
 	int32_t code[EPT];
 #pragma unroll
 	for (int k = 0; k < EPT; ++k) code[k] = requant_code_f(bf[k], requant_factor(bplan.r, bplan.s));
+	if (a.branch_tap.codes) {
+#pragma unroll
+		for (int k = 0; k < EPT; ++k) {
+			const int i = threadIdx.x + k * BS;
+			if (i < H) a.branch_tap.codes[(size_t)t * a.branch_tap.ld + i] = (int8_t)code[k];
+		}
+		if (threadIdx.x == 0) a.branch_tap.scale[t] = bplan.out;
+	}
 	if (threadIdx.x < 255) {
 		const int64_t r_h = reciprocal_fast(ss.m);
 		const int64_t kx = composed_exponent(bplan.out.e, ss.e);
@@ -2316,6 +2324,26 @@ __global__ __launch_bounds__(BS) void k_residual_norm(sslm_launch::ResidualArgs 
 		if (threadIdx.x == 0 && st2 > 0) set_status(a.status, slot, a.layer, st2);
 	}
 	KT(6);
+}
+
+// debug taps of the gate and up funnels: columns [j0, j1) of row t, thread-strided as the callers
+// hold them; `scales`: this block also writes the row's two scales
+template <int BS, int EPT>
+__device__ __forceinline__ void tap_gate_up_impl(const sslm_launch::ActArgs& a, int t, int j0, int j1,
+                                                 const int32_t (&gc)[EPT], const int32_t (&uc)[EPT], Scale gs,
+                                                 Scale us, bool scales) {
+#pragma unroll
+	for (int k = 0; k < EPT; ++k) {
+		const int i = j0 + threadIdx.x + k * BS;
+		if (i < j1) {
+			a.gate_tap.codes[(size_t)t * a.gate_tap.ld + i] = (int8_t)gc[k];
+			a.up_tap.codes[(size_t)t * a.up_tap.ld + i] = (int8_t)uc[k];
+		}
+	}
+	if (scales && threadIdx.x == 0) {
+		a.gate_tap.scale[t] = gs;
+		a.up_tap.scale[t] = us;
+	}
 }
 
 // gate/up funnels -> MlpActSite (forward_sites.cpp:796-864) -> act funnel.  The sigmoid of a
@@ -2389,6 +2417,7 @@ void k_mlp_act(sslm_launch::ActArgs a) {
 		gc[k] = requant_code_f(gf[k], requant_factor(gp.r, gp.s));
 		uc[k] = requant_code_f(uf[k], requant_factor(up.r, up.s));
 	}
+	if (a.gate_tap.codes) tap_gate_up_impl<BS, EPT>(a, t, 0, I, gc, uc, gp.out, up.out, true);
 	__syncthreads();
 	// The loader admits only the canonical SiLU table (values in [0, 32768]) and the sigmoid
 	// interpolates between its entries, so |code * sig * code| <= 127 * 32768 * 127 < 2^31.
@@ -2461,6 +2490,7 @@ __global__ __launch_bounds__(BS) void k_mlp_act_s1(sslm_launch::ActArgs a, int p
 		gc[k] = requant_code_f(gf[k], requant_factor(gp.r, gp.s));
 		uc[k] = requant_code_f(uf[k], requant_factor(up.r, up.s));
 	}
+	if (a.gate_tap.codes) tap_gate_up_impl<BS, EPT>(a, t, j0, j1, gc, uc, gp.out, up.out, sl == 0);
 	__syncthreads();
 	uint32_t mx = 0;
 	int32_t* prow = a.prod + (size_t)t * I;
@@ -2632,6 +2662,10 @@ __global__ __launch_bounds__(BS) void k_attention(sslm_launch::AttnArgs a, int u
 #pragma unroll
 		for (int j = 0; j < D / 16; ++j) q[j] = *(const v4i*)(s_qc + 16 * j);
 		qs = plan.out;
+		if (a.q_tap.codes) {
+			if (threadIdx.x < D) a.q_tap.codes[(size_t)t * a.q_tap.ld + (size_t)h * D + threadIdx.x] = s_qc[threadIdx.x];
+			if (threadIdx.x == 0 && h == 0) a.q_tap.scale[t] = qs;
+		}
 	}
 	// i-exp constants of the row's scale (every thread, redundantly)
 	int32_t st = kOk;
@@ -3054,6 +3088,15 @@ __global__ __launch_bounds__(64 * NW, NW == 4 ? 3 : 1) void k_attention_tiled(ss
 	__syncthreads();
 	if (threadIdx.x < nt && s_ok[threadIdx.x] == kOk && s_rf[threadIdx.x] == 0)
 		a.ctx_maxpart[(size_t)h * kPartLd + t0 + threadIdx.x] = s_mab[threadIdx.x];
+}
+
+// Debug capture (sslm_hip_debug_capture): row t of a site buffer, and its scale, into the
+// capture area.  One block per row.
+__global__ __launch_bounds__(256) void k_debug_gather(const int8_t* src, const Scale* ssrc, const int32_t* idx, int n,
+                                                      int8_t* dst, Scale* sdst, int ld) {
+	const int t = blockIdx.x, r = idx ? idx[t] : t;
+	for (int i = threadIdx.x; i < n; i += 256) dst[(size_t)t * ld + i] = src[(size_t)r * n + i];
+	if (threadIdx.x == 0) sdst[t] = ssrc[r];
 }
 
 // LoRA intermediate (forward_sites.cpp:1066-1086): u[k] = clamp(amp_fold(A[k] . x))
@@ -3761,6 +3804,11 @@ void topk_candidates(const int32_t* logits, int V, int M, const uint8_t* const* 
                      hipStream_t s) {
 	if (M <= 0) return;
 	hipLaunchKernelGGL(k_topk, dim3(M), dim3(kTopKBlock), 0, s, logits, V, mask_page, k, out);
+}
+
+void debug_gather(const int8_t* src, const Scale* ssrc, const int32_t* idx, int n, int M, int8_t* dst, Scale* sdst,
+                  int ld, hipStream_t s) {
+	if (M > 0) hipLaunchKernelGGL(k_debug_gather, dim3(M), dim3(256), 0, s, src, ssrc, idx, n, dst, sdst, ld);
 }
 
 void argmax_finalize(const unsigned long long* keys, int ntiles, int M, int32_t* out_tokens, hipStream_t s) {

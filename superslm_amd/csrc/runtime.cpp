@@ -309,6 +309,11 @@ struct sslm_model_s {
 	std::vector<DevLayer> layers;
 	int8_t *embed, *head;
 	int8_t* head_pk = nullptr;  // packed decode copy of the LM head, or null
+	// sslm_hip_debug_capture: every site of every layer of the last launch sequence of at most
+	// dbg_tokens tokens, codes [layer][site][token][dbg_ld] and scales [layer][site][token]
+	int dbg_tokens = 0, dbg_ld = 0;
+	int8_t* dbg_codes = nullptr;
+	Scale* dbg_scales = nullptr;
 	int32_t *final_gain, *silu;
 	int64_t *rope_cos, *rope_sin;
 	Scale embed_site, final_site;
@@ -769,6 +774,28 @@ bool fused_attention_enabled() {
 	return on;
 }
 
+// Sites of the debug capture, in the oracle's trace numbering (site 6 holds q after RoPE).
+constexpr int kDbgSites = 11;
+enum DbgSite {
+	kDbgAttnNorm = 0, kDbgCtx = 1, kDbgAttnRes = 2, kDbgMlpNorm = 3, kDbgAct = 4, kDbgMlpRes = 5, kDbgQRot = 6,
+	kDbgO = 7, kDbgGate = 8, kDbgUp = 9, kDbgDown = 10
+};
+
+bool dbg_on(sslm_model m, int M) { return m->dbg_codes && M <= m->dbg_tokens; }
+
+sslm_launch::SiteTap dbg_tap(sslm_model m, int l, int site) {
+	const size_t cell = (size_t)l * kDbgSites + site;
+	return sslm_launch::SiteTap{m->dbg_codes + cell * m->dbg_tokens * m->dbg_ld, m->dbg_scales + cell * m->dbg_tokens,
+	                            m->dbg_ld};
+}
+
+void dbg_gather(sslm_model m, Track& w, int l, int site, const int8_t* src, const Scale* sc, const int32_t* idx, int n,
+                int M) {
+	const sslm_launch::SiteTap tp = dbg_tap(m, l, site);
+	sslm_launch::debug_gather(src, sc, idx, n, M, tp.codes, tp.scale, tp.ld, w.stream);
+	ck(hipGetLastError());
+}
+
 // The stream (committed hidden state) a launch sequence reads and commits: decode batches use
 // the per-slot state, prefill chunks the chunk rows.
 struct StreamRef {
@@ -791,9 +818,11 @@ void run_layers(sslm_model m, Track& w, int M, StreamRef st, int l0, int l1, ssl
 		ck(hipGetLastError());
 	}
 	const bool fused = decode && sslm_launch::gemv_eligible(M, H) && fused_attention_enabled();
+	const bool dbg = dbg_on(m, M);
 	for (int l = l0; l < l1; ++l) {
 		const DevLayer& lw = m->layers[l];
 		RawIn raw{};  // the last projection's split-K partials, when it split
+		if (dbg) dbg_gather(m, w, l, kDbgAttnNorm, w.normed, w.normed_scale, nullptr, H, M);
 		// q | k | v projection (forward_sites.cpp:1699-1735)
 		{
 			const int pj[3] = {0, 1, 2};
@@ -816,6 +845,7 @@ void run_layers(sslm_model m, Track& w, int M, StreamRef st, int l0, int l1, ssl
 			a.rope_cos = m->rope_cos;
 			a.rope_sin = m->rope_sin;
 			a.sat = m->sat;
+			if (dbg) a.q_tap = dbg_tap(m, l, kDbgQRot);
 			ProfScope p(s, kProfAttn, 0, 0);
 			sslm_launch::attention_decode(a, s);
 			ck(hipGetLastError());
@@ -861,6 +891,7 @@ void run_layers(sslm_model m, Track& w, int M, StreamRef st, int l0, int l1, ssl
 					ck(hipGetLastError());
 				}
 			}
+			if (dbg) dbg_gather(m, w, l, kDbgQRot, w.q_rot, w.q_scale, nullptr, H, M);
 			sslm_launch::AttnArgs aa = attn_args(m, w, l, M);
 			aa.q_rot = w.q_rot;
 			aa.q_scale = w.q_scale;
@@ -887,6 +918,7 @@ void run_layers(sslm_model m, Track& w, int M, StreamRef st, int l0, int l1, ssl
 			ProfScope p(s, kProfRow, 0, 0);
 			sslm_launch::funnel(a, s);
 			ck(hipGetLastError());
+			if (dbg) dbg_gather(m, w, l, kDbgCtx, w.ctx, w.ctx_scale, nullptr, H, M);
 		}
 		{  // o_proj (forward_sites.cpp:1907-1914)
 			const int pj[1] = {3};
@@ -919,9 +951,14 @@ void run_layers(sslm_model m, Track& w, int M, StreamRef st, int l0, int l1, ssl
 			a.layer = l;
 			a.status = m->status;
 			a.raw = raw;
+			if (dbg) a.branch_tap = dbg_tap(m, l, kDbgO);
 			ProfScope p(s, kProfRow, 0, 0);
 			sslm_launch::residual_norm(a, s);
 			ck(hipGetLastError());
+			if (dbg) {
+				dbg_gather(m, w, l, kDbgAttnRes, w.attn_stream, w.attn_stream_scale, nullptr, H, M);
+				dbg_gather(m, w, l, kDbgMlpNorm, w.mlp_normed, w.mlp_scale, nullptr, H, M);
+			}
 		}
 		{  // gate | up (forward_sites.cpp:1938-1955)
 			const int pj[2] = {4, 5};
@@ -950,12 +987,17 @@ void run_layers(sslm_model m, Track& w, int M, StreamRef st, int l0, int l1, ssl
 			a.prod = w.act_prod;
 			a.act_maxpart = w.act_maxpart;
 			a.gu_scale = w.gu_scale;
+			if (dbg) {
+				a.gate_tap = dbg_tap(m, l, kDbgGate);
+				a.up_tap = dbg_tap(m, l, kDbgUp);
+			}
 			ProfScope p(s, kProfRow, 0, 0);
 			// decode rows: one block per (row, column slice) in two launches, instead of one
 			// block per row that leaves most CUs idle
 			if (decode && sslm_launch::mlp_act_sliced_ok(a)) sslm_launch::mlp_act_sliced(a, s);
 			else sslm_launch::mlp_act(a, s);
 			ck(hipGetLastError());
+			if (dbg) dbg_gather(m, w, l, kDbgAct, w.act, w.act_scale, nullptr, I, M);
 		}
 		{  // down_proj (forward_sites.cpp:1969-1977)
 			const int pj[1] = {6};
@@ -990,9 +1032,11 @@ void run_layers(sslm_model m, Track& w, int M, StreamRef st, int l0, int l1, ssl
 			a.layer = l;
 			a.status = m->status;
 			a.raw = raw;
+			if (dbg) a.branch_tap = dbg_tap(m, l, kDbgDown);
 			ProfScope p(s, kProfRow, 0, 0);
 			sslm_launch::residual_norm(a, s);
 			ck(hipGetLastError());
+			if (dbg) dbg_gather(m, w, l, kDbgMlpRes, st.codes, st.scale, st.idx, H, M);
 		}
 	}
 }
@@ -1536,6 +1580,10 @@ void free_model(sslm_model m) {
 	m->graphs.clear();
 	for (void* p : m->owned) (void)hipFree(p);
 	m->owned.clear();
+	if (m->dbg_codes) (void)hipFree(m->dbg_codes);
+	if (m->dbg_scales) (void)hipFree(m->dbg_scales);
+	m->dbg_codes = nullptr;
+	m->dbg_scales = nullptr;
 	for_each_track(m, [](Track& w) {
 		free_track_buffers(w);
 		if (w.stream) (void)hipStreamDestroy(w.stream);
@@ -1646,7 +1694,7 @@ sslm_status prefill_tokens(sslm_model m, sslm_seq s, const int32_t* tokens, int 
 		                        std::to_string((uintptr_t)m->pool_dev) + "|" + std::to_string(w.gen);
 		// a span shape is captured the second time it is seen: one-off shapes launch directly
 		try {
-			if (graphs_enabled() && !prof_enabled() && m->graph_seen[key]++ > 0)
+			if (graphs_enabled() && !prof_enabled() && !m->dbg_codes && m->graph_seen[key]++ > 0)
 				ck(hipGraphLaunch(graph_of(m, key, w.stream, body), w.stream));
 			else
 				body();
@@ -2082,7 +2130,7 @@ static sslm_status decode_batch(sslm_model m, sslm_seq* seqs, int32_t n, const s
 	Track& t0 = m->tracks[0];
 	const size_t ntr = m->tracks.size();
 	const bool one_per_track = units.size() <= ntr && lg.size() <= (size_t)kMaxTokens;
-	const bool use_graph = one_per_track && graphs_enabled() && !prof_enabled();
+	const bool use_graph = one_per_track && graphs_enabled() && !prof_enabled() && !m->dbg_codes;
 	std::deque<std::vector<TokenInfo>> h_tok;  // deque: references to earlier entries stay valid
 	std::deque<std::vector<int32_t>> h_i32;
 	std::deque<std::vector<const uint8_t*>> h_ptr;
@@ -3128,6 +3176,53 @@ int32_t sslm_hip_debug_site(sslm_model model, int32_t site, int32_t row, int8_t*
 		ck(hipMemcpy(codes, src + (size_t)row * n, n, hipMemcpyDeviceToHost));
 		Scale h{};
 		ck(hipMemcpy(&h, sc + row, sizeof(Scale), hipMemcpyDeviceToHost));
+		scale_me[0] = h.m;
+		scale_me[1] = h.e;
+		return SSLM_OK;
+	});
+	return st == SSLM_OK ? n : -1;
+}
+
+sslm_status sslm_hip_debug_capture(sslm_model model, int32_t max_tokens) {
+	if (!model || max_tokens < 0 || max_tokens > kPartLd) return SSLM_INVALID_ARGUMENT;
+	sslm_model m = model;
+	std::lock_guard<std::mutex> lk(m->mu);
+	return guarded([&]() -> sslm_status {
+		for_each_track(m, [](Track& w) { ck(hipStreamSynchronize(w.stream)); });
+		if (m->dbg_codes) ck(hipFree(m->dbg_codes));
+		if (m->dbg_scales) ck(hipFree(m->dbg_scales));
+		m->dbg_codes = nullptr;
+		m->dbg_scales = nullptr;
+		m->dbg_tokens = 0;
+		if (max_tokens == 0) return SSLM_OK;
+		drop_graphs(m);  // captured graphs would skip the capture copies
+		const int ld = std::max(m->H, m->I);
+		const size_t cells = (size_t)m->L * kDbgSites * max_tokens;
+		ck(hipMalloc(&m->dbg_codes, cells * ld));
+		ck(hipMalloc(&m->dbg_scales, cells * sizeof(Scale)));
+		ck(hipMemset(m->dbg_codes, 0, cells * ld));
+		ck(hipMemset(m->dbg_scales, 0, cells * sizeof(Scale)));
+		m->dbg_ld = ld;
+		m->dbg_tokens = max_tokens;
+		return SSLM_OK;
+	});
+}
+
+int32_t sslm_hip_debug_capture_read(sslm_model model, int32_t layer, int32_t site, int32_t token, int8_t* codes,
+                                    int64_t* scale_me) {
+	if (!model || !codes || !scale_me) return -1;
+	sslm_model m = model;
+	std::lock_guard<std::mutex> lk(m->mu);
+	if (!m->dbg_codes || layer < 0 || layer >= m->L || site < 0 || site >= kDbgSites || token < 0 ||
+	    token >= m->dbg_tokens)
+		return -1;
+	const int n = (site == kDbgAct || site == kDbgGate || site == kDbgUp) ? m->I : m->H;
+	const sslm_launch::SiteTap tp = dbg_tap(m, layer, site);
+	const sslm_status st = guarded([&]() -> sslm_status {
+		for_each_track(m, [](Track& w) { ck(hipStreamSynchronize(w.stream)); });
+		ck(hipMemcpy(codes, tp.codes + (size_t)token * tp.ld, n, hipMemcpyDeviceToHost));
+		Scale h{};
+		ck(hipMemcpy(&h, tp.scale + token, sizeof(Scale), hipMemcpyDeviceToHost));
 		scale_me[0] = h.m;
 		scale_me[1] = h.e;
 		return SSLM_OK;

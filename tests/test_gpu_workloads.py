@@ -97,10 +97,11 @@ def test_config4_shape_against_reference(budget, chunk, fx, sm7, hip_lib):
 
 @pytest.mark.timeout(900)
 def test_config4_full_size_properties(sm7, hip_lib):
-    """32 sequences with 2048-token prompts (one chunk each) decoded together at budget 28, and a
-    33rd sequence with sequence 0's prompt in four 512-token chunks decoded alone at budget 1:
-    its KV after prefill, its tokens and its final KV equal sequence 0's."""
-    B, ctx, steps = 32, 2048, 4
+    """32 sequences with 2048-token prompts (one chunk each) decoded together at budget 28 for 256
+    greedy steps (contexts grow to 2304 positions, as configuration 4 states), and a 33rd sequence
+    with sequence 0's prompt in four 512-token chunks decoded alone at budget 1: its KV after
+    prefill, its 256 tokens and its final KV equal sequence 0's."""
+    B, ctx, steps = 32, 2048, 256
     L = sm7.config.layers
     model = Model(hip_lib, sm7.to_array())
     pool = model.pool(B + 1)
