@@ -1644,8 +1644,12 @@ void put_tokens(Track& w, const std::vector<TokenInfo>& ti) {
 // Tokens one prefill launch sequence takes: the whole admitted span up to kPartLd (the token
 // stride of the funnels' partial maxima), unless the per-token attention must keep rows longer
 // than LDS holds in global scratch (query-tiled attention switched off at a long context cap).
+// SSLM_HIP_PREFILL_SPAN (read per call; tests use it) lowers the limit, forcing several spans.
 int prefill_limit(sslm_model m) {
-	return (sslm_launch::attention_in_lds(m->cap) || sslm_launch::tiled_attention_enabled()) ? kPartLd : kMaxTokens;
+	int lim = (sslm_launch::attention_in_lds(m->cap) || sslm_launch::tiled_attention_enabled()) ? kPartLd : kMaxTokens;
+	const char* e = getenv("SSLM_HIP_PREFILL_SPAN");
+	if (e && atoi(e) > 0) lim = std::min(lim, atoi(e));
+	return lim;
 }
 
 // The prefill track with room for T tokens (grown in steps of kMaxTokens; graphs that captured
@@ -1674,6 +1678,29 @@ sslm_status prefill_tokens(sslm_model m, sslm_seq s, const int32_t* tokens, int 
 	std::deque<std::vector<TokenInfo>> staged;  // host copies stay alive until the sync below
 	int done = 0;
 	int last_T = 0;
+	// Several spans land K/V rows and clamp counts span by span, before a later span can refuse;
+	// the reference runs the whole call as one batch.  The call's rows [ctx, ctx + n) of every
+	// layer's K and V and the slot's clamp counter are saved first and put back on a refusal, which
+	// reproduces the reference exactly for refusals before its first landing (embedding, layer 0
+	// RMSNorm and q funnel); for a refusal at a later layer the reference keeps the landings it made,
+	// which no later call reads (positions past the committed context) but a blob or KV peek shows.
+	const bool multi = n > P;
+	int8_t* kv_save = nullptr;
+	unsigned long long* sat_save = nullptr;
+	const size_t run = (size_t)n * m->D, runs = (size_t)m->L * 2 * m->NKV, pitch = (size_t)m->cap * m->D;
+	int8_t* const block = s->pool->dev + (size_t)s->block * s->pool->block_size + (size_t)s->context_length * m->D;
+	if (multi) {
+		ck(hipMalloc(&kv_save, run * runs + 64));
+		sat_save = (unsigned long long*)(kv_save + ((run * runs + 7) & ~(size_t)7));
+		ck(hipMemcpy2DAsync(kv_save, run, block, pitch, run, runs, hipMemcpyDeviceToDevice, w.stream));
+		ck(hipMemcpyAsync(sat_save, m->sat + s->slot, 8, hipMemcpyDeviceToDevice, w.stream));
+	}
+	struct SaveGuard {
+		int8_t* p;
+		~SaveGuard() {
+			if (p) (void)hipFree(p);
+		}
+	} save_guard{kv_save};
 	while (done < n) {
 		const int T = std::min(P, n - done);
 		staged.emplace_back(T);
@@ -1713,6 +1740,11 @@ sslm_status prefill_tokens(sslm_model m, sslm_seq s, const int32_t* tokens, int 
 	prof_collect();
 	if (word != 0) {
 		ck(hipMemset(m->status + s->slot, 0, 4));
+		if (multi) {
+			ck(hipMemcpy2DAsync(block, pitch, kv_save, run, run, runs, hipMemcpyDeviceToDevice, w.stream));
+			ck(hipMemcpyAsync(m->sat + s->slot, sat_save, 8, hipMemcpyDeviceToDevice, w.stream));
+			ck(hipStreamSynchronize(w.stream));
+		}
 		return map_forward_status(word);
 	}
 	// the span's last row becomes the sequence's stream state

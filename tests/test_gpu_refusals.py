@@ -128,6 +128,32 @@ def test_refusal_in_second_span_commits_nothing(hip_lib, ref_lib):
     assert h[1] == h[3], "a refused prefill changed the sequence"
 
 
+def test_multi_span_prefill_matches_reference(monkeypatch, hip_lib, ref_lib):
+    """The multi-span commit path (spans of at most 256 tokens forced by SSLM_HIP_PREFILL_SPAN, so
+    an 1100-token prefill runs as five launch sequences): a clean 1100-token prompt prefills and
+    decodes as the reference's single batched call does, and the zero-embedding refusal at index
+    700 -- in the third span, after two spans have landed K/V rows and clamp counts -- commits
+    nothing: status, consumed, the blob and the whole KV block equal the reference's."""
+    monkeypatch.setenv("SSLM_HIP_PREFILL_SPAN", "256")
+    bad = 5
+    sm, art = _zero_embed_model(bad)
+    rng = np.random.default_rng(17)
+    prompt = rng.integers(0, sm.config.vocab, size=1100)
+    prompt[prompt == bad] = bad + 1
+    clean = prompt.copy()
+    prompt[700] = bad
+    L = sm.config.layers
+    print("case multi-span prefill: clean", flush=True)
+    steps = [("prefill", clean, 1100), ("save",), ("kv",)] + _decode_until(2, L, L) + [("save",)]
+    _run_both(hip_lib, ref_lib, art, steps, "multi-span clean prefill")
+    print("case multi-span prefill: refusal in the third span", flush=True)
+    steps = [("prefill", clean[:40], 64), ("save",), ("prefill", prompt, 1100), ("save",), ("kv",),
+             ("prefill", clean[40:300], 300), ("save",), ("kv",)] + _decode_until(2, L, L) + [("save",)]
+    h, _ = _run_both(hip_lib, ref_lib, art, steps, "multi-span refusal at index 700")
+    assert h[2][0] != 0 and h[2][1] == 0, h[2]  # refused, nothing consumed
+    assert h[1] == h[3], "a refused multi-span prefill changed the sequence"
+
+
 def test_admission_stops_match_reference(hip_lib, ref_lib):
     """Admission pre-scan (src/sslm_abi.cpp:1451-1510): an out-of-range id at index 700 admits
     the 700 tokens before it; a prompt crossing the context cap admits the headroom."""

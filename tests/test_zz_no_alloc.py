@@ -74,3 +74,23 @@ def test_noalloc_rejects_sizes_beyond_maximum(hip_lib):
         rc, codes, _, st = _call(L, dev, L.sslm_hip_gemm_requant_noalloc, a, w, fold, True)
         assert rc == 1  # SSLM_INVALID_ARGUMENT
         assert (codes == 99).all() and (st == 5).all()  # nothing launched
+
+
+def test_noalloc_on_stream_and_in_graph_replays(tmp_path):
+    """The callers the entry point is for: a created stream, and HIP graph capture.  One captured
+    call replayed three times with new inputs in the same buffers and eager work between replays;
+    each replay equals the allocating entry point (tests/noalloc_graph_check.cpp, built here)."""
+    import os
+    import shutil
+    import subprocess
+    from conftest import HIP_SO, ROOT
+    if shutil.which("hipcc") is None:
+        pytest.skip("hipcc not available")
+    obj, exe = str(tmp_path / "check.o"), str(tmp_path / "noalloc_graph_check")
+    subprocess.run(["hipcc", "-O1", "-std=c++17", "-w", "--offload-arch=gfx950", "-c",
+                    os.path.join(ROOT, "tests", "noalloc_graph_check.cpp"), "-o", obj], check=True)
+    libdir = os.path.dirname(HIP_SO)
+    subprocess.run(["hipcc", obj, "-L" + libdir, "-lsslm_hip", "-Wl,-rpath," + libdir, "-o", exe], check=True)
+    print("case noalloc graph capture", flush=True)
+    r = subprocess.run([exe], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0 and r.stdout.strip().startswith("ok"), (r.returncode, r.stdout, r.stderr[-2000:])
