@@ -108,8 +108,8 @@ def traffic_from(fetch_csv, write_csv):
     `bench.py --phase decode --pmc-steps --calibrate` (decode steps only, so the dispatches are the
     step's own mix): FETCH_SIZE and WRITE_SIZE (KiB per dispatch), each scaled by what the counter
     reads for the calibration copy of known size, averaged per (kernel, grid) and over every
-    M <= 16 GEMV dispatch (k_gemv<1, ...>, k_gemv_p<1, ...> and k_gemv_w; the prompts' prefill runs
-    M = 32 instances, k_gemv<2, ...> and k_gemv_p<2, ...>)."""
+    M <= 16 GEMV dispatch (k_gemv_pk<1, ...>, k_gemv_sk<1, ...> and k_gemv_w; the prompts' prefill
+    runs M = 32 instances, k_gemv_pk<2, ...> and k_gemv_sk<2, ...>)."""
     def per_dispatch(path, counter):
         vals, meta = defaultdict(float), {}
         for r in csv.DictReader(open(path)):
@@ -129,7 +129,7 @@ def traffic_from(fetch_csv, write_csv):
     w_scale = CALIBRATION_BYTES / (max(write[copy_key]) * 1024.0)
     kernels = []
     for (name, blocks), fv in sorted(fetch.items(), key=lambda kv: kv[0][1]):
-        if "k_gemv<1," not in name and "k_gemv_p<1," not in name and "k_gemv_w<" not in name:
+        if "k_gemv_pk<1," not in name and "k_gemv_sk<1," not in name and "k_gemv_w<" not in name:
             continue
         f = np.mean(fv) * 1024.0 * f_scale
         w = np.mean(write.get((name, blocks), [0.0])) * 1024.0 * w_scale
@@ -212,6 +212,27 @@ def extras(hip, model, pool, cfg, sm, rng, args, line):
     for s in seqs:
         s.release()
     ad.release()
+    return out
+
+
+def vendor_gemm_reference():
+    """AMD's own int8 GEMMs (hipBLASLt best candidate, rocBLAS gemm_ex) on the chunk's four projection
+    shapes with raw int32 output, each over 28 rotating weight copies (./bench_vendor_gemm, built by
+    __graft_entry__.build() from bench_vendor_gemm.cpp; a child process with its own HIP state).
+    A reference point for the prefill GEMM roofline; None when the program is not built."""
+    exe = os.path.join(ROOT, "bench_vendor_gemm")
+    if not os.path.exists(exe):
+        return None
+    r = subprocess.run([exe], capture_output=True, text=True, timeout=300)
+    if r.returncode != 0:
+        print(f"[bench] bench_vendor_gemm failed: {r.stderr[-500:]}", file=sys.stderr, flush=True)
+        return None
+    out = json.loads(r.stdout.strip().splitlines()[-1])
+    out["what"] = ("hipBLASLt (best of its heuristic candidates) and rocBLAS int8 x int8 -> int32 GEMMs on the "
+                   "512-token chunk's q|k|v, o, gate|up and down shapes, 28 rotating weight copies each; plain "
+                   "GEMMs, no fold / funnel epilogue; pass_tops_best = one layer's 2MNK over the faster "
+                   "library's per-layer sum")
+    print(f"[bench] vendor int8 GEMM reference: {out['pass_tops_best']} TOPS per layer pass", file=sys.stderr, flush=True)
     return out
 
 
@@ -421,6 +442,21 @@ def main():
             gbs = g_bytes[c] / (g_us[c] * 1e-6) / 1e9
             by_class[name] = {"us_per_launch": round(g_us[c] / g_n[c], 2), "bytes_per_launch": g_bytes[c] // g_n[c],
                               "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
+        # reference point: the same launch sequence with every GEMV replaced by a plain streaming
+        # read of its (packed) weight buffer -- the HBM rate this launch structure reaches at all
+        L_.sslm_hip_bench_read_floor.restype = ctypes.c_int32
+        L_.sslm_hip_bench_read_floor.argtypes = L_.sslm_hip_bench_decode_gemv.argtypes
+        r_us, r_bytes, r_n = (ctypes.c_double * 6)(), (ctypes.c_int64 * 6)(), (ctypes.c_int64 * 6)()
+        if L_.sslm_hip_bench_read_floor(model.handle, B, 10, r_us, r_bytes, r_n, 6) != 1:
+            raise RuntimeError("sslm_hip_bench_read_floor failed")
+        read_floor = {"frac": round(r_bytes[0] / (r_us[0] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                      "us_per_pass": round(r_us[0], 2), "gemv_us_per_pass": round(g_us[0], 2),
+                      "by_class": {name: {"us_per_launch": round(r_us[c] / r_n[c], 2),
+                                          "frac": round(r_bytes[c] / (r_us[c] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+                                   for c, name in enumerate(("q|k|v", "o", "gate|up", "down", "lm_head"), start=1)},
+                      "what": "the same 113 launches, bytes and order with each GEMV replaced by a plain "
+                              "streaming read of its weight buffer (k_stream_read): the HBM fraction a "
+                              "launch sequence of this shape reaches at all"}
         traffic = None
         if os.path.exists(TRAFFIC_FILE):
             traffic = json.load(open(TRAFFIC_FILE)).get("mean_traffic_bytes_per_launch")
@@ -454,7 +490,9 @@ def main():
                        "intermediate": cfg.inter, "vocab": cfg.vocab},
             "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-                         "kernel": "decode GEMV (k_gemv with projection epilogues, k_gemv_w for o, down and the LM head): the 113 GEMV launches of one step at M = 16 (28 layers' "
+                         "kernel": "decode GEMV on the packed weight copy (k_gemv_pk for q|k|v, o and gate|up with "
+                                   "their epilogues, k_gemv_sk split-K planes for down, k_gemv_w for the LM head): "
+                                   "the 113 GEMV launches of one step at M = 16 (28 layers' "
                                    "q|k|v, o, gate|up, down with their own weights, then the LM head) back to back "
                                    "between two HIP events on the library's stream, so every weight byte streams "
                                    "from HBM as in a step: algorithmic bytes per pass / pass time (launch gaps "
@@ -463,7 +501,8 @@ def main():
                          "bytes_per_launch": g_bytes[0] // max(1, g_n[0]),
                          "us_per_launch": round(g_us[0] / max(1, g_n[0]), 3),
                          "launches_per_pass": g_n[0],
-                         "by_class": by_class},
+                         "by_class": by_class,
+                         "read_floor": read_floor},
             "decode_step_hbm_floor_ms": round(floor_bytes / (HBM_PEAK_GBS * 1e9) * 1e3, 4),
             "decode_step_hbm_frac": round(floor_bytes / (HBM_PEAK_GBS * 1e9) / (ms_step * 1e-3), 4),
             "cpu_baseline": None,
@@ -522,6 +561,9 @@ def main():
                                     "us_per_pass": round(p_us[0], 2), "launches_per_pass": p_n[0]},
                "prefill_profile_ms": {"gemm_ms": round(pms[0], 3), "attention_ms": round(pms[2], 3),
                                       "row_ms": round(pms[3], 3), "launches": int(sum(pla))}}
+        vendor = vendor_gemm_reference()
+        if vendor:
+            pre["prefill_roofline"]["vendor_reference"] = vendor
         if line is None:
             line = {"metric": METRIC, "value": round(prefill_tops, 2), "unit": "TOPS", "n_gpus": 1, "steps": 5,
                     "warmup": 2, "ms_per_step": round(pre_s * 1e3, 3), "higher_is_better": True,

@@ -198,6 +198,12 @@ void sslm_hip_profile_reset(void);
  * Returns 1, or -1.  Sequence state is not touched. */
 int32_t sslm_hip_bench_decode_gemv(sslm_model model, int32_t M, int32_t iters, double* us, int64_t* bytes,
                                    int64_t* shapes, int32_t cap);
+/* The same passes as sslm_hip_bench_decode_gemv with every GEMV replaced by a plain streaming
+ * read of its weight buffer (the packed decode copy where there is one): the HBM rate a launch
+ * sequence of that shape -- the same launches, bytes and order -- reaches at all.  bytes[] count
+ * the weight bytes read.  No counterpart in the reference; a bench reference point. */
+int32_t sslm_hip_bench_read_floor(sslm_model model, int32_t M, int32_t iters, double* us, int64_t* bytes,
+                                  int64_t* shapes, int32_t cap);
 /* The projection GEMMs of one M-token prefill chunk (65 <= M <= 512) -- every layer's q|k|v, o,
  * gate|up and down, each layer's own weights, the layer loop's launch shapes -- back to back
  * `iters` times between two HIP events on the model's stream.  Writes us[0] = mean

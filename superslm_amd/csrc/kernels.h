@@ -364,6 +364,8 @@ struct SlotCopyArgs {
 void slot_state_copy(const SlotCopyArgs& a, int n, bool restore, hipStream_t s);
 
 // per-tile argmax keys -> token ids (lowest index among equal maxima)
+// Bench reference: one streaming read of `bytes` bytes (a multiple of 16) of device memory.
+void stream_read(const void* p, int64_t bytes, int* sink, hipStream_t s);
 // Debug capture: rows t < M of src (row idx[t], or t when idx is null) of n codes and their scales
 // into dst[t * ld] / sdst[t].
 void debug_gather(const int8_t* src, const Scale* ssrc, const int32_t* idx, int n, int M, int8_t* dst, Scale* sdst,

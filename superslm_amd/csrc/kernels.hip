@@ -3090,6 +3090,24 @@ __global__ __launch_bounds__(64 * NW, NW == 4 ? 3 : 1) void k_attention_tiled(ss
 		a.ctx_maxpart[(size_t)h * kPartLd + t0 + threadIdx.x] = s_mab[threadIdx.x];
 }
 
+// Bench reference: a plain streaming read of `bytes` (a multiple of 16), four 16-byte loads per
+// thread in flight, XOR-reduced into a sink that is written only on an impossible value.  The
+// decode GEMV bench runs it over the same weight buffers in the same launch order as the GEMV
+// pass, as the HBM rate a launch sequence of that shape can reach at all.
+__global__ __launch_bounds__(256) void k_stream_read(const v4i* p, int64_t nvec, int* sink) {
+	int64_t i = (int64_t)blockIdx.x * 1024 + threadIdx.x;
+	const int64_t stride = (int64_t)gridDim.x * 1024;
+	v4i acc = v4i{0, 0, 0, 0};
+	for (; i < nvec; i += stride) {
+		v4i t[4];
+#pragma unroll
+		for (int u = 0; u < 4; ++u) t[u] = i + u * 256 < nvec ? p[i + u * 256] : v4i{0, 0, 0, 0};
+#pragma unroll
+		for (int u = 0; u < 4; ++u) acc ^= t[u];
+	}
+	if ((acc[0] ^ acc[1] ^ acc[2] ^ acc[3]) == 0x5eed5eed) sink[0] = 1;
+}
+
 // Debug capture (sslm_hip_debug_capture): row t of a site buffer, and its scale, into the
 // capture area.  One block per row.
 __global__ __launch_bounds__(256) void k_debug_gather(const int8_t* src, const Scale* ssrc, const int32_t* idx, int n,
@@ -3804,6 +3822,12 @@ void topk_candidates(const int32_t* logits, int V, int M, const uint8_t* const* 
                      hipStream_t s) {
 	if (M <= 0) return;
 	hipLaunchKernelGGL(k_topk, dim3(M), dim3(kTopKBlock), 0, s, logits, V, mask_page, k, out);
+}
+
+void stream_read(const void* p, int64_t bytes, int* sink, hipStream_t s) {
+	const int64_t nvec = bytes / 16;
+	const int blocks = (int)std::max<int64_t>(1, std::min<int64_t>(1024, (nvec + 1023) / 1024));
+	hipLaunchKernelGGL(k_stream_read, dim3(blocks), dim3(256), 0, s, (const v4i*)p, nvec, sink);
 }
 
 void debug_gather(const int8_t* src, const Scale* ssrc, const int32_t* idx, int n, int M, int8_t* dst, Scale* sdst,

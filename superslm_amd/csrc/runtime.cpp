@@ -3044,8 +3044,10 @@ sslm_status sslm_hip_copy(void* dst, const void* src, size_t bytes, int kind) {
 sslm_status sslm_hip_synchronize(void) { return hipDeviceSynchronize() == hipSuccess ? SSLM_OK : SSLM_INVALID_ARGUMENT; }
 
 
-int32_t sslm_hip_bench_decode_gemv(sslm_model model, int32_t M, int32_t iters, double* us, int64_t* bytes,
-                                   int64_t* shapes, int32_t cap) {
+// read_only: each launch is a plain streaming read of the GEMV's weight buffer (the packed copy
+// where there is one) instead of the GEMV; bytes then count the weight bytes read.
+static int32_t bench_gemv_pass(sslm_model model, int32_t M, int32_t iters, double* us, int64_t* bytes,
+                               int64_t* shapes, int32_t cap, bool read_only) {
 	if (!model || M < 1 || M > 64 || iters < 1 || cap < 1) return -1;
 	sslm_model m = model;
 	std::lock_guard<std::mutex> lk(m->mu);
@@ -3070,22 +3072,31 @@ int32_t sslm_hip_bench_decode_gemv(sslm_model model, int32_t M, int32_t iters, d
 		int32_t* scratch_status = nullptr;
 		ck(hipMalloc(&scratch_status, (size_t)kSlotCapacity * sizeof(int32_t)));
 		ck(hipMemsetAsync(scratch_status, 0, (size_t)kSlotCapacity * sizeof(int32_t), w.stream));
+		// the bytes one launch counts: algorithmic GEMV traffic, or the weight bytes a read moves
+		auto launch_bytes = [&](const GemmArgs& g) -> int64_t {
+			if (read_only) return g.wp ? (int64_t)sslm_launch::packed_bytes(g.N, g.K) : (int64_t)g.N * g.K;
+			return (int64_t)g.N * g.K + (int64_t)g.M * g.K + 12LL * g.N + (g.epi.argmax_key ? 0 : (int64_t)g.M * g.N * 4);
+		};
 		int64_t seq_bytes = 0;
 		for (GemmArgs& g : gs) {
 			g.epi.status = scratch_status;
-			seq_bytes += (int64_t)g.N * g.K + (int64_t)g.M * g.K + 12LL * g.N + (g.epi.argmax_key ? 0 : (int64_t)g.M * g.N * 4);
+			seq_bytes += launch_bytes(g);
 		}
+		auto launch = [&](const GemmArgs& g) {
+			if (read_only) sslm_launch::stream_read(g.wp ? g.wp : g.w, launch_bytes(g), scratch_status, w.stream);
+			else sslm_launch::gemm(g, w.stream);
+		};
 		hipEvent_t a, b;
 		ck(hipEventCreate(&a));
 		ck(hipEventCreate(&b));
 		// one timed pass set over the launches whose index i satisfies keep(i)
 		auto timed = [&](auto keep) {
 			for (size_t i = 0; i < gs.size(); ++i)  // warm (instruction caches, TLB)
-				if (keep(i)) sslm_launch::gemm(gs[i], w.stream);
+				if (keep(i)) launch(gs[i]);
 			ck(hipEventRecord(a, w.stream));
 			for (int it = 0; it < iters; ++it)
 				for (size_t i = 0; i < gs.size(); ++i)
-					if (keep(i)) sslm_launch::gemm(gs[i], w.stream);
+					if (keep(i)) launch(gs[i]);
 			ck(hipEventRecord(b, w.stream));
 			ck(hipEventSynchronize(b));
 			float ms = 0;
@@ -3105,10 +3116,10 @@ int32_t sslm_hip_bench_decode_gemv(sslm_model model, int32_t M, int32_t iters, d
 				auto keep = [&](size_t i) { return c == 5 ? i == head : (i < head && (int)(i % 4) == c - 1); };
 				double total = 0;
 				for (int it = 0; it < iters; ++it) {
-					for (const GemmArgs& g : gs) sslm_launch::gemm(g, w.stream);
+					for (const GemmArgs& g : gs) launch(g);
 					ck(hipEventRecord(a, w.stream));
 					for (size_t i = 0; i < gs.size(); ++i)
-						if (keep(i)) sslm_launch::gemm(gs[i], w.stream);
+						if (keep(i)) launch(gs[i]);
 					ck(hipEventRecord(b, w.stream));
 					ck(hipEventSynchronize(b));
 					float ms = 0;
@@ -3120,7 +3131,7 @@ int32_t sslm_hip_bench_decode_gemv(sslm_model model, int32_t M, int32_t iters, d
 				for (size_t i = 0; i < gs.size(); ++i)
 					if (keep(i)) {
 						const GemmArgs& g = gs[i];
-						by += (int64_t)g.N * g.K + (int64_t)g.M * g.K + 12LL * g.N + (g.epi.argmax_key ? 0 : (int64_t)g.M * g.N * 4);
+						by += launch_bytes(g);
 						++n;
 					}
 				bytes[c] = by;
@@ -3134,6 +3145,16 @@ int32_t sslm_hip_bench_decode_gemv(sslm_model model, int32_t M, int32_t iters, d
 		return SSLM_OK;
 	});
 	return st == SSLM_OK ? 1 : -1;
+}
+
+int32_t sslm_hip_bench_decode_gemv(sslm_model model, int32_t M, int32_t iters, double* us, int64_t* bytes,
+                                   int64_t* shapes, int32_t cap) {
+	return bench_gemv_pass(model, M, iters, us, bytes, shapes, cap, false);
+}
+
+int32_t sslm_hip_bench_read_floor(sslm_model model, int32_t M, int32_t iters, double* us, int64_t* bytes,
+                                  int64_t* shapes, int32_t cap) {
+	return bench_gemv_pass(model, M, iters, us, bytes, shapes, cap, true);
 }
 
 int32_t sslm_hip_bench_prefill_gemm(sslm_model model, int32_t M, int32_t iters, double* us, int64_t* ops,
