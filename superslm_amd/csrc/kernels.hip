@@ -2594,6 +2594,31 @@ __global__ __launch_bounds__(BS) void k_attention(sslm_launch::AttnArgs a, int u
 	const int8_t* blk = a.kv_pool + (int64_t)ti.block * a.block_bytes;
 	const int64_t half = a.cap * (int64_t)a.NKV * D;
 	int8_t* kstore = a.kv_pool + (int64_t)ti.block * a.block_bytes + (int64_t)a.layer * half * 2 + (int64_t)kvh * a.cap * D;
+	// The K row this thread scores first (position threadIdx.x) and the V rows it multiplies first
+	// (positions pg + i * PG, dimensions 16 dq .. + 15) are issued right after the loads of the
+	// q|k|v post-processing: the cache rows before `pos` do not depend on it, so their round trip
+	// overlaps it.  (Loads complete in order for the wait counter, so the post-processing's own
+	// loads go first, unconditionally, and nothing waits on a load issued after the prefetch.)  In
+	// the fused form position `pos` itself is written by this launch and is read from LDS instead,
+	// so it is never loaded here (its slot loads row 0, unused).
+	constexpr int VPF = 2;  // V rows per thread issued ahead
+	const int8_t* kbase = blk + (int64_t)a.layer * half * 2 + (int64_t)kvh * a.cap * D;
+	const int8_t* vbase = kbase + half;
+	const int dq = threadIdx.x % TPR, pg = threadIdx.x / TPR;
+	v4i kpre[D / 16], vpre[VPF];
+	auto prefetch = [&]() {
+		const int64_t width_est = pos + 1;
+		const int64_t p0 = threadIdx.x;
+		const int64_t pr = (p0 < width_est && (!FUSED || p0 != pos) && p0 < a.cap) ? p0 : 0;
+#pragma unroll
+		for (int j = 0; j < D / 16; ++j) kpre[j] = load16(kbase + pr * D + 16 * j);
+#pragma unroll
+		for (int i = 0; i < VPF; ++i) {
+			const int64_t p = pg + (int64_t)i * PG;
+			const int64_t pv = (p < width_est && (!FUSED || p != pos) && p < a.cap) ? p : 0;
+			vpre[i] = load16(vbase + pv * D + 16 * dq);
+		}
+	};
 	v4i q[D / 16];
 	Scale qs;
 	if (!FUSED) {
@@ -2602,23 +2627,22 @@ __global__ __launch_bounds__(BS) void k_attention(sslm_launch::AttnArgs a, int u
 #pragma unroll
 		for (int j = 0; j < D / 16; ++j) q[j] = load16(qrow + 16 * j);
 		if (threadIdx.x == 0) s_st = a.status[ti.slot];
+		prefetch();
 	} else {
 		const int H = a.H, KVH = a.NKV * D, i = threadIdx.x;
 		const Scale ns = a.in_scale[t];
 		const bool pos_ok = pos >= 0 && pos < a.cap;
-		uint32_t qmx = part_max32<BS>(a.q_maxpart, 0, H / 16, t);
-		int2 qv = make_int2(0, 0);
-		longlong2 kk = make_longlong2(0, 0), vv = make_longlong2(0, 0);
-		int32_t c = 0, sn = 0;
-		if (i < PAIRS) {
-			qv = ((const int2*)(a.q_f + (size_t)t * H + (size_t)h * D))[i];
-			const int64_t* kvrow = a.kv_f + (size_t)t * 2 * KVH + (size_t)kvh * D;
-			kk = ((const longlong2*)kvrow)[i];
-			vv = ((const longlong2*)(kvrow + KVH))[i];
-			const int64_t pp = pos_ok ? pos : 0;
-			c = (int32_t)a.rope_cos[pp * PAIRS + i];
-			sn = (int32_t)a.rope_sin[pp * PAIRS + i];
-		}
+		// the post-processing's loads, unconditional from clamped indices (see the prefetch above)
+		const int ntq = H / 16, ic = i < PAIRS ? i : PAIRS - 1;
+		const uint32_t qm0 = a.q_maxpart[(size_t)(i < ntq ? i : ntq - 1) * kPartLd + t];
+		int2 qv = ((const int2*)(a.q_f + (size_t)t * H + (size_t)h * D))[ic];
+		const int64_t* kvrow = a.kv_f + (size_t)t * 2 * KVH + (size_t)kvh * D;
+		longlong2 kk = ((const longlong2*)kvrow)[ic], vv = ((const longlong2*)(kvrow + KVH))[ic];
+		const int64_t pp = pos_ok ? pos : 0;
+		int32_t c = (int32_t)a.rope_cos[pp * PAIRS + ic], sn = (int32_t)a.rope_sin[pp * PAIRS + ic];
+		prefetch();
+		uint32_t qmx = i < ntq ? qm0 : 0u;
+		for (int k2 = i + BS; k2 < ntq; k2 += BS) qmx = max(qmx, a.q_maxpart[(size_t)k2 * kPartLd + t]);
 		const int64_t rtk = a.r_t_k[kvh], rtv = a.r_t_v[kvh];
 		const int64_t k_e = composed_exponent(ns.e, a.e_t_k[kvh]), v_e = composed_exponent(ns.e, a.e_t_v[kvh]);
 		if (threadIdx.x == 0) s_st = a.status[ti.slot];
@@ -2686,18 +2710,17 @@ __global__ __launch_bounds__(BS) void k_attention(sslm_launch::AttnArgs a, int u
 	}
 	const bool live = st == kOk && width >= 1 && width <= a.cap;
 	int64_t* ex = use_lds ? dyn : a.scratch + ((int64_t)t * a.NH + h) * a.cap;
-	const int8_t* kbase = blk + (int64_t)a.layer * half * 2 + (int64_t)kvh * a.cap * D;
-	const int8_t* vbase = kbase + half;
-	// pass 1: scores (int32-exact dots) and the row max
+	// pass 1: scores (int32-exact dots) and the row max; the first position's row was issued at entry
 	int64_t mx = INT64_MIN;
 	if (live) {
 #pragma unroll 2
 		for (int64_t p = threadIdx.x; p < width; p += BS) {
 			const int8_t* kr = kbase + p * D;
+			const bool first = p == (int64_t)threadIdx.x;
 			int32_t acc = 0;
 #pragma unroll
 			for (int j = 0; j < D / 16; ++j) {
-				const v4i kw = FUSED && p == pos ? *(const v4i*)(s_kc + 16 * j) : load16(kr + 16 * j);
+				const v4i kw = FUSED && p == pos ? *(const v4i*)(s_kc + 16 * j) : (first ? kpre[j] : load16(kr + 16 * j));
 				acc = __builtin_amdgcn_sdot4(q[j].x, kw.x, acc, false);
 				acc = __builtin_amdgcn_sdot4(q[j].y, kw.y, acc, false);
 				acc = __builtin_amdgcn_sdot4(q[j].z, kw.z, acc, false);
@@ -2770,14 +2793,30 @@ __global__ __launch_bounds__(BS) void k_attention(sslm_launch::AttnArgs a, int u
 	// pass 4: context = sum_p prob * V[p].  A thread owns 16 dimensions (one 16-byte load per
 	// row) of every PG-th position; the loop is unrolled so several rows are in flight.  The sums
 	// are exact in int32: the probabilities of a row add up to at most 2^15.
-	const int dq = threadIdx.x % TPR, pg = threadIdx.x / TPR;
 	int32_t acc[16];
 #pragma unroll
 	for (int j = 0; j < 16; ++j) acc[j] = 0;
 	{
 		const int8_t* vc = vbase + 16 * dq;
+		// the first VPF rows of this thread were issued at entry
+#pragma unroll
+		for (int i = 0; i < VPF; ++i) {
+			const int64_t p = pg + (int64_t)i * PG;
+			if (p < width) {
+				const v4i v = FUSED && p == pos ? *(const v4i*)(s_vc + 16 * dq) : vpre[i];
+				const int32_t pr = (int32_t)ex[p];
+#pragma unroll
+				for (int w = 0; w < 4; ++w) {
+					const int32_t x = v[w];
+					acc[4 * w] += pr * (int32_t)(int8_t)(x & 0xff);
+					acc[4 * w + 1] += pr * (int32_t)(int8_t)((x >> 8) & 0xff);
+					acc[4 * w + 2] += pr * (int32_t)(int8_t)((x >> 16) & 0xff);
+					acc[4 * w + 3] += pr * (x >> 24);
+				}
+			}
+		}
 #pragma unroll 4
-		for (int64_t p = pg; p < width; p += PG) {
+		for (int64_t p = pg + (int64_t)VPF * PG; p < width; p += PG) {
 			const v4i v = FUSED && p == pos ? *(const v4i*)(s_vc + 16 * dq) : load16(vc + p * D);
 			const int32_t pr = (int32_t)ex[p];
 #pragma unroll
