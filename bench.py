@@ -279,6 +279,22 @@ def config4(hip, args):
                           "prefill_tok_s": round(B * ctx / pre_s, 1), "decode_tok_s": round(B * steps / dt, 1),
                           "decode_ms_per_step": round(dt * 1e3 / steps, 3), "decode_steps": steps}}
     print(f"[bench] config4 decode: {out['config4_7b']['decode_tok_s']} tok/s", file=sys.stderr, flush=True)
+    # per-class kernel time of a few more steps under the runtime's HIP-event profiler (graphs off
+    # while it runs; contexts 2307-2314)
+    n_prof = 8
+    profile(hip, True)
+    for _ in range(n_prof):
+        model.decode_step(seqs, cfg.layers)
+    hip.lib.sslm_hip_synchronize()
+    ms, la, by, op = profile_read(hip)
+    profile(hip, False)
+    per_layer = lambda c: round(ms[c] * 1e3 / (n_prof * cfg.layers), 2)
+    kv_bytes = B * cfg.kv_heads * 2 * cfg.head_dim * 2310  # one layer's K and V rows at ~2310 positions
+    attn_us = per_layer(2)
+    out["config4_7b"]["decode_us_per_layer"] = {"attention": attn_us, "gemm": per_layer(0), "rows": per_layer(3),
+                                                "lm_head_per_step": round(ms[1] * 1e3 / n_prof, 2)}
+    out["config4_7b"]["decode_attention_kv_gbs"] = round(kv_bytes / (attn_us * 1e-6) / 1e9, 1)
+    print(f"[bench] config4 decode per layer: attention {attn_us} us", file=sys.stderr, flush=True)
     for s in seqs:
         s.release()
     pool.close()

@@ -621,25 +621,36 @@ SSLM_HD bool iexp_small_ok(int64_t q_ln2, int64_t q_b, int64_t m_ceiling) {
 	const int64_t ab = q_b < 0 ? -q_b : q_b;
 	return q_ln2 >= 1 && q_ln2 <= kI32Max / 30 && ab <= kI32Max - q_ln2 && m_ceiling > 0;
 }
-SSLM_HD int64_t iexp_small(int64_t shifted, int32_t q_ln2, double inv_ln2, int32_t q_b, int64_t q_c,
-                           int64_t m_ceiling) {
+// iexp_small in two halves: the quotient z = floor(x / q_ln2) and remainder r of x = -shifted
+// (clipped at 30 q_ln2), packed as z << 27 | r (r < q_ln2 <= 2^31 / 30 < 2^27, z <= 30), then the
+// value from them -- so a caller may keep the 32-bit pair and finish the value later.
+SSLM_HD uint32_t iexp_small_zr(int64_t shifted, int32_t q_ln2, double inv_ln2) {
 	const int32_t lim = 30 * q_ln2;
 	const int32_t x = shifted < -(int64_t)lim ? lim : (int32_t)(-shifted);
+	// x / q_ln2 <= 30 and the double estimate is within 30 * 2^-52 of it, while a quotient that
+	// is not an integer is at least 1 / q_ln2 >= 2^-31 below the next one: the truncation is
+	// floor(x / q_ln2) or, for an exact quotient estimated low, one less.  One corrective step
+	// each way (selects, no loop) therefore gives the exact quotient and remainder.
 	int32_t z = (int32_t)((double)x * inv_ln2);
 	z = z < 0 ? 0 : (z > 30 ? 30 : z);
 	int32_t r = x - z * q_ln2;
-	while (r < 0) {
-		--z;
-		r += q_ln2;
-	}
-	while (r >= q_ln2) {
-		++z;
-		r -= q_ln2;
-	}
-	const int32_t base = q_b - r;
+	const bool lo = r < 0;
+	z = lo ? z - 1 : z;
+	r = lo ? r + q_ln2 : r;
+	const bool hi = r >= q_ln2;
+	z = hi ? z + 1 : z;
+	r = hi ? r - q_ln2 : r;
+	return (uint32_t)z << 27 | (uint32_t)r;
+}
+SSLM_HD int64_t iexp_small_value(uint32_t zr, int32_t q_b, int64_t q_c, int64_t m_ceiling) {
+	const int32_t base = q_b - (int32_t)(zr & ((1u << 27) - 1u));
 	const uint32_t ab = base < 0 ? 0u - (uint32_t)base : (uint32_t)base;
-	const uint64_t v = ((uint64_t)ab * ab + (uint64_t)q_c) >> z;
+	const uint64_t v = ((uint64_t)ab * ab + (uint64_t)q_c) >> (zr >> 27);
 	return v > (uint64_t)m_ceiling ? -1 : (int64_t)v;
+}
+SSLM_HD int64_t iexp_small(int64_t shifted, int32_t q_ln2, double inv_ln2, int32_t q_b, int64_t q_c,
+                           int64_t m_ceiling) {
+	return iexp_small_value(iexp_small_zr(shifted, q_ln2, inv_ln2), q_b, q_c, m_ceiling);
 }
 
 // The Q15 probability floor((e << 15) / d) for 0 <= e <= d < 2^38 in doubles: e 2^15 and d are

@@ -237,7 +237,16 @@ struct AttnArgs {
 	const int64_t* rope_sin;
 	unsigned long long* sat;    // [slots]
 	SiteTap q_tap;              // attention_decode: the rotated q codes of each head, and the q scale
+	int32_t wcap;               // attention_decode: score rows of the grouped kernel, a multiple of 128
+	                            // at least every width (pos + 1) of the launch (group_width_cap)
 };
+// The grouped decode kernel's score-row length for a launch whose widest row is `max_width`:
+// rounded up to 512 (so a decode graph keyed by it is re-recorded once per 512 positions), at
+// most the cap rounded up to 128.
+inline int32_t group_width_cap(int64_t max_width, int64_t cap) {
+	const int64_t b = (max_width + 511) / 512 * 512, c = (cap + 127) / 128 * 128;
+	return (int32_t)(b < c ? b : c);
+}
 // `one_sequence`: the launch holds one sequence's consecutive positions (a prefill chunk), so
 // the query-tiled kernel may run (unless SSLM_HIP_TILED_ATTN=0).
 void attention(const AttnArgs& a, hipStream_t s, bool one_sequence = false);
@@ -246,6 +255,12 @@ bool tiled_attention_enabled();
 // valid when every token of the launch belongs to a different sequence, so no token attends to
 // a position another block of the launch writes.
 void attention_decode(const AttnArgs& a, hipStream_t s);
+// attention_decode runs one block per (token, KV head) for this launch shape when the shape fits
+// (SSLM_HIP_GROUPED_ATTN=1 forces it wherever it fits, =0 turns it off)
+bool grouped_attention_chosen(int M, int NKV, int64_t cap);
+// Queries and sets the grouped decode kernel's LDS attributes for head size D and group size G
+// (once per process; call before any capture).  False when the runtime refuses them.
+bool attention_prepare(int D, int G);
 // the attention row (cap int64 values) lives in LDS up to this context capacity, else in
 // AttnArgs::scratch ([M, NH, cap] int64)
 constexpr int64_t kAttnLdsCap = 6144;

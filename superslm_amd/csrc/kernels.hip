@@ -3129,6 +3129,455 @@ __global__ __launch_bounds__(64 * NW, NW == 4 ? 3 : 1) void k_attention_tiled(ss
 		a.ctx_maxpart[(size_t)h * kPartLd + t0 + threadIdx.x] = s_mab[threadIdx.x];
 }
 
+// Decode attention over long contexts, one block per (token, KV head): the KV group's G query
+// heads are the rows of the MFMA tiles, so each K and V row is read once for all of them.  One
+// block per (query head, token) reads every K/V byte G times (7 at the 7B shape); at ~2,000
+// positions those re-reads, served by L2 and the memory-side cache, were what bounded the
+// per-head kernel.  The arithmetic is k_attention's (forward_sites.cpp:1791-1905), element by
+// element:
+//   * prologue: the q|k|v post-processing of the fused kernel for the whole group -- the q funnel
+//     from the projection's tile maxima, q codes and RoPE(q) of the G heads, and the K/V landing
+//     and RoPE(K) of the KV head at `pos`, which this block alone writes to the cache and keeps in
+//     LDS (no block reads what another writes);
+//   * pass 1: int32-exact scores Q.K^T on v_mfma_i32_16x16x64_i8 (A = the G query rows, zero rows
+//     past G; B = 16 key rows), kept in LDS ([G][cap] int32) with the row maxima; K rows are
+//     issued a group of steps ahead of the group being scored;
+//   * pass 2: i-exp values and row sums over every (row, position), spread over all threads; then
+//     the Q15 probabilities, each overwriting its score as three 7-bit parts;
+//   * pass 3: per step of KB positions, the parts staged as int8 MFMA operands, V rows staged in
+//     LDS as stored (issued a group of steps ahead) and P.V on MFMA through gfx950's
+//     byte-transposing LDS read, as k_attention_tiled does;
+//   * epilogue: per head the ctx fold, outputs and the per-head tile maximum.
+// Refusals are reported per head exactly as the per-head kernel reports them.
+template <int D, int NW, int GM>
+__global__ __launch_bounds__(64 * NW, 1) void k_attention_group(sslm_launch::AttnArgs a) {
+	constexpr int TQ = 16, BS = 64 * NW, KB = 16 * NW, NC = (D + 63) / 64, DT = D / 16, PS = KB + 16, VS = D + 16;
+	constexpr int PAIRS = D / 2, DTW = (DT + NW - 1) / NW, VCH = KB * (D / 16), VPT = (VCH + BS - 1) / BS;
+	// K and V rows are issued R steps at a time, one group of R steps ahead of the one consumed:
+	// a step's rows alone (16 KB per block at D = 128) leave the CU waiting a round trip per step
+	constexpr int R = D <= 128 ? 4 : 2;
+	extern __shared__ __attribute__((aligned(16))) int32_t s_sc[];     // [G][wcap] scores
+	__shared__ __attribute__((aligned(16))) int8_t s_p[2][3][TQ][PS];  // probability parts [buffer][part][row][pos]
+	__shared__ __attribute__((aligned(16))) int8_t s_v[2][KB][VS];     // V rows [buffer][pos][dim]
+	__shared__ __attribute__((aligned(16))) int8_t s_qc[TQ][D];     // the rows' rotated q codes
+	__shared__ __attribute__((aligned(16))) int8_t s_kc[D], s_vc[D];
+	__shared__ int64_t s_red[NW][TQ];
+	__shared__ uint32_t s_qm[NW], s_mab[TQ], s_rf[TQ];
+	__shared__ int32_t s_st, s_rmx[TQ];
+	__shared__ int32_t s_dump[BS];  // where rows G .. GM - 1 of the softmax loops store
+	const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, ri = lane & 15, g = lane >> 4, i = threadIdx.x;
+	const int G = a.NH / a.NKV, H = a.H, KVH = a.NKV * D;
+	const int t = blockIdx.x / a.NKV, kvh = blockIdx.x % a.NKV, h0 = kvh * G;
+	const TokenInfo ti = a.tok[t];
+	const int64_t pos = ti.pos, width = pos + 1, cap = a.cap;
+	const bool pos_ok = pos >= 0 && pos < cap;
+	const int64_t half = cap * (int64_t)KVH;
+	const int8_t* kbase = a.kv_pool + (int64_t)ti.block * a.block_bytes + (int64_t)a.layer * half * 2 + (int64_t)kvh * cap * D;
+	const int8_t* vbase = kbase + half;
+	// ---- prologue loads, unconditional from clamped indices, then the first K step ahead ----
+	const int ntq = H / 16;
+	const uint32_t qm0 = a.q_maxpart[(size_t)(i < ntq ? i : ntq - 1) * kPartLd + t];
+	const int qi = i < G * PAIRS ? i : G * PAIRS - 1, qr = qi / PAIRS, qj = qi % PAIRS;
+	const int2 qv = ((const int2*)(a.q_f + (size_t)t * H + (size_t)(h0 + qr) * D))[qj];
+	const int ki = i < PAIRS ? i : PAIRS - 1;
+	const int64_t* kvrow = a.kv_f + (size_t)t * 2 * KVH + (size_t)kvh * D;
+	const longlong2 kk = ((const longlong2*)kvrow)[ki], vv = ((const longlong2*)(kvrow + KVH))[ki];
+	const int64_t pp = pos_ok ? pos : 0;
+	const int32_t cq = (int32_t)a.rope_cos[pp * PAIRS + qj], sq = (int32_t)a.rope_sin[pp * PAIRS + qj];
+	const int32_t ck = (int32_t)a.rope_cos[pp * PAIRS + ki], sk = (int32_t)a.rope_sin[pp * PAIRS + ki];
+	const Scale ns = a.in_scale[t];
+	auto load_k = [&](int blk, v4i (&kb)[NC]) {
+		const int64_t p = (int64_t)blk * KB + wave * 16 + ri;
+		const int64_t pr = p < width && p != pos && p < cap ? p : 0;
+#pragma unroll
+		for (int c = 0; c < NC; ++c) {
+			const int off = c * 64 + g * 16;
+			kb[c] = off < D ? load16(kbase + pr * D + off) : v4i{0, 0, 0, 0};
+		}
+	};
+	v4i kb0[R][NC], kb1[R][NC];
+	auto load_kr = [&](int c0, v4i (&kb)[R][NC]) {
+#pragma unroll
+		for (int j = 0; j < R; ++j) load_k(c0 * R + j, kb[j]);
+	};
+	load_kr(0, kb0);
+	uint32_t qmx = i < ntq ? qm0 : 0u;
+	for (int k2 = i + BS; k2 < ntq; k2 += BS) qmx = max(qmx, a.q_maxpart[(size_t)k2 * kPartLd + t]);
+	const int64_t rtk = a.r_t_k[kvh], rtv = a.r_t_v[kvh];
+	const int64_t k_e = composed_exponent(ns.e, a.e_t_k[kvh]), v_e = composed_exponent(ns.e, a.e_t_v[kvh]);
+	const int64_t km = a.khead_m[kvh], ke = a.khead_e[kvh];
+	if (i == 0) s_st = a.status[ti.slot];
+	for (int k2 = i; k2 < TQ * D; k2 += BS) (&s_qc[0][0])[k2] = 0;
+	for (int k2 = i; k2 < 2 * 3 * TQ * PS; k2 += BS) (&s_p[0][0][0][0])[k2] = 0;
+	if (i < TQ) {
+		s_mab[i] = 0;
+		s_rf[i] = 0;
+	}
+	qmx = blk_max32<BS>(qmx, s_qm);
+	if (s_st != 0) return;
+	FunnelPlan plan;
+	int32_t st = funnel_plan(qmx, &ns, 1, a.q_site, &plan);
+	if (st == kOk && !pos_ok) st = kPositionOverCap;
+	if (st != kOk) {  // the same for every head of the token
+		if (i == 0) set_status(a.status, ti.slot, a.layer, st);
+		return;
+	}
+	// K/V landing of this KV head at pos (this block is its only writer)
+	uint32_t sat = 0;
+	if (i < PAIRS) {
+		bool c0, c1, c2, c3, x0;
+		const int64_t k0 = clamp_code(landing_rescale(kk.x, ns.m, rtk, k_e, &c0, &x0));
+		const int64_t k1 = clamp_code(landing_rescale(kk.y, ns.m, rtk, k_e, &c1, &x0));
+		int64_t xr, yr;
+		rope_pair((int32_t)k0, (int32_t)k1, ck, sk, &xr, &yr);
+		const char2 kc = make_char2((char)clamp_code(xr), (char)clamp_code(yr));
+		const char2 vc = make_char2((char)clamp_code(landing_rescale(vv.x, ns.m, rtv, v_e, &c2, &x0)),
+		                            (char)clamp_code(landing_rescale(vv.y, ns.m, rtv, v_e, &c3, &x0)));
+		sat = (uint32_t)c0 + (uint32_t)c1 + (uint32_t)c2 + (uint32_t)c3;
+		((char2*)s_kc)[i] = kc;
+		((char2*)s_vc)[i] = vc;
+		int8_t* kstore = const_cast<int8_t*>(kbase);
+		const int64_t off = pos * D + 2 * i;
+		*(char2*)(kstore + off) = kc;
+		*(char2*)(kstore + half + off) = vc;
+	}
+	{
+		const int32_t ws = wave_sum32((int32_t)sat);
+		if (lane == 0 && ws) atomicAdd(&a.sat[ti.slot], (unsigned long long)ws);
+	}
+	if (i < G * PAIRS) {  // q codes and RoPE of the group's heads
+		int64_t xr, yr;
+		const int32_t x = requant_code_f(qv.x, requant_factor(plan.r, plan.s));
+		const int32_t y = requant_code_f(qv.y, requant_factor(plan.r, plan.s));
+		rope_pair(x, y, cq, sq, &xr, &yr);
+		*(char2*)&s_qc[qr][2 * qj] = make_char2((char)clamp_code(xr), (char)clamp_code(yr));
+	}
+	const Scale qs = plan.out;
+	// i-exp constants of the rows' common scale (the q scale is the token's, km / ke the KV head's)
+	int64_t c_qln2 = 0, c_qb = 0, c_qc = 0, c_M = 0;
+	if (!fits_i32(qs.m) || !fits_i32(km)) {
+		st = kCarriedScaleMantissaOutOfDomain;
+	} else {
+		const Scale sm = combine_scale(qs, Scale{km, ke});
+		if (!fits_i32(sm.m)) st = kCarriedScaleMantissaOutOfDomain;
+		else if (iexp_scale_constants(sm.m, sm.e, a.ln2_q, a.b_q, a.ca_q, &c_qln2, &c_qb, &c_qc) != 0)
+			st = kIExpScaleDerivationOutOfDomain;
+		else {
+			st = check_softmax_width(c_qb, c_qc, width);
+			c_M = softmax_ceiling(c_qb, c_qc);
+		}
+	}
+	__syncthreads();
+	if (a.q_tap.codes) {
+		for (int k2 = i; k2 < G * D; k2 += BS) a.q_tap.codes[(size_t)t * a.q_tap.ld + (size_t)h0 * D + k2] = s_qc[k2 / D][k2 % D];
+		if (i == 0 && kvh == 0) a.q_tap.scale[t] = qs;
+	}
+	// (width <= wcap holds by construction: the host sizes wcap from the launch's positions)
+	const bool live = st == kOk && width >= 1 && width <= cap && width <= a.wcap;
+	if (!live) {  // every head of the group: the same refusal the per-head kernel reports
+		if (i < G) report_head(a.head_status, ti.slot, h0 + i, st != kOk ? st : kPositionOverCap);
+		return;
+	}
+	v4i qa[NC];
+#pragma unroll
+	for (int c = 0; c < NC; ++c) {
+		const int off = c * 64 + g * 16;
+		qa[c] = off < D ? *(const v4i*)&s_qc[ri][off] : v4i{0, 0, 0, 0};
+	}
+	// ---- pass 1: scores and row maxima ----
+	const int nblk = (int)((width + KB - 1) / KB);
+	const int64_t cstride = a.wcap;  // a multiple of KB, at least every width of the launch
+	int32_t mx[4] = {INT32_MIN, INT32_MIN, INT32_MIN, INT32_MIN};
+	auto score_step = [&](int blk, v4i (&kb)[NC]) {
+		const int64_t p = (int64_t)blk * KB + wave * 16 + ri;
+		v4i acc = v4i{0, 0, 0, 0};
+#pragma unroll
+		for (int c = 0; c < NC; ++c) {
+			const int off = c * 64 + g * 16;
+			const v4i b = p == pos && off < D ? *(const v4i*)(s_kc + off) : kb[c];
+			acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(qa[c], b, acc, 0, 0, 0);
+		}
+		if (p < width) {
+#pragma unroll
+			for (int v = 0; v < 4; ++v) {
+				const int r = g * 4 + v;
+				if (r < G) {
+					s_sc[(int64_t)r * cstride + p] = acc[v];
+					mx[v] = max(mx[v], acc[v]);
+				}
+			}
+		}
+	};
+	const int ngr = (nblk + R - 1) / R;  // groups of R steps (steps past the row score nothing)
+	auto score_group = [&](int c0, v4i (&kb)[R][NC]) {
+#pragma unroll
+		for (int j = 0; j < R; ++j) score_step(c0 * R + j, kb[j]);
+	};
+	// the group loads are unconditional (rows past the width read row 0, a cache hit): a load
+	// issued on one path only would make every later wait drain all loads in flight
+	for (int c0 = 0; c0 < ngr; c0 += 2) {
+		load_kr(c0 + 1, kb1);
+		score_group(c0, kb0);
+		if (c0 + 1 >= ngr) break;
+		load_kr(c0 + 2, kb0);
+		score_group(c0 + 1, kb1);
+	}
+#pragma unroll
+	for (int v = 0; v < 4; ++v) {
+		for (int o = 8; o > 0; o >>= 1) mx[v] = max(mx[v], __shfl_xor(mx[v], o, 16));
+		if (ri == 0) s_red[wave][g * 4 + v] = mx[v];
+	}
+	__syncthreads();
+	if (i < TQ) {
+		int64_t m = s_red[0][i];
+		for (int w = 1; w < NW; ++w) m = max(m, s_red[w][i]);
+		s_rmx[i] = (int32_t)m;
+	}
+	__syncthreads();
+	// ---- pass 2: i-exp values and row sums over every (row, position) ----
+	// Every row of the block has the same constants (one token's q scale, one KV head's K scale).
+	// Each score's slot then keeps what the probabilities need: the i-exp value when the ceiling
+	// fits 31 bits, else (32-bit constants) the packed quotient and remainder it is finished from,
+	// else nothing (the value is recomputed from the score).  Positions outer, GM rows inner as
+	// straight-line code: rows G .. GM - 1 repeat row G - 1's inputs, store to a per-thread dummy
+	// slot and are masked out of the refusal bits (their sums are never read), so a thread's rows
+	// are independent chains.
+	const bool esmall = iexp_small_ok(c_qln2, c_qb, c_M), ekeep = c_M < ((int64_t)1 << 31);
+	const double inv_ln2 = c_qln2 >= 1 ? 1.0 / (double)c_qln2 : 0.0;
+	int32_t rmx[GM], ro[GM];  // row r's maximum and offset in s_sc (row G - 1's for padding rows)
+#pragma unroll
+	for (int r = 0; r < GM; ++r) {
+		const int rr = r < G ? r : G - 1;
+		rmx[r] = s_rmx[rr];
+		ro[r] = rr * (int32_t)cstride;
+	}
+	// where row r stores position p: its own slot, or the dummy slot for a padding row
+	auto slot = [&](int r, int64_t p) -> int32_t* { return r < G ? s_sc + ro[r] + (int32_t)p : s_dump + i; };
+	const uint32_t gmask = (1u << G) - 1u;
+	{
+		int64_t sum[GM];
+		uint32_t refused = 0;
+#pragma unroll
+		for (int r = 0; r < GM; ++r) sum[r] = 0;
+		auto pass2 = [&](auto small) {
+			for (int64_t p = i; p < width; p += BS) {
+#pragma unroll
+				for (int r = 0; r < GM; ++r) {
+					const int64_t sh = (int64_t)s_sc[ro[r] + (int32_t)p] - rmx[r];
+					int64_t e;
+					int32_t keep;
+					if constexpr (decltype(small)::value) {
+						const uint32_t zr = iexp_small_zr(sh, (int32_t)c_qln2, inv_ln2);
+						e = iexp_small_value(zr, (int32_t)c_qb, c_qc, c_M);
+						keep = ekeep ? (int32_t)(e < 0 ? 0 : e) : (int32_t)zr;
+					} else {
+						e = iexp_fast(sh, c_qln2, inv_ln2, c_qb, c_qc, c_M);
+						keep = (int32_t)(e < 0 ? 0 : e);
+					}
+					refused |= (e < 0 ? 1u : 0u) << r;
+					sum[r] += e < 0 ? 0 : e;
+					if (decltype(small)::value || ekeep) *slot(r, p) = keep;
+				}
+			}
+		};
+		if (esmall) pass2(std::true_type{});
+		else pass2(std::false_type{});
+		refused &= gmask;
+#pragma unroll
+		for (int r = 0; r < GM; ++r) {
+			if (r < G) {
+				const int64_t ws = wave_sum_i64(sum[r]);
+				if (lane == 0) s_red[wave][r] = ws;
+			}
+		}
+		if (refused) atomicOr(&s_rf[0], refused);  // bit r: row r refused somewhere
+	}
+	__syncthreads();
+	const uint32_t rf = s_rf[0];
+	if (i < G && (rf >> i & 1)) report_head(a.head_status, ti.slot, h0 + i, kSoftmaxKernelRefusedAfterGateAccepted);
+	// Q15 probabilities p = (e << 15) / max(total, 1) of every (row, position), each overwriting
+	// its slot as the three 7-bit parts p >> 14 | (p >> 7 & 127) << 8 | (p & 127) << 16 (zero for
+	// a refused row).  e <= total, so a quotient is at most 2^15.
+	{
+		int64_t dn[GM];
+		double di[GM], dd[GM];
+		bool dsm = true, live_r[GM];
+#pragma unroll
+		for (int r = 0; r < GM; ++r) {
+			const int rr = r < G ? r : G - 1;
+			int64_t tot = 0;
+			for (int w = 0; w < NW; ++w) tot += s_red[w][rr];
+			dn[r] = tot > 1 ? tot : 1;
+			di[r] = 1.0 / (double)dn[r];
+			dd[r] = (double)dn[r];
+			dsm = dsm && div_q15_small_ok(dn[r]);
+			live_r[r] = !(rf >> rr & 1);
+		}
+		// kept: 0 the value, 1 the packed quotient and remainder, 2 nothing (the score)
+		auto probs = [&](auto kept, auto qsmall) {
+			constexpr int K = decltype(kept)::value;
+			for (int64_t p = i; p < width; p += BS) {
+				int32_t w[GM];
+#pragma unroll
+				for (int r = 0; r < GM; ++r) {
+					const int32_t v = s_sc[ro[r] + (int32_t)p];
+					int64_t e;
+					if constexpr (K == 0) e = v;
+					else if constexpr (K == 1) e = iexp_small_value((uint32_t)v, (int32_t)c_qb, c_qc, c_M);
+					else e = iexp_fast((int64_t)v - rmx[r], c_qln2, inv_ln2, c_qb, c_qc, c_M);
+					int32_t pr;
+					if constexpr (decltype(qsmall)::value) pr = div_q15_small(e, dd[r], di[r]);
+					else pr = (int32_t)div_rcp(e << 15, dn[r], di[r], 32768);
+					pr = live_r[r] && e > 0 ? pr : 0;
+					w[r] = (pr >> 14) | ((pr >> 7) & 127) << 8 | (pr & 127) << 16;
+				}
+				// every row read before any is overwritten (a padding row reads row G - 1)
+#pragma unroll
+				for (int r = 0; r < GM; ++r) *slot(r, p) = w[r];
+			}
+		};
+		using I0 = std::integral_constant<int, 0>;
+		using I1 = std::integral_constant<int, 1>;
+		using I2 = std::integral_constant<int, 2>;
+		if (ekeep && dsm) probs(I0{}, std::true_type{});
+		else if (ekeep) probs(I0{}, std::false_type{});
+		else if (esmall && dsm) probs(I1{}, std::true_type{});
+		else if (esmall) probs(I1{}, std::false_type{});
+		else probs(I2{}, std::false_type{});
+	}
+	__syncthreads();
+	// ---- pass 3: Q15 probabilities and P.V on MFMA ----
+	v4i cacc[DTW][3];
+#pragma unroll
+	for (int d2 = 0; d2 < DTW; ++d2)
+#pragma unroll
+		for (int k = 0; k < 3; ++k) cacc[d2][k] = v4i{0, 0, 0, 0};
+	auto load_v = [&](int blk, v4i (&vr)[VPT]) {
+#pragma unroll
+		for (int u = 0; u < VPT; ++u) {
+			const int c = i + u * BS;
+			const int pr = c / (D / 16), ch = c % (D / 16);
+			const int64_t p = (int64_t)blk * KB + pr;
+			const int64_t pl = p < width && p != pos && p < cap ? p : 0;
+			vr[u] = c < VCH ? load16(vbase + pl * D + ch * 16) : v4i{0, 0, 0, 0};
+		}
+	};
+	v4i vr0[R][VPT], vr1[R][VPT];
+	auto load_vr = [&](int c0, v4i (&vr)[R][VPT]) {
+#pragma unroll
+		for (int j = 0; j < R; ++j) load_v(c0 * R + j, vr[j]);
+	};
+	// Step j's operands are staged into buffer j & 1 while step j - 1's are multiplied from the
+	// other one, so a step costs one barrier: buffer b was last read by the multiply before the
+	// previous barrier.
+	auto stage = [&](int blk, const v4i (&vr)[VPT], int b) {
+		// the step's probability parts of every live row (zero past the width), four positions
+		// of one row per thread: one 16-byte read of the packed parts, three 4-byte writes
+#pragma unroll
+		for (int u = 0; u < (TQ * KB / 4 + BS - 1) / BS; ++u) {
+			const int e4 = i + u * BS;
+			if (e4 < G * (KB / 4)) {
+				const int r = e4 / (KB / 4), pl = 4 * (e4 % (KB / 4));
+				const int64_t p = (int64_t)blk * KB + pl;
+				v4i w = *(const v4i*)&s_sc[(int64_t)r * cstride + p];  // in bounds: cstride is a multiple of KB
+#pragma unroll
+				for (int q = 0; q < 4; ++q) w[q] = p + q < width ? w[q] : 0;
+				// byte q of part k = byte k of word q
+				*(int32_t*)&s_p[b][0][r][pl] = (w[0] & 0xff) | (w[1] & 0xff) << 8 | (w[2] & 0xff) << 16 | (w[3] & 0xff) << 24;
+				*(int32_t*)&s_p[b][1][r][pl] = (w[0] >> 8 & 0xff) | (w[1] >> 8 & 0xff) << 8 | (w[2] >> 8 & 0xff) << 16 |
+				                               (w[3] >> 8 & 0xff) << 24;
+				*(int32_t*)&s_p[b][2][r][pl] = (w[0] >> 16 & 0xff) | (w[1] >> 16 & 0xff) << 8 | (w[2] >> 16 & 0xff) << 16 |
+				                               (w[3] >> 16 & 0xff) << 24;
+			}
+		}
+#pragma unroll
+		for (int u = 0; u < VPT; ++u) {
+			const int c = i + u * BS;
+			if (c < VCH) {
+				const int pr = c / (D / 16), ch = c % (D / 16);
+				const int64_t p = (int64_t)blk * KB + pr;
+				*(v4i*)&s_v[b][pr][ch * 16] = p == pos ? *(const v4i*)(s_vc + ch * 16) : vr[u];
+			}
+		}
+	};
+	auto multiply = [&](int b) {
+#pragma unroll
+		for (int d2 = 0; d2 < DTW; ++d2) {
+			const int dt = wave + NW * d2;
+			if (dt < DT) {
+#pragma unroll
+				for (int kk2 = 0; kk2 < KB / 64; ++kk2) {
+					const int8_t* vp = &s_v[b][kk2 * 64 + g * 16 + (ri >> 1)][dt * 16 + 8 * (ri & 1)];
+					const v2i lo = __builtin_amdgcn_ds_read_tr8_b64_v2i32((__attribute__((address_space(3))) v2i*)vp);
+					const v2i hi =
+					    __builtin_amdgcn_ds_read_tr8_b64_v2i32((__attribute__((address_space(3))) v2i*)(vp + 8 * VS));
+					const v4i bv = v4i{lo.x, lo.y, hi.x, hi.y};
+#pragma unroll
+					for (int k = 0; k < 3; ++k) {
+						const v4i pa = *(const v4i*)&s_p[b][k][ri][kk2 * 64 + g * 16];
+						cacc[d2][k] = __builtin_amdgcn_mfma_i32_16x16x64_i8(pa, bv, cacc[d2][k], 0, 0, 0);
+					}
+				}
+			}
+		}
+	};
+	// V rows in groups of R steps, one group ahead: an iteration multiplies steps c0 R .. c0 R +
+	// 2R - 1 (groups c0 in vr0 and c0 + 1 in vr1) and stages each next step; group c0 + 1 is issued
+	// at its start (vr1's last reader was the previous iteration), group c0 + 2 once vr0's last
+	// step is staged
+	load_vr(0, vr0);
+	stage(0, vr0[0], 0);
+	__syncthreads();
+	// (the group loads are unconditional, as in pass 1)
+	for (int c0 = 0; c0 * R < nblk; c0 += 2) {
+		load_vr(c0 + 1, vr1);
+#pragma unroll
+		for (int jj = 0; jj < 2 * R; ++jj) {
+			const int j = c0 * R + jj;
+			if (jj == R - 1) load_vr(c0 + 2, vr0);
+			if (j >= nblk) break;
+			if (j + 1 < nblk) {
+				if (jj + 1 < R) stage(j + 1, vr0[jj + 1 < R ? jj + 1 : 0], (j + 1) & 1);
+				else if (jj + 1 < 2 * R) stage(j + 1, vr1[jj + 1 - R < R ? jj + 1 - R : 0], (j + 1) & 1);
+				else stage(j + 1, vr0[0], (j + 1) & 1);
+			}
+			multiply(j & 1);
+			__syncthreads();
+		}
+	}
+	// ---- epilogue: recombine, per-head fold, store, per-head maximum ----
+	int32_t f0[4], f1[4], f2[4];
+	bool rok[4];
+#pragma unroll
+	for (int v = 0; v < 4; ++v) {
+		const int r = g * 4 + v;
+		rok[v] = r < G && !(rf >> r & 1);
+		const int32_t* cf = a.ctx_fold + 3 * (h0 + (r < G ? r : 0));
+		f0[v] = cf[0];
+		f1[v] = cf[1];
+		f2[v] = cf[2];
+	}
+#pragma unroll
+	for (int d2 = 0; d2 < DTW; ++d2) {
+		const int dt = wave + NW * d2;
+		if (dt < DT) {
+			const int d = dt * 16 + ri;
+#pragma unroll
+			for (int v = 0; v < 4; ++v) {
+				const int r = g * 4 + v;
+				const int32_t c = (int32_t)(((uint32_t)cacc[d2][0][v] << 14) + ((uint32_t)cacc[d2][1][v] << 7) +
+				                            (uint32_t)cacc[d2][2][v]);
+				const int64_t f = apply_fold(c, f0[v], f1[v], f2[v]);
+				if (rok[v]) a.ctx_f[(size_t)t * H + (size_t)(h0 + r) * D + d] = sat_i32(f);
+				const uint32_t m = dpp_max16(rok[v] ? sat_abs_u32(f) : 0u);
+				if (ri == 0 && rok[v]) atomicMax(&s_mab[r], m);
+			}
+		}
+	}
+	__syncthreads();
+	if (i < G && !(rf >> i & 1)) a.ctx_maxpart[(size_t)(h0 + i) * kPartLd + t] = s_mab[i];
+}
+
 // Bench reference: a plain streaming read of `bytes` (a multiple of 16), four 16-byte loads per
 // thread in flight, XOR-reduced into a sink that is written only on an impossible value.  The
 // decode GEMV bench runs it over the same weight buffers in the same launch order as the GEMV
@@ -3769,7 +4218,96 @@ bool tiled_attention_enabled() {
 	}();
 	return on;
 }
-void attention_decode(const AttnArgs& a, hipStream_t s) { launch_attention<true>(a, s); }
+// The grouped decode kernel's dynamic LDS holds the [G][cap] int32 scores; with its static LDS
+// (read from the instantiation once) it must fit the CU's 160 KB, else one block per head runs.
+constexpr size_t kCuLds = 160 * 1024;  // gfx950: LDS per CU (one grouped block per CU)
+
+template <int D, int GM>
+static size_t group_attention_static_lds() {
+	static const size_t stat = [] {
+		const void* fn = reinterpret_cast<const void*>(&k_attention_group<D, 8, GM>);
+		hipFuncAttributes fa{};
+		if (hipFuncGetAttributes(&fa, fn) != hipSuccess) {
+			fprintf(stderr, "sslm_hip: k_attention_group attributes unavailable\n");
+			throw LaunchRefused{"attention_group"};
+		}
+		// allow the block the rest of the CU's LDS for its scores
+		if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)(kCuLds - fa.sharedSizeBytes)) != hipSuccess) {
+			fprintf(stderr, "sslm_hip: k_attention_group dynamic LDS limit refused\n");
+			throw LaunchRefused{"attention_group"};
+		}
+		return (size_t)fa.sharedSizeBytes;
+	}();
+	return stat;
+}
+
+// GM: the group size rounded up to 4, 8 or 16 (the softmax loops' unrolled row count); 0 when
+// the group does not fit the kernel (G * D / 2 <= 512 threads for the q post-processing)
+static int group_rows(int G, int D) {
+	const int gm = G <= 4 ? 4 : (G <= 8 ? 8 : (G <= 16 ? 16 : 0));
+	return gm && G * (D / 2) <= 512 && (D <= 64 || gm <= (D == 128 ? 8 : 4)) ? gm : 0;
+}
+
+template <int D, int GM>
+static bool launch_attention_group_gm(const AttnArgs& a, hipStream_t s) {
+	if (a.wcap < 1 || a.wcap % 128 != 0) return false;
+	const size_t dyn = (size_t)(a.NH / a.NKV) * (size_t)a.wcap * sizeof(int32_t);  // the [G][wcap] int32 scores
+	if (group_attention_static_lds<D, GM>() + dyn > kCuLds) return false;
+	hipLaunchKernelGGL((k_attention_group<D, 8, GM>), dim3(a.M * a.NKV), dim3(512), dyn, s, a);
+	return true;
+}
+
+template <int D>
+static bool launch_attention_group(const AttnArgs& a, hipStream_t s) {
+	switch (group_rows(a.NH / a.NKV, D)) {
+		case 4: return launch_attention_group_gm<D, 4>(a, s);
+		case 8: if constexpr (D <= 128) return launch_attention_group_gm<D, 8>(a, s); else return false;
+		case 16: if constexpr (D <= 64) return launch_attention_group_gm<D, 16>(a, s); else return false;
+		default: return false;
+	}
+}
+
+bool attention_prepare(int D, int G) {
+	try {
+		const int gm = group_rows(G, D);
+		if (D == 32 && gm == 4) (void)group_attention_static_lds<32, 4>();
+		if (D == 32 && gm == 8) (void)group_attention_static_lds<32, 8>();
+		if (D == 32 && gm == 16) (void)group_attention_static_lds<32, 16>();
+		if (D == 64 && gm == 4) (void)group_attention_static_lds<64, 4>();
+		if (D == 64 && gm == 8) (void)group_attention_static_lds<64, 8>();
+		if (D == 64 && gm == 16) (void)group_attention_static_lds<64, 16>();
+		if (D == 128 && gm == 4) (void)group_attention_static_lds<128, 4>();
+		if (D == 128 && gm == 8) (void)group_attention_static_lds<128, 8>();
+		if (D == 256 && gm == 4) (void)group_attention_static_lds<256, 4>();
+	} catch (const LaunchRefused&) {
+		return false;
+	}
+	return true;
+}
+
+bool grouped_attention_chosen(int M, int NKV, int64_t cap) {
+	// read per call: decode graphs carry the choice in their key, so a change takes effect at once
+	const char* e = getenv("SSLM_HIP_GROUPED_ATTN");
+	if (e && e[0]) return e[0] != '0';
+	// a block per (token, KV head) fills enough CUs only for batches of long rows; short rows and
+	// small batches run faster as one block per query head
+	return M * NKV >= 64 && cap >= 1024;
+}
+
+void attention_decode(const AttnArgs& a, hipStream_t s) {
+	if (grouped_attention_chosen(a.M, a.NKV, a.cap)) {
+		bool done = false;
+		switch (a.D) {
+			case 32: done = launch_attention_group<32>(a, s); break;
+			case 64: done = launch_attention_group<64>(a, s); break;
+			case 128: done = launch_attention_group<128>(a, s); break;
+			case 256: done = launch_attention_group<256>(a, s); break;
+			default: break;
+		}
+		if (done) return;  // else the shape does not fit the grouped kernel: one block per head
+	}
+	launch_attention<true>(a, s);
+}
 
 void funnel(const FunnelArgs& a, hipStream_t s) {
 	const int need = row_ept(a.N, kFunnelBS);

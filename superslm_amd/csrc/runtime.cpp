@@ -181,6 +181,7 @@ struct sslm_adapter_s {
 struct Track {
 	hipStream_t stream = nullptr;
 	int capacity = 0;  // tokens per launch
+	int32_t attn_wcap = 0;  // decode: the grouped attention's score-row length for the current unit
 	TokenInfo* tok;
 	int32_t *tok_ids, *ident, *slot_idx, *out_tokens;
 	int8_t *hid_chunk, *normed, *q_rot, *ctx, *attn_stream, *mlp_normed, *act, *final_codes;
@@ -748,6 +749,7 @@ sslm_launch::AttnArgs attn_args(sslm_model m, Track& w, int l, int M) {
 	a.NKV = m->NKV;
 	a.D = m->D;
 	a.cap = m->cap;
+	a.wcap = w.attn_wcap > 0 ? w.attn_wcap : sslm_launch::group_width_cap(m->cap, m->cap);
 	a.tok = w.tok;
 	a.khead_m = lw.khead_m;
 	a.khead_e = lw.khead_e;
@@ -1548,6 +1550,11 @@ bool build_device_model(sslm_model m, std::string* err) {
 	// of a decode step concurrently
 	m->tracks.resize(kTracks);
 	for (int i = 0; i < kTracks; ++i) alloc_track(m, m->tracks[i], i == 0 ? kMaxTokens : kTrackTokens, i == 0);
+	// kernel attributes are queried and set here, outside any graph capture
+	if (!sslm_launch::attention_prepare(m->D, m->NH / m->NKV)) {
+		*err = "decode attention kernel attributes could not be set";
+		return false;
+	}
 	return true;
 }
 
@@ -2166,10 +2173,17 @@ static sslm_status decode_batch(sslm_model m, sslm_seq* seqs, int32_t n, const s
 	std::deque<std::vector<TokenInfo>> h_tok;  // deque: references to earlier entries stay valid
 	std::deque<std::vector<int32_t>> h_i32;
 	std::deque<std::vector<const uint8_t*>> h_ptr;
+	// the grouped decode attention's score rows for a unit: from its widest row (pos + 1)
+	auto unit_wcap = [&](const Unit& un) {
+		int64_t mw = 1;
+		for (int i : un.idx) mw = std::max<int64_t>(mw, (int64_t)seqs[i]->context_length + 1);
+		return sslm_launch::group_width_cap(mw, m->cap);
+	};
 	auto stage_unit = [&](size_t u, hipStream_t s) {
 		const Unit& un = units[u];
 		Track& w = m->tracks[u % ntr];
 		const int M = (int)un.idx.size();
+		w.attn_wcap = unit_wcap(un);
 		h_tok.emplace_back(M);
 		std::vector<TokenInfo>& ti = h_tok.back();
 		h_i32.emplace_back(M);
@@ -2194,6 +2208,8 @@ static sslm_status decode_batch(sslm_model m, sslm_seq* seqs, int32_t n, const s
 		const Unit& un = units[u];
 		Track& w = m->tracks[u % ntr];
 		const int M = (int)un.idx.size();
+		w.attn_wcap = unit_wcap(un);
+		w.attn_wcap = unit_wcap(un);
 		// snapshot of the rows this unit changes, restored if an earlier sequence of the call refuses
 		sslm_launch::slot_state_copy(slot_copy_args(m, w.tok, (int)un.l0, (int)un.l1), M, false, w.stream);
 		ck(hipGetLastError());
@@ -2265,7 +2281,9 @@ static sslm_status decode_batch(sslm_model m, sslm_seq* seqs, int32_t n, const s
 					const Unit& un = units[u];
 					const std::string key = "u" + std::to_string(u % ntr) + "|" + std::to_string(un.idx.size()) + "|" +
 					                        std::to_string(un.l0) + "|" + std::to_string(un.l1) + "|" +
-					                        std::to_string((uintptr_t)un.ad) + "|" + std::to_string((uintptr_t)m->pool_dev);
+					                        std::to_string((uintptr_t)un.ad) + "|" + std::to_string((uintptr_t)m->pool_dev) +
+					                        (sslm_launch::grouped_attention_chosen((int)un.idx.size(), m->NKV, m->cap)
+					                             ? "|g" + std::to_string(unit_wcap(un)) : "");
 					capturing = true;
 					const hipGraphExec_t ge = graph_of(m, key, w.stream, [&] { launch_unit(u); });
 					capturing = false;

@@ -29,13 +29,17 @@ def _run(lib, art, prompts, calls, budget):
     return toks, kv, blobs
 
 
+@pytest.mark.parametrize("grouped", ["0", "1"])
 @pytest.mark.parametrize("lengths,budget,calls", [((1100, 1500, 1023), 2, 6), ((1100, 1500, 1023), 1, 9),
                                                   ((1020, 1018), 2, 12)])
-def test_long_rows_match_reference(lengths, budget, calls, hip_lib, ref_lib):
+def test_long_rows_match_reference(lengths, budget, calls, grouped, hip_lib, ref_lib, monkeypatch):
+    """grouped "1" forces decode attention to one block per (sequence, KV head), "0" to one block
+    per query head."""
+    monkeypatch.setenv("SSLM_HIP_GROUPED_ATTN", grouped)
     sm, art = synthetic("long")
     rng = np.random.default_rng(sum(lengths) + budget)
     prompts = [rng.integers(0, sm.config.vocab, size=n) for n in lengths]
-    print(f"case long decode lengths={lengths} budget={budget}", flush=True)
+    print(f"case long decode lengths={lengths} budget={budget} grouped={grouped}", flush=True)
     r = _run(ref_lib, art, prompts, calls, budget)
     h = _run(hip_lib, art, prompts, calls, budget)
     assert h[0] == r[0], f"tokens differ: hip {h[0]} ref {r[0]}"

@@ -177,10 +177,14 @@ def _bias_edit(layer, scale):
     return edit
 
 
-def test_numeric_refusal_at_later_layer(hip_lib, ref_lib):
+@pytest.mark.parametrize("grouped", ["0", "1"])
+def test_numeric_refusal_at_later_layer(grouped, hip_lib, ref_lib, monkeypatch):
     """A q bias pushed far out of range at layer 1 makes the q|k|v funnel refuse there (layer 0
     runs normally): prefill refuses and commits nothing; a sliced decode (budget 1) commits layer
-    0 and refuses at layer 1, leaving the sequence at layer 1, as the reference does."""
+    0 and refuses at layer 1, leaving the sequence at layer 1, as the reference does.  Decode
+    attention (where the q funnel runs) as one block per query head ("0") and one per KV head
+    ("1")."""
+    monkeypatch.setenv("SSLM_HIP_GROUPED_ATTN", grouped)
     from superslm_amd.sslm_artifact import CONFIGS, build_synthetic
     sm = build_synthetic(CONFIGS["small"], seed=7, edit=_bias_edit(1, 1 << 34))
     art = sm.to_bytes()
@@ -267,11 +271,14 @@ def _batch_script(lib, art, prompts, bad_index, bad_token, budget, calls):
 _LAYERS = [None]  # layer count of the model under test
 
 
+@pytest.mark.parametrize("grouped", ["0", "1"])
 @pytest.mark.parametrize("budget", [1, 2])
-def test_batched_decode_stops_at_first_refusal(budget, hip_lib, ref_lib):
+def test_batched_decode_stops_at_first_refusal(budget, grouped, hip_lib, ref_lib, monkeypatch):
     """A batch of three whose middle sequence refuses its pending token at layer 0: the first
     sequence advances, the refusing one and the one after it are left as they were (outputs
-    untouched, blobs unchanged), status as the reference's -- every call, at budget 1 and 2."""
+    untouched, blobs unchanged), status as the reference's -- every call, at budget 1 and 2, with
+    decode attention as one block per query head ("0") and one per KV head ("1")."""
+    monkeypatch.setenv("SSLM_HIP_GROUPED_ATTN", grouped)
     bad = 5
     sm, art = _zero_embed_model(bad)
     _LAYERS[0] = sm.config.layers

@@ -87,10 +87,14 @@ def sm7(fx):
 
 
 @pytest.mark.timeout(900)
-@pytest.mark.parametrize("budget,chunk", [(28, 128), (1, 50)])
-def test_config4_shape_against_reference(budget, chunk, fx, sm7, hip_lib):
+@pytest.mark.parametrize("budget,chunk,grouped", [(28, 128, ""), (1, 50, ""), (28, 128, "1")])
+def test_config4_shape_against_reference(budget, chunk, grouped, fx, sm7, hip_lib, monkeypatch):
+    """grouped "1": decode attention as one block per (sequence, KV head) with its 7 query heads
+    as the MFMA rows (the form batches of long rows take by themselves)."""
     want = fx["c4"]
-    print(f"case config4 7B budget={budget} chunk={chunk}", flush=True)
+    if grouped:
+        monkeypatch.setenv("SSLM_HIP_GROUPED_ATTN", grouped)
+    print(f"case config4 7B budget={budget} chunk={chunk} grouped={grouped}", flush=True)
     got = W.run_c4(hip_lib, sm7, budget, chunk)
     assert got == want
 
@@ -100,7 +104,8 @@ def test_config4_full_size_properties(sm7, hip_lib):
     """32 sequences with 2048-token prompts (one chunk each) decoded together at budget 28 for 256
     greedy steps (contexts grow to 2304 positions, as configuration 4 states), and a 33rd sequence
     with sequence 0's prompt in four 512-token chunks decoded alone at budget 1: its KV after
-    prefill, its 256 tokens and its final KV equal sequence 0's."""
+    prefill, its 256 tokens and its final KV equal sequence 0's.  The batch's decode attention runs
+    one block per (sequence, KV head), the solo sequence's one block per query head."""
     B, ctx, steps = 32, 2048, 256
     L = sm7.config.layers
     model = Model(hip_lib, sm7.to_array())
