@@ -294,3 +294,30 @@ def test_batched_decode_stops_at_first_refusal(budget, grouped, hip_lib, ref_lib
         assert hh[1] == rr[1], (c, hh[1], rr[1])
         for i in range(3):
             assert hh[2][i] == rr[2][i], f"call {c}: blob of sequence {i} differs"
+
+
+ATTN_MODES = {"head": "0", "group": "1"}
+
+
+@pytest.mark.parametrize("shift", [40, -40])
+@pytest.mark.parametrize("mode", list(ATTN_MODES))
+def test_attention_refusal_in_decode(mode, shift, hip_lib, ref_lib, monkeypatch):
+    """Layer 1's second K head scale shifted by 2^shift: the i-exp constants of that KV group's
+    heads refuse (the loader accepts the artifact).  A sequence restored with a pending token
+    commits layer 0 at budget 1, then refuses at layer 1's attention, call after call, with the
+    reference's status, K/V rows and saturation count (every KV group lands before attention);
+    decode attention as one block per query head and one per (sequence, KV group)."""
+    monkeypatch.setenv("SSLM_HIP_GROUPED_ATTN", ATTN_MODES[mode])
+    from superslm_amd.sslm_artifact import CONFIGS, build_synthetic
+
+    def edit(m):
+        km, ke = m.consts["layer1.softmax_khead1"]
+        m.consts["layer1.softmax_khead1"] = (km, ke + shift)
+    sm = build_synthetic(CONFIGS["tiny"], seed=7, edit=edit)
+    L = sm.config.layers
+    # (a fresh sequence's blob with a pending token: a prefill refused at the attention stage
+    # leaves staged K/V past the committed context that differs by design)
+    steps = [("restore_patched", CURRENT_TOKEN_OFFSET, "<i", 3),
+             ("decode", 1), ("save",), ("decode", 1), ("save",), ("decode", 1), ("save",), ("decode", L), ("save",)]
+    h, _ = _run_both(hip_lib, ref_lib, sm.to_bytes(), steps, f"attention refusal {mode} shift={shift}")
+    assert h[1] == (0, -1) and h[3][0] != 0, (h[1], h[3])
