@@ -236,6 +236,34 @@ def vendor_gemm_reference():
     return out
 
 
+def gemv_class_passes(hip, model, M):
+    """Per projection class: the GEMV pass (all layers' launches of one class back to back) and the
+    same launches as plain streaming reads of their weights, at M tokens; fractions of 8 TB/s."""
+    L_ = hip.lib
+    L_.sslm_hip_bench_decode_gemv.restype = ctypes.c_int32
+    L_.sslm_hip_bench_decode_gemv.argtypes = [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32] + \
+        [ctypes.c_void_p] * 3 + [ctypes.c_int32]
+    L_.sslm_hip_bench_read_floor.restype = ctypes.c_int32
+    L_.sslm_hip_bench_read_floor.argtypes = L_.sslm_hip_bench_decode_gemv.argtypes
+    out = {}
+    res = []
+    for fn in (L_.sslm_hip_bench_decode_gemv, L_.sslm_hip_bench_read_floor):
+        us, by, n = (ctypes.c_double * 6)(), (ctypes.c_int64 * 6)(), (ctypes.c_int64 * 6)()
+        if fn(model.handle, M, 5, us, by, n, 6) != 1:
+            raise RuntimeError("GEMV class pass failed")
+        res.append((us, by, n))
+    (gu, gb, gn), (ru, rb, rn) = res
+    for c, name in enumerate(("q|k|v", "o", "gate|up", "down", "lm_head"), start=1):
+        out[name] = {"us_per_launch": round(gu[c] / gn[c], 2), "MB_per_launch": round(gb[c] / gn[c] / 1e6, 2),
+                     "frac": round(gb[c] / (gu[c] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                     "read_us_per_launch": round(ru[c] / rn[c], 2),
+                     "read_frac": round(rb[c] / (ru[c] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+    out["pass"] = {"frac": round(gb[0] / (gu[0] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                   "read_frac": round(rb[0] / (ru[0] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                   "us": round(gu[0], 1), "read_us": round(ru[0], 1)}
+    return out
+
+
 def config4(hip, args):
     """BASELINE configuration 4 at one GPU's share: the 7B shape (H 3584, I 18944, 28 layers,
     28 / 4 heads, context cap 4608), 32 sequences each prefilled with a 2048-token prompt in one
@@ -295,6 +323,7 @@ def config4(hip, args):
                                                 "lm_head_per_step": round(ms[1] * 1e3 / n_prof, 2)}
     out["config4_7b"]["decode_attention_kv_gbs"] = round(kv_bytes / (attn_us * 1e-6) / 1e9, 1)
     print(f"[bench] config4 decode per layer: attention {attn_us} us", file=sys.stderr, flush=True)
+    out["config4_7b"]["decode_gemv_by_class"] = gemv_class_passes(hip, model, B)
     for s in seqs:
         s.release()
     pool.close()

@@ -239,6 +239,7 @@ struct AttnArgs {
 	SiteTap q_tap;              // attention_decode: the rotated q codes of each head, and the q scale
 	int32_t wcap;               // attention_decode: score rows of the grouped kernel, a multiple of 128
 	                            // at least every width (pos + 1) of the launch (group_width_cap)
+	int32_t row_halves;         // attention_decode, grouped kernel: 1, or 2 blocks per (token, KV group)
 };
 // The grouped decode kernel's score-row length for a launch whose widest row is `max_width`:
 // rounded up to 512 (so a decode graph keyed by it is re-recorded once per 512 positions), at
@@ -258,6 +259,9 @@ void attention_decode(const AttnArgs& a, hipStream_t s);
 // attention_decode runs one block per (token, KV head) for this launch shape when the shape fits
 // (SSLM_HIP_GROUPED_ATTN=1 forces it wherever it fits, =0 turns it off)
 bool grouped_attention_chosen(int M, int NKV, int64_t cap);
+// blocks per (token, KV group) of the grouped decode attention: 2 splits the group's query heads
+// in halves (SSLM_HIP_GROUP_HALVES=1|2 overrides)
+int group_row_halves(int M, int NKV, int G);
 // Queries and sets the grouped decode kernel's LDS attributes for head size D and group size G
 // (once per process; call before any capture).  False when the runtime refuses them.
 bool attention_prepare(int D, int G);

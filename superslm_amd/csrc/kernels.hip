@@ -3166,8 +3166,20 @@ __global__ __launch_bounds__(64 * NW, 1) void k_attention_group(sslm_launch::Att
 	__shared__ int32_t s_st, s_rmx[TQ];
 	__shared__ int32_t s_dump[BS];  // where rows G .. GM - 1 of the softmax loops store
 	const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, ri = lane & 15, g = lane >> 4, i = threadIdx.x;
-	const int G = a.NH / a.NKV, H = a.H, KVH = a.NKV * D;
-	const int t = blockIdx.x / a.NKV, kvh = blockIdx.x % a.NKV, h0 = kvh * G;
+	const int H = a.H, KVH = a.NKV * D, GG = a.NH / a.NKV;
+	// a.row_halves = 2: two blocks per (token, KV group), numbered 16 k + 8 h + x (x < 8) for group
+	// 8 k + x and row half h, so both halves sit on XCD x (blocks go to the XCDs round-robin) and
+	// the second reads the group's K/V from that XCD's L2; ids past the last group exit
+	int gi = blockIdx.x, rh = 0;
+	if (a.row_halves == 2) {
+		gi = (blockIdx.x >> 4) * 8 + (blockIdx.x & 7);
+		rh = (blockIdx.x >> 3) & 1;
+		if (gi >= a.M * a.NKV) return;
+	}
+	const int t = gi / a.NKV, kvh = gi % a.NKV;
+	// this block's rows: heads h0 .. h0 + G - 1 of the group (all of them, or one half)
+	const int gh = a.row_halves == 2 ? (GG + 1) / 2 : GG;
+	const int G = rh == 0 ? gh : GG - gh, h0 = kvh * GG + rh * gh;
 	const TokenInfo ti = a.tok[t];
 	const int64_t pos = ti.pos, width = pos + 1, cap = a.cap;
 	const bool pos_ok = pos >= 0 && pos < cap;
@@ -3222,7 +3234,8 @@ __global__ __launch_bounds__(64 * NW, 1) void k_attention_group(sslm_launch::Att
 		if (i == 0) set_status(a.status, ti.slot, a.layer, st);
 		return;
 	}
-	// K/V landing of this KV head at pos (this block is its only writer)
+	// K/V landing of this KV head at pos: every block of the group keeps it in LDS, row half 0's
+	// writes it to the cache and counts its saturations (no block reads what another writes)
 	uint32_t sat = 0;
 	if (i < PAIRS) {
 		bool c0, c1, c2, c3, x0;
@@ -3233,13 +3246,15 @@ __global__ __launch_bounds__(64 * NW, 1) void k_attention_group(sslm_launch::Att
 		const char2 kc = make_char2((char)clamp_code(xr), (char)clamp_code(yr));
 		const char2 vc = make_char2((char)clamp_code(landing_rescale(vv.x, ns.m, rtv, v_e, &c2, &x0)),
 		                            (char)clamp_code(landing_rescale(vv.y, ns.m, rtv, v_e, &c3, &x0)));
-		sat = (uint32_t)c0 + (uint32_t)c1 + (uint32_t)c2 + (uint32_t)c3;
 		((char2*)s_kc)[i] = kc;
 		((char2*)s_vc)[i] = vc;
-		int8_t* kstore = const_cast<int8_t*>(kbase);
-		const int64_t off = pos * D + 2 * i;
-		*(char2*)(kstore + off) = kc;
-		*(char2*)(kstore + half + off) = vc;
+		if (rh == 0) {  // the group's writer
+			sat = (uint32_t)c0 + (uint32_t)c1 + (uint32_t)c2 + (uint32_t)c3;
+			int8_t* kstore = const_cast<int8_t*>(kbase);
+			const int64_t off = pos * D + 2 * i;
+			*(char2*)(kstore + off) = kc;
+			*(char2*)(kstore + half + off) = vc;
+		}
 	}
 	{
 		const int32_t ws = wave_sum32((int32_t)sat);
@@ -3270,7 +3285,7 @@ __global__ __launch_bounds__(64 * NW, 1) void k_attention_group(sslm_launch::Att
 	__syncthreads();
 	if (a.q_tap.codes) {
 		for (int k2 = i; k2 < G * D; k2 += BS) a.q_tap.codes[(size_t)t * a.q_tap.ld + (size_t)h0 * D + k2] = s_qc[k2 / D][k2 % D];
-		if (i == 0 && kvh == 0) a.q_tap.scale[t] = qs;
+		if (i == 0 && kvh == 0 && rh == 0) a.q_tap.scale[t] = qs;
 	}
 	// (width <= wcap holds by construction: the host sizes wcap from the launch's positions)
 	const bool live = st == kOk && width >= 1 && width <= cap && width <= a.wcap;
@@ -4248,18 +4263,26 @@ static int group_rows(int G, int D) {
 	return gm && G * (D / 2) <= 512 && (D <= 64 || gm <= (D == 128 ? 8 : 4)) ? gm : 0;
 }
 
+// rows per block: the group, or its first half (the second takes the rest)
+static int group_block_rows(const AttnArgs& a) {
+	const int G = a.NH / a.NKV;
+	return a.row_halves == 2 ? (G + 1) / 2 : G;
+}
+
 template <int D, int GM>
 static bool launch_attention_group_gm(const AttnArgs& a, hipStream_t s) {
-	if (a.wcap < 1 || a.wcap % 128 != 0) return false;
-	const size_t dyn = (size_t)(a.NH / a.NKV) * (size_t)a.wcap * sizeof(int32_t);  // the [G][wcap] int32 scores
+	if (a.wcap < 1 || a.wcap % 128 != 0 || !(a.row_halves == 1 || a.row_halves == 2)) return false;
+	const size_t dyn = (size_t)group_block_rows(a) * (size_t)a.wcap * sizeof(int32_t);  // the [rows][wcap] int32 scores
 	if (group_attention_static_lds<D, GM>() + dyn > kCuLds) return false;
-	hipLaunchKernelGGL((k_attention_group<D, 8, GM>), dim3(a.M * a.NKV), dim3(512), dyn, s, a);
+	const int groups = a.M * a.NKV;
+	const int grid = a.row_halves == 2 ? (groups + 7) / 8 * 16 : groups;  // see the block numbering
+	hipLaunchKernelGGL((k_attention_group<D, 8, GM>), dim3(grid), dim3(512), dyn, s, a);
 	return true;
 }
 
 template <int D>
 static bool launch_attention_group(const AttnArgs& a, hipStream_t s) {
-	switch (group_rows(a.NH / a.NKV, D)) {
+	switch (group_rows(group_block_rows(a), D)) {
 		case 4: return launch_attention_group_gm<D, 4>(a, s);
 		case 8: if constexpr (D <= 128) return launch_attention_group_gm<D, 8>(a, s); else return false;
 		case 16: if constexpr (D <= 64) return launch_attention_group_gm<D, 16>(a, s); else return false;
@@ -4267,7 +4290,15 @@ static bool launch_attention_group(const AttnArgs& a, hipStream_t s) {
 	}
 }
 
+static bool attention_prepare_rows(int D, int G);
+
 bool attention_prepare(int D, int G) {
+	for (const int rows : {G, (G + 1) / 2})
+		if (!attention_prepare_rows(D, rows)) return false;
+	return true;
+}
+
+static bool attention_prepare_rows(int D, int G) {
 	try {
 		const int gm = group_rows(G, D);
 		if (D == 32 && gm == 4) (void)group_attention_static_lds<32, 4>();
@@ -4283,6 +4314,13 @@ bool attention_prepare(int D, int G) {
 		return false;
 	}
 	return true;
+}
+
+int group_row_halves(int M, int NKV, int G) {
+	const char* e = getenv("SSLM_HIP_GROUP_HALVES");  // read per call, as below
+	if (e && e[0]) return e[0] == '2' && G >= 2 ? 2 : 1;
+	// two blocks per group while that still leaves no CU with two
+	return G >= 2 && 2 * M * NKV <= 256 ? 2 : 1;
 }
 
 bool grouped_attention_chosen(int M, int NKV, int64_t cap) {

@@ -750,6 +750,7 @@ sslm_launch::AttnArgs attn_args(sslm_model m, Track& w, int l, int M) {
 	a.D = m->D;
 	a.cap = m->cap;
 	a.wcap = w.attn_wcap > 0 ? w.attn_wcap : sslm_launch::group_width_cap(m->cap, m->cap);
+	a.row_halves = sslm_launch::group_row_halves(M, m->NKV, m->NH / m->NKV);
 	a.tok = w.tok;
 	a.khead_m = lw.khead_m;
 	a.khead_e = lw.khead_e;
@@ -2283,7 +2284,10 @@ static sslm_status decode_batch(sslm_model m, sslm_seq* seqs, int32_t n, const s
 					                        std::to_string(un.l0) + "|" + std::to_string(un.l1) + "|" +
 					                        std::to_string((uintptr_t)un.ad) + "|" + std::to_string((uintptr_t)m->pool_dev) +
 					                        (sslm_launch::grouped_attention_chosen((int)un.idx.size(), m->NKV, m->cap)
-					                             ? "|g" + std::to_string(unit_wcap(un)) : "");
+					                             ? "|g" + std::to_string(unit_wcap(un)) + "h" +
+					                                   std::to_string(sslm_launch::group_row_halves(
+					                                       (int)un.idx.size(), m->NKV, m->NH / m->NKV))
+					                             : "");
 					capturing = true;
 					const hipGraphExec_t ge = graph_of(m, key, w.stream, [&] { launch_unit(u); });
 					capturing = false;

@@ -272,18 +272,21 @@ def test_tiled_prefill_attention_matches_reference(waves, hip_lib, ref_lib, monk
         model.close()
 
 
+@pytest.mark.parametrize("halves", ["1", "2"])
 @pytest.mark.parametrize("name", ["tiny", "small", "medium"])
-def test_grouped_decode_attention_matches_reference(name, hip_lib, ref_lib, monkeypatch):
+def test_grouped_decode_attention_matches_reference(name, halves, hip_lib, ref_lib, monkeypatch):
     """Decode attention forced to one block per (sequence, KV head), the group's query heads the
-    rows of the MFMA tiles (G = 2, 4, 4; D = 32, 64, 128): tokens and every KV byte as the
-    reference, at budget 1 and at the full depth, decoding past the prompt."""
+    rows of the MFMA tiles (G = 2, 4, 4; D = 32, 64, 128), or two blocks per group each taking half
+    of its heads (halves "2"): tokens and every KV byte as the reference, at budget 1 and at the
+    full depth, decoding past the prompt."""
     monkeypatch.setenv("SSLM_HIP_GROUPED_ATTN", "1")
+    monkeypatch.setenv("SSLM_HIP_GROUP_HALVES", halves)
     sm, art = synthetic(name)
     rng = np.random.default_rng(23)
     prompt = rng.integers(0, sm.config.vocab, size=40)
     L = sm.config.layers
     for budget in sorted({1, L}):
-        print(f"case grouped attention {name} budget={budget}", flush=True)
+        print(f"case grouped attention {name} halves={halves} budget={budget}", flush=True)
         r = _run(ref_lib, art, prompt, 8, budget)
         h = _run(hip_lib, art, prompt, 8, budget)
         assert np.array_equal(h[1], r[1]), "KV after prefill differs"

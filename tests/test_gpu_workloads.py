@@ -87,13 +87,15 @@ def sm7(fx):
 
 
 @pytest.mark.timeout(900)
-@pytest.mark.parametrize("budget,chunk,grouped", [(28, 128, ""), (1, 50, ""), (28, 128, "1")])
+@pytest.mark.parametrize("budget,chunk,grouped", [(28, 128, ""), (1, 50, ""), (28, 128, "1"), (28, 128, "1h")])
 def test_config4_shape_against_reference(budget, chunk, grouped, fx, sm7, hip_lib, monkeypatch):
     """grouped "1": decode attention as one block per (sequence, KV head) with its 7 query heads
-    as the MFMA rows (the form batches of long rows take by themselves)."""
+    as the MFMA rows; "1h": two blocks per (sequence, KV head), 4 and 3 of its heads (the form
+    batches of long rows take by themselves)."""
     want = fx["c4"]
     if grouped:
-        monkeypatch.setenv("SSLM_HIP_GROUPED_ATTN", grouped)
+        monkeypatch.setenv("SSLM_HIP_GROUPED_ATTN", "1")
+        monkeypatch.setenv("SSLM_HIP_GROUP_HALVES", "2" if grouped == "1h" else "1")
     print(f"case config4 7B budget={budget} chunk={chunk} grouped={grouped}", flush=True)
     got = W.run_c4(hip_lib, sm7, budget, chunk)
     assert got == want
