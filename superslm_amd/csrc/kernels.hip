@@ -3165,6 +3165,7 @@ __global__ __launch_bounds__(64 * NW, 1) void k_attention_group(sslm_launch::Att
 	__shared__ uint32_t s_qm[NW], s_mab[TQ], s_rf[TQ];
 	__shared__ int32_t s_st, s_rmx[TQ];
 	__shared__ int32_t s_dump[BS];  // where rows G .. GM - 1 of the softmax loops store
+	__shared__ int64_t s_cst[5];     // the rows' i-exp constants and verdict (one thread derives them)
 	const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, ri = lane & 15, g = lane >> 4, i = threadIdx.x;
 	const int H = a.H, KVH = a.NKV * D, GG = a.NH / a.NKV;
 	// a.row_halves = 2: two blocks per (token, KV group), numbered 16 k + 8 h + x (x < 8) for group
@@ -3191,7 +3192,11 @@ __global__ __launch_bounds__(64 * NW, 1) void k_attention_group(sslm_launch::Att
 	const uint32_t qm0 = a.q_maxpart[(size_t)(i < ntq ? i : ntq - 1) * kPartLd + t];
 	const int qi = i < G * PAIRS ? i : G * PAIRS - 1, qr = qi / PAIRS, qj = qi % PAIRS;
 	const int2 qv = ((const int2*)(a.q_f + (size_t)t * H + (size_t)(h0 + qr) * D))[qj];
-	const int ki = i < PAIRS ? i : PAIRS - 1;
+	// the prologue's three independent jobs run on different waves: q codes on threads
+	// [0, G PAIRS), the K/V landing on the last PAIRS threads, the i-exp constants on one thread
+	// between them (or the last, when the others leave none free)
+	constexpr int LB = BS - PAIRS;  // first landing thread
+	const int ki = i >= LB ? i - LB : 0;
 	const int64_t* kvrow = a.kv_f + (size_t)t * 2 * KVH + (size_t)kvh * D;
 	const longlong2 kk = ((const longlong2*)kvrow)[ki], vv = ((const longlong2*)(kvrow + KVH))[ki];
 	const int64_t pp = pos_ok ? pos : 0;
@@ -3219,8 +3224,8 @@ __global__ __launch_bounds__(64 * NW, 1) void k_attention_group(sslm_launch::Att
 	const int64_t k_e = composed_exponent(ns.e, a.e_t_k[kvh]), v_e = composed_exponent(ns.e, a.e_t_v[kvh]);
 	const int64_t km = a.khead_m[kvh], ke = a.khead_e[kvh];
 	if (i == 0) s_st = a.status[ti.slot];
-	for (int k2 = i; k2 < TQ * D; k2 += BS) (&s_qc[0][0])[k2] = 0;
-	for (int k2 = i; k2 < 2 * 3 * TQ * PS; k2 += BS) (&s_p[0][0][0][0])[k2] = 0;
+	for (int k2 = i; k2 < TQ * D / 16; k2 += BS) ((v4i*)&s_qc[0][0])[k2] = v4i{0, 0, 0, 0};
+	for (int k2 = i; k2 < 2 * 3 * TQ * PS / 16; k2 += BS) ((v4i*)&s_p[0][0][0][0])[k2] = v4i{0, 0, 0, 0};
 	if (i < TQ) {
 		s_mab[i] = 0;
 		s_rf[i] = 0;
@@ -3237,7 +3242,7 @@ __global__ __launch_bounds__(64 * NW, 1) void k_attention_group(sslm_launch::Att
 	// K/V landing of this KV head at pos: every block of the group keeps it in LDS, row half 0's
 	// writes it to the cache and counts its saturations (no block reads what another writes)
 	uint32_t sat = 0;
-	if (i < PAIRS) {
+	if (i >= LB) {
 		bool c0, c1, c2, c3, x0;
 		const int64_t k0 = clamp_code(landing_rescale(kk.x, ns.m, rtk, k_e, &c0, &x0));
 		const int64_t k1 = clamp_code(landing_rescale(kk.y, ns.m, rtk, k_e, &c1, &x0));
@@ -3246,12 +3251,12 @@ __global__ __launch_bounds__(64 * NW, 1) void k_attention_group(sslm_launch::Att
 		const char2 kc = make_char2((char)clamp_code(xr), (char)clamp_code(yr));
 		const char2 vc = make_char2((char)clamp_code(landing_rescale(vv.x, ns.m, rtv, v_e, &c2, &x0)),
 		                            (char)clamp_code(landing_rescale(vv.y, ns.m, rtv, v_e, &c3, &x0)));
-		((char2*)s_kc)[i] = kc;
-		((char2*)s_vc)[i] = vc;
+		((char2*)s_kc)[ki] = kc;
+		((char2*)s_vc)[ki] = vc;
 		if (rh == 0) {  // the group's writer
 			sat = (uint32_t)c0 + (uint32_t)c1 + (uint32_t)c2 + (uint32_t)c3;
 			int8_t* kstore = const_cast<int8_t*>(kbase);
-			const int64_t off = pos * D + 2 * i;
+			const int64_t off = pos * D + 2 * ki;
 			*(char2*)(kstore + off) = kc;
 			*(char2*)(kstore + half + off) = vc;
 		}
@@ -3269,20 +3274,30 @@ __global__ __launch_bounds__(64 * NW, 1) void k_attention_group(sslm_launch::Att
 	}
 	const Scale qs = plan.out;
 	// i-exp constants of the rows' common scale (the q scale is the token's, km / ke the KV head's)
-	int64_t c_qln2 = 0, c_qb = 0, c_qc = 0, c_M = 0;
-	if (!fits_i32(qs.m) || !fits_i32(km)) {
-		st = kCarriedScaleMantissaOutOfDomain;
-	} else {
-		const Scale sm = combine_scale(qs, Scale{km, ke});
-		if (!fits_i32(sm.m)) st = kCarriedScaleMantissaOutOfDomain;
-		else if (iexp_scale_constants(sm.m, sm.e, a.ln2_q, a.b_q, a.ca_q, &c_qln2, &c_qb, &c_qc) != 0)
-			st = kIExpScaleDerivationOutOfDomain;
-		else {
-			st = check_softmax_width(c_qb, c_qc, width);
-			c_M = softmax_ceiling(c_qb, c_qc);
+	if (i == (LB - 1 >= G * PAIRS ? LB - 1 : BS - 1)) {
+		int64_t q0 = 0, q1 = 0, q2 = 0, q3 = 0;
+		int32_t cst = kOk;
+		if (!fits_i32(qs.m) || !fits_i32(km)) {
+			cst = kCarriedScaleMantissaOutOfDomain;
+		} else {
+			const Scale sm = combine_scale(qs, Scale{km, ke});
+			if (!fits_i32(sm.m)) cst = kCarriedScaleMantissaOutOfDomain;
+			else if (iexp_scale_constants(sm.m, sm.e, a.ln2_q, a.b_q, a.ca_q, &q0, &q1, &q2) != 0)
+				cst = kIExpScaleDerivationOutOfDomain;
+			else {
+				cst = check_softmax_width(q1, q2, width);
+				q3 = softmax_ceiling(q1, q2);
+			}
 		}
+		s_cst[0] = q0;
+		s_cst[1] = q1;
+		s_cst[2] = q2;
+		s_cst[3] = q3;
+		s_cst[4] = cst;
 	}
 	__syncthreads();
+	const int64_t c_qln2 = s_cst[0], c_qb = s_cst[1], c_qc = s_cst[2], c_M = s_cst[3];
+	st = (int32_t)s_cst[4];
 	if (a.q_tap.codes) {
 		for (int k2 = i; k2 < G * D; k2 += BS) a.q_tap.codes[(size_t)t * a.q_tap.ld + (size_t)h0 * D + k2] = s_qc[k2 / D][k2 % D];
 		if (i == 0 && kvh == 0 && rh == 0) a.q_tap.scale[t] = qs;
