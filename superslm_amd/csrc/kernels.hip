@@ -3155,7 +3155,7 @@ __global__ __launch_bounds__(64 * NW, 1) void k_attention_group(sslm_launch::Att
 	constexpr int PAIRS = D / 2, DTW = (DT + NW - 1) / NW, VCH = KB * (D / 16), VPT = (VCH + BS - 1) / BS;
 	// K and V rows are issued R steps at a time, one group of R steps ahead of the one consumed:
 	// a step's rows alone (16 KB per block at D = 128) leave the CU waiting a round trip per step
-	constexpr int R = D <= 128 ? 4 : 2;
+	constexpr int R = D <= 128 ? 4 : 2, RK = R;  // V and K steps per group
 	extern __shared__ __attribute__((aligned(16))) int32_t s_sc[];     // [G][wcap] scores
 	__shared__ __attribute__((aligned(16))) int8_t s_p[2][3][TQ][PS];  // probability parts [buffer][part][row][pos]
 	__shared__ __attribute__((aligned(16))) int8_t s_v[2][KB][VS];     // V rows [buffer][pos][dim]
@@ -3182,6 +3182,11 @@ __global__ __launch_bounds__(64 * NW, 1) void k_attention_group(sslm_launch::Att
 	const int gh = a.row_halves == 2 ? (GG + 1) / 2 : GG;
 	const int G = rh == 0 ? gh : GG - gh, h0 = kvh * GG + rh * gh;
 	const TokenInfo ti = a.tok[t];
+	// the KV head's scalar constants and the status word first: their round trip overlaps the
+	// vector loads below instead of following them
+	const int64_t rtk = a.r_t_k[kvh], rtv = a.r_t_v[kvh], etk = a.e_t_k[kvh], etv = a.e_t_v[kvh];
+	const int64_t km = a.khead_m[kvh], ke = a.khead_e[kvh];
+	const int32_t status0 = a.status[ti.slot];
 	const int64_t pos = ti.pos, width = pos + 1, cap = a.cap;
 	const bool pos_ok = pos >= 0 && pos < cap;
 	const int64_t half = cap * (int64_t)KVH;
@@ -3212,18 +3217,18 @@ __global__ __launch_bounds__(64 * NW, 1) void k_attention_group(sslm_launch::Att
 			kb[c] = off < D ? load16(kbase + pr * D + off) : v4i{0, 0, 0, 0};
 		}
 	};
-	v4i kb0[R][NC], kb1[R][NC];
-	auto load_kr = [&](int c0, v4i (&kb)[R][NC]) {
+	v4i kb0[RK][NC], kb1[RK][NC];
+	auto load_kr = [&](int c0, v4i (&kb)[RK][NC]) {
 #pragma unroll
-		for (int j = 0; j < R; ++j) load_k(c0 * R + j, kb[j]);
+		for (int j = 0; j < RK; ++j) load_k(c0 * RK + j, kb[j]);
 	};
 	load_kr(0, kb0);
 	uint32_t qmx = i < ntq ? qm0 : 0u;
 	for (int k2 = i + BS; k2 < ntq; k2 += BS) qmx = max(qmx, a.q_maxpart[(size_t)k2 * kPartLd + t]);
-	const int64_t rtk = a.r_t_k[kvh], rtv = a.r_t_v[kvh];
-	const int64_t k_e = composed_exponent(ns.e, a.e_t_k[kvh]), v_e = composed_exponent(ns.e, a.e_t_v[kvh]);
-	const int64_t km = a.khead_m[kvh], ke = a.khead_e[kvh];
-	if (i == 0) s_st = a.status[ti.slot];
+	const int64_t k_e = composed_exponent(ns.e, etk), v_e = composed_exponent(ns.e, etv);
+	// one reading of the status word for the whole block (another block of the token may set it
+	// while this one runs)
+	if (i == 0) s_st = status0;
 	for (int k2 = i; k2 < TQ * D / 16; k2 += BS) ((v4i*)&s_qc[0][0])[k2] = v4i{0, 0, 0, 0};
 	for (int k2 = i; k2 < 2 * 3 * TQ * PS / 16; k2 += BS) ((v4i*)&s_p[0][0][0][0])[k2] = v4i{0, 0, 0, 0};
 	if (i < TQ) {
@@ -3338,10 +3343,10 @@ __global__ __launch_bounds__(64 * NW, 1) void k_attention_group(sslm_launch::Att
 			}
 		}
 	};
-	const int ngr = (nblk + R - 1) / R;  // groups of R steps (steps past the row score nothing)
-	auto score_group = [&](int c0, v4i (&kb)[R][NC]) {
+	const int ngr = (nblk + RK - 1) / RK;  // groups of RK steps (steps past the row score nothing)
+	auto score_group = [&](int c0, v4i (&kb)[RK][NC]) {
 #pragma unroll
-		for (int j = 0; j < R; ++j) score_step(c0 * R + j, kb[j]);
+		for (int j = 0; j < RK; ++j) score_step(c0 * RK + j, kb[j]);
 	};
 	// the group loads are unconditional (rows past the width read row 0, a cache hit): a load
 	// issued on one path only would make every later wait drain all loads in flight
