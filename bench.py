@@ -293,9 +293,14 @@ def config4(hip, args):
     hip.lib.sslm_hip_synchronize()
     pre_s = time.perf_counter() - t0
     print(f"[bench] config4 prefill {B} x {ctx}: {pre_s:.2f} s, {B * ctx / pre_s:.0f} tok/s", file=sys.stderr, flush=True)
+    # attention kernel time of the first decode steps (rows of 2,049-2,050 positions) under the
+    # HIP-event profiler; they are the warm steps of the timed run below
+    profile(hip, True)
     for _ in range(3):
         model.decode_step(seqs, cfg.layers)
     hip.lib.sslm_hip_synchronize()
+    ms0, la0, _, _ = profile_read(hip)
+    profile(hip, False)
     steps = 253
     t0 = time.perf_counter()
     for _ in range(steps):
@@ -308,7 +313,7 @@ def config4(hip, args):
                           "decode_ms_per_step": round(dt * 1e3 / steps, 3), "decode_steps": steps}}
     print(f"[bench] config4 decode: {out['config4_7b']['decode_tok_s']} tok/s", file=sys.stderr, flush=True)
     # per-class kernel time of a few more steps under the runtime's HIP-event profiler (graphs off
-    # while it runs; contexts 2307-2314)
+    # while it runs; contexts 2308-2315)
     n_prof = 8
     profile(hip, True)
     for _ in range(n_prof):
@@ -321,6 +326,8 @@ def config4(hip, args):
     attn_us = per_layer(2)
     out["config4_7b"]["decode_us_per_layer"] = {"attention": attn_us, "gemm": per_layer(0), "rows": per_layer(3),
                                                 "lm_head_per_step": round(ms[1] * 1e3 / n_prof, 2)}
+    # (one attention launch per layer; the first call after a prefill only takes logits)
+    out["config4_7b"]["decode_attention_us_per_layer_first_steps"] = round(ms0[2] * 1e3 / max(1, la0[2]), 2)
     out["config4_7b"]["decode_attention_kv_gbs"] = round(kv_bytes / (attn_us * 1e-6) / 1e9, 1)
     print(f"[bench] config4 decode per layer: attention {attn_us} us", file=sys.stderr, flush=True)
     out["config4_7b"]["decode_gemv_by_class"] = gemv_class_passes(hip, model, B)

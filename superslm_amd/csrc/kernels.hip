@@ -3357,6 +3357,24 @@ __global__ __launch_bounds__(64 * NW, 1) void k_attention_group(sslm_launch::Att
 		load_kr(c0 + 2, kb0);
 		score_group(c0 + 1, kb1);
 	}
+	// the first V steps do not depend on the softmax: they are in flight through passes 2 and 3's
+	// arithmetic
+	auto load_v = [&](int blk, v4i (&vr)[VPT]) {
+#pragma unroll
+		for (int u = 0; u < VPT; ++u) {
+			const int c = i + u * BS;
+			const int pr = c / (D / 16), ch = c % (D / 16);
+			const int64_t p = (int64_t)blk * KB + pr;
+			const int64_t pl = p < width && p != pos && p < cap ? p : 0;
+			vr[u] = c < VCH ? load16(vbase + pl * D + ch * 16) : v4i{0, 0, 0, 0};
+		}
+	};
+	v4i vr0[R][VPT], vr1[R][VPT];
+	auto load_vr = [&](int c0, v4i (&vr)[R][VPT]) {
+#pragma unroll
+		for (int j = 0; j < R; ++j) load_v(c0 * R + j, vr[j]);
+	};
+	load_vr(0, vr0);
 #pragma unroll
 	for (int v = 0; v < 4; ++v) {
 		for (int o = 8; o > 0; o >>= 1) mx[v] = max(mx[v], __shfl_xor(mx[v], o, 16));
@@ -3487,21 +3505,6 @@ __global__ __launch_bounds__(64 * NW, 1) void k_attention_group(sslm_launch::Att
 	for (int d2 = 0; d2 < DTW; ++d2)
 #pragma unroll
 		for (int k = 0; k < 3; ++k) cacc[d2][k] = v4i{0, 0, 0, 0};
-	auto load_v = [&](int blk, v4i (&vr)[VPT]) {
-#pragma unroll
-		for (int u = 0; u < VPT; ++u) {
-			const int c = i + u * BS;
-			const int pr = c / (D / 16), ch = c % (D / 16);
-			const int64_t p = (int64_t)blk * KB + pr;
-			const int64_t pl = p < width && p != pos && p < cap ? p : 0;
-			vr[u] = c < VCH ? load16(vbase + pl * D + ch * 16) : v4i{0, 0, 0, 0};
-		}
-	};
-	v4i vr0[R][VPT], vr1[R][VPT];
-	auto load_vr = [&](int c0, v4i (&vr)[R][VPT]) {
-#pragma unroll
-		for (int j = 0; j < R; ++j) load_v(c0 * R + j, vr[j]);
-	};
 	// Step j's operands are staged into buffer j & 1 while step j - 1's are multiplied from the
 	// other one, so a step costs one barrier: buffer b was last read by the multiply before the
 	// previous barrier.
@@ -3560,7 +3563,6 @@ __global__ __launch_bounds__(64 * NW, 1) void k_attention_group(sslm_launch::Att
 	// 2R - 1 (groups c0 in vr0 and c0 + 1 in vr1) and stages each next step; group c0 + 1 is issued
 	// at its start (vr1's last reader was the previous iteration), group c0 + 2 once vr0's last
 	// step is staged
-	load_vr(0, vr0);
 	stage(0, vr0[0], 0);
 	__syncthreads();
 	// (the group loads are unconditional, as in pass 1)
