@@ -3208,6 +3208,16 @@ __global__ __launch_bounds__(64 * NW, 1) void k_attention_group(sslm_launch::Att
 	const int32_t cq = (int32_t)a.rope_cos[pp * PAIRS + qj], sq = (int32_t)a.rope_sin[pp * PAIRS + qj];
 	const int32_t ck = (int32_t)a.rope_cos[pp * PAIRS + ki], sk = (int32_t)a.rope_sin[pp * PAIRS + ki];
 	const Scale ns = a.in_scale[t];
+	// the ctx fold parameters of this lane's output rows (heads h0 + 4 g + v), for the epilogue
+	int32_t f0[4], f1[4], f2[4];
+#pragma unroll
+	for (int v = 0; v < 4; ++v) {
+		const int r = g * 4 + v;
+		const int32_t* cf = a.ctx_fold + 3 * (h0 + (r < G ? r : 0));
+		f0[v] = cf[0];
+		f1[v] = cf[1];
+		f2[v] = cf[2];
+	}
 	auto load_k = [&](int blk, v4i (&kb)[NC]) {
 		const int64_t p = (int64_t)blk * KB + wave * 16 + ri;
 		const int64_t pr = p < width && p != pos && p < cap ? p : 0;
@@ -3583,17 +3593,9 @@ __global__ __launch_bounds__(64 * NW, 1) void k_attention_group(sslm_launch::Att
 		}
 	}
 	// ---- epilogue: recombine, per-head fold, store, per-head maximum ----
-	int32_t f0[4], f1[4], f2[4];
 	bool rok[4];
 #pragma unroll
-	for (int v = 0; v < 4; ++v) {
-		const int r = g * 4 + v;
-		rok[v] = r < G && !(rf >> r & 1);
-		const int32_t* cf = a.ctx_fold + 3 * (h0 + (r < G ? r : 0));
-		f0[v] = cf[0];
-		f1[v] = cf[1];
-		f2[v] = cf[2];
-	}
+	for (int v = 0; v < 4; ++v) rok[v] = g * 4 + v < G && !(rf >> (g * 4 + v) & 1);
 #pragma unroll
 	for (int d2 = 0; d2 < DTW; ++d2) {
 		const int dt = wave + NW * d2;
