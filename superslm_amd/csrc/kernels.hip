@@ -2571,6 +2571,7 @@ __global__ __launch_bounds__(BS) void k_attention(sslm_launch::AttnArgs a, int u
 	__shared__ int32_t s_ctx[BS * 16];  // pass 4 partial sums: PG position groups x D
 	__shared__ __attribute__((aligned(16))) int8_t s_qc[D], s_kc[D], s_vc[D];
 	__shared__ int32_t s_st;
+	__shared__ int64_t s_cst[5];  // FUSED: the i-exp constants and verdict (one thread derives them)
 	constexpr int TPR = D / 16, PG = BS / TPR, PAIRS = D / 2;  // pass 4: threads per row, row groups
 	static_assert(BS >= PAIRS, "one thread per RoPE pair");
 	// XCD-aware order: workgroups go round-robin to the 8 XCDs (block id mod 8), so the R query
@@ -2630,10 +2631,19 @@ __global__ __launch_bounds__(BS) void k_attention(sslm_launch::AttnArgs a, int u
 		prefetch();
 	} else {
 		const int H = a.H, KVH = a.NKV * D, i = threadIdx.x;
+		// the KV head's scalar constants and the status word first: their round trip overlaps the
+		// vector loads below instead of following them
+		const int64_t rtk = a.r_t_k[kvh], rtv = a.r_t_v[kvh], etk = a.e_t_k[kvh], etv = a.e_t_v[kvh];
+		const int32_t status0 = a.status[ti.slot];
 		const Scale ns = a.in_scale[t];
 		const bool pos_ok = pos >= 0 && pos < a.cap;
-		// the post-processing's loads, unconditional from clamped indices (see the prefetch above)
-		const int ntq = H / 16, ic = i < PAIRS ? i : PAIRS - 1;
+		// The three independent jobs of the post-processing run on different waves: q codes and
+		// RoPE(q) on threads [0, PAIRS), the K/V landing on the last PAIRS threads, the i-exp
+		// constants on one thread between them (or the last, when BS = 2 PAIRS).  Each thread's
+		// loads are unconditional from clamped indices (see the prefetch above); pair index ic
+		// is its q pair or its K/V pair.
+		constexpr int LB = BS - PAIRS;  // first landing thread
+		const int ntq = H / 16, ic = i < PAIRS ? i : (i >= LB ? i - LB : 0);
 		const uint32_t qm0 = a.q_maxpart[(size_t)(i < ntq ? i : ntq - 1) * kPartLd + t];
 		int2 qv = ((const int2*)(a.q_f + (size_t)t * H + (size_t)h * D))[ic];
 		const int64_t* kvrow = a.kv_f + (size_t)t * 2 * KVH + (size_t)kvh * D;
@@ -2643,9 +2653,9 @@ __global__ __launch_bounds__(BS) void k_attention(sslm_launch::AttnArgs a, int u
 		prefetch();
 		uint32_t qmx = i < ntq ? qm0 : 0u;
 		for (int k2 = i + BS; k2 < ntq; k2 += BS) qmx = max(qmx, a.q_maxpart[(size_t)k2 * kPartLd + t]);
-		const int64_t rtk = a.r_t_k[kvh], rtv = a.r_t_v[kvh];
-		const int64_t k_e = composed_exponent(ns.e, a.e_t_k[kvh]), v_e = composed_exponent(ns.e, a.e_t_v[kvh]);
-		if (threadIdx.x == 0) s_st = a.status[ti.slot];
+		const int64_t k_e = composed_exponent(ns.e, etk), v_e = composed_exponent(ns.e, etv);
+		// one reading of the status word for the whole block (another block may set it meanwhile)
+		if (threadIdx.x == 0) s_st = status0;
 		qmx = blk_max32<BS>(qmx, s_qm);
 		if (s_st != 0) return;
 		FunnelPlan plan;
@@ -2656,7 +2666,7 @@ __global__ __launch_bounds__(BS) void k_attention(sslm_launch::AttnArgs a, int u
 			return;
 		}
 		uint32_t sat = 0;
-		if (i < PAIRS) {
+		if (i >= LB) {  // the K/V landing of pair ic
 			bool c0, c1, c2, c3, x0;
 			const int64_t k0 = clamp_code(landing_rescale(kk.x, ns.m, rtk, k_e, &c0, &x0));
 			const int64_t k1 = clamp_code(landing_rescale(kk.y, ns.m, rtk, k_e, &c1, &x0));
@@ -2666,17 +2676,42 @@ __global__ __launch_bounds__(BS) void k_attention(sslm_launch::AttnArgs a, int u
 			const char2 vc = make_char2((char)clamp_code(landing_rescale(vv.x, ns.m, rtv, v_e, &c2, &x0)),
 			                            (char)clamp_code(landing_rescale(vv.y, ns.m, rtv, v_e, &c3, &x0)));
 			sat = (uint32_t)c0 + (uint32_t)c1 + (uint32_t)c2 + (uint32_t)c3;
-			((char2*)s_kc)[i] = kc;
-			((char2*)s_vc)[i] = vc;
+			((char2*)s_kc)[ic] = kc;
+			((char2*)s_vc)[ic] = vc;
 			if (h % group == 0) {  // the group's writer
-				const int64_t off = pos * D + 2 * i;
+				const int64_t off = pos * D + 2 * ic;
 				*(char2*)(kstore + off) = kc;
 				*(char2*)(kstore + half + off) = vc;
 			}
+		}
+		if (i < PAIRS) {  // q codes and RoPE(q) of pair i
+			int64_t xr, yr;
 			const int32_t x = requant_code_f(qv.x, requant_factor(plan.r, plan.s));
 			const int32_t y = requant_code_f(qv.y, requant_factor(plan.r, plan.s));
 			rope_pair(x, y, c, sn, &xr, &yr);
 			((char2*)s_qc)[i] = make_char2((char)clamp_code(xr), (char)clamp_code(yr));
+		}
+		if (i == (LB - 1 >= PAIRS ? LB - 1 : BS - 1)) {  // the i-exp constants of the row's scale
+			const Scale qsp = plan.out;
+			int64_t q0 = 0, q1 = 0, q2 = 0, q3 = 0;
+			int32_t cst = kOk;
+			if (!fits_i32(qsp.m) || !fits_i32(km)) {
+				cst = kCarriedScaleMantissaOutOfDomain;
+			} else {
+				const Scale sm = combine_scale(qsp, Scale{km, ke});
+				if (!fits_i32(sm.m)) cst = kCarriedScaleMantissaOutOfDomain;
+				else if (iexp_scale_constants(sm.m, sm.e, a.ln2_q, a.b_q, a.ca_q, &q0, &q1, &q2) != 0)
+					cst = kIExpScaleDerivationOutOfDomain;
+				else {
+					cst = check_softmax_width(q1, q2, pos + 1);
+					q3 = softmax_ceiling(q1, q2);
+				}
+			}
+			s_cst[0] = q0;
+			s_cst[1] = q1;
+			s_cst[2] = q2;
+			s_cst[3] = q3;
+			s_cst[4] = cst;
 		}
 		if (h % group == 0) {  // the writer counts the saturations of its landing
 			const int32_t ws = wave_sum32((int32_t)sat);
@@ -2691,11 +2726,17 @@ __global__ __launch_bounds__(BS) void k_attention(sslm_launch::AttnArgs a, int u
 			if (threadIdx.x == 0 && h == 0) a.q_tap.scale[t] = qs;
 		}
 	}
-	// i-exp constants of the row's scale (every thread, redundantly)
+	// i-exp constants of the row's scale (FUSED: derived above; else every thread, redundantly)
 	int32_t st = kOk;
 	int64_t c_qln2 = 0, c_qb = 0, c_qc = 0, c_M = 0;
 	const int64_t width = pos + 1;
-	if (!fits_i32(qs.m) || !fits_i32(km)) {
+	if (FUSED) {
+		c_qln2 = s_cst[0];
+		c_qb = s_cst[1];
+		c_qc = s_cst[2];
+		c_M = s_cst[3];
+		st = (int32_t)s_cst[4];
+	} else if (!fits_i32(qs.m) || !fits_i32(km)) {
 		st = kCarriedScaleMantissaOutOfDomain;
 	} else {
 		const Scale sm = combine_scale(qs, Scale{km, ke});
