@@ -1797,6 +1797,20 @@ __device__ __forceinline__ uint32_t part_max32(const uint32_t* part, int tile0, 
 	return m;
 }
 
+// part_max32 for ntiles <= PER * BS as straight-line code: every thread issues its PER loads at
+// once from clamped indices (a maximum ignores the repeats), so the partials cost one round trip
+// rather than one per loop iteration
+template <int BS, int PER>
+__device__ __forceinline__ uint32_t part_max32_fixed(const uint32_t* part, int tile0, int ntiles, int t) {
+	uint32_t v[PER];
+#pragma unroll
+	for (int k = 0; k < PER; ++k) v[k] = part[(size_t)(tile0 + min((int)threadIdx.x + k * BS, ntiles - 1)) * kPartLd + t];
+	uint32_t m = 0;
+#pragma unroll
+	for (int k = 0; k < PER; ++k) m = max(m, v[k]);
+	return m;
+}
+
 template <int BS>
 __device__ __forceinline__ uint64_t blk_max(uint64_t v, uint64_t* slots) {
 	v = wave_max_u64(v);
@@ -2445,6 +2459,9 @@ void k_mlp_act(sslm_launch::ActArgs a) {
 	if (threadIdx.x == 0) a.act_scale[t] = ap.out;
 }
 
+// 16-column tiles of a gate or up row the sliced SiLU reads maxima of (I <= 20480, row_geometry_ok)
+constexpr int kActSliceTiles = 20480 / 16;
+
 // mlp_act over column slices (forward_sites.cpp:796-869): block (t, s) takes columns
 // [s * per, (s + 1) * per) of row t.  Part 1: the gate and up funnels from the projection's
 // tile maxima (every block derives the same plans), the SiLU-LUT sigmoid table, the products
@@ -2467,10 +2484,18 @@ __global__ __launch_bounds__(BS) void k_mlp_act_s1(sslm_launch::ActArgs a, int p
 		gf[k] = i < j1 ? gfr[i] : 0;
 		uf[k] = i < j1 ? ufr[i] : 0;
 	}
-	uint32_t gm = part_max32<BS>(a.gu_maxpart, 0, I / 16, t);
-	uint32_t um = part_max32<BS>(a.gu_maxpart, I / 16, I / 16, t);
+	// the tile maxima (I / 16 <= kActSliceTiles per row) and the SiLU table as straight-line loads
+	uint32_t gm = part_max32_fixed<BS, (kActSliceTiles + BS - 1) / BS>(a.gu_maxpart, 0, I / 16, t);
+	uint32_t um = part_max32_fixed<BS, (kActSliceTiles + BS - 1) / BS>(a.gu_maxpart, I / 16, I / 16, t);
 	const Scale inc = a.in_scale[t];
-	for (int i = threadIdx.x; i < 1025; i += BS) s_silu[i] = a.silu[i];
+	{
+		int32_t sv[(1025 + BS - 1) / BS];
+#pragma unroll
+		for (int k = 0; k < (1025 + BS - 1) / BS; ++k) sv[k] = a.silu[min((int)threadIdx.x + k * BS, 1024)];
+#pragma unroll
+		for (int k = 0; k < (1025 + BS - 1) / BS; ++k)
+			if (threadIdx.x + k * BS < 1025) s_silu[threadIdx.x + k * BS] = sv[k];
+	}
 	if (threadIdx.x == 0) s_st = a.status[slot];
 	blk_max32x2<BS>(gm, um, s_gu);
 	if (s_st != 0) return;
@@ -2528,8 +2553,9 @@ __global__ __launch_bounds__(BS) void k_mlp_act_s2(sslm_launch::ActArgs a, int p
 		const int i = j0 + threadIdx.x + k * BS;
 		w[k] = i < j1 ? prow[i] : 0;
 	}
-	uint32_t mx = 0;
-	for (int i = 0; i < S; ++i) mx = max(mx, a.act_maxpart[(size_t)i * kPartLd + t]);
+	uint32_t mx = 0;  // over the S slices' maxima: straight-line loads from clamped indices
+#pragma unroll
+	for (int i = 0; i < sslm_launch::kMaxActSlices; ++i) mx = max(mx, a.act_maxpart[(size_t)min(i, S - 1) * kPartLd + t]);
 	const Scale inc2[2] = {a.gu_scale[2 * t], a.gu_scale[2 * t + 1]};
 	if (threadIdx.x == 0) s_st = a.status[slot];
 	__syncthreads();
