@@ -1790,24 +1790,29 @@ __device__ __forceinline__ int32_t blk_sum32(int32_t v, int32_t* slots) {
 
 // this thread's share of the max over tiles [tile0, tile0 + ntiles) of a per-(tile, token)
 // partial array (32-bit); combine across the block with blk_max32
-template <int BS>
-__device__ __forceinline__ uint32_t part_max32(const uint32_t* part, int tile0, int ntiles, int t) {
-	uint32_t m = 0;
-	for (int i = threadIdx.x; i < ntiles; i += BS) m = max(m, part[(size_t)(tile0 + i) * kPartLd + t]);
-	return m;
+// Elements threadIdx.x + k * BS (k < EPT) of a row of n >= 1 elements, 0 beyond n.  The loads
+// are unconditional (clamped indices): a load under a per-lane branch makes the compiler wait
+// for it before the branch joins, so guarded loads cost one memory round trip each.
+template <int BS, int EPT, typename T>
+__device__ __forceinline__ void load_row(const T* row, int n, int32_t (&out)[EPT]) {
+	T v[EPT];
+#pragma unroll
+	for (int k = 0; k < EPT; ++k) v[k] = row[min((int)threadIdx.x + k * BS, n - 1)];
+#pragma unroll
+	for (int k = 0; k < EPT; ++k) out[k] = (int)threadIdx.x + k * BS < n ? (int32_t)v[k] : 0;
 }
 
-// part_max32 for ntiles <= PER * BS as straight-line code: every thread issues its PER loads at
-// once from clamped indices (a maximum ignores the repeats), so the partials cost one round trip
-// rather than one per loop iteration
+// The maximum over per-tile partial maxima [tile0, tile0 + ntiles) of token t, for ntiles <= PER * BS,
+// as straight-line code: every thread issues its PER loads at once from clamped indices, so the
+// partials cost one memory round trip rather than one per loop iteration
 template <int BS, int PER>
 __device__ __forceinline__ uint32_t part_max32_fixed(const uint32_t* part, int tile0, int ntiles, int t) {
 	uint32_t v[PER];
 #pragma unroll
-	for (int k = 0; k < PER; ++k) v[k] = part[(size_t)(tile0 + min((int)threadIdx.x + k * BS, ntiles - 1)) * kPartLd + t];
+	for (int k = 0; k < PER; ++k) v[k] = part[(size_t)(tile0 + min((int)threadIdx.x + k * BS, max(ntiles - 1, 0))) * kPartLd + t];
 	uint32_t m = 0;
 #pragma unroll
-	for (int k = 0; k < PER; ++k) m = max(m, v[k]);
+	for (int k = 0; k < PER; ++k) m = max(m, (int)threadIdx.x + k * BS < ntiles ? v[k] : 0u);
 	return m;
 }
 
@@ -1946,12 +1951,8 @@ __global__ __launch_bounds__(BS) void k_rmsnorm(sslm_launch::RowNormArgs a, int 
 	const int slot = tok[t].slot;
 	const int8_t* hrow = a.in_codes + (size_t)a.in_idx[t] * a.ld_in;
 	int32_t h[EPT], g[EPT];
-#pragma unroll
-	for (int k = 0; k < EPT; ++k) {
-		const int i = threadIdx.x + k * BS;
-		h[k] = i < H ? hrow[i] : 0;
-		g[k] = i < H ? a.gain[i] : 0;
-	}
+	load_row<BS>(hrow, H, h);
+	load_row<BS>(a.gain, H, g);
 	if (threadIdx.x == 0) s_st = status[slot];
 	const int32_t st = rmsnorm_regs<BS, EPT>(h, g, H, a.site, a.out + (size_t)t * H, &a.out_scale[t],
 	                                         a.out_recip ? &a.out_recip[t] : nullptr, fd, s_sum, s_max, &s_st);
@@ -1997,12 +1998,12 @@ __global__ __launch_bounds__(BS) void k_qkv_post(sslm_launch::QkvPostArgs a) {
 		if (!ok) qmx = kBad32;
 	} else {
 		const int2* qf = (const int2*)(a.q_f + (size_t)t * H);
+		int2 qr[EQ];
 #pragma unroll
-		for (int k = 0; k < EQ; ++k) {
-			const int p = threadIdx.x + k * BS;
-			qv[k] = p < H / 2 ? qf[p] : make_int2(0, 0);
-		}
-		qmx = part_max32<BS>(a.q_maxpart, 0, H / 16, t);
+		for (int k = 0; k < EQ; ++k) qr[k] = qf[min((int)threadIdx.x + k * BS, H / 2 - 1)];  // clamped: no per-lane branch
+#pragma unroll
+		for (int k = 0; k < EQ; ++k) qv[k] = (int)threadIdx.x + k * BS < H / 2 ? qr[k] : make_int2(0, 0);
+		qmx = part_max32_fixed<BS, (2 * EQ + 15) / 16>(a.q_maxpart, 0, H / 16, t);  // H <= 2 * EQ * BS
 	}
 	if (threadIdx.x == 0) s_st = a.status[ti.slot];
 	// K/V landing (LandingRescale at the normed scale, per kv head) and RoPE(K)
@@ -2181,12 +2182,8 @@ __global__ __launch_bounds__(BS) void k_funnel(sslm_launch::FunnelArgs a) {
 	const int slot = a.tok[t].slot;
 	const int32_t* frow = a.f + (size_t)t * a.ld_f;
 	int32_t f[EPT];
-#pragma unroll
-	for (int k = 0; k < EPT; ++k) {
-		const int i = threadIdx.x + k * BS;
-		f[k] = i < N ? frow[i] : 0;
-	}
-	uint32_t mx = part_max32<BS>(a.maxpart, 0, a.ntiles, t);
+	load_row<BS>(frow, N, f);
+	uint32_t mx = part_max32_fixed<BS, (EPT + 15) / 16>(a.maxpart, 0, a.ntiles, t);  // ntiles <= N / 16 + 1
 	Scale inc{0, 0};
 	if (a.incoming) inc = a.incoming[t];
 	if (threadIdx.x == 0) {
@@ -2232,7 +2229,20 @@ __global__ __launch_bounds__(BS) void k_residual_norm(sslm_launch::ResidualArgs 
 	const Scale bin = a.branch_in[t];
 	const int32_t* bfr = a.branch_f + (size_t)t * H;
 	const int8_t* srow = a.stream + (size_t)sidx * H;
+	const Scale ss = a.stream_scale[sidx];
+	const int32_t status0 = a.status[slot];  // broadcast from thread 0's copy below
 	int32_t bf[EPT], g[EPT], sv[EPT];
+	// the stream row and gains first: issued ahead of the raw planes, they share its round trip
+	load_row<BS>(srow, H, sv);
+	{  // without a norm the gain loads read this token's branch row (H valid int32) and are dropped:
+	   // no branch around them, so nothing waits on them here
+		const int32_t* gsrc = a.gain ? a.gain : (RS > 0 ? a.raw.part + (size_t)t * a.raw.ld : bfr);
+		load_row<BS>(gsrc, H, g);
+		int32_t gmask = a.gain ? -1 : 0;
+		asm volatile("" : "+v"(gmask));  // opaque: the loads cannot be sunk into a branch on the mask
+#pragma unroll
+		for (int k = 0; k < EPT; ++k) g[k] &= gmask;
+	}
 	uint32_t bmx = 0;
 	if (RS > 0) {
 		int j[EPT];
@@ -2251,16 +2261,9 @@ __global__ __launch_bounds__(BS) void k_residual_norm(sslm_launch::ResidualArgs 
 		}
 		if (!ok) bmx = kBad32;
 	}
-#pragma unroll
-	for (int k = 0; k < EPT; ++k) {
-		const int i = threadIdx.x + k * BS;
-		if (RS == 0) bf[k] = i < H ? bfr[i] : 0;
-		sv[k] = i < H ? srow[i] : 0;
-		g[k] = (a.gain && i < H) ? a.gain[i] : 0;
-	}
-	if (RS == 0) bmx = part_max32<BS>(a.branch_maxpart, 0, H / 16, t);
-	const Scale ss = a.stream_scale[sidx];
-	if (threadIdx.x == 0) s_st = a.status[slot];
+	if (RS == 0) load_row<BS>(bfr, H, bf);
+	if (RS == 0) bmx = part_max32_fixed<BS, (EPT + 15) / 16>(a.branch_maxpart, 0, H / 16, t);
+	if (threadIdx.x == 0) s_st = status0;
 	bmx = blk_max32<BS>(bmx, s_b);
 	KT(1);
 	if (s_st != 0) return;
@@ -2399,16 +2402,12 @@ void k_mlp_act(sslm_launch::ActArgs a) {
 		}
 		if (!(okg && oku)) gm = kBad32;
 	} else {
-#pragma unroll
-		for (int k = 0; k < EPT; ++k) {
-			const int i = threadIdx.x + k * BS;
-			gf[k] = i < I ? gfr[i] : 0;
-			uf[k] = i < I ? ufr[i] : 0;
-		}
+		load_row<BS>(gfr, I, gf);
+		load_row<BS>(ufr, I, uf);
 	}
 	if (RS == 0) {
-		gm = part_max32<BS>(a.gu_maxpart, 0, I / 16, t);
-		um = part_max32<BS>(a.gu_maxpart, I / 16, I / 16, t);
+		gm = part_max32_fixed<BS, (EPT + 15) / 16>(a.gu_maxpart, 0, I / 16, t);
+		um = part_max32_fixed<BS, (EPT + 15) / 16>(a.gu_maxpart, I / 16, I / 16, t);
 	}
 	const Scale inc = a.in_scale[t];
 	for (int i = threadIdx.x; i < 1025; i += BS) s_silu[i] = a.silu[i];
