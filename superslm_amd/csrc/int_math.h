@@ -544,7 +544,8 @@ SSLM_HD int32_t check_softmax_width(int64_t q_b, int64_t q_c, int64_t width) {
 	s128 m128 = (s128)q_b * q_b + (s128)q_c;
 	if (m128 > (s128)kI64Max || m128 > (s128)kSoftmaxMaxSafe) return kSoftmaxRowWidthOutOfDomain;
 	int64_t m = (int64_t)m128;
-	if (m != 0 && width > kI64Max / m) return kSoftmaxRowWidthOutOfDomain;
+	// width > floor(INT64_MAX / m)  <=>  width * m > INT64_MAX  (width, m >= 1): no 64-bit division
+	if (m != 0 && (u128)(uint64_t)width * (uint64_t)m > (u128)kI64Max) return kSoftmaxRowWidthOutOfDomain;
 	return kOk;
 }
 

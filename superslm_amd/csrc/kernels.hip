@@ -1794,12 +1794,20 @@ __device__ __forceinline__ int32_t blk_sum32(int32_t v, int32_t* slots) {
 // are unconditional (clamped indices): a load under a per-lane branch makes the compiler wait
 // for it before the branch joins, so guarded loads cost one memory round trip each.
 template <int BS, int EPT, typename T>
-__device__ __forceinline__ void load_row(const T* row, int n, int32_t (&out)[EPT]) {
-	T v[EPT];
+__device__ __forceinline__ void load_row_raw(const T* row, int n, T (&v)[EPT]) {
 #pragma unroll
 	for (int k = 0; k < EPT; ++k) v[k] = row[min((int)threadIdx.x + k * BS, n - 1)];
+}
+template <int BS, int EPT, typename T>
+__device__ __forceinline__ void row_take(const T (&v)[EPT], int n, int32_t (&out)[EPT]) {
 #pragma unroll
 	for (int k = 0; k < EPT; ++k) out[k] = (int)threadIdx.x + k * BS < n ? (int32_t)v[k] : 0;
+}
+template <int BS, int EPT, typename T>
+__device__ __forceinline__ void load_row(const T* row, int n, int32_t (&out)[EPT]) {
+	T v[EPT];
+	load_row_raw<BS>(row, n, v);
+	row_take<BS>(v, n, out);
 }
 
 // The maximum over per-tile partial maxima [tile0, tile0 + ntiles) of token t, for ntiles <= PER * BS,
@@ -2181,20 +2189,24 @@ __global__ __launch_bounds__(BS) void k_funnel(sslm_launch::FunnelArgs a) {
 	const int t = blockIdx.x, N = a.N;
 	const int slot = a.tok[t].slot;
 	const int32_t* frow = a.f + (size_t)t * a.ld_f;
-	int32_t f[EPT];
-	load_row<BS>(frow, N, f);
+	// the maxima, scales and status words first, then the row: the plan needs only the former, so
+	// the block reduction and the plan run while the row is in flight
 	uint32_t mx = part_max32_fixed<BS, (EPT + 15) / 16>(a.maxpart, 0, a.ntiles, t);  // ntiles <= N / 16 + 1
 	Scale inc{0, 0};
 	if (a.incoming) inc = a.incoming[t];
+	const int32_t st0 = a.status[slot];
+	const int32_t hs0 = (a.head_status ? a.head_status : a.status)[slot];
+	const int32_t hs = a.head_status ? hs0 : kHeadStatusNone;  // the first refusing head of the attention
+	int32_t fv[EPT];
+	load_row_raw<BS>(frow, N, fv);
 	if (threadIdx.x == 0) {
-		if (a.head_status) {  // the first refusing head of the attention that produced this row
-			const int32_t hs = a.head_status[slot];
-			if (hs != kHeadStatusNone) {
-				set_status(a.status, slot, a.layer, hs & 0xff);
-				a.head_status[slot] = kHeadStatusNone;
-			}
+		int32_t sv = st0;
+		if (hs != kHeadStatusNone) {  // rare: resolve the attention's refusal into the status
+			set_status(a.status, slot, a.layer, hs & 0xff);
+			a.head_status[slot] = kHeadStatusNone;
+			sv = a.status[slot];
 		}
-		s_st = a.status[slot];
+		s_st = sv;
 	}
 	mx = blk_max32<BS>(mx, s_m);
 	if (s_st != 0) return;
@@ -2204,6 +2216,8 @@ __global__ __launch_bounds__(BS) void k_funnel(sslm_launch::FunnelArgs a) {
 		if (threadIdx.x == 0) set_status(a.status, slot, a.layer, st);
 		return;
 	}
+	int32_t f[EPT];
+	row_take<BS>(fv, N, f);
 	int8_t* out = a.out + (size_t)t * N;
 #pragma unroll
 	for (int k = 0; k < EPT; ++k) {
@@ -2381,6 +2395,25 @@ void k_mlp_act(sslm_launch::ActArgs a) {
 	const int32_t* ufr = gfr + I;
 	int32_t gf[EPT], uf[EPT];
 	uint32_t gm = 0, um = 0;
+	// Without raw planes the plans need only the tile maxima: those, the SiLU table, the scale
+	// and the status word are issued first and the rows after them, so the reductions, the
+	// plans and the sigmoid table run while the rows are in flight.
+	int32_t sv[(1025 + BS - 1) / BS];
+#pragma unroll
+	for (int k = 0; k < (1025 + BS - 1) / BS; ++k) sv[k] = a.silu[min((int)threadIdx.x + k * BS, 1024)];
+	if (RS == 0) {
+		gm = part_max32_fixed<BS, (EPT + 15) / 16>(a.gu_maxpart, 0, I / 16, t);
+		um = part_max32_fixed<BS, (EPT + 15) / 16>(a.gu_maxpart, I / 16, I / 16, t);
+	}
+	const Scale inc = a.in_scale[t];
+	const int32_t st0 = a.status[slot];
+	int32_t gv[EPT], uv[EPT];
+	if (RS == 0) {
+		// every wave's small loads ahead of any wave's row loads in the CU's memory queue
+		__syncthreads();
+		load_row_raw<BS>(gfr, I, gv);
+		load_row_raw<BS>(ufr, I, uv);
+	}
 	if (RS > 0) {
 		int jg[EPT], ju[EPT];
 		bool live[EPT];
@@ -2401,17 +2434,11 @@ void k_mlp_act(sslm_launch::ActArgs a) {
 			um = max(um, sat_abs_u32(vu[k]));
 		}
 		if (!(okg && oku)) gm = kBad32;
-	} else {
-		load_row<BS>(gfr, I, gf);
-		load_row<BS>(ufr, I, uf);
 	}
-	if (RS == 0) {
-		gm = part_max32_fixed<BS, (EPT + 15) / 16>(a.gu_maxpart, 0, I / 16, t);
-		um = part_max32_fixed<BS, (EPT + 15) / 16>(a.gu_maxpart, I / 16, I / 16, t);
-	}
-	const Scale inc = a.in_scale[t];
-	for (int i = threadIdx.x; i < 1025; i += BS) s_silu[i] = a.silu[i];
-	if (threadIdx.x == 0) s_st = a.status[slot];
+#pragma unroll
+	for (int k = 0; k < (1025 + BS - 1) / BS; ++k)
+		if (threadIdx.x + k * BS < 1025) s_silu[threadIdx.x + k * BS] = sv[k];
+	if (threadIdx.x == 0) s_st = st0;
 	blk_max32x2<BS>(gm, um, s_gu);
 	if (s_st != 0) return;
 	FunnelPlan gp, up;
@@ -2424,6 +2451,10 @@ void k_mlp_act(sslm_launch::ActArgs a) {
 	}
 	const Scale gs = gp.out;
 	if (threadIdx.x < 256) sig[threadIdx.x] = silu_sigmoid_q15(s_silu, (int8_t)(threadIdx.x - 128), gs.m, (int)gs.e);
+	if (RS == 0) {
+		row_take<BS>(gv, I, gf);
+		row_take<BS>(uv, I, uf);
+	}
 	int32_t gc[EPT], uc[EPT];
 #pragma unroll
 	for (int k = 0; k < EPT; ++k) {
@@ -2476,26 +2507,27 @@ __global__ __launch_bounds__(BS) void k_mlp_act_s1(sslm_launch::ActArgs a, int p
 	const int j0 = sl * per, j1 = min(I, j0 + per);
 	const int32_t* gfr = a.gu_f + (size_t)t * 2 * I;
 	const int32_t* ufr = gfr + I;
-	int32_t gf[EPT], uf[EPT];
-#pragma unroll
-	for (int k = 0; k < EPT; ++k) {
-		const int i = j0 + threadIdx.x + k * BS;
-		gf[k] = i < j1 ? gfr[i] : 0;
-		uf[k] = i < j1 ? ufr[i] : 0;
-	}
-	// the tile maxima (I / 16 <= kActSliceTiles per row) and the SiLU table as straight-line loads
+	// The tile maxima (I / 16 <= kActSliceTiles per row), the SiLU table, the scale and the status
+	// word as straight-line loads, then the slice (clamped to it): the plans need only the former,
+	// so the reductions, the plans and the sigmoid table run while the slice is in flight.
 	uint32_t gm = part_max32_fixed<BS, (kActSliceTiles + BS - 1) / BS>(a.gu_maxpart, 0, I / 16, t);
 	uint32_t um = part_max32_fixed<BS, (kActSliceTiles + BS - 1) / BS>(a.gu_maxpart, I / 16, I / 16, t);
 	const Scale inc = a.in_scale[t];
-	{
-		int32_t sv[(1025 + BS - 1) / BS];
+	const int32_t st0 = a.status[slot];
+	int32_t sv[(1025 + BS - 1) / BS];
 #pragma unroll
-		for (int k = 0; k < (1025 + BS - 1) / BS; ++k) sv[k] = a.silu[min((int)threadIdx.x + k * BS, 1024)];
+	for (int k = 0; k < (1025 + BS - 1) / BS; ++k) sv[k] = a.silu[min((int)threadIdx.x + k * BS, 1024)];
+	int32_t gv[EPT], uv[EPT];
 #pragma unroll
-		for (int k = 0; k < (1025 + BS - 1) / BS; ++k)
-			if (threadIdx.x + k * BS < 1025) s_silu[threadIdx.x + k * BS] = sv[k];
+	for (int k = 0; k < EPT; ++k) {
+		const int i = j0 + min((int)threadIdx.x + k * BS, j1 - j0 - 1);
+		gv[k] = gfr[i];
+		uv[k] = ufr[i];
 	}
-	if (threadIdx.x == 0) s_st = a.status[slot];
+#pragma unroll
+	for (int k = 0; k < (1025 + BS - 1) / BS; ++k)
+		if (threadIdx.x + k * BS < 1025) s_silu[threadIdx.x + k * BS] = sv[k];
+	if (threadIdx.x == 0) s_st = st0;
 	blk_max32x2<BS>(gm, um, s_gu);
 	if (s_st != 0) return;
 	FunnelPlan gp, up;
@@ -2508,6 +2540,13 @@ __global__ __launch_bounds__(BS) void k_mlp_act_s1(sslm_launch::ActArgs a, int p
 	}
 	const Scale gs = gp.out;
 	if (threadIdx.x < 256) sig[threadIdx.x] = silu_sigmoid_q15(s_silu, (int8_t)(threadIdx.x - 128), gs.m, (int)gs.e);
+	int32_t gf[EPT], uf[EPT];
+#pragma unroll
+	for (int k = 0; k < EPT; ++k) {
+		const bool in = j0 + (int)threadIdx.x + k * BS < j1;
+		gf[k] = in ? gv[k] : 0;
+		uf[k] = in ? uv[k] : 0;
+	}
 	int32_t gc[EPT], uc[EPT];
 #pragma unroll
 	for (int k = 0; k < EPT; ++k) {
@@ -2596,7 +2635,8 @@ __global__ __launch_bounds__(BS) void k_attention(sslm_launch::AttnArgs a, int u
 	__shared__ int32_t s_ctx[BS * 16];  // pass 4 partial sums: PG position groups x D
 	__shared__ __attribute__((aligned(16))) int8_t s_qc[D], s_kc[D], s_vc[D];
 	__shared__ int32_t s_st;
-	__shared__ int64_t s_cst[5];  // FUSED: the i-exp constants and verdict (one thread derives them)
+	__shared__ int64_t s_cst[5];  // FUSED: the i-exp constants and their status (one thread derives them)
+	__shared__ int32_t s_vd;      // FUSED: the q funnel's verdict
 	constexpr int TPR = D / 16, PG = BS / TPR, PAIRS = D / 2;  // pass 4: threads per row, row groups
 	static_assert(BS >= PAIRS, "one thread per RoPE pair");
 	// XCD-aware order: workgroups go round-robin to the 8 XCDs (block id mod 8), so the R query
@@ -2662,13 +2702,19 @@ __global__ __launch_bounds__(BS) void k_attention(sslm_launch::AttnArgs a, int u
 		const int32_t status0 = a.status[ti.slot];
 		const Scale ns = a.in_scale[t];
 		const bool pos_ok = pos >= 0 && pos < a.cap;
-		// The three independent jobs of the post-processing run on different waves: q codes and
-		// RoPE(q) on threads [0, PAIRS), the K/V landing on the last PAIRS threads, the i-exp
-		// constants on one thread between them (or the last, when BS = 2 PAIRS).  Each thread's
-		// loads are unconditional from clamped indices (see the prefetch above); pair index ic
-		// is its q pair or its K/V pair.
-		constexpr int LB = BS - PAIRS;  // first landing thread
-		const int ntq = H / 16, ic = i < PAIRS ? i : (i >= LB ? i - LB : 0);
+		// The independent jobs of the post-processing run on different waves: q codes and RoPE(q)
+		// on threads [0, PAIRS) (after the q funnel's plan), the K landing and RoPE(K) on the last
+		// PAIRS threads and the V landing on [PAIRS, 2 PAIRS) when that range is free (else on the
+		// K threads), neither waiting for the plan.  The i-exp constants need the plan and are
+		// derived by one thread after the post-processing barrier, while pass 1 runs; nothing
+		// reads them before pass 1's reduction.  Each thread's loads are unconditional from
+		// clamped indices (see the prefetch above); pair index ic is its q, K or V pair.
+		constexpr int LB = BS - PAIRS;  // first K landing thread
+		constexpr bool SPLITV = 3 * PAIRS < BS;  // V landing on threads [PAIRS, 2 PAIRS)
+		constexpr int CST = LB - 1 >= (SPLITV ? 2 * PAIRS : PAIRS) ? LB - 1 : BS - 1;  // i-exp constants
+		const bool kthr = i >= LB, vthr = SPLITV ? (i >= PAIRS && i < 2 * PAIRS) : kthr;
+		const int ntq = H / 16;
+		const int ic = i < PAIRS ? i : (kthr ? i - LB : (vthr ? i - PAIRS : 0));
 		const uint32_t qm0 = a.q_maxpart[(size_t)(i < ntq ? i : ntq - 1) * kPartLd + t];
 		int2 qv = ((const int2*)(a.q_f + (size_t)t * H + (size_t)h * D))[ic];
 		const int64_t* kvrow = a.kv_f + (size_t)t * 2 * KVH + (size_t)kvh * D;
@@ -2683,40 +2729,52 @@ __global__ __launch_bounds__(BS) void k_attention(sslm_launch::AttnArgs a, int u
 		if (threadIdx.x == 0) s_st = status0;
 		qmx = blk_max32<BS>(qmx, s_qm);
 		if (s_st != 0) return;
-		FunnelPlan plan;
-		int32_t st = funnel_plan(qmx, &ns, 1, a.q_site, &plan);
-		if (st == kOk && !pos_ok) st = kPositionOverCap;
-		if (st != kOk) {  // the same for every head of the token
-			if (threadIdx.x == 0) set_status(a.status, ti.slot, a.layer, st);
-			return;
-		}
 		uint32_t sat = 0;
-		if (i >= LB) {  // the K/V landing of pair ic
-			bool c0, c1, c2, c3, x0;
+		char2 kc = make_char2(0, 0), vc = make_char2(0, 0);
+		if (kthr) {  // the K landing and RoPE(K) of pair ic
+			bool c0, c1, x0;
 			const int64_t k0 = clamp_code(landing_rescale(kk.x, ns.m, rtk, k_e, &c0, &x0));
 			const int64_t k1 = clamp_code(landing_rescale(kk.y, ns.m, rtk, k_e, &c1, &x0));
 			int64_t xr, yr;
 			rope_pair((int32_t)k0, (int32_t)k1, c, sn, &xr, &yr);
-			const char2 kc = make_char2((char)clamp_code(xr), (char)clamp_code(yr));
-			const char2 vc = make_char2((char)clamp_code(landing_rescale(vv.x, ns.m, rtv, v_e, &c2, &x0)),
-			                            (char)clamp_code(landing_rescale(vv.y, ns.m, rtv, v_e, &c3, &x0)));
-			sat = (uint32_t)c0 + (uint32_t)c1 + (uint32_t)c2 + (uint32_t)c3;
+			kc = make_char2((char)clamp_code(xr), (char)clamp_code(yr));
+			sat += (uint32_t)c0 + (uint32_t)c1;
 			((char2*)s_kc)[ic] = kc;
+		}
+		if (vthr) {  // the V landing of pair ic
+			bool c2, c3, x0;
+			vc = make_char2((char)clamp_code(landing_rescale(vv.x, ns.m, rtv, v_e, &c2, &x0)),
+			                (char)clamp_code(landing_rescale(vv.y, ns.m, rtv, v_e, &c3, &x0)));
+			sat += (uint32_t)c2 + (uint32_t)c3;
 			((char2*)s_vc)[ic] = vc;
-			if (h % group == 0) {  // the group's writer
-				const int64_t off = pos * D + 2 * ic;
-				*(char2*)(kstore + off) = kc;
-				*(char2*)(kstore + half + off) = vc;
+		}
+		// the q funnel's plan, on the waves that use it (wave-uniform condition)
+		FunnelPlan plan{};
+		if (i < PAIRS || (i >> 6) == (CST >> 6)) {
+			int32_t st = funnel_plan(qmx, &ns, 1, a.q_site, &plan);
+			if (st == kOk && !pos_ok) st = kPositionOverCap;
+			if (threadIdx.x == 0) {  // the verdict, the same for every head of the token
+				s_vd = st;
+				if (st != kOk) set_status(a.status, ti.slot, a.layer, st);
+			}
+			if (st == kOk && i < PAIRS) {  // q codes and RoPE(q) of pair i
+				int64_t xr, yr;
+				const int32_t x = requant_code_f(qv.x, requant_factor(plan.r, plan.s));
+				const int32_t y = requant_code_f(qv.y, requant_factor(plan.r, plan.s));
+				rope_pair(x, y, c, sn, &xr, &yr);
+				((char2*)s_qc)[i] = make_char2((char)clamp_code(xr), (char)clamp_code(yr));
 			}
 		}
-		if (i < PAIRS) {  // q codes and RoPE(q) of pair i
-			int64_t xr, yr;
-			const int32_t x = requant_code_f(qv.x, requant_factor(plan.r, plan.s));
-			const int32_t y = requant_code_f(qv.y, requant_factor(plan.r, plan.s));
-			rope_pair(x, y, c, sn, &xr, &yr);
-			((char2*)s_qc)[i] = make_char2((char)clamp_code(xr), (char)clamp_code(yr));
+		__syncthreads();
+		if (s_vd != kOk) return;  // the plan refused: no K/V store, no saturation count
+		if (h % group == 0) {  // the group's writer stores the landed K/V and counts its saturations
+			const int64_t off = pos * D + 2 * ic;
+			if (kthr) *(char2*)(kstore + off) = kc;
+			if (vthr) *(char2*)(kstore + half + off) = vc;
+			const int32_t ws = wave_sum32((int32_t)sat);
+			if ((threadIdx.x & 63) == 0 && ws) atomicAdd(&a.sat[ti.slot], (unsigned long long)ws);
 		}
-		if (i == (LB - 1 >= PAIRS ? LB - 1 : BS - 1)) {  // the i-exp constants of the row's scale
+		if (i == CST) {  // the i-exp constants of the row's scale
 			const Scale qsp = plan.out;
 			int64_t q0 = 0, q1 = 0, q2 = 0, q3 = 0;
 			int32_t cst = kOk;
@@ -2738,29 +2796,19 @@ __global__ __launch_bounds__(BS) void k_attention(sslm_launch::AttnArgs a, int u
 			s_cst[3] = q3;
 			s_cst[4] = cst;
 		}
-		if (h % group == 0) {  // the writer counts the saturations of its landing
-			const int32_t ws = wave_sum32((int32_t)sat);
-			if ((threadIdx.x & 63) == 0 && ws) atomicAdd(&a.sat[ti.slot], (unsigned long long)ws);
-		}
-		__syncthreads();
 #pragma unroll
 		for (int j = 0; j < D / 16; ++j) q[j] = *(const v4i*)(s_qc + 16 * j);
-		qs = plan.out;
 		if (a.q_tap.codes) {
 			if (threadIdx.x < D) a.q_tap.codes[(size_t)t * a.q_tap.ld + (size_t)h * D + threadIdx.x] = s_qc[threadIdx.x];
-			if (threadIdx.x == 0 && h == 0) a.q_tap.scale[t] = qs;
+			if (threadIdx.x == 0 && h == 0) a.q_tap.scale[t] = plan.out;
 		}
 	}
-	// i-exp constants of the row's scale (FUSED: derived above; else every thread, redundantly)
+	// i-exp constants of the row's scale (FUSED: derived by one thread during pass 1 and read
+	// after its reduction; else every thread, redundantly)
 	int32_t st = kOk;
 	int64_t c_qln2 = 0, c_qb = 0, c_qc = 0, c_M = 0;
 	const int64_t width = pos + 1;
 	if (FUSED) {
-		c_qln2 = s_cst[0];
-		c_qb = s_cst[1];
-		c_qc = s_cst[2];
-		c_M = s_cst[3];
-		st = (int32_t)s_cst[4];
 	} else if (!fits_i32(qs.m) || !fits_i32(km)) {
 		st = kCarriedScaleMantissaOutOfDomain;
 	} else {
@@ -2774,7 +2822,7 @@ __global__ __launch_bounds__(BS) void k_attention(sslm_launch::AttnArgs a, int u
 			c_M = softmax_ceiling(c_qb, c_qc);
 		}
 	}
-	const bool live = st == kOk && width >= 1 && width <= a.cap;
+	const bool live = (FUSED || st == kOk) && width >= 1 && width <= a.cap;
 	int64_t* ex = use_lds ? dyn : a.scratch + ((int64_t)t * a.NH + h) * a.cap;
 	// pass 1: scores (int32-exact dots) and the row max; the first position's row was issued at entry
 	int64_t mx = INT64_MIN;
@@ -2798,6 +2846,13 @@ __global__ __launch_bounds__(BS) void k_attention(sslm_launch::AttnArgs a, int u
 	}
 	mx = blk_max_i64<BS>(mx, s_mx);
 	if (!FUSED && s_st != 0) return;
+	if (FUSED) {
+		c_qln2 = s_cst[0];
+		c_qb = s_cst[1];
+		c_qc = s_cst[2];
+		c_M = s_cst[3];
+		st = (int32_t)s_cst[4];
+	}
 	if (st != kOk) {
 		if (threadIdx.x == 0) report_head(a.head_status, ti.slot, h, st);
 		return;
