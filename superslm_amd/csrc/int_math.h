@@ -667,6 +667,26 @@ SSLM_HD int32_t div_q15_small(int64_t e, double d, double inv) {
 	return (int32_t)q;
 }
 
+// floor(v 2^32 / root) for a code v in [-128, 127] and 1 <= root < 2^24 (the RMSNorm's
+// per-code quotient, forward_sites.cpp:410-459: floor for v >= 0, -ceil(|v| 2^32 / root) below),
+// given inv = 1.0 / root.  n = |v| 2^32 <= 2^39 is exact in a double and the estimate n inv is
+// within one of the quotient; q root <= n + root < 2^53 is exact too, so fma gives the exact
+// remainder for the one-step correction.
+SSLM_HD int64_t norm_fd(int32_t v, double root, double inv) {
+	const double n = ldexp((double)(v < 0 ? -v : v), 32);
+	double q = floor(n * inv);
+	double r = fma(-q, root, n);
+	if (r < 0.0) {
+		q -= 1.0;
+		r += root;
+	} else if (r >= root) {
+		q += 1.0;
+		r -= root;
+	}
+	const int64_t qi = (int64_t)q;
+	return v >= 0 ? qi : -(qi + (r > 0.0 ? 1 : 0));
+}
+
 SSLM_HD int64_t softmax_ceiling(int64_t q_b, int64_t q_c) {
 	s128 m128 = (s128)q_b * q_b + (s128)q_c;
 	bool usable = m128 <= (s128)kI64Max && m128 >= 1 && m128 <= (s128)kSoftmaxMaxSafe;

@@ -1907,8 +1907,8 @@ constexpr int32_t kSkipped = -1;  // the slot had already failed: nothing writte
 // (zero beyond H) with gains `g`.  `prior` (LDS, or null) is the slot status read before entry.
 template <int BS, int EPT>
 __device__ __forceinline__ int32_t rmsnorm_regs(const int32_t (&h)[EPT], const int32_t (&g)[EPT], int H, Scale site,
-                                                int8_t* out, Scale* out_scale, int64_t* out_recip, int64_t* fd,
-                                                int32_t* s_sum, uint32_t* s_max, const int32_t* prior) {
+                                                int8_t* out, Scale* out_scale, int64_t* out_recip, int32_t* s_sum,
+                                                uint32_t* s_max, const int32_t* prior) {
 	int32_t ss = 0;  // sum of squared int8 codes: < 2^14 * H, exact in int32
 #pragma unroll
 	for (int k = 0; k < EPT; ++k) ss += h[k] * h[k];
@@ -1917,17 +1917,14 @@ __device__ __forceinline__ int32_t rmsnorm_regs(const int32_t (&h)[EPT], const i
 	if (prior && *prior != 0) return kSkipped;
 	int64_t root = isqrt_fast(div_floor_pos((int64_t)ss << 32, (int64_t)H));
 	root = root > 1 ? root : 1;
-	if (threadIdx.x < 256) {  // floor((v << 32) / root) for every int8 v
-		const int64_t v = ((int64_t)threadIdx.x - 128) << 32;
-		fd[threadIdx.x] = v >= 0 ? div_floor_pos(v, root) : -div_floor_pos(-v + root - 1, root);
-	}
-	__syncthreads();
+	// floor((v << 32) / root) per element from one shared reciprocal (root < 2^23)
+	const double rd = (double)root, inv = 1.0 / rd;
 	KT(11);
 	int64_t w[EPT];
 	uint32_t mx = 0;
 #pragma unroll
 	for (int k = 0; k < EPT; ++k) {
-		w[k] = fd[h[k] + 128] * (int64_t)g[k];
+		w[k] = norm_fd(h[k], rd, inv) * (int64_t)g[k];
 		mx = max(mx, sat_abs_u32(w[k]));
 	}
 	mx = blk_max32<BS>(mx, s_max);
@@ -1951,7 +1948,6 @@ __device__ __forceinline__ int32_t rmsnorm_regs(const int32_t (&h)[EPT], const i
 template <int BS, int EPT>
 __global__ __launch_bounds__(BS) void k_rmsnorm(sslm_launch::RowNormArgs a, int H, const TokenInfo* tok,
                                               int32_t* status, int32_t layer) {
-	__shared__ int64_t fd[256];
 	__shared__ int32_t s_sum[BS / 64];
 	__shared__ uint32_t s_max[BS / 64];
 	__shared__ int32_t s_st;
@@ -1963,7 +1959,7 @@ __global__ __launch_bounds__(BS) void k_rmsnorm(sslm_launch::RowNormArgs a, int 
 	load_row<BS>(a.gain, H, g);
 	if (threadIdx.x == 0) s_st = status[slot];
 	const int32_t st = rmsnorm_regs<BS, EPT>(h, g, H, a.site, a.out + (size_t)t * H, &a.out_scale[t],
-	                                         a.out_recip ? &a.out_recip[t] : nullptr, fd, s_sum, s_max, &s_st);
+	                                         a.out_recip ? &a.out_recip[t] : nullptr, s_sum, s_max, &s_st);
 	if (threadIdx.x == 0 && st > 0) set_status(status, slot, layer, st);
 }
 
@@ -2233,7 +2229,6 @@ template <int BS, int EPT, int RS>
 __global__ __launch_bounds__(BS) void k_residual_norm(sslm_launch::ResidualArgs a) {
 	__shared__ uint32_t s_b[BS / 64], s_r[BS / 64], s_n[BS / 64];
 	__shared__ int32_t s_ss[BS / 64];
-	__shared__ int64_t fd[256];
 	__shared__ int64_t land[256];  // landed branch value per branch code (code + 127)
 	__shared__ int32_t s_st;
 	const int t = blockIdx.x, H = a.H;
@@ -2351,7 +2346,7 @@ __global__ __launch_bounds__(BS) void k_residual_norm(sslm_launch::ResidualArgs 
 	KT(5);
 	if (a.gain) {
 		const int32_t st2 = rmsnorm_regs<BS, EPT>(c, g, H, a.norm_site, a.norm_out + (size_t)t * H, &a.norm_scale[t],
-		                                          a.norm_recip ? &a.norm_recip[t] : nullptr, fd, s_ss, s_n, nullptr);
+		                                          a.norm_recip ? &a.norm_recip[t] : nullptr, s_ss, s_n, nullptr);
 		if (threadIdx.x == 0 && st2 > 0) set_status(a.status, slot, a.layer, st2);
 	}
 	KT(6);
@@ -2774,7 +2769,7 @@ __global__ __launch_bounds__(BS) void k_attention(sslm_launch::AttnArgs a, int u
 			const int32_t ws = wave_sum32((int32_t)sat);
 			if ((threadIdx.x & 63) == 0 && ws) atomicAdd(&a.sat[ti.slot], (unsigned long long)ws);
 		}
-		if (i == CST) {  // the i-exp constants of the row's scale
+		if ((i >> 6) == (CST >> 6)) {  // the i-exp constants of the row's scale: wave-uniform, so scalar code
 			const Scale qsp = plan.out;
 			int64_t q0 = 0, q1 = 0, q2 = 0, q3 = 0;
 			int32_t cst = kOk;
@@ -2790,11 +2785,13 @@ __global__ __launch_bounds__(BS) void k_attention(sslm_launch::AttnArgs a, int u
 					q3 = softmax_ceiling(q1, q2);
 				}
 			}
-			s_cst[0] = q0;
-			s_cst[1] = q1;
-			s_cst[2] = q2;
-			s_cst[3] = q3;
-			s_cst[4] = cst;
+			if (i == CST) {
+				s_cst[0] = q0;
+				s_cst[1] = q1;
+				s_cst[2] = q2;
+				s_cst[3] = q3;
+				s_cst[4] = cst;
+			}
 		}
 #pragma unroll
 		for (int j = 0; j < D / 16; ++j) q[j] = *(const v4i*)(s_qc + 16 * j);

@@ -85,4 +85,22 @@ int main(int argc, char** argv) {
 		if (q1 != q2) { if (bq < 10) printf("div_q15_small mismatch %lld/%lld: %lld vs %d\n", (long long)e, (long long)d, (long long)q1, q2); ++bq; }
 	}
 	printf("div_q15_small: %ld mismatches\n", bq);
+	// the RMSNorm per-code quotient: every code against the table form, every root up to 2^16
+	// and random roots up to 2^24 (the norm's roots stay below 2^23)
+	long bn = 0, nn = 0;
+	auto fd_table = [](int64_t v, int64_t root) {
+		const int64_t x = v << 32;
+		return x >= 0 ? div_floor_pos(x, root) : -div_floor_pos(-x + root - 1, root);
+	};
+	for (int64_t it = 0; it < (1 << 16) + N / 8; ++it) {
+		int64_t root = it < (1 << 16) ? 1 + it : 1 + (int64_t)(rng() % (1ull << 24));
+		if (it % 1009 == 0) root = (1ll << 24) - 1 - (int64_t)(rng() % 4);
+		const double rd = (double)root, inv = 1.0 / rd;
+		for (int v = -128; v < 128; ++v) {
+			++nn;
+			const int64_t a = fd_table(v, root), b = norm_fd(v, rd, inv);
+			if (a != b) { if (bn < 10) printf("norm_fd mismatch v=%d root=%lld: %lld vs %lld\n", v, (long long)root, (long long)a, (long long)b); ++bn; }
+		}
+	}
+	printf("norm_fd: %ld cases, %ld mismatches\n", nn, bn);
 }

@@ -1,6 +1,6 @@
-"""The exact fast forms used by the attention kernels (`iexp_fast`, `div_rcp` in
-superslm_amd/csrc/int_math.h) against the forms they replace (`iexp_element`, restating
-src/intmath.cpp:580-668, and `div_floor_pos`): the header is compiled for the host and both forms
+"""The exact fast forms used by the attention and RMSNorm kernels (`iexp_fast`, `div_rcp`,
+`norm_fd` in superslm_amd/csrc/int_math.h) against the forms they replace (`iexp_element`,
+restating src/intmath.cpp:580-668, and `div_floor_pos`): the header is compiled for the host and both forms
 run on the same random and edge-case inputs (q_ln2 up to kI64Max / 30, i-exp values up to the
 2^47 ceiling, divisors up to 2^60)."""
 import os
@@ -23,6 +23,8 @@ def test_fast_forms_match(tmp_path):
     assert "iexp: " in out and ", 0 mismatches" in out.splitlines()[0]
     assert "div: 0 mismatches" in out
     assert "div_q15_small: 0 mismatches" in out
+    norm = [l for l in out.splitlines() if l.startswith("norm_fd:")][0]
+    assert norm.endswith(", 0 mismatches") and int(norm.split()[1]) > 16_000_000
     small = [l for l in out.splitlines() if l.startswith("iexp_small:")][0]
     assert small.endswith(", 0 mismatches") and int(small.split("(")[1].split(" accepted")[0]) > 10000
     accepted = int(out.split("(")[1].split(" accepted")[0])
