@@ -3283,7 +3283,8 @@ __global__ __launch_bounds__(64 * NW, 1) void k_attention_group(sslm_launch::Att
 	__shared__ uint32_t s_qm[NW], s_mab[TQ], s_rf[TQ];
 	__shared__ int32_t s_st, s_rmx[TQ];
 	__shared__ int32_t s_dump[BS];  // where rows G .. GM - 1 of the softmax loops store
-	__shared__ int64_t s_cst[5];     // the rows' i-exp constants and verdict (one thread derives them)
+	__shared__ int64_t s_cst[5];     // the rows' i-exp constants and their status (one thread derives them)
+	__shared__ int32_t s_vd;         // the q plan's verdict
 	const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, ri = lane & 15, g = lane >> 4, i = threadIdx.x;
 	const int H = a.H, KVH = a.NKV * D, GG = a.NH / a.NKV;
 	// a.row_halves = 2: two blocks per (token, KV group), numbered 16 k + 8 h + x (x < 8) for group
@@ -3315,11 +3316,16 @@ __global__ __launch_bounds__(64 * NW, 1) void k_attention_group(sslm_launch::Att
 	const uint32_t qm0 = a.q_maxpart[(size_t)(i < ntq ? i : ntq - 1) * kPartLd + t];
 	const int qi = i < G * PAIRS ? i : G * PAIRS - 1, qr = qi / PAIRS, qj = qi % PAIRS;
 	const int2 qv = ((const int2*)(a.q_f + (size_t)t * H + (size_t)(h0 + qr) * D))[qj];
-	// the prologue's three independent jobs run on different waves: q codes on threads
-	// [0, G PAIRS), the K/V landing on the last PAIRS threads, the i-exp constants on one thread
-	// between them (or the last, when the others leave none free)
-	constexpr int LB = BS - PAIRS;  // first landing thread
-	const int ki = i >= LB ? i - LB : 0;
+	// The prologue's independent jobs run on different waves: q codes on threads [0, G PAIRS)
+	// after the q plan, the K landing and RoPE(K) on the last PAIRS threads and the V landing on
+	// the PAIRS threads before them when the q codes leave those free (else on the K threads),
+	// neither waiting for the plan.  The i-exp constants, which only pass 2 needs, are derived by
+	// thread 0 at the start of pass 1 and read after pass 1's reduction.
+	constexpr int LB = BS - PAIRS;  // first K landing thread
+	const bool kthr = i >= LB;
+	const bool splitv = G * PAIRS <= LB - PAIRS;  // block-uniform
+	const bool vthr = splitv ? (i >= LB - PAIRS && i < LB) : kthr;
+	const int ki = kthr ? i - LB : (vthr ? i - (LB - PAIRS) : 0);
 	const int64_t* kvrow = a.kv_f + (size_t)t * 2 * KVH + (size_t)kvh * D;
 	const longlong2 kk = ((const longlong2*)kvrow)[ki], vv = ((const longlong2*)(kvrow + KVH))[ki];
 	const int64_t pp = pos_ok ? pos : 0;
@@ -3365,49 +3371,59 @@ __global__ __launch_bounds__(64 * NW, 1) void k_attention_group(sslm_launch::Att
 	}
 	qmx = blk_max32<BS>(qmx, s_qm);
 	if (s_st != 0) return;
-	FunnelPlan plan;
-	int32_t st = funnel_plan(qmx, &ns, 1, a.q_site, &plan);
-	if (st == kOk && !pos_ok) st = kPositionOverCap;
-	if (st != kOk) {  // the same for every head of the token
-		if (i == 0) set_status(a.status, ti.slot, a.layer, st);
-		return;
-	}
-	// K/V landing of this KV head at pos: every block of the group keeps it in LDS, row half 0's
-	// writes it to the cache and counts its saturations (no block reads what another writes)
+	// K/V landing of this KV head at pos: every block of the group keeps it in LDS; row half 0's
+	// writes it to the cache and counts its saturations once the plan has passed (no block reads
+	// what another writes)
 	uint32_t sat = 0;
-	if (i >= LB) {
-		bool c0, c1, c2, c3, x0;
+	char2 kc = make_char2(0, 0), vc = make_char2(0, 0);
+	if (kthr) {
+		bool c0, c1, x0;
 		const int64_t k0 = clamp_code(landing_rescale(kk.x, ns.m, rtk, k_e, &c0, &x0));
 		const int64_t k1 = clamp_code(landing_rescale(kk.y, ns.m, rtk, k_e, &c1, &x0));
 		int64_t xr, yr;
 		rope_pair((int32_t)k0, (int32_t)k1, ck, sk, &xr, &yr);
-		const char2 kc = make_char2((char)clamp_code(xr), (char)clamp_code(yr));
-		const char2 vc = make_char2((char)clamp_code(landing_rescale(vv.x, ns.m, rtv, v_e, &c2, &x0)),
-		                            (char)clamp_code(landing_rescale(vv.y, ns.m, rtv, v_e, &c3, &x0)));
+		kc = make_char2((char)clamp_code(xr), (char)clamp_code(yr));
+		sat += (uint32_t)c0 + (uint32_t)c1;
 		((char2*)s_kc)[ki] = kc;
+	}
+	if (vthr) {
+		bool c2, c3, x0;
+		vc = make_char2((char)clamp_code(landing_rescale(vv.x, ns.m, rtv, v_e, &c2, &x0)),
+		                (char)clamp_code(landing_rescale(vv.y, ns.m, rtv, v_e, &c3, &x0)));
+		sat += (uint32_t)c2 + (uint32_t)c3;
 		((char2*)s_vc)[ki] = vc;
-		if (rh == 0) {  // the group's writer
-			sat = (uint32_t)c0 + (uint32_t)c1 + (uint32_t)c2 + (uint32_t)c3;
-			int8_t* kstore = const_cast<int8_t*>(kbase);
-			const int64_t off = pos * D + 2 * ki;
-			*(char2*)(kstore + off) = kc;
-			*(char2*)(kstore + half + off) = vc;
+	}
+	// the q plan on the q threads (whole waves when G PAIRS is a multiple of 64)
+	FunnelPlan plan{};
+	if (i < G * PAIRS) {
+		int32_t st0 = funnel_plan(qmx, &ns, 1, a.q_site, &plan);
+		if (st0 == kOk && !pos_ok) st0 = kPositionOverCap;
+		if (i == 0) {  // the verdict, the same for every head of the token
+			s_vd = st0;
+			if (st0 != kOk) set_status(a.status, ti.slot, a.layer, st0);
+		}
+		if (st0 == kOk) {  // q codes and RoPE of the group's heads
+			int64_t xr, yr;
+			const int32_t x = requant_code_f(qv.x, requant_factor(plan.r, plan.s));
+			const int32_t y = requant_code_f(qv.y, requant_factor(plan.r, plan.s));
+			rope_pair(x, y, cq, sq, &xr, &yr);
+			*(char2*)&s_qc[qr][2 * qj] = make_char2((char)clamp_code(xr), (char)clamp_code(yr));
 		}
 	}
-	{
+	__syncthreads();
+	if (s_vd != kOk) return;
+	if (rh == 0) {  // the group's writer
+		int8_t* kstore = const_cast<int8_t*>(kbase);
+		const int64_t off = pos * D + 2 * ki;
+		if (kthr) *(char2*)(kstore + off) = kc;
+		if (vthr) *(char2*)(kstore + half + off) = vc;
 		const int32_t ws = wave_sum32((int32_t)sat);
 		if (lane == 0 && ws) atomicAdd(&a.sat[ti.slot], (unsigned long long)ws);
 	}
-	if (i < G * PAIRS) {  // q codes and RoPE of the group's heads
-		int64_t xr, yr;
-		const int32_t x = requant_code_f(qv.x, requant_factor(plan.r, plan.s));
-		const int32_t y = requant_code_f(qv.y, requant_factor(plan.r, plan.s));
-		rope_pair(x, y, cq, sq, &xr, &yr);
-		*(char2*)&s_qc[qr][2 * qj] = make_char2((char)clamp_code(xr), (char)clamp_code(yr));
-	}
 	const Scale qs = plan.out;
-	// i-exp constants of the rows' common scale (the q scale is the token's, km / ke the KV head's)
-	if (i == (LB - 1 >= G * PAIRS ? LB - 1 : BS - 1)) {
+	// i-exp constants of the rows' common scale (the q scale is the token's, km / ke the KV
+	// head's), read after pass 1's reduction
+	if (i == 0) {
 		int64_t q0 = 0, q1 = 0, q2 = 0, q3 = 0;
 		int32_t cst = kOk;
 		if (!fits_i32(qs.m) || !fits_i32(km)) {
@@ -3428,17 +3444,14 @@ __global__ __launch_bounds__(64 * NW, 1) void k_attention_group(sslm_launch::Att
 		s_cst[3] = q3;
 		s_cst[4] = cst;
 	}
-	__syncthreads();
-	const int64_t c_qln2 = s_cst[0], c_qb = s_cst[1], c_qc = s_cst[2], c_M = s_cst[3];
-	st = (int32_t)s_cst[4];
 	if (a.q_tap.codes) {
 		for (int k2 = i; k2 < G * D; k2 += BS) a.q_tap.codes[(size_t)t * a.q_tap.ld + (size_t)h0 * D + k2] = s_qc[k2 / D][k2 % D];
 		if (i == 0 && kvh == 0 && rh == 0) a.q_tap.scale[t] = qs;
 	}
-	// (width <= wcap holds by construction: the host sizes wcap from the launch's positions)
-	const bool live = st == kOk && width >= 1 && width <= cap && width <= a.wcap;
-	if (!live) {  // every head of the group: the same refusal the per-head kernel reports
-		if (i < G) report_head(a.head_status, ti.slot, h0 + i, st != kOk ? st : kPositionOverCap);
+	// (width <= wcap holds by construction: the host sizes wcap from the launch's positions; the
+	// passed plan implies width <= cap)
+	if (!(width >= 1 && width <= cap && width <= a.wcap)) {
+		if (i < G) report_head(a.head_status, ti.slot, h0 + i, kPositionOverCap);
 		return;
 	}
 	v4i qa[NC];
@@ -3515,6 +3528,12 @@ __global__ __launch_bounds__(64 * NW, 1) void k_attention_group(sslm_launch::Att
 		s_rmx[i] = (int32_t)m;
 	}
 	__syncthreads();
+	const int64_t c_qln2 = s_cst[0], c_qb = s_cst[1], c_qc = s_cst[2], c_M = s_cst[3];
+	const int32_t st = (int32_t)s_cst[4];
+	if (st != kOk) {  // every head of the group: the same refusal the per-head kernel reports
+		if (i < G) report_head(a.head_status, ti.slot, h0 + i, st);
+		return;
+	}
 	// ---- pass 2: i-exp values and row sums over every (row, position) ----
 	// Every row of the block has the same constants (one token's q scale, one KV head's K scale).
 	// Each score's slot then keeps what the probabilities need: the i-exp value when the ceiling
