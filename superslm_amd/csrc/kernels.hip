@@ -535,6 +535,128 @@ __global__ __launch_bounds__(256) void k_gemv_p(GemmArgs g) {
 }
 
 // ------------------------------------------------------------------------------------------
+// LM head on the packed decode copy (M <= 32, K <= 4096), persistent: one block per CU walks the
+// 16-column tiles blockIdx.x, + gridDim.x, ...; wave w keeps K chunks w CPW .. + CPW of the MB
+// 16-token row groups in registers for the whole launch and loads the next tile's weight chunks
+// while it multiplies the current tile's, two register sets alternating (the loop body is two
+// steps, so the wait counts stay exact).  The four partial sums meet in a double-buffered LDS
+// slot; every wave finishes one token row of each 4-token group: the per (token, tile) greedy
+// key of k_gemv_w (the larger logit, then the smaller index; a schema-masked token's logit counts
+// as INT32_MIN).  Each block reads the activation rows once for all its tiles, where one block
+// per tile pair read them once per 32 columns.
+// ------------------------------------------------------------------------------------------
+__device__ __forceinline__ const int8_t* pk_lane(const int8_t* wp, int tile, int C, int lane);
+
+constexpr int kHeadMaxSteps = 64;  // tiles per block of k_gemv_head (the launch sizes its grid to fit)
+
+template <int MB, int CPW>
+__global__ __launch_bounds__(256) void k_gemv_head(GemmArgs g) {
+	__shared__ v4i red[2][kGemvWaves][MB][64];
+	// the block's keys, stored after the loop: a global store inside it (stores count in the
+	// vector-memory counter) left the waits before each step's MFMAs draining the next tile's loads
+	__shared__ uint64_t s_key[kHeadMaxSteps][MB * 16];
+	const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, ri = lane & 15, grp = lane >> 4;
+	const int C = g.K >> 7, T = (g.N + 15) / 16;
+	const v4i z = v4i{0, 0, 0, 0};
+	const Epilogue& e = g.epi;
+	// this lane's epilogue tokens (mb * 16 + 4 grp + wave) and their schema pages: a mask byte
+	// travels with each tile's weights, read from a valid address whether or not a page is set, so
+	// no wait inside the loop drains the next tile's loads
+	const uint8_t* pgp[MB];
+	bool masked[MB];
+#pragma unroll
+	for (int mb = 0; mb < MB; ++mb) {
+		const int tk = min(mb * 16 + grp * 4 + wave, g.M - 1);
+		const uint8_t* pg = e.mask_page ? e.mask_page[tk] : nullptr;
+		masked[mb] = pg != nullptr;
+		pgp[mb] = pg ? pg : (const uint8_t*)g.wp;
+	}
+	struct Tile {
+		v4i b[CPW][2];
+		uint8_t mbits[MB];
+	};
+	auto load_tile = [&](int t, Tile& d) {
+		const int tc = min(t, T - 1);
+		const int8_t* tp = pk_lane(g.wp, tc, C, lane);
+#pragma unroll
+		for (int i = 0; i < CPW; ++i) {
+			const int c = min(wave * CPW + i, C - 1);
+			d.b[i][0] = load16(tp + (size_t)c * 2048);
+			d.b[i][1] = load16(tp + (size_t)c * 2048 + 1024);
+		}
+		const int jm = min(tc * 16 + ri, g.N - 1) >> 3;  // within the packed copy when no page is set
+		// a global-space load: through a generic pointer it would be a flat load, which counts in
+		// both wait counters and made every LDS wait of the epilogue drain the weight loads
+#pragma unroll
+		for (int mb = 0; mb < MB; ++mb)
+			d.mbits[mb] = ((const __attribute__((address_space(1))) uint8_t*)pgp[mb])[masked[mb] ? jm : 0];
+	};
+	Tile t0buf, t1buf;
+	int tile = blockIdx.x, it = 0;
+	load_tile(tile, t0buf);  // the first tile's weights go out before the activations
+	v4i x[MB][CPW][2];
+#pragma unroll
+	for (int mb = 0; mb < MB; ++mb) {
+		const int r = mb * 16 + ri;
+		const bool rok = r < g.M;
+		const int8_t* arow = g.a + (size_t)(rok ? r : g.M - 1) * g.lda + grp * 16;
+#pragma unroll
+		for (int i = 0; i < CPW; ++i) {
+			const int c = wave * CPW + i;
+			const int cc = c < C ? c : C - 1;
+			const v4i a0 = load16(arow + cc * 128), a1 = load16(arow + cc * 128 + 64);
+			x[mb][i][0] = rok && c < C ? a0 : z;  // chunks past K multiply clamped weights by zero
+			x[mb][i][1] = rok && c < C ? a1 : z;
+		}
+	}
+	auto step = [&](int tl, int k, Tile& cur, Tile& nxt) {
+		load_tile(tl + (int)gridDim.x, nxt);
+		v4i acc[MB];
+#pragma unroll
+		for (int mb = 0; mb < MB; ++mb) {
+			acc[mb] = z;
+#pragma unroll
+			for (int i = 0; i < CPW; ++i) {
+				acc[mb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(x[mb][i][0], cur.b[i][0], acc[mb], 0, 0, 0);
+				acc[mb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(x[mb][i][1], cur.b[i][1], acc[mb], 0, 0, 0);
+			}
+			red[k & 1][wave][mb][lane] = acc[mb];
+		}
+		__syncthreads();
+		const int j = tl * 16 + ri;
+#pragma unroll
+		for (int mb = 0; mb < MB; ++mb) {
+			int32_t tot = 0;
+#pragma unroll
+			for (int w = 0; w < kGemvWaves; ++w) tot += ((const int32_t*)&red[k & 1][w][mb][lane])[wave];
+			const int tk = mb * 16 + grp * 4 + wave;
+			const int32_t lv = masked[mb] && j < g.N && !((cur.mbits[mb] >> (j & 7)) & 1u) ? INT32_MIN : tot;
+			uint64_t key = j < g.N ? ((uint64_t)((uint32_t)lv ^ 0x80000000u) << 32) | (0xffffffffu - (uint32_t)j) : 0;
+#pragma unroll
+			for (int o = 8; o > 0; o >>= 1) {
+				const uint64_t k2 = __shfl_xor(key, o, 16);
+				key = k2 > key ? k2 : key;
+			}
+			if (ri == 0) s_key[k][tk] = key;
+		}
+	};
+	while (tile < T) {
+		step(tile, it, t0buf, t1buf);
+		tile += gridDim.x;
+		++it;
+		if (tile >= T) break;
+		step(tile, it, t1buf, t0buf);
+		tile += gridDim.x;
+		++it;
+	}
+	__syncthreads();
+	for (int q = threadIdx.x; q < it * MB * 16; q += 256) {
+		const int k = q / (MB * 16), tk = q % (MB * 16);
+		if (tk < g.M) e.argmax_key[(size_t)tk * e.key_ld + (int)blockIdx.x + k * (int)gridDim.x] = s_key[k][tk];
+	}
+}
+
+// ------------------------------------------------------------------------------------------
 // Decode GEMV, wave-per-tile form (M <= 16), for the launches with no projection epilogue: raw
 // int32 accumulators (one plane, or split-K planes the consumer adds) and LM-head argmax keys.
 // A block of 4 waves covers 4 consecutive 16-column tiles and one K range (split s of
@@ -2620,8 +2742,12 @@ __global__ __launch_bounds__(BS) void k_mlp_act_s2(sslm_launch::ActArgs a, int p
 // RoPE(K) of its KV group at the current position (forward_sites.cpp:1281-1418, :1748-1787).
 // The group's first head writes that K/V to the cache; every head reads position `pos` from its
 // own LDS copy, so no block reads what another block of the launch writes.
-template <int BS, int D, bool FUSED>
-__global__ __launch_bounds__(BS) void k_attention(sslm_launch::AttnArgs a, int use_lds) {
+// LDSROW: the row's scores / i-exp values / probabilities live in LDS (else in the launch's global
+// scratch).  A compile-time choice: one pointer that may address either space is a generic one,
+// and its flat accesses count in both wait counters, so every LDS wait would also wait for the
+// K/V loads in flight.
+template <int BS, int D, bool FUSED, bool LDSROW>
+__global__ __launch_bounds__(BS) void k_attention(sslm_launch::AttnArgs a) {
 	extern __shared__ int64_t dyn[];
 	__shared__ int64_t s_mx[BS / 64];
 	__shared__ int64_t s_sum[BS / 64];
@@ -2820,7 +2946,7 @@ __global__ __launch_bounds__(BS) void k_attention(sslm_launch::AttnArgs a, int u
 		}
 	}
 	const bool live = (FUSED || st == kOk) && width >= 1 && width <= a.cap;
-	int64_t* ex = use_lds ? dyn : a.scratch + ((int64_t)t * a.NH + h) * a.cap;
+	int64_t* ex = LDSROW ? dyn : a.scratch + ((int64_t)t * a.NH + h) * a.cap;
 	// pass 1: scores (int32-exact dots) and the row max; the first position's row was issued at entry
 	int64_t mx = INT64_MIN;
 	if (live) {
@@ -4147,9 +4273,35 @@ static bool launch_gemv_sk(const GemmArgs& g, hipStream_t s) {
 	return false;
 }
 
+// k_gemv_head takes LM-head launches (argmax keys, no raw output) on the packed copy at M <= 32,
+// K <= 4096 (at most 8 chunks per wave); SSLM_HIP_HEAD_PK=0 keeps them on the generic GEMVs
+static bool head_pk_ok(const GemmArgs& g) {
+	static const bool on = [] {
+		const char* e = getenv("SSLM_HIP_HEAD_PK");
+		return !(e && atoi(e) == 0);
+	}();
+	return on && g.wp && g.epi.argmax_key && !g.epi.raw_out && g.splits <= 1 && g.M >= 1 && g.M <= 32 &&
+	       g.K % 128 == 0 && g.K <= 4096;
+}
+
+template <int MB>
+static bool launch_gemv_head(const GemmArgs& g, hipStream_t s) {
+	const int C = g.K / 128, need = (C + kGemvWaves - 1) / kGemvWaves, T = (g.N + 15) / 16;
+	const int grid = std::min(T, std::max(device_cus(), (T + kHeadMaxSteps - 1) / kHeadMaxSteps));
+	switch (need <= 3 ? 3 : (need <= 4 ? 4 : (need <= 7 ? 7 : 8))) {
+		case 3: hipLaunchKernelGGL((k_gemv_head<MB, 3>), dim3(grid), dim3(256), 0, s, g); return true;
+		case 4: hipLaunchKernelGGL((k_gemv_head<MB, 4>), dim3(grid), dim3(256), 0, s, g); return true;
+		case 7: hipLaunchKernelGGL((k_gemv_head<MB, 7>), dim3(grid), dim3(256), 0, s, g); return true;
+		default: hipLaunchKernelGGL((k_gemv_head<MB, 8>), dim3(grid), dim3(256), 0, s, g); return true;
+	}
+}
+
 void gemm(const GemmArgs& g, hipStream_t s) {
 	if (g.M <= 0 || g.N <= 0) return;
 	check_gemm_outputs(g);
+	if (head_pk_ok(g)) {
+		if (g.M > 16 ? launch_gemv_head<2>(g, s) : launch_gemv_head<1>(g, s)) return;
+	}
 	if (gemv_eligible(g.M, g.K) && g.wp && g.M <= kPkMaxM && !g.epi.argmax_key) {
 		if (g.splits > 1 && sk_ok(g.M, g.K, &g)) {
 			if (launch_gemv_sk(g, s)) return;
@@ -4358,10 +4510,22 @@ static void launch_attention(const AttnArgs& a, hipStream_t s) {
 	const dim3 grid(per_xcd * 8 * (a.NH / a.NKV));  // see the XCD-aware order in k_attention
 	const size_t dyn = use_lds ? lds : 0;
 	switch (a.D) {
-		case 32: hipLaunchKernelGGL((k_attention<kBlock, 32, FUSED>), grid, dim3(kBlock), dyn, s, a, use_lds); break;
-		case 64: hipLaunchKernelGGL((k_attention<kBlock, 64, FUSED>), grid, dim3(kBlock), dyn, s, a, use_lds); break;
-		case 128: hipLaunchKernelGGL((k_attention<kBlock, 128, FUSED>), grid, dim3(kBlock), dyn, s, a, use_lds); break;
-		case 256: hipLaunchKernelGGL((k_attention<kBlock, 256, FUSED>), grid, dim3(kBlock), dyn, s, a, use_lds); break;
+		case 32:
+			if (use_lds) hipLaunchKernelGGL((k_attention<kBlock, 32, FUSED, true>), grid, dim3(kBlock), dyn, s, a);
+			else hipLaunchKernelGGL((k_attention<kBlock, 32, FUSED, false>), grid, dim3(kBlock), dyn, s, a);
+			break;
+		case 64:
+			if (use_lds) hipLaunchKernelGGL((k_attention<kBlock, 64, FUSED, true>), grid, dim3(kBlock), dyn, s, a);
+			else hipLaunchKernelGGL((k_attention<kBlock, 64, FUSED, false>), grid, dim3(kBlock), dyn, s, a);
+			break;
+		case 128:
+			if (use_lds) hipLaunchKernelGGL((k_attention<kBlock, 128, FUSED, true>), grid, dim3(kBlock), dyn, s, a);
+			else hipLaunchKernelGGL((k_attention<kBlock, 128, FUSED, false>), grid, dim3(kBlock), dyn, s, a);
+			break;
+		case 256:
+			if (use_lds) hipLaunchKernelGGL((k_attention<kBlock, 256, FUSED, true>), grid, dim3(kBlock), dyn, s, a);
+			else hipLaunchKernelGGL((k_attention<kBlock, 256, FUSED, false>), grid, dim3(kBlock), dyn, s, a);
+			break;
 		default: no_instance("attention", a.D);
 	}
 }
