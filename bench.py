@@ -108,8 +108,8 @@ def traffic_from(fetch_csv, write_csv):
     `bench.py --phase decode --pmc-steps --calibrate` (decode steps only, so the dispatches are the
     step's own mix): FETCH_SIZE and WRITE_SIZE (KiB per dispatch), each scaled by what the counter
     reads for the calibration copy of known size, averaged per (kernel, grid) and over every
-    M <= 16 GEMV dispatch (k_gemv_pk<1, ...>, k_gemv_sk<1, ...> and k_gemv_w; the prompts' prefill
-    runs M = 32 instances, k_gemv_pk<2, ...> and k_gemv_sk<2, ...>)."""
+    M <= 16 GEMV dispatch (k_gemv_pk<1, ...>, k_gemv_sk<1, ...> and the LM head's k_gemv_head<1, ...>;
+    the prompts' prefill runs M = 32 instances, k_gemv_pk<2, ...> and k_gemv_sk<2, ...>)."""
     def per_dispatch(path, counter):
         vals, meta = defaultdict(float), {}
         for r in csv.DictReader(open(path)):
@@ -129,7 +129,7 @@ def traffic_from(fetch_csv, write_csv):
     w_scale = CALIBRATION_BYTES / (max(write[copy_key]) * 1024.0)
     kernels = []
     for (name, blocks), fv in sorted(fetch.items(), key=lambda kv: kv[0][1]):
-        if "k_gemv_pk<1," not in name and "k_gemv_sk<1," not in name and "k_gemv_w<" not in name:
+        if "k_gemv_pk<1," not in name and "k_gemv_sk<1," not in name and "k_gemv_head<1," not in name:
             continue
         f = np.mean(fv) * 1024.0 * f_scale
         w = np.mean(write.get((name, blocks), [0.0])) * 1024.0 * w_scale
@@ -543,7 +543,7 @@ def main():
             "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                          "kernel": "decode GEMV on the packed weight copy (k_gemv_pk for q|k|v, o and gate|up with "
-                                   "their epilogues, k_gemv_sk split-K planes for down, k_gemv_w for the LM head): "
+                                   "their epilogues, k_gemv_sk split-K planes for down, k_gemv_head for the LM head): "
                                    "the 113 GEMV launches of one step at M = 16 (28 layers' "
                                    "q|k|v, o, gate|up, down with their own weights, then the LM head) back to back "
                                    "between two HIP events on the library's stream, so every weight byte streams "
