@@ -198,3 +198,16 @@ def test_wide_mixed_schema_batch_matches_reference(hip_lib, ref_lib):
         h = _mixed(hip_lib, art, L, L, mode, n=72)
         assert h[0] == r[0], "tokens differ"
         assert h[1] == r[1] and h[2] == r[2] and h[3] == r[3]
+
+
+def test_mid_mixed_schema_batch_matches_reference(hip_lib, ref_lib):
+    """24 sequences in one call: the LM head runs on the packed copy with two 16-token row groups
+    (k_gemv_head<2, ...>), the schema masks applied in its argmax epilogue."""
+    sm, art = schema_artifact()
+    L = sm.config.layers
+    for mode in (0, 1):
+        print(f"case mid mixed mode={mode}", flush=True)
+        r = _mixed(ref_lib, art, L, L, mode, n=24)
+        h = _mixed(hip_lib, art, L, L, mode, n=24)
+        assert h[0] == r[0], "tokens differ"
+        assert h[1] == r[1] and h[2] == r[2] and h[3] == r[3]
