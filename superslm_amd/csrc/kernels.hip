@@ -2239,7 +2239,8 @@ __global__ __launch_bounds__(BS) void k_qkv_post(sslm_launch::QkvPostArgs a) {
 	if ((threadIdx.x & 63) == 0 && sat) atomicAdd(&a.sat[ti.slot], (unsigned long long)sat);
 }
 
-__global__ __launch_bounds__(256) void k_slot_state_copy(sslm_launch::SlotCopyArgs a, int restore) {
+// Looped form of k_slot_state_copy for rows or K/V spans past its fixed per-thread counts.
+__global__ __launch_bounds__(256) void k_slot_state_copy_any(sslm_launch::SlotCopyArgs a, int restore) {
 	const TokenInfo ti = a.tok[blockIdx.x];
 	const int64_t slot = ti.slot;
 	int8_t* live = a.codes + slot * a.H;
@@ -2257,7 +2258,6 @@ __global__ __launch_bounds__(256) void k_slot_state_copy(sslm_launch::SlotCopyAr
 			a.snap_sat[slot] = a.sat[slot];
 		}
 	}
-	// the K and V rows of layers [l0, l1) at the token's position, 16 bytes per thread
 	const int KVH = a.NKV * a.D, per_layer = 2 * KVH;
 	if (ti.pos < 0 || ti.pos >= a.cap) return;
 	const int64_t half = a.cap * (int64_t)KVH;
@@ -2270,6 +2270,63 @@ __global__ __launch_bounds__(256) void k_slot_state_copy(sslm_launch::SlotCopyAr
 		int4* sp = (int4*)(srow + (int64_t)l * per_layer + r);
 		if (restore) *kvp = *sp;
 		else *sp = *kvp;
+	}
+}
+
+// Every load of the block is issued before the first store (16-byte vectors, clamped indices, a
+// fixed unrolled count per thread), so the copy is one memory round trip rather than one per
+// loop iteration.
+constexpr int kSnapKvPer = 8;  // K/V chunks of 16 bytes per thread: (l1 - l0) 2 NKV D <= 32 KB
+
+__global__ __launch_bounds__(256) void k_slot_state_copy(sslm_launch::SlotCopyArgs a, int restore) {
+	const TokenInfo ti = a.tok[blockIdx.x];
+	const int64_t slot = ti.slot;
+	int8_t* live = a.codes + slot * a.H;
+	int8_t* snap = a.snap_codes + slot * a.H;
+	const int8_t* csrc = restore ? snap : live;
+	int8_t* cdst = restore ? live : snap;
+	// the stream row: H / 16 vectors (H is a multiple of 16), one per thread
+	const int nv = a.H / 16, vi = min((int)threadIdx.x, nv - 1);
+	const int4 cv = ((const int4*)csrc)[vi];
+	const Scale sc = restore ? a.snap_scale[slot] : a.scale[slot];
+	const unsigned long long sv = restore ? a.snap_sat[slot] : a.sat[slot];
+	// the K and V rows of layers [l0, l1) at the token's position
+	const int KVH = a.NKV * a.D, per_layer = 2 * KVH;
+	const bool pos_ok = ti.pos >= 0 && ti.pos < a.cap;
+	const int64_t pos = pos_ok ? ti.pos : 0;
+	const int64_t half = a.cap * (int64_t)KVH;
+	int8_t* blk = a.kv_pool + (int64_t)ti.block * a.block_bytes;
+	int8_t* srow = a.snap_kv + slot * a.snap_kv_ld;
+	const int nc = (a.l1 - a.l0) * per_layer / 16;
+	int4* kvp[kSnapKvPer];
+	int4* sp[kSnapKvPer];
+	int4 kv[kSnapKvPer];
+#pragma unroll
+	for (int k = 0; k < kSnapKvPer; ++k) {
+		const int c = min((int)threadIdx.x + k * 256, nc - 1);
+		const int e = c * 16, l = a.l0 + e / per_layer, r = e % per_layer;
+		const int kvsel = r >= KVH, hd = (r - kvsel * KVH) / a.D, d = (r - kvsel * KVH) % a.D;
+		kvp[k] = (int4*)(blk + (int64_t)l * half * 2 + kvsel * half + ((int64_t)hd * a.cap + pos) * a.D + d);
+		sp[k] = (int4*)(srow + (int64_t)l * per_layer + r);
+		kv[k] = restore ? *sp[k] : *kvp[k];
+	}
+	if ((int)threadIdx.x < nv) ((int4*)cdst)[threadIdx.x] = cv;
+	if (threadIdx.x == 0) {
+		if (restore) {
+			a.scale[slot] = sc;
+			a.sat[slot] = sv;
+		} else {
+			a.snap_scale[slot] = sc;
+			a.snap_sat[slot] = sv;
+		}
+	}
+	if (!pos_ok) return;
+#pragma unroll
+	for (int k = 0; k < kSnapKvPer; ++k) {
+		if ((int)threadIdx.x + k * 256 < nc) {
+			if (restore) *kvp[k] = kv[k];
+			else *sp[k] = kv[k];
+		}
 	}
 }
 
@@ -4495,7 +4552,11 @@ void qkv_post(const QkvPostArgs& a, hipStream_t s) {
 }
 
 void slot_state_copy(const SlotCopyArgs& a, int n, bool restore, hipStream_t s) {
-	hipLaunchKernelGGL(k_slot_state_copy, dim3(n), dim3(256), 0, s, a, restore ? 1 : 0);
+	const int64_t nc = (int64_t)(a.l1 - a.l0) * 2 * a.NKV * a.D / 16;
+	if (a.H % 16 == 0 && a.H <= 16 * 256 && nc >= 1 && nc <= 256 * kSnapKvPer)
+		hipLaunchKernelGGL(k_slot_state_copy, dim3(n), dim3(256), 0, s, a, restore ? 1 : 0);
+	else
+		hipLaunchKernelGGL(k_slot_state_copy_any, dim3(n), dim3(256), 0, s, a, restore ? 1 : 0);
 }
 
 void kv_commit(const QkvPostArgs& a, hipStream_t s) {
