@@ -796,13 +796,18 @@ __global__ __launch_bounds__(256) void k_pack_gemv(const int8_t* w, int N, int K
 // maximum, stores, in straight-line code) or kPkGeneral (any projection epilogue).
 enum PkEpi { kPkRaw = 0, kPkFunnel = 1, kPkGeneral = 2 };
 
-template <int MB, int NT, int CPW, int EPI>
-__global__ __launch_bounds__(256) void k_gemv_pk(GemmArgs g) {
-	__shared__ v4i red[2][kGemvWaves][MB][64];
+// NW = 8 (two row groups, K past 16 chunks): eight waves of CPW chunks each instead of four, so a
+// wave's activation rows stay in registers (at four waves and seven chunks the compiler reloaded
+// them before each MFMA, and every such wait also waited for the prefetched weights); wave w then
+// finishes token row w % 4 of row group w / 4.
+template <int MB, int NT, int CPW, int EPI, int NW = kGemvWaves>
+__global__ __launch_bounds__(64 * NW) void k_gemv_pk(GemmArgs g) {
+	static_assert(NW == kGemvWaves || (NW == 2 * kGemvWaves && MB == 2), "eight waves only for two row groups");
+	__shared__ v4i red[2][NW][MB][64];
 	const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, ri = lane & 15, grp = lane >> 4;
 	const int C = g.K >> 7, T = (g.N + 15) / 16;
 	const v4i z = v4i{0, 0, 0, 0};
-	// the weights of the first two tiles go out first: they need only wp, K and N
+	// the first tile's weights go out first: they need only wp, K and N
 	// a tile's weights, and its column's fold parameters, bias and segment fields, all fetched two
 	// tiles ahead so that no epilogue waits on a load
 	struct Slot {
@@ -824,7 +829,6 @@ __global__ __launch_bounds__(256) void k_gemv_pk(GemmArgs g) {
 		}
 	};
 	load_w(0, S[0]);
-	if (NT > 1) load_w(1, S[1]);
 	v4i x[MB][CPW][2];
 #pragma unroll
 	for (int mb = 0; mb < MB; ++mb) {
@@ -841,6 +845,8 @@ __global__ __launch_bounds__(256) void k_gemv_pk(GemmArgs g) {
 			x[mb][i][1] = ok ? a1 : z;
 		}
 	}
+	// the second tile's weights after the activations, so the first tile's MFMAs wait for neither
+	if (NT > 1) load_w(1, S[1]);
 	const Epilogue& e = g.epi;
 	int32_t* const raw_out = e.raw_out;
 	constexpr bool proj = EPI != kPkRaw;
@@ -867,7 +873,7 @@ __global__ __launch_bounds__(256) void k_gemv_pk(GemmArgs g) {
 	const Scale* const in_scale = e.in_scale;
 #pragma unroll
 	for (int mb = 0; mb < MB; ++mb) {
-		const int tk = min(mb * 16 + grp * 4 + wave, g.M - 1);
+		const int tk = min(mb * 16 + grp * 4 + (wave & 3), g.M - 1);
 		p_rcp[mb] = EPI == kPkGeneral ? *(in_recip ? in_recip + tk : (const int64_t*)wp) : 0;
 		p_ein[mb] = EPI == kPkGeneral ? (in_scale ? in_scale + tk : (const Scale*)wp)->e : 0;
 	}
@@ -904,10 +910,11 @@ __global__ __launch_bounds__(256) void k_gemv_pk(GemmArgs g) {
 		const int jj = j - sg.n_begin;
 #pragma unroll
 		for (int mb = 0; mb < MB; ++mb) {
+			if (NW != kGemvWaves && mb != (wave >> 2)) continue;  // (wave-uniform)
 			int32_t tot = 0;
 #pragma unroll
-			for (int w = 0; w < kGemvWaves; ++w) tot += ((const int32_t*)&red[i & 1][w][mb][lane])[wave];
-			const int tk = mb * 16 + grp * 4 + wave;
+			for (int w = 0; w < NW; ++w) tot += ((const int32_t*)&red[i & 1][w][mb][lane])[wave & 3];
+			const int tk = mb * 16 + grp * 4 + (wave & 3);
 			const bool live = col_ok && tk < g.M;
 			if (EPI == kPkRaw) {
 				if (live) raw_out[(size_t)tk * g.N + j] = tot;
@@ -4273,6 +4280,16 @@ static int pk_epi(const GemmArgs& g) {
 
 template <int MB, int NT, int EPI>
 static bool launch_pk_nt(const GemmArgs& g, int grid, int cpw, hipStream_t s) {
+	if constexpr (MB == 2 && NT >= 5) {
+		// two row groups over more than 16 chunks and several tiles per block: eight waves of 4
+		// (7B gate|up at M = 32: 30.5 -> 29.1 us; with 2-3 tiles per block, q|k|v and o, the
+		// larger block's fixed costs lost more: 8.6 -> 9.6 and 6.8 -> 7.5 us)
+		if (cpw > 4) {
+			if ((g.K / 128 + 7) / 8 > 4) return false;
+			hipLaunchKernelGGL((k_gemv_pk<MB, NT, 4, EPI, 2 * kGemvWaves>), dim3(grid), dim3(64 * 2 * kGemvWaves), 0, s, g);
+			return true;
+		}
+	}
 	switch (cpw) {
 #define X(W) \
 	case W: hipLaunchKernelGGL((k_gemv_pk<MB, NT, W, EPI>), dim3(grid), dim3(256), 0, s, g); return true;
