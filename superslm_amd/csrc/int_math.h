@@ -317,34 +317,56 @@ struct FunnelOut {
 	Scale out;
 };
 
-// By-value form with at most two incoming factors.  Inlined: in the row kernels its inputs are
-// wave-uniform, so it compiles to scalar code.
-SSLM_HD FunnelOut funnel_plan_v(uint64_t d_prime, int n_in, Scale in0, Scale in1, Scale site) {
-	FunnelOut o{};
-	o.st = kCarriedScaleMantissaOutOfDomain;
-	if ((n_in > 0 && !fits_i32(in0.m)) || (n_in > 1 && !fits_i32(in1.m))) return o;
-	if (!fits_i32(site.m)) return o;
-	if (d_prime < 1) d_prime = 1;
-	if (d_prime > ((uint64_t)1 << 31)) {
-		o.st = kChainInputOutOfDomain;
-		return o;
+// reciprocal_fast for a normalized dn in [2^30, 2^31), the only divisors a funnel plan has.  On the
+// GPU the estimate of 2^62 / dn is the hardware double reciprocal refined by one Newton step
+// (relative error near 2^-50, so within one of the quotient, which lies in (2^31, 2^32]) and
+// converted with one unsigned 32-bit conversion (it saturates at 2^32 - 1 only for dn = 2^30,
+// which the first correction step lifts to 2^32); the reference's two correction steps follow.
+// Checked equal to reciprocal_fast for every dn in [2^30, 2^31) by tests/reciprocal_norm_check.
+SSLM_HD int64_t reciprocal_norm(int64_t dn) {
+#if defined(__HIP_DEVICE_COMPILE__)
+	const double dd = (double)dn;
+	double r = __builtin_amdgcn_rcp(dd);
+	r = fma(r, fma(-dd, r, 1.0), r);
+	int64_t y = (int64_t)__double2uint_rz(4611686018427387904.0 * r);
+	for (int i = 0; i < 2; ++i) {
+		const int64_t res2 = (((int64_t)1 << 62) - y * dn) * 2;
+		y += res2 >= dn ? 1 : (res2 < -dn ? -1 : 0);
 	}
+	return y;
+#else
+	return reciprocal_fast(dn);
+#endif
+}
+
+// By-value form with at most two incoming factors.  Inlined: in the row kernels its inputs are
+// wave-uniform, so it compiles to scalar code.  Every part is computed and the status is chosen
+// at the end, in the reference's order (the incoming and site mantissas, then D', then the folds):
+// without early returns the reciprocal and the scale folds interleave (a dependent chain of plans
+// took 318 ns each with them, 198 ns without and with reciprocal_norm).
+SSLM_HD FunnelOut funnel_plan_v(uint64_t d_prime, int n_in, Scale in0, Scale in1, Scale site) {
+	const bool ok_in = !((n_in > 0 && !fits_i32(in0.m)) || (n_in > 1 && !fits_i32(in1.m))) && fits_i32(site.m);
+	const uint64_t d = d_prime < 1 ? 1 : d_prime;
+	const bool ok_d = d <= ((uint64_t)1 << 31);
 	int s;
-	const int64_t dn = normalize_scale((int64_t)d_prime, &s);
-	const int64_t r = reciprocal_fast(dn);
+	const int64_t dn = normalize_scale((int64_t)(ok_d ? d : 1), &s);
+	const int64_t r = reciprocal_norm(dn);
 	Scale run = site;
+	bool ok_mid = true;
 	if (n_in > 0) {
 		run = in0;
 		if (n_in > 1) {
 			run = combine_scale(run, in1);
-			if (!fits_i32(run.m)) return o;
+			ok_mid = fits_i32(run.m);
 		}
 		run = combine_scale(run, site);
 	}
-	if (!fits_i32(run.m)) return o;
+	const bool ok1 = fits_i32(run.m);
 	run = combine_scale(run, Scale{dn, -(int64_t)s});
-	if (!fits_i32(run.m)) return o;
-	o.st = kOk;
+	const bool ok2 = fits_i32(run.m);
+	FunnelOut o{};
+	o.st = !ok_in ? kCarriedScaleMantissaOutOfDomain
+	              : (!ok_d ? kChainInputOutOfDomain : (ok_mid && ok1 && ok2 ? kOk : kCarriedScaleMantissaOutOfDomain));
 	o.s = s;
 	o.r = r;
 	o.out = run;
