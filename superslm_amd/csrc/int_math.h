@@ -160,9 +160,8 @@ SSLM_HD int64_t div_floor_pos(int64_t n, int64_t d) {
 // round_half_up(2^62 / dn) for a canonical dn in [2^30, 2^31) -- the value the reference's
 // corrected-Newton DynamicScaleReciprocal returns on that domain (src/intmath.cpp:303-333; its
 // contract, include/superslm/intmath.h:124-131, is correct rounding over the whole normalized
-// domain).  Outside it the reference recurrence itself is replayed.
-SSLM_HD int64_t reciprocal_fast(int64_t dn) {
-	if (dn < ((int64_t)1 << 30) || dn >= ((int64_t)1 << 31)) return reciprocal(dn);
+// domain) -- from a correctly rounded double quotient and the reference's correction rule.
+SSLM_HD int64_t reciprocal_div(int64_t dn) {
 	int64_t y = (int64_t)(4611686018427387904.0 / (double)dn);
 	for (int i = 0; i < 2; ++i) {  // the reference's correction rule: -dn <= 2(2^62 - y dn) < dn
 		// y is within a few units of 2^62 / dn < 2^32, so y * dn < 2^63 and the residue is small:
@@ -175,6 +174,19 @@ SSLM_HD int64_t reciprocal_fast(int64_t dn) {
 		}
 	}
 	return y;
+}
+
+SSLM_HD int64_t reciprocal_norm(int64_t dn);
+
+// reciprocal_div on the normalized domain (reciprocal_norm on the GPU: the same values, by an
+// exhaustive check); outside it the reference recurrence itself is replayed.
+SSLM_HD int64_t reciprocal_fast(int64_t dn) {
+	if (dn < ((int64_t)1 << 30) || dn >= ((int64_t)1 << 31)) return reciprocal(dn);
+#if defined(__HIP_DEVICE_COMPILE__)
+	return reciprocal_norm(dn);
+#else
+	return reciprocal_div(dn);
+#endif
 }
 
 // src/intmath.cpp:476-490 -- clamp(round_away(x*127*R / 2^(62-s)), +-127).
@@ -246,12 +258,17 @@ SSLM_HD int64_t isqrt(int64_t n) {
 
 // floor(sqrt(n)) -- the value isqrt() returns for every int64 n (0 for n <= 0) -- from a
 // double-precision estimate corrected with exact 64-bit squares.
+// The double estimate is within one of floor(sqrt(n)) for every int64 n (n rounds to a double by
+// at most 2^10, which moves the root by far less than one; the root rounds by at most 2^-21), so
+// two fixed correction steps each way replace the loops (no loop: straight-line code on the GPU;
+// (r + 1)^2 <= 3037000500^2 < 2^64 cannot wrap).
 SSLM_HD int64_t isqrt_fast(int64_t n) {
-	if (n <= 0) return 0;
-	const uint64_t un = (uint64_t)n;
-	uint64_t r = (uint64_t)sqrt((double)n);
-	while (r * r > un) --r;
-	while ((r + 1) * (r + 1) <= un) ++r;
+	const uint64_t un = n > 0 ? (uint64_t)n : 0;
+	uint64_t r = (uint64_t)sqrt((double)un);
+#pragma unroll
+	for (int i = 0; i < 2; ++i) r -= r * r > un ? 1 : 0;
+#pragma unroll
+	for (int i = 0; i < 2; ++i) r += (r + 1) * (r + 1) <= un ? 1 : 0;
 	return (int64_t)r;
 }
 
@@ -317,12 +334,12 @@ struct FunnelOut {
 	Scale out;
 };
 
-// reciprocal_fast for a normalized dn in [2^30, 2^31), the only divisors a funnel plan has.  On the
+// reciprocal_div for a normalized dn in [2^30, 2^31), the only divisors a funnel plan has.  On the
 // GPU the estimate of 2^62 / dn is the hardware double reciprocal refined by one Newton step
 // (relative error near 2^-50, so within one of the quotient, which lies in (2^31, 2^32]) and
 // converted with one unsigned 32-bit conversion (it saturates at 2^32 - 1 only for dn = 2^30,
 // which the first correction step lifts to 2^32); the reference's two correction steps follow.
-// Checked equal to reciprocal_fast for every dn in [2^30, 2^31) by tests/reciprocal_norm_check.
+// Checked equal to reciprocal_div for every dn in [2^30, 2^31) by tests/reciprocal_norm_check.
 SSLM_HD int64_t reciprocal_norm(int64_t dn) {
 #if defined(__HIP_DEVICE_COMPILE__)
 	const double dd = (double)dn;
@@ -335,7 +352,7 @@ SSLM_HD int64_t reciprocal_norm(int64_t dn) {
 	}
 	return y;
 #else
-	return reciprocal_fast(dn);
+	return reciprocal_div(dn);
 #endif
 }
 

@@ -1,6 +1,6 @@
 """The GPU reciprocal of the funnel plans (`reciprocal_norm`, superslm_amd/csrc/int_math.h:
 double reciprocal, one Newton step, one u32 conversion, the reference's two correction steps)
-equals `reciprocal_fast` -- round_half_up(2^62 / dn), src/intmath.cpp:303-333, pinned against the
+equals `reciprocal_div` -- round_half_up(2^62 / dn), src/intmath.cpp:303-333, pinned against the
 oracle by the host tests -- for every normalized divisor dn in [2^30, 2^31).  The check program
 is built by __graft_entry__.build() (tests/reciprocal_norm_check.hip)."""
 import os
