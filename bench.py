@@ -421,7 +421,7 @@ def main():
         return
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
-              "(sequences shard across GPUs with no exchange; see DESIGN.md)", file=sys.stderr)
+              "(decode sequences shard across GPUs with no exchange: each GPU runs its own pool)", file=sys.stderr)
         sys.exit(2)
 
     hip = SslmLib(os.path.join(ROOT, "superslm_amd", "libsslm_hip.so"))
