@@ -3361,7 +3361,17 @@ __global__ __launch_bounds__(64 * NW, NW == 4 ? 3 : 1) void k_attention_tiled(ss
 	for (int i = 0; i < DTW; ++i)
 #pragma unroll
 		for (int k = 0; k < 3; ++k) cacc[i][k] = v4i{0, 0, 0, 0};
+	// a step's V rows are issued before its probabilities are computed and stored to LDS after
+	// them (16-byte copies; rows past the cap repeat the last one)
+	constexpr int VCH = KB * (D / 16), VPT = (VCH + 64 * NW - 1) / (64 * NW);  // V chunks per thread
 	for (int blk = 0; blk < nblk; ++blk) {
+		v4i vr[VPT];
+#pragma unroll
+		for (int u = 0; u < VPT; ++u) {
+			const int c = min((int)threadIdx.x + u * 64 * NW, VCH - 1);
+			const int64_t pos = min(blk * KB + c / (D / 16), (int)a.cap - 1);
+			vr[u] = load16(vbase + pos * D + (c % (D / 16)) * 16);
+		}
 		int p;
 		v4i s = v4i{0, 0, 0, 0};
 		if (ecache) p = blk * KB + wave * 16 + ri;
@@ -3380,11 +3390,11 @@ __global__ __launch_bounds__(64 * NW, NW == 4 ? 3 : 1) void k_attention_tiled(ss
 			s_p[1][g * 4 + v][pl] = (int8_t)((pr >> 7) & 127);
 			s_p[2][g * 4 + v][pl] = (int8_t)(pr & 127);
 		}
-		// the step's V rows, as stored (16-byte copies; rows past the cap repeat the last one)
-		for (int c = threadIdx.x; c < KB * (D / 16); c += 64 * NW) {
-			const int pr = c / (D / 16), ch = c % (D / 16);
-			const int64_t pos = min(blk * KB + pr, (int)a.cap - 1);
-			*(v4i*)&s_v[pr][ch * 16] = load16(vbase + pos * D + ch * 16);
+		// the step's V rows, as stored
+#pragma unroll
+		for (int u = 0; u < VPT; ++u) {
+			const int c = (int)threadIdx.x + u * 64 * NW;
+			if (c < VCH) *(v4i*)&s_v[c / (D / 16)][(c % (D / 16)) * 16] = vr[u];
 		}
 		__syncthreads();
 #pragma unroll
