@@ -72,6 +72,12 @@ __device__ __forceinline__ uint32_t sat_abs_u32(int64_t v) {
 	return a > 0xfffffffeull ? 0xfffffffeu : (uint32_t)a;
 }
 
+// The row of a one-block-per-row launch: workgroups go to the 8 XCDs in turn (block b on XCD
+// b % 8), so giving each XCD a contiguous run of rows keeps a tile-major maxima array's lines
+// ([tile][row], 32 rows to a line) in one XCD's L2 instead of fetched by all eight.  Identity
+// when the row count is not a multiple of 8.
+__device__ __forceinline__ int xcd_row(int b, int n) { return (n & 7) ? b : (b & 7) * (n >> 3) + (b >> 3); }
+
 __device__ __forceinline__ int32_t sat_i32(int64_t v) {
 	return v > kI32Max ? kI32Max : (v < kI32Min ? kI32Min : (int32_t)v);
 }
@@ -2099,7 +2105,7 @@ template <int BS, int EQ, int RS>
 __global__ __launch_bounds__(BS) void k_qkv_post(sslm_launch::QkvPostArgs a) {
 	__shared__ uint32_t s_red[BS / 64];
 	__shared__ int32_t s_st;
-	const int t = blockIdx.x;
+	const int t = xcd_row(blockIdx.x, gridDim.x);
 	const TokenInfo ti = a.tok[t];
 	const Scale ns = a.in_scale[t];
 	const int H = a.H, D = a.D, pairs = D / 2;
@@ -2368,7 +2374,7 @@ template <int BS, int EPT>
 __global__ __launch_bounds__(BS) void k_funnel(sslm_launch::FunnelArgs a) {
 	__shared__ uint32_t s_m[BS / 64];
 	__shared__ int32_t s_st;
-	const int t = blockIdx.x, N = a.N;
+	const int t = xcd_row(blockIdx.x, gridDim.x), N = a.N;
 	const int slot = a.tok[t].slot;
 	const int32_t* frow = a.f + (size_t)t * a.ld_f;
 	// the maxima, scales and status words first, then the row: the plan needs only the former, so
@@ -2570,7 +2576,7 @@ void k_mlp_act(sslm_launch::ActArgs a) {
 	__shared__ int32_t sig[256];
 	__shared__ int32_t s_silu[1025];  // the SiLU node table, loaded with the row
 	__shared__ int32_t s_st;
-	const int t = blockIdx.x, I = a.I;
+	const int t = xcd_row(blockIdx.x, gridDim.x), I = a.I;
 	const int slot = a.tok[t].slot;
 	const int32_t* gfr = a.gu_f + (size_t)t * 2 * I;
 	const int32_t* ufr = gfr + I;
