@@ -2300,7 +2300,7 @@ __global__ __launch_bounds__(256) void k_slot_state_copy(sslm_launch::SlotCopyAr
 	int8_t* cdst = restore ? live : snap;
 	// the stream row: H / 16 vectors (H is a multiple of 16), one per thread
 	const int nv = a.H / 16, vi = min((int)threadIdx.x, nv - 1);
-	const int4 cv = ((const int4*)csrc)[vi];
+	const v4i cv = load16(csrc + vi * 16);
 	const Scale sc = restore ? a.snap_scale[slot] : a.scale[slot];
 	const unsigned long long sv = restore ? a.snap_sat[slot] : a.sat[slot];
 	// the K and V rows of layers [l0, l1) at the token's position
@@ -2311,19 +2311,20 @@ __global__ __launch_bounds__(256) void k_slot_state_copy(sslm_launch::SlotCopyAr
 	int8_t* blk = a.kv_pool + (int64_t)ti.block * a.block_bytes;
 	int8_t* srow = a.snap_kv + slot * a.snap_kv_ld;
 	const int nc = (a.l1 - a.l0) * per_layer / 16;
-	int4* kvp[kSnapKvPer];
-	int4* sp[kSnapKvPer];
-	int4 kv[kSnapKvPer];
+	// vector loads and stores (ext_vector_type) keep kv[] in registers
+	int8_t* kvp[kSnapKvPer];
+	int8_t* sp[kSnapKvPer];
+	v4i kv[kSnapKvPer];
 #pragma unroll
 	for (int k = 0; k < kSnapKvPer; ++k) {
 		const int c = min((int)threadIdx.x + k * 256, nc - 1);
 		const int e = c * 16, l = a.l0 + e / per_layer, r = e % per_layer;
 		const int kvsel = r >= KVH, hd = (r - kvsel * KVH) / a.D, d = (r - kvsel * KVH) % a.D;
-		kvp[k] = (int4*)(blk + (int64_t)l * half * 2 + kvsel * half + ((int64_t)hd * a.cap + pos) * a.D + d);
-		sp[k] = (int4*)(srow + (int64_t)l * per_layer + r);
-		kv[k] = restore ? *sp[k] : *kvp[k];
+		kvp[k] = blk + (int64_t)l * half * 2 + kvsel * half + ((int64_t)hd * a.cap + pos) * a.D + d;
+		sp[k] = srow + (int64_t)l * per_layer + r;
+		kv[k] = load16(restore ? sp[k] : kvp[k]);
 	}
-	if ((int)threadIdx.x < nv) ((int4*)cdst)[threadIdx.x] = cv;
+	if ((int)threadIdx.x < nv) *(v4i*)(cdst + threadIdx.x * 16) = cv;
 	if (threadIdx.x == 0) {
 		if (restore) {
 			a.scale[slot] = sc;
@@ -2337,8 +2338,7 @@ __global__ __launch_bounds__(256) void k_slot_state_copy(sslm_launch::SlotCopyAr
 #pragma unroll
 	for (int k = 0; k < kSnapKvPer; ++k) {
 		if ((int)threadIdx.x + k * 256 < nc) {
-			if (restore) *kvp[k] = kv[k];
-			else *sp[k] = kv[k];
+			*(v4i*)(restore ? kvp[k] : sp[k]) = kv[k];
 		}
 	}
 }

@@ -2210,7 +2210,6 @@ static sslm_status decode_batch(sslm_model m, sslm_seq* seqs, int32_t n, const s
 		Track& w = m->tracks[u % ntr];
 		const int M = (int)un.idx.size();
 		w.attn_wcap = unit_wcap(un);
-		w.attn_wcap = unit_wcap(un);
 		// snapshot of the rows this unit changes, restored if an earlier sequence of the call refuses
 		sslm_launch::slot_state_copy(slot_copy_args(m, w.tok, (int)un.l0, (int)un.l1), M, false, w.stream);
 		ck(hipGetLastError());
