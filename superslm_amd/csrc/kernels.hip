@@ -2387,14 +2387,18 @@ __global__ __launch_bounds__(BS) void k_funnel(sslm_launch::FunnelArgs a) {
 	const int32_t hs = a.head_status ? hs0 : kHeadStatusNone;  // the first refusing head of the attention
 	int32_t fv[EPT];
 	load_row_raw<BS>(frow, N, fv);
+	asm volatile("" ::"s"(st0), "s"(hs0));  // both status loads issued together, ahead of the branch
 	if (threadIdx.x == 0) {
-		int32_t sv = st0;
+		// each branch stores its own value: through a join, the rare path's re-read would make
+		// the common path wait for every load of wave 0 (its row included) before the reduction
 		if (hs != kHeadStatusNone) {  // rare: resolve the attention's refusal into the status
 			set_status(a.status, slot, a.layer, hs & 0xff);
 			a.head_status[slot] = kHeadStatusNone;
-			sv = a.status[slot];
+			s_st = a.status[slot];
+			asm volatile("" ::: "memory");
+		} else {
+			s_st = st0;
 		}
-		s_st = sv;
 	}
 	mx = blk_max32<BS>(mx, s_m);
 	if (s_st != 0) return;
