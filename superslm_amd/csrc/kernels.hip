@@ -2715,6 +2715,9 @@ __global__ __launch_bounds__(BS) void k_mlp_act_s1(sslm_launch::ActArgs a, int p
 		gv[k] = gfr[i];
 		uv[k] = ufr[i];
 	}
+	// the status word held from here: left to the compiler, its load sinks below the slice's and
+	// thread 0's store to LDS waits for the whole slice before the reduction
+	asm volatile("" ::"s"(st0));
 #pragma unroll
 	for (int k = 0; k < (1025 + BS - 1) / BS; ++k)
 		if (threadIdx.x + k * BS < 1025) s_silu[threadIdx.x + k * BS] = sv[k];
